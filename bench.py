@@ -1,0 +1,280 @@
+"""Paged decode-attention benchmark of the packed INT2/INT4 KV cache on one MI355X.
+
+Workload: an Ouro-1.4B-shaped layer, 16 query/KV heads,
+head_dim 128, 4 loops, batch 32, 8192 history tokens per sequence, one
+query token per sequence, page size 16, schedule [2,32]x3+[4,32] with the
+INT4 anchor at loop 3, least-squares coefficients, seeded random-sign
+Hadamard rotations on K and V.  One step = one decode step of the layer:
+the three residual-loop calls and the anchor-loop call.  The BF16 paged
+baseline runs the same four calls over a BF16 cache of the same shape.
+
+Prints ONE JSON line on stdout; everything else goes to stderr.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import platform
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+if ROOT not in sys.path:
+    sys.path.insert(0, ROOT)
+
+PEAK_HBM_GBPS = 8000.0
+SCHEDULE = ((2, 32), (2, 32), (2, 32), (4, 32))
+ANCHOR = 3
+
+
+def log(*args):
+    print(*args, file=sys.stderr, flush=True)
+
+
+def staged_call_bytes(batch, history, heads, dim, page_tokens, loop):
+    """Algorithmic HBM bytes of one decode call (packed pages + Q/K/V/out + page table)."""
+    from residualquant_amd.layout import staged_bytes
+
+    pages = (history + page_tokens - 1) // page_tokens
+    per_page = staged_bytes(dim, SCHEDULE, page_tokens, "anchor", ANCHOR, loop)
+    cache = batch * pages * heads * 2 * per_page
+    live = 4 * batch * heads * dim * 2
+    table = batch * pages * 4
+    return cache + live + table
+
+
+def bf16_call_bytes(batch, history, heads, dim):
+    return batch * history * heads * dim * 2 * 2 + 4 * batch * heads * dim * 2 + batch * (history // 16) * 4
+
+
+def build_packed_cache(torch, rq, workloads, batch, history, heads, dim, page_tokens, device, seed):
+    """Quantize synthetic K/V for every history token into a packed paged cache (on the GPU)."""
+    pages = (history + page_tokens - 1) // page_tokens
+    table = workloads.block_tables(batch, pages, seed + 5, device=device)
+    num_blocks = batch * pages
+    width = rq.page_width(dim, SCHEDULE)
+    cache = torch.zeros((2, num_blocks, heads, page_tokens, width), dtype=torch.uint8, device=device)
+    key_rotation = workloads.random_sign_rotation(heads, dim, seed + 3, device=device)
+    value_rotation = workloads.random_sign_rotation(heads, dim, seed + 4, device=device)
+    slots = workloads.history_slots(table, [history] * batch, page_tokens)
+    chunk = 16384
+    for start in range(0, slots.numel(), chunk):
+        part = slots[start:start + chunk]
+        pairs = workloads.loop_kv(part.numel(), heads, dim, len(SCHEDULE), seed + start, device=device)
+        rq.quantize(pairs, cache, part, key_rotation, value_rotation, None, SCHEDULE, "anchor", ANCHOR, "ls")
+        del pairs
+    torch.cuda.synchronize()
+    return cache, table, key_rotation, value_rotation
+
+
+def timed(torch, fn, steps, warmup):
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    start = time.perf_counter()
+    for _ in range(steps):
+        fn()
+    torch.cuda.synchronize()
+    return (time.perf_counter() - start) / steps
+
+
+def kernel_average_ms(torch, ops, fn, reps):
+    """Average split-K kernel duration from HIP events recorded on the launch stream."""
+    fn()
+    torch.cuda.synchronize()
+    ops.timing_read()
+    ops.timing_enable(True)
+    for _ in range(reps):
+        fn()
+    torch.cuda.synchronize()
+    ops.timing_enable(False)
+    ms, launches = ops.timing_read()
+    return ms / max(1, launches), launches
+
+
+def cpu_baseline(torch, rq, workloads, cache, table, key_rotation, value_rotation, query, key, value,
+                 heads, dim, history, page_tokens, budget_s):
+    """The CPU oracle (single thread) on a bounded sample of one residual-loop call."""
+    import numpy as np
+    from oracle import oracle
+
+    oracle.lib()
+    pages = (history + page_tokens - 1) // page_tokens
+    bits = workloads.bf16_bits
+    rows_done, elapsed, total_bytes = 0, 0.0, 0
+    kr, vr = bits(key_rotation), bits(value_rotation)
+    for row in range(query.size(0)):
+        blocks = table[row].long()
+        sub = cache[:, blocks].cpu().numpy()
+        sub_table = np.arange(pages, dtype=np.int32).reshape(1, pages)
+        start = time.perf_counter()
+        oracle.attention(bits(query[row:row + 1]), bits(key[row:row + 1]), bits(value[row:row + 1]), sub,
+                         np.array([0, 1], dtype=np.int32), np.array([history + 1], dtype=np.int32),
+                         sub_table, kr, vr, None, SCHEDULE, "anchor", ANCHOR, 0)
+        elapsed += time.perf_counter() - start
+        rows_done += 1
+        total_bytes += staged_call_bytes(1, history, heads, dim, page_tokens, 0)
+        if elapsed >= budget_s:
+            break
+    return {
+        "value": total_bytes / elapsed / 1e9,
+        "unit": "GB/s",
+        "cores": 1,
+        "kind": "port",
+        "sample": f"{rows_done} of {query.size(0)} rows of one residual-loop call (loop 0), "
+                  f"{history} history tokens x {heads} heads, oracle/rq_oracle.c single-threaded "
+                  f"FP64 attention over restored K/V; {elapsed:.2f} s; host {platform.processor() or 'cpu'}",
+        "us_per_row": elapsed / rows_done * 1e6,
+    }
+
+
+def main():
+    parser = argparse.ArgumentParser(description=__doc__)
+    parser.add_argument("--gpus", type=int, default=1)
+    parser.add_argument("--steps", type=int, default=20)
+    parser.add_argument("--warmup", type=int, default=5)
+    parser.add_argument("--batch", type=int, default=32)
+    parser.add_argument("--history", type=int, default=8192)
+    parser.add_argument("--cpu-budget", type=float, default=10.0,
+                        help="seconds of CPU oracle work for the cpu_baseline sample (0 = skip)")
+    parser.add_argument("--no-bf16", action="store_true")
+    args = parser.parse_args()
+
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one GPU only: this path has no multi-GPU component "
+              "(the reference forbids TP>1 and DCP>1); run with --gpus 1", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+
+    import residualquant_amd as rq
+    from residualquant_amd import ops, workloads
+
+    device = torch.device("cuda:0")
+    torch.cuda.set_device(device)
+    batch, history, heads, dim, page_tokens = args.batch, args.history, 16, 128, 16
+    seed = 2026
+
+    log(f"[bench] building packed cache B={batch} T={history} H={heads} D={dim}")
+    t0 = time.perf_counter()
+    cache, table, key_rotation, value_rotation = build_packed_cache(
+        torch, rq, workloads, batch, history, heads, dim, page_tokens, device, seed)
+    log(f"[bench] packed cache {tuple(cache.shape)} built in {time.perf_counter() - t0:.1f} s")
+
+    generator = torch.Generator(device=device).manual_seed(seed + 7)
+    query = torch.randn((batch, heads, dim), generator=generator, device=device).to(torch.bfloat16)
+    key = torch.randn((batch, heads, dim), generator=generator, device=device).to(torch.bfloat16)
+    value = torch.randn((batch, heads, dim), generator=generator, device=device).to(torch.bfloat16)
+    output = torch.empty_like(query)
+    qsl = torch.arange(batch + 1, dtype=torch.int32, device=device)
+    seq_lens = torch.full((batch,), history + 1, dtype=torch.int32, device=device)
+    workspace = torch.empty(ops.attention_workspace_bytes(batch, heads, dim, table.size(1), page_tokens),
+                            dtype=torch.uint8, device=device)
+
+    def call(loop):
+        rq.attention(query, key, value, cache, output, qsl, seq_lens, table, key_rotation, value_rotation,
+                     None, SCHEDULE, "anchor", ANCHOR, loop, workspace=workspace)
+
+    def step():
+        for loop in range(len(SCHEDULE)):
+            call(loop)
+
+    step_s = timed(torch, step, args.steps, args.warmup)
+    step_bytes = sum(staged_call_bytes(batch, history, heads, dim, page_tokens, loop) for loop in range(4))
+    log(f"[bench] packed step {step_s * 1e6:.1f} us")
+
+    residual_ms, residual_launches = kernel_average_ms(torch, ops, lambda: call(0), max(10, args.steps))
+    anchor_ms, _ = kernel_average_ms(torch, ops, lambda: call(ANCHOR), max(10, args.steps))
+    residual_bytes = staged_call_bytes(batch, history, heads, dim, page_tokens, 0)
+    anchor_bytes = staged_call_bytes(batch, history, heads, dim, page_tokens, ANCHOR)
+    residual_gbps = residual_bytes / (residual_ms * 1e-3) / 1e9
+    log(f"[bench] residual decode kernel {residual_ms * 1e3:.1f} us ({residual_gbps:.0f} GB/s), "
+        f"anchor {anchor_ms * 1e3:.1f} us")
+
+    bf16 = None
+    if not args.no_bf16:
+        del workspace
+        bf16_cache = torch.randn((2, cache.size(1), heads, page_tokens, dim), device=device,
+                                 generator=generator).to(torch.bfloat16)
+        bf16_ws = torch.empty(ops.attention_workspace_bytes(batch, heads, dim, table.size(1), page_tokens),
+                              dtype=torch.uint8, device=device)
+
+        def bf16_call():
+            rq.paged_attention_bf16(query, key, value, bf16_cache, output, qsl, seq_lens, table,
+                                    workspace=bf16_ws)
+
+        def bf16_step():
+            for _ in range(4):
+                bf16_call()
+
+        bf16_step_s = timed(torch, bf16_step, args.steps, args.warmup)
+        bf16_ms, _ = kernel_average_ms(torch, ops, bf16_call, max(10, args.steps))
+        bytes_bf16 = bf16_call_bytes(batch, history, heads, dim)
+        bf16 = {
+            "us_per_step": bf16_step_s * 1e6,
+            "us_per_call_kernel": bf16_ms * 1e3,
+            "kernel_GBps": bytes_bf16 / (bf16_ms * 1e-3) / 1e9,
+            "bytes_per_call": bytes_bf16,
+            "step_speedup_packed_vs_bf16": bf16_step_s / step_s,
+        }
+        log(f"[bench] bf16 step {bf16_step_s * 1e6:.1f} us, kernel {bf16_ms * 1e3:.1f} us "
+            f"({bf16['kernel_GBps']:.0f} GB/s)")
+        del bf16_cache, bf16_ws
+
+    cpu = None
+    if args.cpu_budget > 0:
+        log("[bench] cpu baseline (oracle) ...")
+        cpu = cpu_baseline(torch, rq, workloads, cache, table, key_rotation, value_rotation, query, key,
+                           value, heads, dim, history, page_tokens, args.cpu_budget)
+        log(f"[bench] cpu {cpu['value']:.3f} GB/s")
+
+    result = {
+        "metric": "paged decode-attn µs/step + achieved HBM GB/s (% peak), INT2/INT4 vs bf16, 1 GPU",
+        "value": step_bytes / step_s / 1e9,
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": step_s * 1e3,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "int2/int4 packed codes, fp32 accumulate",
+        "data": "synthetic (seeded anchor N(0,1) + loop residuals N(0,0.15^2), random-sign Hadamard rotations)",
+        "config": {
+            "workload": "C2 paged decode attention, Ouro-1.4B-shaped layer",
+            "batch": batch, "history_tokens": history, "heads": heads, "head_dim": dim, "loops": 4,
+            "page_tokens": page_tokens, "schedule": "[2,32]x3+[4,32] anchor 3 ls",
+            "step": "3 residual-loop calls + 1 anchor-loop call (prepare + split-K decode + merge each)",
+        },
+        "us_per_step": step_s * 1e6,
+        "pct_peak_step": 100.0 * step_bytes / step_s / 1e9 / PEAK_HBM_GBPS,
+        "bytes_per_step": step_bytes,
+        "tokens_per_s": batch / step_s,
+        "decode_kernel": {
+            "residual_loop_us": residual_ms * 1e3,
+            "anchor_loop_us": anchor_ms * 1e3,
+            "residual_loop_bytes": residual_bytes,
+            "anchor_loop_bytes": anchor_bytes,
+            "anchor_loop_GBps": anchor_bytes / (anchor_ms * 1e-3) / 1e9,
+        },
+        "roofline": {
+            "bound": "hbm",
+            "achieved": residual_gbps,
+            "peak": PEAK_HBM_GBPS,
+            "unit": "GB/s",
+            "frac": residual_gbps / PEAK_HBM_GBPS,
+            "traffic": None,
+            "kernel": "decode_kernel<128,4,32,2,32,true> (residual loop), "
+                      f"{residual_launches} HIP-event-timed launches",
+        },
+        "bf16_baseline": bf16,
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(result), flush=True)
+
+
+if __name__ == "__main__":
+    main()

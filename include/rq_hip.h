@@ -1,0 +1,153 @@
+/*
+ * rq_hip.h - C ABI of the MI355X-native ResidualQuant packed KV-cache path.
+ *
+ * One shared library (residualquant_amd/librq_hip.so, built for gfx950 with
+ * hipcc) exports these symbols.  Every entry point takes plain device
+ * pointers, sizes and strides (in elements), enqueues on the caller's HIP
+ * stream and returns 0 on success or a negative RQ_E* code; the message of
+ * the last failure on the calling thread is rq_last_error().  Validation of
+ * sizes, schedules and alignment happens on the host before any device work.
+ *
+ * Reference interface (heejunkim00/ResidualQuant, paths relative to
+ * plugins/residual_quantization/csrc/): the pybind11 ops attention()/quantize()
+ * declared at common/api.h:11-31 and exported at dispatch/binding.cpp:19-38.
+ */
+#ifndef RQ_HIP_H
+#define RQ_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#include <hip/hip_runtime_api.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum {
+    RQ_OK = 0,
+    RQ_EINVAL = -1,    /* invalid argument (TORCH_CHECK in the reference) */
+    RQ_ENOKERNEL = -2, /* no kernel for this geometry/schedule (kernel_registry.h:66-72) */
+    RQ_ELAUNCH = -3,   /* HIP launch or runtime error */
+    RQ_ENOSPACE = -4   /* workspace smaller than rq_attention_workspace_bytes() */
+};
+
+/* reference_mode */
+enum { RQ_MODE_ANCHOR = 0, RQ_MODE_ADJACENT = 1 };
+/* coefficient_method (quantize/types.h:4: Unit, Norm, LeastSquares) */
+enum { RQ_COEF_UNIT = 0, RQ_COEF_NORM = 1, RQ_COEF_LS = 2 };
+
+/* Library version, (major << 16) | minor. */
+int rq_version(void);
+
+/* Message of the last failed call on this thread ("" if none). */
+const char* rq_last_error(void);
+
+/*
+ * Bytes of one token row of a packed page: sum over records of
+ * D*bits/8 + 2*D/group + 2.  Replaces QuantizationRecord::Bytes /
+ * PackedLayout::PageWidth (common/cache.cuh:14-17, :78-80) and
+ * DeferredKVGroup.page_width (src/residual_quantization/install_model.py:34-38).
+ * Returns a negative code for an invalid schedule.
+ */
+int rq_page_width(int head_dim, int records, const int* bits, const int* groups);
+
+/*
+ * Quantize-on-write of one completed loop group into the paged cache.
+ * Replaces quantize() (quantize/api.cpp:8-95 -> launch_quantize,
+ * quantize/launch.cuh:43-86 -> quantize_kernel, quantize/kernel.cuh:332-355).
+ *
+ * key_ptrs[r], value_ptrs[r]: BF16 [rows_r, heads, head_dim], channel stride
+ *   1, head stride head_dim, token stride key_strides[r] / value_strides[r]
+ *   (elements); input_rows = min over inputs of rows_r (must be >= tokens).
+ * kv_cache: UINT8 [2, num_blocks, heads, page_tokens, page_width], contiguous.
+ * slot_mapping: INT64 [tokens]; slot < 0 leaves the cache untouched.
+ * key_rotation / value_rotation: FP16 [heads, D, D] or NULL (y = x . R).
+ * key_mean: FP32 [records, heads, D] or NULL (subtracted from K after rotation).
+ * bits[r], groups[r]: record schedule in loop order.
+ */
+int rq_quantize(int records, const void* const* key_ptrs, const int64_t* key_strides,
+                const void* const* value_ptrs, const int64_t* value_strides, int64_t input_rows,
+                void* kv_cache, int64_t num_blocks, int heads, int page_tokens, int page_width,
+                const int64_t* slot_mapping, int64_t tokens, int head_dim,
+                const void* key_rotation, const void* value_rotation, const float* key_mean,
+                const int* bits, const int* groups, int reference_mode, int anchor_index,
+                int coefficient, hipStream_t stream);
+
+/*
+ * Device workspace that rq_attention needs for `rows` query rows (query.size(0))
+ * and a page table of `max_pages` columns (block_table.size(1)).  Depends
+ * only on host shapes, so a captured graph can reuse one allocation.
+ */
+size_t rq_attention_workspace_bytes(int64_t rows, int heads, int head_dim, int64_t max_pages,
+                                    int page_tokens);
+
+/*
+ * Split-K paged decode attention over packed pages for loop `loop_index`.
+ * Replaces attention() (attention/api.cpp:8-115 -> launch_attention,
+ * attention/launch.cuh:33-132 -> prepare/compute/merge kernels).
+ *
+ * query, key, value, output: BF16 [rows, heads, head_dim] with the given
+ *   token strides (elements); key/value are the current token (not yet in
+ *   the cache).  Row i belongs to the request b with
+ *   query_start_loc[b] <= i < query_start_loc[b+1] and attends to
+ *   seq_lens[b]-1 history tokens read through block_table[b][t/page_tokens].
+ * block_table: INT32 [>= requests, max_pages], row stride block_table_stride.
+ * workspace: device memory of at least rq_attention_workspace_bytes(...).
+ */
+int rq_attention(const void* query, int64_t query_stride, const void* key, int64_t key_stride,
+                 const void* value, int64_t value_stride, void* output, int64_t output_stride,
+                 int64_t rows, int heads, int head_dim, const void* kv_cache, int64_t num_blocks,
+                 int page_tokens, int page_width, const int32_t* query_start_loc,
+                 const int32_t* seq_lens, int64_t requests, const int32_t* block_table,
+                 int64_t block_table_stride, int64_t max_pages, const void* key_rotation,
+                 const void* value_rotation, const float* key_mean, int records,
+                 const int* bits, const int* groups, int reference_mode, int anchor_index,
+                 int loop_index, void* workspace, size_t workspace_bytes, hipStream_t stream);
+
+/*
+ * Restore the BF16 K/V of `loop_index` at the given slots (rotated space,
+ * K including its mean): the record value the quantizer keeps as its
+ * reference (quantize/kernel.cuh:160-203; attention/compute.cuh:28-197).
+ * key_out / value_out: BF16 [tokens, heads, head_dim], contiguous; slot < 0
+ * gives zeros.  No counterpart op in the reference's Python surface; it
+ * exposes the reconstruction both reference kernels perform internally.
+ */
+int rq_dequantize(const void* kv_cache, int64_t num_blocks, int heads, int page_tokens,
+                  int page_width, const int64_t* slots, int64_t tokens, int head_dim,
+                  const float* key_mean, int records, const int* bits, const int* groups,
+                  int reference_mode, int anchor_index, int loop_index, void* key_out,
+                  void* value_out, hipStream_t stream);
+
+/*
+ * BF16 paged decode attention with the same split-K skeleton: the
+ * comparison baseline of the decode metric.  Cache BF16
+ * [2, num_blocks, heads, page_tokens, head_dim], contiguous.  No counterpart
+ * in the reference (it compares against vLLM's own BF16 backend).
+ */
+int rq_paged_attention_bf16(const void* query, int64_t query_stride, const void* key,
+                            int64_t key_stride, const void* value, int64_t value_stride,
+                            void* output, int64_t output_stride, int64_t rows, int heads,
+                            int head_dim, const void* cache, int64_t num_blocks, int page_tokens,
+                            const int32_t* query_start_loc, const int32_t* seq_lens,
+                            int64_t requests, const int32_t* block_table,
+                            int64_t block_table_stride, int64_t max_pages, void* workspace,
+                            size_t workspace_bytes, hipStream_t stream);
+
+/*
+ * Kernel timing for measurement: when enabled, rq_attention and
+ * rq_paged_attention_bf16 record HIP events around their split-K kernel on
+ * the caller's stream; rq_timing_read() synchronizes the recorded events and
+ * returns the summed milliseconds and the launch count, then clears them.
+ */
+void rq_timing_enable(int enabled);
+int rq_timing_read(double* milliseconds, int64_t* launches);
+
+/* Split-K sizing: target number of split-K workgroups per launch (0 = default). */
+void rq_set_split_target(int workgroups);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* RQ_HIP_H */

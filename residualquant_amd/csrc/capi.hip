@@ -1,0 +1,454 @@
+// extern "C" entry points of librq_hip.so (declared in include/rq_hip.h).
+//
+// Host-side validation mirrors the reference's TORCH_CHECKs
+// (plugins/residual_quantization/csrc/quantize/api.cpp:18-85,
+// attention/api.cpp:23-104, dispatch/kernel_registry.h:42-72) for what a
+// pointer-and-size interface can see; dtype/device/stride checks of tensors
+// belong to the caller (residualquant_amd/ops.py).  Every failure returns a
+// negative code and leaves its message in rq_last_error() for the thread.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cstdarg>
+#include <cstdio>
+#include <mutex>
+#include <string>
+#include <vector>
+
+#include "../../include/rq_hip.h"
+#include "rq_kernels.h"
+
+namespace {
+
+thread_local std::string g_last_error;
+
+int fail(int code, const char* format, ...) {
+    char buffer[512];
+    va_list args;
+    va_start(args, format);
+    std::vsnprintf(buffer, sizeof(buffer), format, args);
+    va_end(args);
+    g_last_error = buffer;
+    return code;
+}
+
+int ok() {
+    g_last_error.clear();
+    return RQ_OK;
+}
+
+int check_launch(hipError_t status, const char* what) {
+    if (status != hipSuccess) return fail(RQ_ELAUNCH, "%s: %s", what, hipGetErrorString(status));
+    return ok();
+}
+
+// Supported geometry: the head dims and page sizes the reference registers
+// (dispatch/schedules.cuh:147-148, attention/compute.cuh:279-282) and INT2/INT4
+// records with groups of 16 or 32 (common/cache.cuh:31-34, :82-96).
+int validate_schedule(int head_dim, int records, const int* bits, const int* groups, int page_tokens,
+                      int reference_mode, int anchor_index, int heads) {
+    if (records < 1 || records > 4 || bits == nullptr || groups == nullptr)
+        return fail(RQ_EINVAL, "A nonempty group of at most 4 records is required");
+    if (reference_mode != RQ_MODE_ANCHOR && reference_mode != RQ_MODE_ADJACENT)
+        return fail(RQ_EINVAL, "Unknown packed reference mode: %d", reference_mode);
+    for (int r = 0; r < records; ++r) {
+        if ((bits[r] != 2 && bits[r] != 4) || (groups[r] != 16 && groups[r] != 32) ||
+            head_dim % groups[r] != 0)
+            return fail(RQ_ENOKERNEL,
+                        "No compiled packed HIP kernel for heads=%d, head_dim=%d, record %d=(%d, %d)",
+                        heads, head_dim, r, bits[r], groups[r]);
+    }
+    if ((head_dim != 96 && head_dim != 128) || (page_tokens != 16 && page_tokens != 32) ||
+        anchor_index < 0 || anchor_index >= records ||
+        (reference_mode == RQ_MODE_ADJACENT && records > 1 && anchor_index != 0))
+        return fail(RQ_ENOKERNEL,
+                    "No compiled packed HIP kernel for heads=%d, head_dim=%d, record count=%d, "
+                    "reference_mode=%s, anchor_index=%d, page_tokens=%d",
+                    heads, head_dim, records, reference_mode == RQ_MODE_ANCHOR ? "anchor" : "adjacent",
+                    anchor_index, page_tokens);
+    return RQ_OK;
+}
+
+void fill_regions(int head_dim, int records, const int* bits, const int* groups, int page_tokens,
+                  rq::RecordRegion* regions) {
+    int offset = 0;
+    for (int r = 0; r < records; ++r) {
+        regions[r].offset = page_tokens * offset;
+        regions[r].bits = bits[r];
+        regions[r].group = groups[r];
+        regions[r].code_bytes = head_dim * bits[r] / 8;
+        regions[r].groups = head_dim / groups[r];
+        offset += rq::record_bytes(head_dim, bits[r], groups[r]);
+    }
+}
+
+// ---------------------------------------------------------------- split sizing
+
+std::mutex g_device_mutex;
+std::vector<int> g_compute_units;
+int g_split_target = 0;
+
+int compute_units() {
+    int device = 0;
+    if (hipGetDevice(&device) != hipSuccess) return 256;
+    std::lock_guard<std::mutex> lock(g_device_mutex);
+    if ((int)g_compute_units.size() <= device) g_compute_units.resize(device + 1, 0);
+    if (g_compute_units[device] == 0) {
+        int units = 0;
+        if (hipDeviceGetAttribute(&units, hipDeviceAttributeMultiprocessorCount, device) != hipSuccess ||
+            units <= 0)
+            units = 256;
+        g_compute_units[device] = units;
+    }
+    return g_compute_units[device];
+}
+
+// Splits per (row, head): enough workgroups for several resident waves of
+// the whole device, at least 4 pages per split, at most rq::kMaxSplits.
+int split_count(int64_t rows, int heads, int64_t max_pages) {
+    int64_t target;
+    {
+        std::lock_guard<std::mutex> lock(g_device_mutex);
+        target = g_split_target;
+    }
+    if (target <= 0) target = 4LL * compute_units();
+    const int64_t pairs = std::max<int64_t>(1, rows * heads);
+    int64_t splits = (target + pairs - 1) / pairs;
+    const int64_t by_pages = std::max<int64_t>(1, (max_pages + 3) / 4);
+    splits = std::min<int64_t>(splits, std::min<int64_t>(by_pages, rq::kMaxSplits));
+    return (int)std::max<int64_t>(1, splits);
+}
+
+size_t align256(size_t bytes) { return (bytes + 255) & ~size_t(255); }
+
+struct WorkspaceLayout {
+    size_t row_request, prep, partials, total;
+};
+
+WorkspaceLayout workspace_layout(int64_t rows, int heads, int head_dim, int splits) {
+    WorkspaceLayout w;
+    w.row_request = 0;
+    w.prep = align256(sizeof(int32_t) * (size_t)rows);
+    w.partials = w.prep + align256(sizeof(float) * (size_t)rows * heads * rq::kPrepFloats);
+    w.total = w.partials + align256(sizeof(float) * (size_t)rows * heads * splits * (head_dim + 2));
+    return w;
+}
+
+// ---------------------------------------------------------------- timing
+
+struct TimingState {
+    std::mutex mutex;
+    bool enabled = false;
+    std::vector<std::pair<hipEvent_t, hipEvent_t>> pending;
+    std::vector<std::pair<hipEvent_t, hipEvent_t>> free_pairs;
+};
+TimingState g_timing;
+
+bool timing_events(hipStream_t stream, hipEvent_t* begin, hipEvent_t* end) {
+    *begin = *end = nullptr;
+    std::lock_guard<std::mutex> lock(g_timing.mutex);
+    if (!g_timing.enabled) return false;
+    hipStreamCaptureStatus capture = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing(stream, &capture) != hipSuccess || capture != hipStreamCaptureStatusNone)
+        return false;
+    std::pair<hipEvent_t, hipEvent_t> pair;
+    if (!g_timing.free_pairs.empty()) {
+        pair = g_timing.free_pairs.back();
+        g_timing.free_pairs.pop_back();
+    } else {
+        if (hipEventCreate(&pair.first) != hipSuccess) return false;
+        if (hipEventCreate(&pair.second) != hipSuccess) {
+            hipEventDestroy(pair.first);
+            return false;
+        }
+    }
+    g_timing.pending.push_back(pair);
+    *begin = pair.first;
+    *end = pair.second;
+    return true;
+}
+
+}  // namespace
+
+extern "C" {
+
+int rq_version(void) { return (0 << 16) | 1; }
+
+const char* rq_last_error(void) { return g_last_error.c_str(); }
+
+int rq_page_width(int head_dim, int records, const int* bits, const int* groups) {
+    if (records < 1 || records > rq::kMaxRecords || bits == nullptr || groups == nullptr || head_dim <= 0 ||
+        head_dim % 32 != 0)
+        return fail(RQ_EINVAL, "Head dimension must be a positive multiple of 32 with 1-8 records");
+    int width = 0;
+    for (int r = 0; r < records; ++r) {
+        if ((bits[r] != 2 && bits[r] != 4) || groups[r] <= 0 || head_dim % groups[r] != 0)
+            return fail(RQ_EINVAL, "Head dimension must be divisible by every quantization group size");
+        width += rq::record_bytes(head_dim, bits[r], groups[r]);
+    }
+    ok();
+    return width;
+}
+
+int rq_quantize(int records, const void* const* key_ptrs, const int64_t* key_strides,
+                const void* const* value_ptrs, const int64_t* value_strides, int64_t input_rows,
+                void* kv_cache, int64_t num_blocks, int heads, int page_tokens, int page_width,
+                const int64_t* slot_mapping, int64_t tokens, int head_dim, const void* key_rotation,
+                const void* value_rotation, const float* key_mean, const int* bits, const int* groups,
+                int reference_mode, int anchor_index, int coefficient, hipStream_t stream) {
+    if (records < 1 || key_ptrs == nullptr || value_ptrs == nullptr || key_strides == nullptr ||
+        value_strides == nullptr)
+        return fail(RQ_EINVAL, "A nonempty group with one K/V input per record required");
+    if (kv_cache == nullptr || num_blocks < 0 || heads <= 0 || page_tokens <= 0)
+        return fail(RQ_EINVAL,
+                    "Contiguous CUDA UINT8 [2, blocks, heads, page tokens, page width] cache required");
+    int status = validate_schedule(head_dim, records, bits, groups, page_tokens, reference_mode,
+                                   anchor_index, heads);
+    if (status != RQ_OK) return status;
+    if (coefficient < RQ_COEF_UNIT || coefficient > RQ_COEF_LS) return fail(RQ_EINVAL, "Unsupported coefficient");
+    if (tokens < 0 || (tokens > 0 && slot_mapping == nullptr))
+        return fail(RQ_EINVAL, "Contiguous INT64 slot mapping on the cache device required");
+    if (input_rows < tokens) return fail(RQ_EINVAL, "Input has fewer rows than slot mapping");
+    const int width = rq_page_width(head_dim, records, bits, groups);
+    if (width != page_width) return fail(RQ_EINVAL, "Packed cache width differs from records");
+    for (int r = 0; r < records; ++r)
+        if (key_ptrs[r] == nullptr || value_ptrs[r] == nullptr || key_strides[r] < (int64_t)heads * head_dim ||
+            value_strides[r] < (int64_t)heads * head_dim)
+            return fail(RQ_EINVAL, "BF16 [tokens, heads, channels] with packed trailing strides required");
+    if (tokens == 0) return ok();
+
+    rq::QuantizeParams p{};
+    for (int r = 0; r < records; ++r) {
+        p.key_ptrs[r] = static_cast<const uint16_t*>(key_ptrs[r]);
+        p.value_ptrs[r] = static_cast<const uint16_t*>(value_ptrs[r]);
+        p.key_strides[r] = key_strides[r];
+        p.value_strides[r] = value_strides[r];
+    }
+    p.cache = static_cast<uint8_t*>(kv_cache);
+    p.plane_stride = num_blocks * heads * (int64_t)page_tokens * page_width;
+    p.num_blocks = num_blocks;
+    p.slots = slot_mapping;
+    p.tokens = tokens;
+    p.key_rotation = static_cast<const uint16_t*>(key_rotation);
+    p.value_rotation = static_cast<const uint16_t*>(value_rotation);
+    p.key_mean = key_mean;
+    p.heads = heads;
+    p.page_tokens = page_tokens;
+    p.page_width = page_width;
+    p.records = records;
+    p.anchor = anchor_index;
+    // A single-record group is always its own anchor (dispatch/schedules.cuh:99-111).
+    p.adjacent = records > 1 && reference_mode == RQ_MODE_ADJACENT;
+    p.coefficient = coefficient;
+    fill_regions(head_dim, records, bits, groups, page_tokens, p.region);
+    return check_launch(rq::launch_quantize(p, head_dim, stream), "quantize launch");
+}
+
+size_t rq_attention_workspace_bytes(int64_t rows, int heads, int head_dim, int64_t max_pages,
+                                    int page_tokens) {
+    (void)page_tokens;
+    if (rows <= 0 || heads <= 0 || head_dim <= 0) return 256;
+    return workspace_layout(rows, heads, head_dim, split_count(rows, heads, max_pages)).total;
+}
+
+static int attention_common(const void* query, int64_t query_stride, const void* key, int64_t key_stride,
+                            const void* value, int64_t value_stride, void* output, int64_t output_stride,
+                            int64_t rows, int heads, int head_dim, const int32_t* query_start_loc,
+                            const int32_t* seq_lens, int64_t requests, const int32_t* block_table,
+                            int64_t block_table_stride, int64_t max_pages, void* workspace,
+                            size_t workspace_bytes, rq::AttentionParams* p) {
+    if (rows < 0 || heads <= 0) return fail(RQ_EINVAL, "Q/K/V/output must have matching shapes and devices");
+    if (rows > 0 && (query == nullptr || key == nullptr || value == nullptr || output == nullptr))
+        return fail(RQ_EINVAL, "Q/K/V/output must have matching shapes and devices");
+    const int64_t min_stride = (int64_t)heads * head_dim;
+    if (query_stride < min_stride || key_stride < min_stride || value_stride < min_stride ||
+        output_stride < min_stride)
+        return fail(RQ_EINVAL, "BF16 [tokens, heads, channels] with packed trailing strides required");
+    if ((reinterpret_cast<uintptr_t>(query) % 8) != 0 || (reinterpret_cast<uintptr_t>(key) % 8) != 0 ||
+        query_stride % 4 != 0 || key_stride % 4 != 0)
+        return fail(RQ_EINVAL, "Q/K addresses and token strides must be 8-byte aligned");
+    if (requests < 0 || (requests > 0 && (query_start_loc == nullptr || seq_lens == nullptr)))
+        return fail(RQ_EINVAL, "Contiguous INT32 query starts with one final boundary required");
+    if (block_table == nullptr || max_pages < 0 || block_table_stride < max_pages)
+        return fail(RQ_EINVAL, "INT32 page table with packed rows required");
+    const int splits = split_count(rows, heads, max_pages);
+    const WorkspaceLayout layout = workspace_layout(rows, heads, head_dim, splits);
+    if (rows > 0 && (workspace == nullptr || workspace_bytes < layout.total))
+        return fail(RQ_ENOSPACE, "Attention workspace of %zu bytes required (got %zu)", layout.total,
+                    workspace_bytes);
+    uint8_t* ws = static_cast<uint8_t*>(workspace);
+    *p = rq::AttentionParams{};
+    p->query = static_cast<const uint16_t*>(query);
+    p->query_stride = query_stride;
+    p->key = static_cast<const uint16_t*>(key);
+    p->key_stride = key_stride;
+    p->value = static_cast<const uint16_t*>(value);
+    p->value_stride = value_stride;
+    p->output = static_cast<uint16_t*>(output);
+    p->output_stride = output_stride;
+    p->rows = rows;
+    p->heads = heads;
+    p->head_dim = head_dim;
+    p->query_start_loc = query_start_loc;
+    p->seq_lens = seq_lens;
+    p->requests = requests;
+    p->block_table = block_table;
+    p->block_table_stride = block_table_stride;
+    p->max_pages = max_pages;
+    p->row_request = reinterpret_cast<int32_t*>(ws + layout.row_request);
+    p->prep = reinterpret_cast<float*>(ws + layout.prep);
+    p->partials = reinterpret_cast<float*>(ws + layout.partials);
+    p->splits = splits;
+    return RQ_OK;
+}
+
+int rq_attention(const void* query, int64_t query_stride, const void* key, int64_t key_stride,
+                 const void* value, int64_t value_stride, void* output, int64_t output_stride,
+                 int64_t rows, int heads, int head_dim, const void* kv_cache, int64_t num_blocks,
+                 int page_tokens, int page_width, const int32_t* query_start_loc, const int32_t* seq_lens,
+                 int64_t requests, const int32_t* block_table, int64_t block_table_stride,
+                 int64_t max_pages, const void* key_rotation, const void* value_rotation,
+                 const float* key_mean, int records, const int* bits, const int* groups,
+                 int reference_mode, int anchor_index, int loop_index, void* workspace,
+                 size_t workspace_bytes, hipStream_t stream) {
+    int status = validate_schedule(head_dim, records, bits, groups, page_tokens, reference_mode,
+                                   anchor_index, heads);
+    if (status != RQ_OK) return status;
+    if (loop_index < 0 || loop_index >= records) return fail(RQ_EINVAL, "Invalid loop index");
+    if (kv_cache == nullptr || num_blocks < 0)
+        return fail(RQ_EINVAL, "Contiguous UINT8 KV cache on the query device required");
+    if (key_mean != nullptr && (reinterpret_cast<uintptr_t>(key_mean) % 16) != 0)
+        return fail(RQ_EINVAL,
+                    "16-byte aligned contiguous FP32 key mean with matching dimensions required");
+    if (key_rotation != nullptr && (reinterpret_cast<uintptr_t>(key_rotation) % 16) != 0)
+        return fail(RQ_EINVAL, "16-byte aligned key rotation required for asynchronous copies");
+    const int width = rq_page_width(head_dim, records, bits, groups);
+    if (width != page_width) return fail(RQ_EINVAL, "Packed cache width differs from records");
+    const bool adjacent = records > 1 && reference_mode == RQ_MODE_ADJACENT;
+    if (adjacent && loop_index > 0)
+        return fail(RQ_ENOKERNEL,
+                    "No compiled packed HIP kernel for heads=%d, head_dim=%d, record count=%d, "
+                    "reference_mode=adjacent, loop_index=%d (adjacent decode covers loop 0)",
+                    heads, head_dim, records, loop_index);
+    rq::AttentionParams p;
+    status = attention_common(query, query_stride, key, key_stride, value, value_stride, output,
+                              output_stride, rows, heads, head_dim, query_start_loc, seq_lens, requests,
+                              block_table, block_table_stride, max_pages, workspace, workspace_bytes, &p);
+    if (status != RQ_OK) return status;
+    if (rows == 0) return ok();
+    rq::RecordRegion regions[rq::kMaxRecords];
+    fill_regions(head_dim, records, bits, groups, page_tokens, regions);
+    const int anchor = adjacent ? 0 : anchor_index;
+    p.cache = static_cast<const uint8_t*>(kv_cache);
+    p.plane_stride = num_blocks * heads * (int64_t)page_tokens * page_width;
+    p.num_blocks = num_blocks;
+    p.page_tokens = page_tokens;
+    p.page_width = page_width;
+    p.key_rotation = static_cast<const uint16_t*>(key_rotation);
+    p.value_rotation = static_cast<const uint16_t*>(value_rotation);
+    p.anchor = regions[anchor];
+    p.has_residual = loop_index != anchor;
+    p.residual = regions[loop_index];
+    p.key_mean_loop = key_mean ? key_mean + (int64_t)loop_index * heads * head_dim : nullptr;
+    p.key_mean_anchor = (key_mean && p.has_residual) ? key_mean + (int64_t)anchor * heads * head_dim : nullptr;
+    hipEvent_t begin, end;
+    timing_events(stream, &begin, &end);
+    return check_launch(rq::launch_attention(p, stream, begin, end), "attention launch");
+}
+
+int rq_dequantize(const void* kv_cache, int64_t num_blocks, int heads, int page_tokens, int page_width,
+                  const int64_t* slots, int64_t tokens, int head_dim, const float* key_mean, int records,
+                  const int* bits, const int* groups, int reference_mode, int anchor_index, int loop_index,
+                  void* key_out, void* value_out, hipStream_t stream) {
+    int status = validate_schedule(head_dim, records, bits, groups, page_tokens, reference_mode,
+                                   anchor_index, heads);
+    if (status != RQ_OK) return status;
+    if (loop_index < 0 || loop_index >= records) return fail(RQ_EINVAL, "Invalid loop index");
+    if (kv_cache == nullptr || num_blocks < 0 || tokens < 0 || (tokens > 0 && (slots == nullptr ||
+                                                                              key_out == nullptr ||
+                                                                              value_out == nullptr)))
+        return fail(RQ_EINVAL, "Packed cache, slots and BF16 outputs required");
+    const int width = rq_page_width(head_dim, records, bits, groups);
+    if (width != page_width) return fail(RQ_EINVAL, "Packed cache width differs from records");
+    if (tokens == 0) return ok();
+    rq::RestoreParams p{};
+    p.cache = static_cast<const uint8_t*>(kv_cache);
+    p.plane_stride = num_blocks * heads * (int64_t)page_tokens * page_width;
+    p.num_blocks = num_blocks;
+    p.heads = heads;
+    p.page_tokens = page_tokens;
+    p.page_width = page_width;
+    p.head_dim = head_dim;
+    p.slots = slots;
+    p.tokens = tokens;
+    p.key_mean = key_mean;
+    const bool adjacent = records > 1 && reference_mode == RQ_MODE_ADJACENT;
+    p.chain_length = 0;
+    if (adjacent) {
+        for (int r = 0; r <= loop_index; ++r) p.chain[p.chain_length++] = r;
+    } else {
+        p.chain[p.chain_length++] = anchor_index;
+        if (loop_index != anchor_index) p.chain[p.chain_length++] = loop_index;
+    }
+    fill_regions(head_dim, records, bits, groups, page_tokens, p.region);
+    p.key_out = static_cast<uint16_t*>(key_out);
+    p.value_out = static_cast<uint16_t*>(value_out);
+    return check_launch(rq::launch_restore(p, stream), "restore launch");
+}
+
+int rq_paged_attention_bf16(const void* query, int64_t query_stride, const void* key, int64_t key_stride,
+                            const void* value, int64_t value_stride, void* output, int64_t output_stride,
+                            int64_t rows, int heads, int head_dim, const void* cache, int64_t num_blocks,
+                            int page_tokens, const int32_t* query_start_loc, const int32_t* seq_lens,
+                            int64_t requests, const int32_t* block_table, int64_t block_table_stride,
+                            int64_t max_pages, void* workspace, size_t workspace_bytes, hipStream_t stream) {
+    if ((head_dim != 96 && head_dim != 128) || (page_tokens != 16 && page_tokens != 32))
+        return fail(RQ_ENOKERNEL, "No compiled BF16 paged kernel for head_dim=%d, page_tokens=%d", head_dim,
+                    page_tokens);
+    if (cache == nullptr || num_blocks < 0) return fail(RQ_EINVAL, "BF16 paged cache required");
+    rq::AttentionParams p;
+    int status = attention_common(query, query_stride, key, key_stride, value, value_stride, output,
+                                  output_stride, rows, heads, head_dim, query_start_loc, seq_lens, requests,
+                                  block_table, block_table_stride, max_pages, workspace, workspace_bytes, &p);
+    if (status != RQ_OK) return status;
+    if (rows == 0) return ok();
+    p.cache = static_cast<const uint8_t*>(cache);
+    p.plane_stride = num_blocks * heads * (int64_t)page_tokens * head_dim * 2;
+    p.num_blocks = num_blocks;
+    p.page_tokens = page_tokens;
+    p.page_width = head_dim * 2;
+    hipEvent_t begin, end;
+    timing_events(stream, &begin, &end);
+    return check_launch(rq::launch_attention_bf16(p, stream, begin, end), "bf16 attention launch");
+}
+
+void rq_timing_enable(int enabled) {
+    std::lock_guard<std::mutex> lock(g_timing.mutex);
+    g_timing.enabled = enabled != 0;
+}
+
+int rq_timing_read(double* milliseconds, int64_t* launches) {
+    std::lock_guard<std::mutex> lock(g_timing.mutex);
+    double total = 0.0;
+    int64_t count = 0;
+    for (auto& pair : g_timing.pending) {
+        if (hipEventSynchronize(pair.second) != hipSuccess) return fail(RQ_ELAUNCH, "timing event failed");
+        float ms = 0.f;
+        if (hipEventElapsedTime(&ms, pair.first, pair.second) != hipSuccess)
+            return fail(RQ_ELAUNCH, "timing event failed");
+        total += ms;
+        ++count;
+        g_timing.free_pairs.push_back(pair);
+    }
+    g_timing.pending.clear();
+    if (milliseconds) *milliseconds = total;
+    if (launches) *launches = count;
+    return ok();
+}
+
+void rq_set_split_target(int workgroups) {
+    std::lock_guard<std::mutex> lock(g_device_mutex);
+    g_split_target = workgroups;
+}
+
+}  // extern "C"

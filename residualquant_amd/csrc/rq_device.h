@@ -1,0 +1,119 @@
+// Device-side scalar formats and packed-page layout helpers shared by the
+// quantize, restore and attention kernels (gfx950, wave64).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace rq {
+
+// ------------------------------------------------------------------ BF16
+
+// __float2bfloat16_rn semantics: one round-to-nearest-even of an FP32 value.
+__device__ __forceinline__ uint32_t bf16_rn(float f) {
+    uint32_t u = __float_as_uint(f);
+    if ((u & 0x7fffffffu) > 0x7f800000u) return (u >> 16) | 0x40u;
+    u += 0x7fffu + ((u >> 16) & 1u);
+    return u >> 16;
+}
+
+__device__ __forceinline__ float bf16_f32(uint32_t h) { return __uint_as_float(h << 16); }
+
+// One RNE rounding to BF16 of s + err, where (s, err) is an exact TwoSum
+// pair.  BF16 midpoints are FP32 values: only a sum that lands exactly on
+// one of them needs the error term to decide the direction.
+__device__ __forceinline__ uint32_t bf16_round_pair(float s, float err) {
+    uint32_t u = __float_as_uint(s);
+    if ((u & 0xffffu) == 0x8000u && err != 0.0f) {
+        const bool away = (err > 0.0f) == (s > 0.0f);
+        u = away ? u + 1u : u - 1u;
+        s = __uint_as_float(u);
+    }
+    return bf16_rn(s);
+}
+
+// BF16(a*b + c) with a single rounding (the __hfma2 result).  a*b of two
+// BF16 values is exact in FP32; TwoSum recovers the addition error.
+__device__ __forceinline__ uint32_t bf16_fma_rn(float a, float b, float c) {
+    const float p = a * b;
+    const float s = p + c;
+    const float bb = s - p;
+    const float err = (p - (s - bb)) + (c - bb);
+    return bf16_round_pair(s, err);
+}
+
+// BF16(a + b) with a single rounding (the __hadd2 result).
+__device__ __forceinline__ uint32_t bf16_add_rn(float a, float b) {
+    const float s = a + b;
+    const float bb = s - a;
+    const float err = (a - (s - bb)) + (b - bb);
+    return bf16_round_pair(s, err);
+}
+
+// ------------------------------------------------------------------ FP8
+
+// OCP E4M3 decode (bias 7, subnormals m*2^-9), exact in FP32.
+__device__ __forceinline__ float e4m3_f32(uint32_t v) {
+    const uint32_t e = (v >> 3) & 0xfu;
+    const uint32_t m = v & 7u;
+    float magnitude = e ? __uint_as_float(((e + 120u) << 23) | (m << 20))
+                        : (float)m * 0.001953125f;
+    if ((v & 0x7fu) == 0x7fu) magnitude = __uint_as_float(0x7fc00000u);
+    return (v & 0x80u) ? -magnitude : magnitude;
+}
+
+// OCP E4M3 encode: round-to-nearest-even, saturating to +-448, keeping the
+// sign of zero (the satfinite __nv_fp8_e4m3(float) conversion).
+__device__ __forceinline__ uint32_t e4m3_rn(float f) {
+    const uint32_t u = __float_as_uint(f);
+    const uint32_t sign = (u >> 24) & 0x80u;
+    const float a = fabsf(f);
+    if (a != a) return sign | 0x7fu;
+    if (a >= 448.0f) return sign | 0x7eu;
+    if (a < 0.015625f) return sign | (uint32_t)rintf(a * 512.0f);
+    const uint32_t ua = __float_as_uint(a);
+    int exponent = (int)(ua >> 23) - 127;
+    const uint32_t mantissa = ua & 0x7fffffu;
+    uint32_t kept = mantissa >> 20;
+    const uint32_t round_bit = (mantissa >> 19) & 1u;
+    const uint32_t sticky = mantissa & 0x7ffffu;
+    if (round_bit && (sticky || (kept & 1u))) kept++;
+    if (kept == 8u) {
+        kept = 0;
+        exponent++;
+    }
+    uint32_t code = ((uint32_t)(exponent + 7) << 3) | kept;
+    if (code > 0x7eu) code = 0x7eu;
+    return sign | code;
+}
+
+// ------------------------------------------------------------------ order
+
+// min/max with -0 ordered below +0 (commutative for every non-NaN pair).
+__device__ __forceinline__ float min_z(float a, float b) {
+    return (a < b || (a == b && __float_as_uint(a) >> 31)) ? a : b;
+}
+__device__ __forceinline__ float max_z(float a, float b) {
+    return (a > b || (a == b && !(__float_as_uint(a) >> 31))) ? a : b;
+}
+
+// ------------------------------------------------------------------ layout
+
+// Bytes of one token of record (bits, group) at head_dim D
+// (QuantizationRecord::Bytes, common/cache.cuh:14-17).
+__host__ __device__ constexpr int record_bytes(int head_dim, int bits, int group) {
+    return head_dim * bits / 8 + 2 * head_dim / group + 2;
+}
+
+constexpr int kMaxRecords = 8;
+
+// Host-resolved description of one record's region inside a page.
+struct RecordRegion {
+    int offset;      // page_tokens * StorageOffset(record), bytes from the page base
+    int bits;        // 2 or 4
+    int group;       // 16 or 32
+    int code_bytes;  // head_dim * bits / 8
+    int groups;      // head_dim / group
+};
+
+}  // namespace rq

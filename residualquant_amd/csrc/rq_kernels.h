@@ -1,0 +1,99 @@
+// Launch parameters shared between the C ABI (capi.hip) and the kernels.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "rq_device.h"
+
+namespace rq {
+
+// Coefficient methods (same values as RQ_COEF_* in include/rq_hip.h).
+constexpr int RQ_COEF_UNIT_ = 0;
+constexpr int RQ_COEF_NORM_ = 1;
+constexpr int RQ_COEF_LS_ = 2;
+
+struct QuantizeParams {
+    const uint16_t* key_ptrs[kMaxRecords];
+    const uint16_t* value_ptrs[kMaxRecords];
+    int64_t key_strides[kMaxRecords];
+    int64_t value_strides[kMaxRecords];
+    uint8_t* cache;
+    int64_t plane_stride;  // num_blocks * heads * page_tokens * page_width
+    int64_t num_blocks;
+    const int64_t* slots;
+    int64_t tokens;
+    const uint16_t* key_rotation;  // FP16 bits [heads, D, D] or null
+    const uint16_t* value_rotation;
+    const float* key_mean;  // FP32 [records, heads, D] or null
+    int heads, page_tokens, page_width, records, anchor, adjacent, coefficient;
+    RecordRegion region[kMaxRecords];
+};
+
+hipError_t launch_quantize(const QuantizeParams& p, int head_dim, hipStream_t stream);
+
+struct RestoreParams {
+    const uint8_t* cache;
+    int64_t plane_stride, num_blocks;
+    int heads, page_tokens, page_width, head_dim;
+    const int64_t* slots;
+    int64_t tokens;
+    const float* key_mean;
+    int chain_length;            // records restored in order
+    int chain[kMaxRecords];      // record indices, base first
+    RecordRegion region[kMaxRecords];
+    uint16_t* key_out;
+    uint16_t* value_out;
+};
+
+hipError_t launch_restore(const RestoreParams& p, hipStream_t stream);
+
+// Per (row, head) prepared query block in the workspace (floats).
+constexpr int kPrepScalars = 16;   // [0] delta [1] live score [2] q'.mu_A [3..10] Q16 [11..14] Q32
+constexpr int kPrepQuery = 128;    // q' FP32 in log2 units
+constexpr int kPrepPlanes = 64;    // 4 nibble planes x up to 16 words (each order)
+constexpr int kPrepFloats = kPrepScalars + kPrepQuery + 2 * kPrepPlanes;
+constexpr int kMaxSplits = 64;
+
+struct AttentionParams {
+    const uint16_t* query;
+    int64_t query_stride;
+    const uint16_t* key;
+    int64_t key_stride;
+    const uint16_t* value;
+    int64_t value_stride;
+    uint16_t* output;
+    int64_t output_stride;
+    int64_t rows;
+    int heads;
+    int head_dim;
+    const uint8_t* cache;      // packed UINT8 or BF16 pages (baseline)
+    int64_t plane_stride;      // bytes between the K and V planes
+    int64_t num_blocks;
+    int page_tokens;
+    int page_width;            // bytes per token row of a page (packed)
+    const int32_t* query_start_loc;
+    const int32_t* seq_lens;
+    int64_t requests;
+    const int32_t* block_table;
+    int64_t block_table_stride;
+    int64_t max_pages;
+    const uint16_t* key_rotation;
+    const uint16_t* value_rotation;
+    const float* key_mean_loop;    // mu of the current loop [heads, D] or null
+    const float* key_mean_anchor;  // mu of the anchor [heads, D] or null (residual loops only)
+    RecordRegion anchor;
+    RecordRegion residual;
+    int has_residual;
+    int32_t* row_request;  // workspace [rows]
+    float* prep;           // workspace [rows, heads, kPrepFloats]
+    float* partials;       // workspace [rows, heads, splits, D + 2]
+    int splits;
+};
+
+hipError_t launch_attention(const AttentionParams& p, hipStream_t stream, hipEvent_t begin,
+                            hipEvent_t end);
+hipError_t launch_attention_bf16(const AttentionParams& p, hipStream_t stream, hipEvent_t begin,
+                                 hipEvent_t end);
+
+}  // namespace rq
