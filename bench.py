@@ -140,6 +140,8 @@ def main():
     parser.add_argument("--cpu-budget", type=float, default=10.0,
                         help="seconds of CPU oracle work for the cpu_baseline sample (0 = skip)")
     parser.add_argument("--no-bf16", action="store_true")
+    parser.add_argument("--split-target", type=int, default=0,
+                        help="split-K workgroups per decode launch (0 = the library's default)")
     args = parser.parse_args()
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -154,6 +156,8 @@ def main():
 
     device = torch.device("cuda:0")
     torch.cuda.set_device(device)
+    if args.split_target:
+        ops.set_split_target(args.split_target)
     batch, history, heads, dim, page_tokens = args.batch, args.history, 16, 128, 16
     seed = 2026
 

@@ -29,7 +29,8 @@
  *     round-to-nearest-even of the exact value;
  *   - min/max order -0 below +0.
  *
- * Attention is evaluated in FP64 over the exactly restored BF16 K/V.
+ * Attention is evaluated in FP64: keys as the reference decode kernel scores
+ * them (unrounded code*scale+offset terms), values as its BF16 restore.
  *
  * Parity pins (tests/test_oracle_*.py): page widths, bit positions, the
  * exhaustive FP8 table against torch.float8_e4m3fn, BF16 rounding against
@@ -475,13 +476,80 @@ int rq_oracle_dequantize(const uint8_t* cache, int64_t num_blocks, int heads, in
     return 0;
 }
 
+/* Unrounded code*scale + offset of channel c (exact in double). */
+static double record_value_exact(const uint8_t* record_base, int head_dim, int bits, int group,
+                                 int page_tokens, int token, int c) {
+    const int code_bytes = head_dim * bits / 8;
+    const int groups = head_dim / group;
+    const uint8_t* codes = record_base + (size_t)token * code_bytes;
+    const uint8_t* scales = record_base + (size_t)page_tokens * code_bytes;
+    const uint8_t* offsets = scales + (size_t)page_tokens * groups;
+    const unsigned code = (codes[(c * bits) >> 3] >> ((c * bits) & 7)) & ((1u << bits) - 1u);
+    const int g = c / group;
+    return (double)code * (double)rq_oracle_e4m3_to_f32(scales[token * groups + g]) +
+           (double)rq_oracle_e4m3_to_f32(offsets[token * groups + g]);
+}
+
+/*
+ * History key of one token as the reference decode kernel scores it, in
+ * exact arithmetic.  Anchor mode (compute.cuh:397-505, prepare.cuh:203-229):
+ * loop A scores q'.(c.s+o)_A, loop L != A scores
+ * alpha_L*(q'.(c.s+o)_A + q'.bf16(mu_A)) + q'.(c.s+o)_L, both shifted by
+ * -q'.mu_L against the live score; the key below adds mu_L back, which leaves
+ * the softmax unchanged.  Adjacent mode (compute.cuh:120-197, :506-528)
+ * scores the BF16 restore chain without the current loop's mean.
+ */
+static void attention_key(const uint8_t* page, int head_dim, const int* bits, const int* groups,
+                          int page_tokens, int token, int adjacent, int anchor_index, int loop,
+                          const float* mean_base, int heads, int h, double* out) {
+    const float* mean_loop = mean_base ? mean_base + ((size_t)loop * heads + h) * head_dim : NULL;
+    if (adjacent) {
+        uint16_t chain[RQ_ORACLE_MAX_DIM];
+        for (int r = 0; r <= loop; ++r) {
+            const uint8_t* record_base = page + (size_t)page_tokens * record_offset(head_dim, r, bits, groups);
+            const uint16_t alpha = record_alpha(record_base, head_dim, bits[r], groups[r], page_tokens, token);
+            for (int c = 0; c < head_dim; ++c) {
+                uint16_t value = restore_code_value(record_base, head_dim, bits[r], groups[r], page_tokens, token, c);
+                if (mean_base && r != loop)
+                    value = rq_oracle_bf16_add_rn(value, rq_oracle_bf16_rn(mean_base[((size_t)r * heads + h) * head_dim + c]));
+                if (r > 0) value = rq_oracle_bf16_fma_rn(chain[c], alpha, value);
+                chain[c] = value;
+            }
+        }
+        for (int c = 0; c < head_dim; ++c)
+            out[c] = (double)rq_oracle_bf16_to_f32(chain[c]) + (mean_loop ? (double)mean_loop[c] : 0.0);
+        return;
+    }
+    const uint8_t* anchor_base = page + (size_t)page_tokens * record_offset(head_dim, anchor_index, bits, groups);
+    const float* mean_anchor = mean_base ? mean_base + ((size_t)anchor_index * heads + h) * head_dim : NULL;
+    if (loop == anchor_index) {
+        for (int c = 0; c < head_dim; ++c)
+            out[c] = record_value_exact(anchor_base, head_dim, bits[anchor_index], groups[anchor_index],
+                                        page_tokens, token, c) + (mean_loop ? (double)mean_loop[c] : 0.0);
+        return;
+    }
+    const uint8_t* loop_base = page + (size_t)page_tokens * record_offset(head_dim, loop, bits, groups);
+    const double alpha = rq_oracle_bf16_to_f32(record_alpha(loop_base, head_dim, bits[loop], groups[loop],
+                                                            page_tokens, token));
+    for (int c = 0; c < head_dim; ++c) {
+        double anchor = record_value_exact(anchor_base, head_dim, bits[anchor_index], groups[anchor_index],
+                                           page_tokens, token, c);
+        if (mean_anchor) anchor += rq_oracle_bf16_to_f32(rq_oracle_bf16_rn(mean_anchor[c]));
+        out[c] = alpha * anchor +
+                 record_value_exact(loop_base, head_dim, bits[loop], groups[loop], page_tokens, token, c) +
+                 (mean_loop ? (double)mean_loop[c] : 0.0);
+    }
+}
+
 /* ------------------------------------------------------------------ */
 /* decode attention (FP64 over the restored K/V)                        */
 /* ------------------------------------------------------------------ */
 
 /*
  * For each query row i of request b (query_start_loc), head h, loop L:
- *   q' = (q.R_k)/sqrt(D); history t < seq_len-1 scores q'.K_L[t];
+ *   q' = (q.R_k)/sqrt(D); history t < seq_len-1 scores q'.K_L[t] with K_L the
+ *   key the reference decode kernel scores (attention_key above) and V_L[t]
+ *   the BF16 restore (restore_token, compute.cuh:28-107);
  *   live score (q.k_live)/sqrt(D); p = softmax over history + live;
  *   out = (sum_t p_t V_L[t]).R_v^T + p_live v_live   (merge.cuh:66-83,
  *   output.cuh:9-31, compute.cuh:688-726, prepare.cuh:13-54).
@@ -501,7 +569,8 @@ int rq_oracle_attention(
     const int adjacent = records > 1 && reference_mode == 1;
     const int64_t plane_stride = num_blocks * heads * page_tokens * page_width;
     const double scale = 1.0 / sqrt((double)head_dim);
-    uint16_t kbuf[RQ_ORACLE_MAX_DIM], vbuf[RQ_ORACLE_MAX_DIM];
+    uint16_t vbuf[RQ_ORACLE_MAX_DIM];
+    double kexact[RQ_ORACLE_MAX_DIM];
 
     for (int64_t b = 0; b < requests; ++b) {
         const int64_t history = seq_lens[b] > 1 ? seq_lens[b] - 1 : 0;
@@ -538,11 +607,10 @@ int rq_oracle_attention(
                         return -1;
                     }
                     const uint8_t* page = cache + (block * heads + h) * (int64_t)page_tokens * page_width;
-                    restore_token(page, head_dim, records, bits, groups, page_tokens,
-                                  (int)(t % page_tokens), adjacent, anchor_index, loop, key_mean,
-                                  heads, h, kbuf);
+                    attention_key(page, head_dim, bits, groups, page_tokens, (int)(t % page_tokens),
+                                  adjacent, anchor_index, loop, key_mean, heads, h, kexact);
                     double s = 0.0;
-                    for (int c = 0; c < head_dim; ++c) s += qr[c] * (double)rq_oracle_bf16_to_f32(kbuf[c]);
+                    for (int c = 0; c < head_dim; ++c) s += qr[c] * kexact[c];
                     scores[t] = s;
                     if (s > maximum) maximum = s;
                 }

@@ -11,7 +11,7 @@ import os
 import subprocess
 
 PACKAGE_DIR = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.path.join(PACKAGE_DIR, "librq_hip.so")
+LIB_PATH = os.environ.get("RQ_HIP_LIBRARY") or os.path.join(PACKAGE_DIR, "librq_hip.so")
 CSRC_DIR = os.path.join(PACKAGE_DIR, "csrc")
 
 RQ_OK, RQ_EINVAL, RQ_ENOKERNEL, RQ_ELAUNCH, RQ_ENOSPACE = 0, -1, -2, -3, -4

@@ -85,6 +85,7 @@ __global__ __launch_bounds__(128) void prepare_kernel(AttentionParams p) {
     const int wave = c >> 6;
     __shared__ float q_lds[128];
     __shared__ float totals[4][2];
+    __shared__ __attribute__((aligned(16))) _Float16 rotation_lds[D * D];
 
     const int request = find_request(p.query_start_loc, p.requests, row);
     if (head == 0 && c == 0) p.row_request[row] = request;
@@ -97,11 +98,14 @@ __global__ __launch_bounds__(128) void prepare_kernel(AttentionParams p) {
 
     float qr = q;
     if (p.key_rotation != nullptr) {
+        // Stage R_k of this head with 16-byte loads (32 KB at D = 128).
+        const uint4* src = reinterpret_cast<const uint4*>(p.key_rotation + (int64_t)head * D * D);
+        uint4* dst = reinterpret_cast<uint4*>(rotation_lds);
+        for (int i = c; i < D * D / 8; i += 128) dst[i] = src[i];
+        __syncthreads();
         float acc = 0.f;
-        if (active) {
-            const uint16_t* m = p.key_rotation + (int64_t)head * D * D + c;
-            for (int k = 0; k < D; ++k) acc = fmaf(q_lds[k], f16_f32(m[(int64_t)k * D]), acc);
-        }
+        if (active)
+            for (int k = 0; k < D; ++k) acc = fmaf(q_lds[k], (float)rotation_lds[k * D + c], acc);
         qr = acc;
     }
     const float scale = kLog2e / sqrtf((float)D);
@@ -111,7 +115,8 @@ __global__ __launch_bounds__(128) void prepare_kernel(AttentionParams p) {
     float parts[4];
     parts[0] = q * k_live;
     parts[1] = (active && p.key_mean_loop) ? qr * p.key_mean_loop[head * D + c] : 0.f;
-    parts[2] = (active && p.key_mean_anchor) ? qr * p.key_mean_anchor[head * D + c] : 0.f;
+    // The anchor term of residual loops uses the BF16 mean (compute.cuh:327-336).
+    parts[2] = (active && p.key_mean_anchor) ? qr * bf16_f32(bf16_rn(p.key_mean_anchor[head * D + c])) : 0.f;
     parts[3] = fabsf(qr);
 #pragma unroll
     for (int d = 32; d; d >>= 1) {
@@ -175,38 +180,50 @@ struct Codes;
 template <>
 struct Codes<4> {
     uint32_t w[4];
-    __device__ __forceinline__ void load(const uint8_t* p) {
-        const uint4 v = *reinterpret_cast<const uint4*>(p);
-        w[0] = v.x; w[1] = v.y; w[2] = v.z; w[3] = v.w;
-    }
 };
 template <>
 struct Codes<2> {
     uint32_t w[2];
-    __device__ __forceinline__ void load(const uint8_t* p) {
-        const uint2 v = *reinterpret_cast<const uint2*>(p);
-        w[0] = v.x; w[1] = v.y;
-    }
 };
 
-// Scale/offset of the lane's group(s): one byte each for G32, two for G16.
+// Raw buffer resource over one page (wave-uniform, SGPRs): loads take a
+// 32-bit lane offset plus a uniform offset, and reads past the page return 0.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t page_resource(const uint8_t* page, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(page), (short)0, (int)bytes, 0x00020000);
+}
+
+template <int Bits>
+__device__ __forceinline__ void load_codes(__amdgpu_buffer_rsrc_t page, uint32_t offset, uint32_t uniform,
+                                           Codes<Bits>& c) {
+    if constexpr (Bits == 4) {
+        const auto v = __builtin_amdgcn_raw_buffer_load_b128(page, offset, uniform, 0);
+        c.w[0] = v[0]; c.w[1] = v[1]; c.w[2] = v[2]; c.w[3] = v[3];
+    } else {
+        const auto v = __builtin_amdgcn_raw_buffer_load_b64(page, offset, uniform, 0);
+        c.w[0] = v[0]; c.w[1] = v[1];
+    }
+}
+
+// Raw FP8 scale/offset bytes of the lane's group(s): one byte each for G32,
+// two for G16; decoded (exactly, in hardware) where they are used.
 template <int G>
 struct GroupParams {
-    float scale[2], offset[2];
-    __device__ __forceinline__ void load(const uint8_t* scales, const uint8_t* offsets) {
+    uint32_t scales, offsets;
+    __device__ __forceinline__ void load(__amdgpu_buffer_rsrc_t page, uint32_t scale_offset,
+                                         uint32_t offset_offset, uint32_t uniform) {
         if constexpr (G == 32) {
-            const uint32_t s = *scales, o = *offsets;
-            scale[0] = scale[1] = fp8_f32<0>(s);
-            offset[0] = offset[1] = fp8_f32<0>(o);
+            scales = __builtin_amdgcn_raw_buffer_load_b8(page, scale_offset, uniform, 0);
+            offsets = __builtin_amdgcn_raw_buffer_load_b8(page, offset_offset, uniform, 0);
         } else {
-            const uint32_t s = *reinterpret_cast<const uint16_t*>(scales);
-            const uint32_t o = *reinterpret_cast<const uint16_t*>(offsets);
-            scale[0] = fp8_f32<0>(s);
-            scale[1] = fp8_f32<1>(s);
-            offset[0] = fp8_f32<0>(o);
-            offset[1] = fp8_f32<1>(o);
+            scales = __builtin_amdgcn_raw_buffer_load_b16(page, scale_offset, uniform, 0);
+            offsets = __builtin_amdgcn_raw_buffer_load_b16(page, offset_offset, uniform, 0);
         }
     }
+    // Scale / offset of the lane's 16-channel half H.
+    template <int H>
+    __device__ __forceinline__ float scale() const { return fp8_f32<G == 32 ? 0 : H>(scales); }
+    template <int H>
+    __device__ __forceinline__ float offset() const { return fp8_f32<G == 32 ? 0 : H>(offsets); }
 };
 
 // Integer q'.codes over the lane's 32 channels, per 16-channel half.
@@ -241,11 +258,12 @@ __device__ __forceinline__ void code_dots(const Codes<Bits>& codes, const uint32
     }
 #pragma unroll
     for (int h = 0; h < 2; ++h)
-        dot[h] = (int)(d[h][0] + 16u * d[h][1] + 256u * d[h][2] + 4096u * d[h][3]) -
-                 32768 * (int)count[h];
+        dot[h] = (int)(d[h][0] + 16u * d[h][1] + 256u * d[h][2] + 4096u * d[h][3]) - 32768 * (int)count[h];
 }
 
-// acc[c] += weight[half(c)] * code[c] over the lane's 32 channels.
+// acc[c] += weight[half(c)] * code[c] over the lane's 32 channels.  A code c
+// held in a byte is the FP8 E4M3 value c * 2^-9, so v_cvt_pk_f32_fp8 turns two
+// codes into FP32 per instruction; `weight` carries the 2^9 back.
 template <int Bits>
 __device__ __forceinline__ void accumulate_codes(const Codes<Bits>& codes, const float (&weight)[2],
                                                  float (&acc)[32]) {
@@ -253,24 +271,37 @@ __device__ __forceinline__ void accumulate_codes(const Codes<Bits>& codes, const
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             const float w = weight[i >> 1];
-            const uint32_t lo = codes.w[i] & 0x0f0f0f0fu;
-            const uint32_t hi = (codes.w[i] >> 4) & 0x0f0f0f0fu;
-#pragma unroll
-            for (int b = 0; b < 4; ++b) {
-                acc[8 * i + 2 * b] = fmaf(w, (float)((lo >> (8 * b)) & 0xffu), acc[8 * i + 2 * b]);
-                acc[8 * i + 2 * b + 1] = fmaf(w, (float)((hi >> (8 * b)) & 0xffu), acc[8 * i + 2 * b + 1]);
-            }
+            const int lo = (int)(codes.w[i] & 0x0f0f0f0fu);         // channels 0, 2, 4, 6
+            const int hi = (int)((codes.w[i] >> 4) & 0x0f0f0f0fu);  // channels 1, 3, 5, 7
+            const auto l01 = __builtin_amdgcn_cvt_pk_f32_fp8(lo, false);
+            const auto l23 = __builtin_amdgcn_cvt_pk_f32_fp8(lo, true);
+            const auto h01 = __builtin_amdgcn_cvt_pk_f32_fp8(hi, false);
+            const auto h23 = __builtin_amdgcn_cvt_pk_f32_fp8(hi, true);
+            float* a = acc + 8 * i;
+            a[0] = fmaf(w, l01[0], a[0]);
+            a[2] = fmaf(w, l01[1], a[2]);
+            a[4] = fmaf(w, l23[0], a[4]);
+            a[6] = fmaf(w, l23[1], a[6]);
+            a[1] = fmaf(w, h01[0], a[1]);
+            a[3] = fmaf(w, h01[1], a[3]);
+            a[5] = fmaf(w, h23[0], a[5]);
+            a[7] = fmaf(w, h23[1], a[7]);
         }
     } else {
 #pragma unroll
         for (int i = 0; i < 2; ++i) {
             const float w = weight[i];
+            float* a = acc + 16 * i;
 #pragma unroll
             for (int k = 0; k < 4; ++k) {
-                const uint32_t part = (codes.w[i] >> (2 * k)) & 0x03030303u;
-#pragma unroll
-                for (int b = 0; b < 4; ++b)
-                    acc[16 * i + 4 * b + k] = fmaf(w, (float)((part >> (8 * b)) & 0xffu), acc[16 * i + 4 * b + k]);
+                // byte j of part holds channel 4j + k
+                const int part = (int)((codes.w[i] >> (2 * k)) & 0x03030303u);
+                const auto c01 = __builtin_amdgcn_cvt_pk_f32_fp8(part, false);
+                const auto c23 = __builtin_amdgcn_cvt_pk_f32_fp8(part, true);
+                a[k] = fmaf(w, c01[0], a[k]);
+                a[4 + k] = fmaf(w, c01[1], a[4 + k]);
+                a[8 + k] = fmaf(w, c23[0], a[8 + k]);
+                a[12 + k] = fmaf(w, c23[1], a[12 + k]);
             }
         }
     }
@@ -287,33 +318,16 @@ __device__ __forceinline__ void load_planes(const float* prep, int qd, uint32_t 
     }
 }
 
-// Record region addresses for one (page, token, quarter).
-template <int Bits, int G>
-struct RecordView {
-    const uint8_t* codes;
-    const uint8_t* scales;
-    const uint8_t* offsets;
-    const uint8_t* alpha;
-    __device__ __forceinline__ RecordView(const uint8_t* page, const RecordRegion& r, int page_tokens,
-                                          int token, int qd) {
-        const uint8_t* base = page + r.offset;
-        codes = base + token * r.code_bytes + qd * (32 * Bits / 8);
-        scales = base + page_tokens * r.code_bytes + token * r.groups + qd * (32 / G);
-        offsets = scales + page_tokens * r.groups;
-        alpha = base + page_tokens * (r.code_bytes + 2 * r.groups) + 2 * token;
-    }
-};
-
 // Lane part of one record's score: sum over the lane's group(s) of
 // scale * delta * (q_int . codes) + offset * sum(q').
 template <int G>
 __device__ __forceinline__ float record_score(const GroupParams<G>& gp, const int (&dot)[2],
                                               float delta, const float (&q_sum)[2]) {
     if constexpr (G == 32)
-        return gp.scale[0] * (delta * (float)(dot[0] + dot[1])) + gp.offset[0] * q_sum[0];
+        return gp.template scale<0>() * (delta * (float)(dot[0] + dot[1])) + gp.template offset<0>() * q_sum[0];
     else
-        return gp.scale[0] * (delta * (float)dot[0]) + gp.offset[0] * q_sum[0] +
-               gp.scale[1] * (delta * (float)dot[1]) + gp.offset[1] * q_sum[1];
+        return gp.template scale<0>() * (delta * (float)dot[0]) + gp.template offset<0>() * q_sum[0] +
+               gp.template scale<1>() * (delta * (float)dot[1]) + gp.template offset<1>() * q_sum[1];
 }
 
 template <int G>
@@ -326,11 +340,13 @@ __device__ __forceinline__ void group_sums(const float* prep, int qd, float (&q_
     }
 }
 
+constexpr int kReduceBytes = kWaves * 16 * 128 * (int)sizeof(float);
+
 // Writes (m, l, acc[D]) of this split after merging the four waves in LDS.
 template <int D>
 __device__ __forceinline__ void write_partial(float (&acc)[32], float m, float l_lane, int lane,
                                               int wave, bool lane_active, float* partial) {
-    __shared__ float red_acc[kWaves][16][128];
+    __shared__ __attribute__((aligned(16))) float red_acc[kWaves][16][128];
     __shared__ float red_m[kWaves], red_l[kWaves];
     const int t = lane >> 2, qd = lane & 3;
     const float l_wave = token_sum((lane_active && qd == 0) ? l_lane : 0.f);
@@ -397,11 +413,94 @@ __device__ __forceinline__ SplitRange split_range(const AttentionParams& p, int6
     return r;
 }
 
-template <int D, int BA, int GA, int BL, int GL, bool HasL>
-__global__ __launch_bounds__(kDecodeThreads) void decode_kernel(AttentionParams p) {
+// Wave max of one value per token, broadcast to every lane (quad lanes agree).
+__device__ __forceinline__ float wave_max(float x) {
+    x = fmaxf(x, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(x), 0x124, 0xF, 0xF, true)));  // row_ror:4
+    x = fmaxf(x, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(x), 0x128, 0xF, 0xF, true)));  // row_ror:8
+    const float r0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), 0));
+    const float r1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), 16));
+    const float r2 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), 32));
+    const float r3 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), 48));
+    return fmaxf(fmaxf(r0, r1), fmaxf(r2, r3));
+}
+
+__device__ __forceinline__ float quad_sum_fast(float x) {
+    x += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(x), 0xB1, 0xF, 0xF, true));
+    return x + __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(x), 0x4E, 0xF, 0xF, true));
+}
+
+// Integer q'.codes of two units at once, with the nibble planes read from LDS
+// one code word at a time (planes[word][plane], shared by both units).
+template <int Bits>
+__device__ __forceinline__ void code_dots2(const Codes<Bits>& c0, const Codes<Bits>& c1,
+                                           const uint32_t* planes, int (&dot0)[2], int (&dot1)[2]) {
+    uint32_t d0[2][4] = {}, d1[2][4] = {};
+    uint32_t n0[2] = {0u, 0u}, n1[2] = {0u, 0u};
+    constexpr uint32_t kOnes = 0x11111111u;
+    if constexpr (Bits == 4) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int h = i >> 1;
+            const uint4 q = *reinterpret_cast<const uint4*>(planes + 4 * i);
+            const uint32_t qj[4] = {q.x, q.y, q.z, q.w};
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                d0[h][j] = __builtin_amdgcn_udot8(qj[j], c0.w[i], d0[h][j], false);
+                d1[h][j] = __builtin_amdgcn_udot8(qj[j], c1.w[i], d1[h][j], false);
+            }
+            n0[h] = __builtin_amdgcn_udot8(kOnes, c0.w[i], n0[h], false);
+            n1[h] = __builtin_amdgcn_udot8(kOnes, c1.w[i], n1[h], false);
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            const uint32_t e0 = c0.w[i] & 0x33333333u, o0 = (c0.w[i] >> 2) & 0x33333333u;
+            const uint32_t e1 = c1.w[i] & 0x33333333u, o1 = (c1.w[i] >> 2) & 0x33333333u;
+            const uint4 qe = *reinterpret_cast<const uint4*>(planes + 4 * (2 * i));
+            const uint4 qo = *reinterpret_cast<const uint4*>(planes + 4 * (2 * i + 1));
+            const uint32_t ej[4] = {qe.x, qe.y, qe.z, qe.w};
+            const uint32_t oj[4] = {qo.x, qo.y, qo.z, qo.w};
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                d0[i][j] = __builtin_amdgcn_udot8(ej[j], e0, d0[i][j], false);
+                d0[i][j] = __builtin_amdgcn_udot8(oj[j], o0, d0[i][j], false);
+                d1[i][j] = __builtin_amdgcn_udot8(ej[j], e1, d1[i][j], false);
+                d1[i][j] = __builtin_amdgcn_udot8(oj[j], o1, d1[i][j], false);
+            }
+            n0[i] = __builtin_amdgcn_udot8(kOnes, e0, __builtin_amdgcn_udot8(kOnes, o0, n0[i], false), false);
+            n1[i] = __builtin_amdgcn_udot8(kOnes, e1, __builtin_amdgcn_udot8(kOnes, o1, n1[i], false), false);
+        }
+    }
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+        dot0[h] = (int)(d0[h][0] + 16u * d0[h][1] + 256u * d0[h][2] + 4096u * d0[h][3]) - 32768 * (int)n0[h];
+        dot1[h] = (int)(d1[h][0] + 16u * d1[h][1] + 256u * d1[h][2] + 4096u * d1[h][3]) - 32768 * (int)n1[h];
+    }
+}
+
+// Registers of one 16-token unit: K/V codes, raw FP8 parameters, alphas.
+template <int BA, int GA, int BL, int GL, bool HasL>
+struct Unit {
+    Codes<BA> kca, vca;
+    GroupParams<GA> kpa, vpa;
+    Codes<BL> kcl, vcl;
+    GroupParams<GL> kpl, vpl;
+    uint32_t alpha_k_bits, alpha_v_bits;
+};
+
+#ifndef RQ_DECODE_MIN_WAVES
+#define RQ_DECODE_MIN_WAVES 1
+#endif
+
+template <int D, int PT, int BA, int GA, int BL, int GL, bool HasL>
+__global__ __launch_bounds__(kDecodeThreads) __attribute__((amdgpu_waves_per_eu(RQ_DECODE_MIN_WAVES)))
+void decode_kernel(AttentionParams p) {
     constexpr int Quarters = D / 32;
+    constexpr int UnitsPerPage = PT / kUnitTokens;
+    constexpr int CodeA = D * BA / 8, GroupsA = D / GA;
+    constexpr int CodeL = D * BL / 8, GroupsL = D / GL;
     const int lane = threadIdx.x & 63;
-    const int wave = threadIdx.x >> 6;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int t = lane >> 2;
     const int qd = lane & 3;
     const bool lane_active = qd < Quarters;
@@ -410,119 +509,159 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_kernel(AttentionParams 
     const int64_t rh = blockIdx.x / p.splits;
     const int head = (int)(rh % p.heads);
     const int64_t row = rh / p.heads;
+    // Nibble planes of q' per quarter: [quarter][anchor words 0..3 | loop words 0..3][plane]
+    __shared__ __attribute__((aligned(16))) uint32_t planes_lds[4][8][4];
 
     const SplitRange range = split_range(p, row, split);
     if (range.request < 0) return;
     float* partial = p.partials + (rh * p.splits + split) * (int64_t)(D + 2);
 
     const float* prep = p.prep + rh * (int64_t)kPrepFloats;
+    if (threadIdx.x < 128) {
+        // thread -> (quarter, record, word, plane); prep stores [plane][word] per order
+        const int quarter = threadIdx.x >> 5, record = (threadIdx.x >> 4) & 1;
+        const int word = (threadIdx.x >> 2) & 3, plane = threadIdx.x & 3;
+        const int bits = record == 0 ? BA : BL;
+        const uint32_t* base = reinterpret_cast<const uint32_t*>(prep + kPrepScalars + kPrepQuery) +
+                               (bits == 2 ? kPrepPlanes : 0);
+        planes_lds[quarter][record * 4 + word][plane] =
+            quarter < Quarters ? base[plane * 16 + 4 * quarter + word] : 0u;
+    }
     const float delta = prep[0];
     const float q_mean_anchor = prep[2];
     float q_sum_a[2], q_sum_l[2];
     group_sums<GA>(prep, lq, q_sum_a);
     group_sums<GL>(prep, lq, q_sum_l);
-    uint32_t planes_a[4][4], planes_l[4][4];
-    load_planes<BA>(prep, lq, planes_a);
-    if constexpr (HasL) load_planes<BL>(prep, lq, planes_l);
+    __syncthreads();
+    const uint32_t* planes_a = &planes_lds[lq][0][0];
+    const uint32_t* planes_l = &planes_lds[lq][4][0];
+
+    // Per-lane byte offsets inside a page (first 16-token half); the second
+    // half of a 32-token page adds a wave-uniform step per region.
+    const uint32_t off_codes_a = p.anchor.offset + t * CodeA + lq * (32 * BA / 8);
+    const uint32_t off_scale_a = p.anchor.offset + PT * CodeA + t * GroupsA + lq * (32 / GA);
+    const uint32_t off_offs_a = off_scale_a + PT * GroupsA;
+    const uint32_t off_codes_l = p.residual.offset + t * CodeL + lq * (32 * BL / 8);
+    const uint32_t off_scale_l = p.residual.offset + PT * CodeL + t * GroupsL + lq * (32 / GL);
+    const uint32_t off_offs_l = off_scale_l + PT * GroupsL;
+    const uint32_t off_alpha = p.residual.offset + PT * (CodeL + 2 * GroupsL) + 2 * t;
 
     float acc[32];
 #pragma unroll
     for (int i = 0; i < 32; ++i) acc[i] = 0.f;
-    float cst[2] = {0.f, 0.f};
+    float cst0 = 0.f, cst1 = 0.f;
     float m = -INFINITY, l = 0.f;
+
     const int32_t* table = p.block_table + (int64_t)range.request * p.block_table_stride;
-    const int64_t page_bytes = (int64_t)p.page_tokens * p.page_width;
-    const int units_per_page = p.page_tokens / kUnitTokens;
+    const int64_t page_bytes = (int64_t)PT * p.page_width;
+    const int64_t history = range.history;
 
-    for (int64_t u = range.unit_begin + wave; u < range.unit_end; u += kWaves) {
-        const int64_t page_index = u / units_per_page;
-        const int token = (int)(u % units_per_page) * kUnitTokens + t;
-        const int64_t block = table[page_index];
-        if (block < 0 || block >= p.num_blocks) continue;
-        const bool valid = lane_active && page_index * p.page_tokens + token < range.history;
-        const uint8_t* kpage = p.cache + (block * p.heads + head) * page_bytes;
-        const uint8_t* vpage = kpage + p.plane_stride;
-
-        const RecordView<BA, GA> ka(kpage, p.anchor, p.page_tokens, token, lq);
-        const RecordView<BA, GA> va(vpage, p.anchor, p.page_tokens, token, lq);
-        Codes<BA> kcodes_a, vcodes_a;
-        GroupParams<GA> kpar_a, vpar_a;
-        kcodes_a.load(ka.codes);
-        kpar_a.load(ka.scales, ka.offsets);
-        vcodes_a.load(va.codes);
-        vpar_a.load(va.scales, va.offsets);
-
-        Codes<BL> kcodes_l, vcodes_l;
-        GroupParams<GL> kpar_l, vpar_l;
-        float alpha_k = 1.f, alpha_v = 1.f;
+    auto load_unit = [&](int64_t u, Unit<BA, GA, BL, GL, HasL>& d) -> bool {
+        const int64_t page_index = u / UnitsPerPage;
+        const int half = (int)(u % UnitsPerPage);
+        const int block = __builtin_amdgcn_readfirstlane(table[page_index]);
+        if (block < 0 || block >= p.num_blocks) return false;
+        const uint8_t* kbase = p.cache + ((int64_t)block * p.heads + head) * page_bytes;
+        const __amdgpu_buffer_rsrc_t kpage = page_resource(kbase, (uint32_t)page_bytes);
+        const __amdgpu_buffer_rsrc_t vpage = page_resource(kbase + p.plane_stride, (uint32_t)page_bytes);
+        const uint32_t step_codes_a = half * (kUnitTokens * CodeA);
+        const uint32_t step_par_a = half * (kUnitTokens * GroupsA);
+        load_codes<BA>(kpage, off_codes_a, step_codes_a, d.kca);
+        d.kpa.load(kpage, off_scale_a, off_offs_a, step_par_a);
+        load_codes<BA>(vpage, off_codes_a, step_codes_a, d.vca);
+        d.vpa.load(vpage, off_scale_a, off_offs_a, step_par_a);
         if constexpr (HasL) {
-            const RecordView<BL, GL> kl(kpage, p.residual, p.page_tokens, token, lq);
-            const RecordView<BL, GL> vl(vpage, p.residual, p.page_tokens, token, lq);
-            kcodes_l.load(kl.codes);
-            kpar_l.load(kl.scales, kl.offsets);
-            vcodes_l.load(vl.codes);
-            vpar_l.load(vl.scales, vl.offsets);
-            alpha_k = bf16_f32(*reinterpret_cast<const uint16_t*>(kl.alpha));
-            alpha_v = bf16_f32(*reinterpret_cast<const uint16_t*>(vl.alpha));
+            const uint32_t step_codes_l = half * (kUnitTokens * CodeL);
+            const uint32_t step_par_l = half * (kUnitTokens * GroupsL);
+            const uint32_t step_alpha = half * (2 * kUnitTokens);
+            load_codes<BL>(kpage, off_codes_l, step_codes_l, d.kcl);
+            d.kpl.load(kpage, off_scale_l, off_offs_l, step_par_l);
+            load_codes<BL>(vpage, off_codes_l, step_codes_l, d.vcl);
+            d.vpl.load(vpage, off_scale_l, off_offs_l, step_par_l);
+            d.alpha_k_bits = __builtin_amdgcn_raw_buffer_load_b16(kpage, off_alpha, step_alpha, 0);
+            d.alpha_v_bits = __builtin_amdgcn_raw_buffer_load_b16(vpage, off_alpha, step_alpha, 0);
         }
+        return true;
+    };
 
-        // ---- scores
-        int dots_a[2];
-        code_dots<BA>(kcodes_a, planes_a, dots_a);
-        float lane_score = record_score<GA>(kpar_a, dots_a, delta, q_sum_a);
+    // Values of one unit: acc += p * (alpha_v * deq_A + deq_L); offsets go to cst.
+    auto accumulate = [&](const Unit<BA, GA, BL, GL, HasL>& d, float prob) {
+        const float p512 = prob * 512.0f;
+        float w_a[2];
         if constexpr (HasL) {
-            int dots_l[2];
-            code_dots<BL>(kcodes_l, planes_l, dots_l);
-            lane_score = alpha_k * lane_score + record_score<GL>(kpar_l, dots_l, delta, q_sum_l);
+            const float alpha_v = __uint_as_float(d.alpha_v_bits << 16);
+            const float pa = prob * alpha_v;
+            const float pa512 = p512 * alpha_v;
+            w_a[0] = pa512 * d.vpa.template scale<0>();
+            w_a[1] = GA == 32 ? w_a[0] : pa512 * d.vpa.template scale<1>();
+            float w_l[2];
+            w_l[0] = p512 * d.vpl.template scale<0>();
+            w_l[1] = GL == 32 ? w_l[0] : p512 * d.vpl.template scale<1>();
+            cst0 = fmaf(pa, d.vpa.template offset<0>(), fmaf(prob, d.vpl.template offset<0>(), cst0));
+            cst1 = fmaf(pa, d.vpa.template offset<1>(), fmaf(prob, d.vpl.template offset<1>(), cst1));
+            accumulate_codes<BL>(d.vcl, w_l, acc);
+        } else {
+            w_a[0] = p512 * d.vpa.template scale<0>();
+            w_a[1] = GA == 32 ? w_a[0] : p512 * d.vpa.template scale<1>();
+            cst0 = fmaf(prob, d.vpa.template offset<0>(), cst0);
+            cst1 = fmaf(prob, d.vpa.template offset<1>(), cst1);
         }
-        float score = quad_sum(lane_active ? lane_score : 0.f);
-        if constexpr (HasL) score += alpha_k * q_mean_anchor;
-        score = valid ? score : -INFINITY;
+        accumulate_codes<BA>(d.vca, w_a, acc);
+    };
 
-        // ---- online softmax (wave-uniform running maximum)
-        const float unit_max = token_max(score);
+    // Each iteration streams two consecutive 16-token units of the split.
+    const int64_t first = range.unit_begin + 2 * wave;
+    for (int64_t u = first; u < range.unit_end; u += 2 * kWaves) {
+        Unit<BA, GA, BL, GL, HasL> d0, d1;
+        const bool ok0 = load_unit(u, d0);
+        const bool has1 = u + 1 < range.unit_end;
+        const bool ok1 = has1 && load_unit(u + 1, d1);
+        const int64_t pos0 = (u / UnitsPerPage) * PT + (u % UnitsPerPage) * kUnitTokens + t;
+        const int64_t pos1 = ((u + 1) / UnitsPerPage) * PT + ((u + 1) % UnitsPerPage) * kUnitTokens + t;
+        const bool valid0 = ok0 && lane_active && pos0 < history;
+        const bool valid1 = ok1 && lane_active && pos1 < history;
+        if (!ok1) d1 = d0;  // keep the registers defined; unit 1 is masked
+
+        int da0[2], da1[2];
+        code_dots2<BA>(d0.kca, d1.kca, planes_a, da0, da1);
+        float s0 = record_score<GA>(d0.kpa, da0, delta, q_sum_a);
+        float s1 = record_score<GA>(d1.kpa, da1, delta, q_sum_a);
+        if constexpr (HasL) {
+            int dl0[2], dl1[2];
+            code_dots2<BL>(d0.kcl, d1.kcl, planes_l, dl0, dl1);
+            const float mean_part = qd == 0 ? q_mean_anchor : 0.f;
+            s0 = __uint_as_float(d0.alpha_k_bits << 16) * (s0 + mean_part) +
+                 record_score<GL>(d0.kpl, dl0, delta, q_sum_l);
+            s1 = __uint_as_float(d1.alpha_k_bits << 16) * (s1 + mean_part) +
+                 record_score<GL>(d1.kpl, dl1, delta, q_sum_l);
+        }
+        float score0 = quad_sum_fast(lane_active ? s0 : 0.f);
+        float score1 = quad_sum_fast(lane_active ? s1 : 0.f);
+        score0 = valid0 ? score0 : -INFINITY;
+        score1 = valid1 ? score1 : -INFINITY;
+
+        const float unit_max = wave_max(fmaxf(score0, score1));
         if (unit_max > m) {
-            const float factor = m == -INFINITY ? 0.f : exp2f(m - unit_max);
+            const float factor = m == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m - unit_max);
 #pragma unroll
             for (int i = 0; i < 32; ++i) acc[i] *= factor;
-            cst[0] *= factor;
-            cst[1] *= factor;
+            cst0 *= factor;
+            cst1 *= factor;
             l *= factor;
             m = unit_max;
         }
-        const float prob = valid ? exp2f(score - m) : 0.f;
-        l += prob;
-
-        // ---- values: acc += p * (alpha_v * deq_A + deq_L), offsets folded into cst
-        float w_a[2], w_l[2];
-        if constexpr (HasL) {
-            const float pa = prob * alpha_v;
-            w_a[0] = pa * vpar_a.scale[0];
-            w_a[1] = pa * vpar_a.scale[1];
-            w_l[0] = prob * vpar_l.scale[0];
-            w_l[1] = prob * vpar_l.scale[1];
-            if (valid) {
-                cst[0] = fmaf(pa, vpar_a.offset[0], fmaf(prob, vpar_l.offset[0], cst[0]));
-                cst[1] = fmaf(pa, vpar_a.offset[1], fmaf(prob, vpar_l.offset[1], cst[1]));
-            }
-        } else {
-            w_a[0] = prob * vpar_a.scale[0];
-            w_a[1] = prob * vpar_a.scale[1];
-            if (valid) {
-                cst[0] = fmaf(prob, vpar_a.offset[0], cst[0]);
-                cst[1] = fmaf(prob, vpar_a.offset[1], cst[1]);
-            }
-        }
-        if (!valid) {
-            w_a[0] = w_a[1] = 0.f;
-            w_l[0] = w_l[1] = 0.f;
-        }
-        accumulate_codes<BA>(vcodes_a, w_a, acc);
-        if constexpr (HasL) accumulate_codes<BL>(vcodes_l, w_l, acc);
+        const float prob0 = valid0 ? __builtin_amdgcn_exp2f(score0 - m) : 0.f;
+        const float prob1 = valid1 ? __builtin_amdgcn_exp2f(score1 - m) : 0.f;
+        l += prob0 + prob1;
+        accumulate(d0, prob0);
+        accumulate(d1, prob1);
     }
 
 #pragma unroll
-    for (int i = 0; i < 32; ++i) acc[i] += cst[i >> 4];
+    for (int i = 0; i < 16; ++i) {
+        acc[i] += cst0;
+        acc[16 + i] += cst1;
+    }
     write_partial<D>(acc, m, l, lane, wave, lane_active, partial);
 }
 
@@ -622,6 +761,9 @@ __global__ __launch_bounds__(128) void merge_kernel(AttentionParams p) {
     __shared__ float weights[kMaxSplits];
     __shared__ float totals[2];
     __shared__ float history[128];
+    // R_v rows padded by two halves so that lanes reading row c hit distinct banks.
+    constexpr int Stride = D + 2;
+    __shared__ __attribute__((aligned(16))) _Float16 rotation_lds[D * Stride];
     const int request = p.row_request[row];
     if (request < 0) return;
     const int64_t rh = row * p.heads + head;
@@ -649,11 +791,20 @@ __global__ __launch_bounds__(128) void merge_kernel(AttentionParams p) {
     }
     if (p.value_rotation != nullptr) {
         history[c] = h;
+        const uint4* src = reinterpret_cast<const uint4*>(p.value_rotation + (int64_t)head * D * D);
+        for (int i = c; i < D * D / 8; i += 128) {
+            const uint4 v = src[i];
+            uint32_t* dst = reinterpret_cast<uint32_t*>(rotation_lds + (i / (D / 8)) * Stride + (i % (D / 8)) * 8);
+            dst[0] = v.x;
+            dst[1] = v.y;
+            dst[2] = v.z;
+            dst[3] = v.w;
+        }
         __syncthreads();
         if (c < D) {
-            const uint16_t* r = p.value_rotation + (int64_t)head * D * D + (int64_t)c * D;
+            const _Float16* r = rotation_lds + c * Stride;
             float acc = 0.f;
-            for (int k = 0; k < D; ++k) acc = fmaf(history[k], f16_f32(r[k]), acc);
+            for (int k = 0; k < D; ++k) acc = fmaf(history[k], (float)r[k], acc);
             h = acc;
         }
     }
@@ -665,35 +816,42 @@ __global__ __launch_bounds__(128) void merge_kernel(AttentionParams p) {
 
 // ------------------------------------------------------------------ launch
 
-template <int D, int BA, int GA, int BL, int GL, bool HasL>
+template <int D, int PT, int BA, int GA, int BL, int GL, bool HasL>
 void launch_decode(const AttentionParams& p, hipStream_t stream) {
     const unsigned blocks = (unsigned)(p.rows * p.heads * p.splits);
-    hipLaunchKernelGGL((decode_kernel<D, BA, GA, BL, GL, HasL>), dim3(blocks), dim3(kDecodeThreads), 0,
+    hipLaunchKernelGGL((decode_kernel<D, PT, BA, GA, BL, GL, HasL>), dim3(blocks), dim3(kDecodeThreads), 0,
                        stream, p);
 }
 
-template <int D, int BA, int GA>
+template <int D, int PT, int BA, int GA>
 bool dispatch_residual(const AttentionParams& p, hipStream_t stream) {
     if (!p.has_residual) {
-        launch_decode<D, BA, GA, 2, 32, false>(p, stream);
+        launch_decode<D, PT, BA, GA, 2, 32, false>(p, stream);
         return true;
     }
     const int bits = p.residual.bits, group = p.residual.group;
-    if (bits == 2 && group == 32) launch_decode<D, BA, GA, 2, 32, true>(p, stream);
-    else if (bits == 2 && group == 16) launch_decode<D, BA, GA, 2, 16, true>(p, stream);
-    else if (bits == 4 && group == 32) launch_decode<D, BA, GA, 4, 32, true>(p, stream);
-    else if (bits == 4 && group == 16) launch_decode<D, BA, GA, 4, 16, true>(p, stream);
+    if (bits == 2 && group == 32) launch_decode<D, PT, BA, GA, 2, 32, true>(p, stream);
+    else if (bits == 2 && group == 16) launch_decode<D, PT, BA, GA, 2, 16, true>(p, stream);
+    else if (bits == 4 && group == 32) launch_decode<D, PT, BA, GA, 4, 32, true>(p, stream);
+    else if (bits == 4 && group == 16) launch_decode<D, PT, BA, GA, 4, 16, true>(p, stream);
     else return false;
     return true;
 }
 
+template <int D, int PT>
+bool dispatch_anchor_pt(const AttentionParams& p, hipStream_t stream) {
+    const int bits = p.anchor.bits, group = p.anchor.group;
+    if (bits == 4 && group == 32) return dispatch_residual<D, PT, 4, 32>(p, stream);
+    if (bits == 4 && group == 16) return dispatch_residual<D, PT, 4, 16>(p, stream);
+    if (bits == 2 && group == 32) return dispatch_residual<D, PT, 2, 32>(p, stream);
+    if (bits == 2 && group == 16) return dispatch_residual<D, PT, 2, 16>(p, stream);
+    return false;
+}
+
 template <int D>
 bool dispatch_anchor(const AttentionParams& p, hipStream_t stream) {
-    const int bits = p.anchor.bits, group = p.anchor.group;
-    if (bits == 4 && group == 32) return dispatch_residual<D, 4, 32>(p, stream);
-    if (bits == 4 && group == 16) return dispatch_residual<D, 4, 16>(p, stream);
-    if (bits == 2 && group == 32) return dispatch_residual<D, 2, 32>(p, stream);
-    if (bits == 2 && group == 16) return dispatch_residual<D, 2, 16>(p, stream);
+    if (p.page_tokens == 16) return dispatch_anchor_pt<D, 16>(p, stream);
+    if (p.page_tokens == 32) return dispatch_anchor_pt<D, 32>(p, stream);
     return false;
 }
 
