@@ -80,6 +80,30 @@ def timed(torch, fn, steps, warmup):
     return (time.perf_counter() - start) / steps
 
 
+def capture(torch, fn):
+    """Capture fn's launches into one HIP graph (torch.cuda.CUDAGraph is hipGraph on ROCm)."""
+    stream = torch.cuda.Stream()
+    stream.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(stream):
+        fn()
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=stream):
+        fn()
+    torch.cuda.synchronize()
+    return graph
+
+
+def measured_traffic():
+    """HBM bytes per residual-loop decode launch from the committed rocprofv3 counter summary."""
+    path = os.path.join(ROOT, "profiles", "decode_c2_counters.json")
+    if not os.path.exists(path):
+        return None
+    with open(path) as handle:
+        data = json.load(handle)
+    return data.get("residual_loop_traffic_bytes")
+
+
 def kernel_average_ms(torch, ops, fn, reps):
     """Average split-K kernel duration from HIP events recorded on the launch stream."""
     fn()
@@ -142,6 +166,10 @@ def main():
     parser.add_argument("--no-bf16", action="store_true")
     parser.add_argument("--split-target", type=int, default=0,
                         help="split-K workgroups per decode launch (0 = the library's default)")
+    parser.add_argument("--eager", action="store_true",
+                        help="time the step as eager launches instead of one HIP-graph replay")
+    parser.add_argument("--copy-calibration-mib", type=int, default=0,
+                        help="also run a plain FP32 copy kernel of this size (rocprofv3 counter calibration)")
     args = parser.parse_args()
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -185,9 +213,15 @@ def main():
         for loop in range(len(SCHEDULE)):
             call(loop)
 
-    step_s = timed(torch, step, args.steps, args.warmup)
+    eager_s = timed(torch, step, args.steps, args.warmup)
+    graph_s = None
+    if not args.eager:
+        graph = capture(torch, step)
+        graph_s = timed(torch, graph.replay, args.steps, args.warmup)
+    step_s = eager_s if graph_s is None else graph_s
     step_bytes = sum(staged_call_bytes(batch, history, heads, dim, page_tokens, loop) for loop in range(4))
-    log(f"[bench] packed step {step_s * 1e6:.1f} us")
+    log(f"[bench] packed step {step_s * 1e6:.1f} us ({'eager' if graph_s is None else 'graph'}), "
+        f"eager {eager_s * 1e6:.1f} us")
 
     residual_ms, residual_launches = kernel_average_ms(torch, ops, lambda: call(0), max(10, args.steps))
     anchor_ms, _ = kernel_average_ms(torch, ops, lambda: call(ANCHOR), max(10, args.steps))
@@ -214,6 +248,10 @@ def main():
                 bf16_call()
 
         bf16_step_s = timed(torch, bf16_step, args.steps, args.warmup)
+        if not args.eager:
+            bf16_graph = capture(torch, bf16_step)
+            bf16_step_s = timed(torch, bf16_graph.replay, args.steps, args.warmup)
+            del bf16_graph
         bf16_ms, _ = kernel_average_ms(torch, ops, bf16_call, max(10, args.steps))
         bytes_bf16 = bf16_call_bytes(batch, history, heads, dim)
         bf16 = {
@@ -226,6 +264,16 @@ def main():
         log(f"[bench] bf16 step {bf16_step_s * 1e6:.1f} us, kernel {bf16_ms * 1e3:.1f} us "
             f"({bf16['kernel_GBps']:.0f} GB/s)")
         del bf16_cache, bf16_ws
+
+    if args.copy_calibration_mib:
+        n = args.copy_calibration_mib * (1 << 20) // 4
+        src = torch.ones(n, dtype=torch.float32, device=device)
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            torch.mul(src, 1.0, out=dst)
+        torch.cuda.synchronize()
+        log(f"[bench] copy calibration: {args.copy_calibration_mib} MiB read + written per launch")
+        del src, dst
 
     cpu = None
     if args.cpu_budget > 0:
@@ -254,6 +302,8 @@ def main():
             "step": "3 residual-loop calls + 1 anchor-loop call (prepare + split-K decode + merge each)",
         },
         "us_per_step": step_s * 1e6,
+        "us_per_step_eager": eager_s * 1e6,
+        "timing": "one HIP-graph replay of the 4 calls per step" if graph_s is not None else "eager launches",
         "pct_peak_step": 100.0 * step_bytes / step_s / 1e9 / PEAK_HBM_GBPS,
         "bytes_per_step": step_bytes,
         "tokens_per_s": batch / step_s,
@@ -270,7 +320,7 @@ def main():
             "peak": PEAK_HBM_GBPS,
             "unit": "GB/s",
             "frac": residual_gbps / PEAK_HBM_GBPS,
-            "traffic": None,
+            "traffic": measured_traffic(),
             "kernel": "decode_kernel<128,4,32,2,32,true> (residual loop), "
                       f"{residual_launches} HIP-event-timed launches",
         },

@@ -1,0 +1,136 @@
+"""The C ABI library (CPU): it loads, exports every symbol include/rq_hip.h
+declares, and rejects invalid arguments on the host before any device work
+with the reference's error messages (quantize/api.cpp:18-85,
+attention/api.cpp:23-104, dispatch/kernel_registry.h:42-72)."""
+
+from __future__ import annotations
+
+import ctypes
+import os
+import re
+import subprocess
+
+import pytest
+import torch
+
+from residualquant_amd import _lib, ops
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "rq_hip.h")
+
+
+def _declared():
+    text = open(HEADER).read()
+    return set(re.findall(r"^\s*(?:const\s+)?[\w\*\s]+?\b(rq_\w+)\s*\(", text, flags=re.M))
+
+
+@pytest.fixture(scope="module")
+def lib():
+    if not os.path.exists(_lib.LIB_PATH):
+        _lib.build()
+    return _lib.lib()
+
+
+def test_header_declares_exactly_the_exported_list():
+    assert _declared() == set(_lib.EXPORTED_SYMBOLS)
+
+
+def test_library_exports_every_declared_symbol(lib):
+    out = subprocess.run(["nm", "-D", "--defined-only", _lib.LIB_PATH], capture_output=True, text=True,
+                         check=True).stdout
+    exported = {line.split()[-1] for line in out.splitlines() if " T " in line}
+    missing = _declared() - exported
+    assert not missing, missing
+    for name in _declared():
+        assert getattr(lib, name) is not None
+
+
+def _schedule(records):
+    bits = (ctypes.c_int * len(records))(*[r[0] for r in records])
+    groups = (ctypes.c_int * len(records))(*[r[1] for r in records])
+    return bits, groups
+
+
+def test_page_width_known_answers_and_errors(lib):
+    assert lib.rq_page_width(128, 4, *_schedule([(2, 32)] * 3 + [(4, 32)])) == 200
+    assert lib.rq_page_width(128, 4, *_schedule([(2, 16)] * 3 + [(4, 32)])) == 224
+    assert lib.rq_page_width(96, 4, *_schedule([(2, 16)] * 3 + [(4, 32)])) == 170
+    assert lib.rq_page_width(96, 4, *_schedule([(2, 32)] * 3 + [(4, 32)])) == 152
+    assert lib.rq_page_width(128, 1, *_schedule([(2, 48)])) == _lib.RQ_EINVAL
+    assert b"divisible" in lib.rq_last_error()
+    assert lib.rq_page_width(100, 1, *_schedule([(2, 32)])) == _lib.RQ_EINVAL
+
+
+def _quantize_call(lib, records, *, head_dim=128, page_tokens=16, page_width=200, mode=0, anchor=3,
+                   coefficient=2, tokens=4, input_rows=4, width_override=None):
+    count = len(records)
+    fake = ctypes.c_void_p(0x10000)
+    ptrs = (ctypes.c_void_p * count)(*([fake.value] * count))
+    strides = (ctypes.c_int64 * count)(*([16 * head_dim] * count))
+    bits, groups = _schedule(records)
+    return lib.rq_quantize(count, ctypes.cast(ptrs, ctypes.c_void_p), ctypes.cast(strides, ctypes.c_void_p),
+                           ctypes.cast(ptrs, ctypes.c_void_p), ctypes.cast(strides, ctypes.c_void_p), input_rows,
+                           fake, 8, 16, page_tokens, width_override or page_width, fake, tokens, head_dim,
+                           None, None, None, ctypes.cast(bits, ctypes.c_void_p),
+                           ctypes.cast(groups, ctypes.c_void_p), mode, anchor, coefficient, None)
+
+
+G32 = [(2, 32)] * 3 + [(4, 32)]
+
+
+def test_quantize_rejects_before_device_work(lib):
+    assert _quantize_call(lib, G32, coefficient=7) == _lib.RQ_EINVAL
+    assert lib.rq_last_error() == b"Unsupported coefficient"
+    assert _quantize_call(lib, G32, input_rows=3) == _lib.RQ_EINVAL
+    assert lib.rq_last_error() == b"Input has fewer rows than slot mapping"
+    assert _quantize_call(lib, G32, width_override=199) == _lib.RQ_EINVAL
+    assert lib.rq_last_error() == b"Packed cache width differs from records"
+    assert _quantize_call(lib, G32, page_tokens=8) == _lib.RQ_ENOKERNEL
+    assert lib.rq_last_error().startswith(b"No compiled packed HIP kernel for heads=16")
+    assert _quantize_call(lib, G32, mode=1, anchor=3) == _lib.RQ_ENOKERNEL  # adjacent needs anchor 0
+    assert _quantize_call(lib, [(3, 32)]) == _lib.RQ_ENOKERNEL
+    assert _quantize_call(lib, G32, anchor=4) == _lib.RQ_ENOKERNEL
+    assert _quantize_call(lib, G32, tokens=0, input_rows=0) == _lib.RQ_OK  # empty slot mapping: no launch
+
+
+def _attention_call(lib, *, loop=0, workspace=None, workspace_bytes=0, query_stride=16 * 128, records=G32,
+                    page_width=200, query=0x10000):
+    fake = 0x10000
+    bits, groups = _schedule(records)
+    return lib.rq_attention(query, query_stride, fake, 16 * 128, fake, 16 * 128, fake, 16 * 128, 2, 16, 128,
+                            fake, 8, 16, page_width, fake, fake, 2, fake, 4, 4, None, None, None,
+                            len(records), ctypes.cast(bits, ctypes.c_void_p), ctypes.cast(groups, ctypes.c_void_p),
+                            0, 3, loop, workspace, workspace_bytes, None)
+
+
+def test_attention_rejects_before_device_work(lib):
+    assert _attention_call(lib, loop=4) == _lib.RQ_EINVAL
+    assert lib.rq_last_error() == b"Invalid loop index"
+    assert _attention_call(lib, page_width=201) == _lib.RQ_EINVAL
+    assert lib.rq_last_error() == b"Packed cache width differs from records"
+    assert _attention_call(lib, query=0x10004) == _lib.RQ_EINVAL
+    assert lib.rq_last_error() == b"Q/K addresses and token strides must be 8-byte aligned"
+    assert _attention_call(lib, query_stride=16 * 128 + 2) == _lib.RQ_EINVAL
+    assert _attention_call(lib) == _lib.RQ_ENOSPACE
+    assert lib.rq_last_error().startswith(b"Attention workspace of")
+
+
+def test_workspace_size_depends_on_shapes_only(lib):
+    a = lib.rq_attention_workspace_bytes(32, 16, 128, 512, 16)
+    b = lib.rq_attention_workspace_bytes(32, 16, 128, 512, 16)
+    assert a == b and a > 32 * 16 * 130 * 4
+    assert lib.rq_attention_workspace_bytes(64, 16, 128, 512, 16) > a
+
+
+def test_python_ops_mirror_reference_messages():
+    cpu = torch.zeros((2, 16, 128), dtype=torch.bfloat16)
+    cache = torch.zeros((2, 4, 16, 16, 200), dtype=torch.uint8)
+    slots = torch.zeros(2, dtype=torch.int64)
+    with pytest.raises(RuntimeError, match="A nonempty group with one K/V input per record required"):
+        ops.quantize([(cpu, cpu)] * 3, cache, slots, None, None, None, G32, "anchor", 3, "ls")
+    with pytest.raises(RuntimeError, match=r"Contiguous CUDA UINT8 \[2, blocks, heads, page tokens, page width\]"):
+        ops.quantize([(cpu, cpu)] * 4, cache, slots, None, None, None, G32, "anchor", 3, "ls")
+    with pytest.raises(RuntimeError, match=r"BF16 \[tokens, heads, channels\] with packed trailing strides required"):
+        ops.attention(cpu, cpu, cpu, cache, cpu, torch.zeros(3, dtype=torch.int32),
+                      torch.zeros(2, dtype=torch.int32), torch.zeros((2, 4), dtype=torch.int32), None, None, None,
+                      G32, "anchor", 3, 0)
