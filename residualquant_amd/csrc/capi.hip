@@ -216,6 +216,14 @@ int rq_quantize(int records, const void* const* key_ptrs, const int64_t* key_str
         if (key_ptrs[r] == nullptr || value_ptrs[r] == nullptr || key_strides[r] < (int64_t)heads * head_dim ||
             value_strides[r] < (int64_t)heads * head_dim)
             return fail(RQ_EINVAL, "BF16 [tokens, heads, channels] with packed trailing strides required");
+    // The rotation phase reads input rows with 8-byte scalar loads and stages
+    // each FP16 rotation with 16-byte loads.
+    for (int r = 0; r < records; ++r)
+        if (reinterpret_cast<uintptr_t>(key_ptrs[r]) % 8 || reinterpret_cast<uintptr_t>(value_ptrs[r]) % 8 ||
+            key_strides[r] % 4 || value_strides[r] % 4)
+            return fail(RQ_EINVAL, "K/V addresses and token strides must be 8-byte aligned");
+    if (reinterpret_cast<uintptr_t>(key_rotation) % 16 || reinterpret_cast<uintptr_t>(value_rotation) % 16)
+        return fail(RQ_EINVAL, "Rotation addresses must be 16-byte aligned");
     if (tokens == 0) return ok();
 
     rq::QuantizeParams p{};

@@ -8,14 +8,23 @@
 // codes, scattered by slot_mapping into the paged cache.
 //
 // Arithmetic is the canonical order the CPU oracle defines (bit-exact):
-// k-ascending FP32 rotation, per-lane fmaf chains plus the 16,8,4,2,1 xor
-// butterfly for the LS sums, IEEE division/sqrt, RNE satfinite FP8, single
-// rounded BF16 restores.  Contraction is disabled for this file.
+// k-ascending FP32 rotation, per-lane fmaf chains over the 4 channels of
+// each of 32 "canonical lanes" plus the 16,8,4,2,1 xor butterfly for the LS
+// sums, IEEE division/sqrt, RNE satfinite FP8, single rounded BF16 restores.
+// Contraction is disabled for this file.
 //
-// Work mapping: one workgroup = 8 tokens x 1 head x 1 plane, 256 threads.
-// Each 32-lane half-wave owns one token; lane l owns channels 4l..4l+3 of
-// every record, so the coefficient butterfly and the group min/max stay inside
-// the half-wave and the rotated rows never leave registers.
+// Work mapping: one workgroup = one (head, plane) and a run of tokens; its 16
+// waves share the FP32 rotation in LDS.  A wave takes 4 tokens per pass, 16
+// lanes per token.  Lane j of a token owns canonical lanes j and j + 16, i.e.
+// channels 4j..4j+3 and 64+4j..64+4j+3 of every record, in both phases:
+//  - rotation: per k, one LDS broadcast read brings x[token][k][records],
+//    two 16-byte reads bring the lane's 8 rotation entries, and the
+//    8 * records FMAs are plain VOP2 v_fmac_f32 (the full-rate form; the
+//    v_fma_mix and DPP forms issue at half rate).  Inputs are staged per
+//    wave as FP32 in a double-buffered LDS chunk of 32 k.
+//  - commit: the xor-16 level of the butterfly is the in-lane sum of the two
+//    canonical lanes, the other levels and the group min/max run across the
+//    16 lanes of the token with DPP and ds_swizzle.
 #include "rq_device.h"
 #include "rq_kernels.h"
 
@@ -25,241 +34,370 @@ namespace rq {
 
 namespace {
 
-constexpr int kTileTokens = 8;
-constexpr int kQuantizeThreads = 256;
+constexpr int kQuantizeWaves = 16;
+constexpr int kQuantizeThreads = 64 * kQuantizeWaves;
+constexpr int kWaveTokens = 4;    // tokens per wave per pass, 16 lanes each
+constexpr int kChunk = 32;        // k per staged input chunk
+constexpr int kStageRecords = 4;  // record slots per staged (token, k)
 
-__device__ __forceinline__ float shfl_xor32(float v, int mask) { return __shfl_xor(v, mask, 32); }
+// ---------------------------------------------------------------- lanes
 
-// Commit one record of one token (kernel.cuh:33-228).  All 32 lanes of the
-// half-wave call this together; `store` masks the global writes only.
-template <int D>
-__device__ __forceinline__ void commit_record(const float (&y)[4], bool is_anchor, bool restore,
-                                              int coefficient, const float (&mean)[4],
-                                              bool has_mean, uint32_t (&reference)[4],
-                                              const RecordRegion& region, uint8_t* page,
-                                              int token, int page_tokens, int lane, bool store) {
-    const bool active = lane * 4 < D;
-    float previous[4] = {0.f, 0.f, 0.f, 0.f};
-    float x[4];
+template <int Distance>
+__device__ __forceinline__ float swizzle_xor(float v) {
+    // ds_swizzle bit mode inside 32 lanes: and 0x1f, or 0, xor Distance.
+    return __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(v), 0x1f | (Distance << 10)));
+}
+
+template <int Control>
+__device__ __forceinline__ float dpp(float v) {
+    return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), Control, 0xf, 0xf, false));
+}
+
+constexpr int kXor1 = 0xB1;   // quad_perm [1,0,3,2]
+constexpr int kXor2 = 0x4E;   // quad_perm [2,3,0,1]
+constexpr int kXor8 = 0x128;  // row_ror:8 inside 16 lanes
+
+// The xor butterfly of kernel.cuh:15-20 over the 32 canonical partials, given
+// this lane's two (canonical lanes j and j + 16): the distance-16 level is
+// their in-lane sum, distances 8, 4, 2, 1 pair lanes j ^ d of the token.
+__device__ __forceinline__ float butterfly_sum(float low, float high) {
+    float v = low + high;
+    v += dpp<kXor8>(v);
+    v += swizzle_xor<4>(v);
+    v += dpp<kXor2>(v);
+    v += dpp<kXor1>(v);
+    return v;
+}
+
+// IEEE-754 minimum/maximum: -0 orders below +0 (the min_z/max_z order).
+__device__ __forceinline__ float fmin_z(float a, float b) { return __builtin_elementwise_minimum(a, b); }
+__device__ __forceinline__ float fmax_z(float a, float b) { return __builtin_elementwise_maximum(a, b); }
+
+// Both E4M3 codes of a group with one v_cvt_pk_fp8_f32 (RNE; the med3 clamp
+// to +-448 gives the satfinite behaviour of __nv_fp8_e4m3).
+__device__ __forceinline__ uint32_t e4m3_pair(float low_value, float high_value) {
+    const float a = __builtin_amdgcn_fmed3f(low_value, -448.0f, 448.0f);
+    const float b = __builtin_amdgcn_fmed3f(high_value, -448.0f, 448.0f);
+    return (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(a, b, 0, false) & 0xffffu;
+}
+
+__device__ __forceinline__ float e4m3_value(uint32_t code) {
+    return __builtin_amdgcn_cvt_f32_fp8((int)code, 0);
+}
+
+// ---------------------------------------------------------------- commit
+
+// Commit one record of one token (kernel.cuh:33-228) for the lane's two
+// canonical lanes (h = 0: channels 4j.., h = 1: channels 64+4j..).  All 16
+// lanes of the token call this together; `store` masks the global writes.
+//
+// The division (x - offset) / scale uses the exact reciprocal y = RN(1/scale)
+// and one correction step, q = RN(q0 + RN(a - q0 * scale) * y) with
+// q0 = RN(a * y): for every E4M3 scale this equals the IEEE quotient (checked
+// exhaustively over all FP32 mantissas).  code * scale + offset is exact in
+// FP32 (E4M3 operands, 4-bit codes), and a BF16 + BF16 sum rounded once from
+// FP32 equals its single-rounded value, so the anchor restore needs no
+// TwoSum; the residual chain of adjacent mode keeps it.
+__device__ __forceinline__ void commit_record(float (&x)[2][4], const bool (&active)[2], bool is_anchor,
+                                              bool restore, int coefficient, const float (&mean)[2][4],
+                                              bool has_mean, uint32_t (&reference)[2][4],
+                                              const RecordRegion& region, uint8_t* page, int token,
+                                              int page_tokens, int j, bool store, const float* inverse_scale) {
+    float previous[2][4];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        x[i] = active ? y[i] : 0.f;
-        if (!is_anchor && active) previous[i] = bf16_f32(reference[i]);
-    }
+    for (int h = 0; h < 2; ++h)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) previous[h][i] = (!is_anchor && active[h]) ? bf16_f32(reference[h][i]) : 0.f;
 
     float alpha = 1.0f;
     if (!is_anchor && coefficient != RQ_COEF_UNIT_) {
-        float numerator = 0.f, denominator = 0.f;
+        float numerator[2] = {0.f, 0.f}, denominator[2] = {0.f, 0.f};
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            numerator = coefficient == RQ_COEF_NORM_ ? fmaf(x[i], x[i], numerator)
-                                                     : fmaf(x[i], previous[i], numerator);
-            denominator = fmaf(previous[i], previous[i], denominator);
-        }
+        for (int h = 0; h < 2; ++h)
 #pragma unroll
-        for (int distance = 16; distance; distance >>= 1) {
-            numerator += shfl_xor32(numerator, distance);
-            denominator += shfl_xor32(denominator, distance);
-        }
+            for (int i = 0; i < 4; ++i) {
+                numerator[h] = coefficient == RQ_COEF_NORM_ ? fmaf(x[h][i], x[h][i], numerator[h])
+                                                            : fmaf(x[h][i], previous[h][i], numerator[h]);
+                denominator[h] = fmaf(previous[h][i], previous[h][i], denominator[h]);
+            }
+        const float num = butterfly_sum(numerator[0], numerator[1]);
+        const float den = butterfly_sum(denominator[0], denominator[1]);
         if (coefficient == RQ_COEF_NORM_)
-            alpha = denominator > 0.f ? sqrtf(numerator) / fmaxf(sqrtf(denominator), 1e-6f) : 0.f;
+            alpha = den > 0.f ? sqrtf(num) / fmaxf(sqrtf(den), 1e-6f) : 0.f;
         else
-            alpha = numerator / fmaxf(denominator, 1e-12f);
+            alpha = num / fmaxf(den, 1e-12f);
     }
     const uint32_t stored_alpha = bf16_rn(alpha);
     alpha = bf16_f32(stored_alpha);
 
-    float low = __uint_as_float(0x7f800000u), high = __uint_as_float(0xff800000u);
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        if (!is_anchor) x[i] = fmaf(-previous[i], alpha, x[i]);
-        if (has_mean) x[i] = x[i] - mean[i];
-        if (active) {
-            low = min_z(low, x[i]);
-            high = max_z(high, x[i]);
-        }
-    }
-    // A group spans 4 lanes (G16) or 8 lanes (G32).
-    if (region.group == 32) {
-        low = min_z(low, shfl_xor32(low, 4));
-        high = max_z(high, shfl_xor32(high, 4));
-    }
-    low = min_z(low, shfl_xor32(low, 2));
-    high = max_z(high, shfl_xor32(high, 2));
-    low = min_z(low, shfl_xor32(low, 1));
-    high = max_z(high, shfl_xor32(high, 1));
-
     const int bits = region.bits;
-    const float center = (low + high) * 0.5f;
-    const float radius = bits == 2 ? ((high - low) * 0.9f) * 0.5f : (high - low) * 0.5f;
     const float levels = bits == 2 ? 3.0f : 15.0f;
-    const uint32_t offset_code = e4m3_rn(center - radius);
-    const uint32_t scale_code = e4m3_rn((2.0f * radius) / levels);
-    const float scale = e4m3_f32(scale_code);
-    const float offset = e4m3_f32(offset_code);
-
-    uint32_t packed = 0;
-    uint32_t codes[4];
+    uint32_t packed[2];
+    uint32_t parameters[2];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        uint32_t code = 0;
-        if (scale > 0.f) {
-            const float normalized = (x[i] - offset) / scale;
-            const float lower = floorf(normalized);
-            float rounded = lower + ((normalized - lower) > 0.5f ? 1.0f : 0.0f);
-            rounded = fminf(fmaxf(rounded, 0.0f), levels);
-            code = (uint32_t)rounded;
-        }
-        codes[i] = code;
-        packed |= code << (i * bits);
-    }
-
-    if (restore) {
-        float mean_bf[4];
-#pragma unroll
-        for (int i = 0; i < 4; ++i) mean_bf[i] = bf16_f32(bf16_rn(mean[i]));
+    for (int h = 0; h < 2; ++h) {
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            uint32_t value = bf16_fma_rn((float)codes[i], scale, offset);
-            if (has_mean) value = bf16_add_rn(bf16_f32(value), mean_bf[i]);
-            if (!is_anchor) value = bf16_fma_rn(bf16_f32(reference[i]), alpha, bf16_f32(value));
-            reference[i] = value;
+            if (!is_anchor) x[h][i] = fmaf(-previous[h][i], alpha, x[h][i]);
+            if (has_mean) x[h][i] = x[h][i] - mean[h][i];
+        }
+        float low = fmin_z(fmin_z(x[h][0], x[h][1]), fmin_z(x[h][2], x[h][3]));
+        float high = fmax_z(fmax_z(x[h][0], x[h][1]), fmax_z(x[h][2], x[h][3]));
+        // A group spans 4 canonical lanes (G16) or 8 (G32), all with the same h;
+        // idle canonical lanes (head_dim 96) form groups of their own.
+        if (region.group == 32) {
+            low = fmin_z(low, swizzle_xor<4>(low));
+            high = fmax_z(high, swizzle_xor<4>(high));
+        }
+        low = fmin_z(low, dpp<kXor2>(low));
+        high = fmax_z(high, dpp<kXor2>(high));
+        low = fmin_z(low, dpp<kXor1>(low));
+        high = fmax_z(high, dpp<kXor1>(high));
+
+        const float center = (low + high) * 0.5f;
+        const float radius = bits == 2 ? ((high - low) * 0.9f) * 0.5f : (high - low) * 0.5f;
+        parameters[h] = e4m3_pair(center - radius, (2.0f * radius) / levels);
+        const float offset = e4m3_value(parameters[h] & 0xffu);
+        const float scale = e4m3_value(parameters[h] >> 8);
+        // RN(1/scale); 0 for a zero (or NaN) scale, which yields code 0.
+        const float reciprocal = inverse_scale[(parameters[h] >> 8) & 0x7fu];
+
+        packed[h] = 0;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            // |a| <= 2^100 keeps q0 finite; beyond it the code saturates anyway.
+            const float a = __builtin_amdgcn_fmed3f(x[h][i] - offset, -0x1p100f, 0x1p100f);
+            const float q0 = a * reciprocal;
+            const float r = fmaf(-q0, scale, a);
+            const float q = fmaf(r, reciprocal, q0);
+            // floor(q) + (frac(q) > 0.5) == ceil(q - 0.5), clamped to [0, levels].
+            const uint32_t code = (uint32_t)__builtin_amdgcn_fmed3f(ceilf(q - 0.5f), 0.0f, levels);
+            packed[h] |= code << (i * bits);
+            if (restore) {
+                uint32_t value = bf16_rn(fmaf((float)code, scale, offset));
+                if (has_mean) value = bf16_rn(bf16_f32(value) + bf16_f32(bf16_rn(mean[h][i])));
+                if (!is_anchor) value = bf16_fma_rn(bf16_f32(reference[h][i]), alpha, bf16_f32(value));
+                reference[h][i] = value;
+            }
         }
     }
 
-    if (store && active) {
+    if (store) {
         uint8_t* record = page + region.offset;
-        uint8_t* token_codes = record + (int64_t)token * region.code_bytes;
-        if (bits == 2) {
-            token_codes[lane] = (uint8_t)packed;
-        } else {
-            *reinterpret_cast<uint16_t*>(token_codes + 2 * lane) = (uint16_t)packed;
-        }
+        uint8_t* token_codes = record + token * region.code_bytes;
+        uint8_t* group_parameters = record + page_tokens * region.code_bytes;
         const int lanes_per_group = region.group / 4;
-        if (lane % lanes_per_group == 0) {
-            uint8_t* parameters = record + (int64_t)page_tokens * region.code_bytes;
-            const int index = token * region.groups + lane / lanes_per_group;
-            parameters[index] = (uint8_t)scale_code;
-            parameters[page_tokens * region.groups + index] = (uint8_t)offset_code;
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            if (!active[h]) continue;
+            const int lane = j + 16 * h;
+            if (bits == 2) {
+                token_codes[lane] = (uint8_t)packed[h];
+            } else {
+                *reinterpret_cast<uint16_t*>(token_codes + 2 * lane) = (uint16_t)packed[h];
+            }
+            if (lane % lanes_per_group == 0) {
+                const int index = token * region.groups + lane / lanes_per_group;
+                group_parameters[index] = (uint8_t)(parameters[h] >> 8);
+                group_parameters[page_tokens * region.groups + index] = (uint8_t)(parameters[h] & 0xffu);
+            }
         }
-        if (lane == 0) {
-            uint8_t* target = record + (int64_t)page_tokens * (region.code_bytes + 2 * region.groups) +
-                              2 * token;
+        if (j == 0) {
+            uint8_t* target = record + page_tokens * (region.code_bytes + 2 * region.groups) + 2 * token;
             *reinterpret_cast<uint16_t*>(target) = (uint16_t)stored_alpha;
         }
     }
 }
 
+// ---------------------------------------------------------------- kernel
+
 template <int D, int R, int A>
-__global__ __launch_bounds__(kQuantizeThreads) void quantize_kernel(QuantizeParams p) {
-    // Rotation kept as FP16 in LDS (converted by v_fma_mix on use) plus the
-    // tile's inputs transposed to [token][channel][record] FP32.
-    __shared__ _Float16 rotation_lds[D * D];
-    __shared__ float input_lds[kTileTokens * D * R];
+__global__ __launch_bounds__(kQuantizeThreads) void quantize_kernel(QuantizeParams p, int block_tokens) {
+    // FP32 rotation [k][D], per-record key means [R][D], the per-wave input
+    // stage [wave][buffer][token][k][record] and RN(1/scale) per E4M3 code.
+    __shared__ float stage[kQuantizeWaves][2][kWaveTokens][kChunk][kStageRecords];
+    __shared__ float rotation_lds[D * D];
+    __shared__ float mean_lds[R * D];
+    __shared__ float inverse_scale[128];
 
     const int plane = blockIdx.z;
     const int head = blockIdx.y;
-    const int half = threadIdx.x >> 5;
-    const int lane = threadIdx.x & 31;
-    const int64_t first = (int64_t)blockIdx.x * kTileTokens;
-    const int64_t n = first + half;
-
-    int64_t slot = -1;
-    if (n < p.tokens) slot = p.slots[n];
-    const bool valid = slot >= 0 && slot / p.page_tokens < p.num_blocks;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int lane64 = threadIdx.x & 63;
+    const int group = lane64 >> 4;  // token of the pass
+    const int j = lane64 & 15;
+    const bool active[2] = {4 * j < D, 4 * (j + 16) < D};
+    const int column[2] = {4 * j, active[1] ? 64 + 4 * j : 64};
 
     const uint16_t* rotation = plane == 0 ? p.key_rotation : p.value_rotation;
-    float y[R][4];
-
     if (rotation != nullptr) {
-        const uint16_t* matrix = rotation + (int64_t)head * D * D;
-        for (int i = threadIdx.x; i < D * D; i += kQuantizeThreads)
-            rotation_lds[i] = __builtin_bit_cast(_Float16, matrix[i]);
-        for (int i = threadIdx.x; i < kTileTokens * R * D; i += kQuantizeThreads) {
-            const int t = i / (R * D);
-            const int r = (i / D) % R;
-            const int k = i % D;
-            const int64_t nn = first + t;
-            float v = 0.f;
-            if (nn < p.tokens) {
-                const int64_t s = p.slots[nn];
-                if (s >= 0 && s / p.page_tokens < p.num_blocks) {
-                    const uint16_t* src = plane == 0 ? p.key_ptrs[r] + nn * p.key_strides[r]
-                                                     : p.value_ptrs[r] + nn * p.value_strides[r];
-                    v = bf16_f32(src[head * D + k]);
-                }
+        const uint4* source = reinterpret_cast<const uint4*>(rotation + (int64_t)head * D * D);
+        for (int i = threadIdx.x; i < D * D / 8; i += kQuantizeThreads) {
+            const uint4 v = source[i];
+            const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+            float f[8];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                f[2 * e] = (float)__builtin_bit_cast(_Float16, (uint16_t)(w[e] & 0xffffu));
+                f[2 * e + 1] = (float)__builtin_bit_cast(_Float16, (uint16_t)(w[e] >> 16));
             }
-            input_lds[(t * D + k) * R + r] = v;
-        }
-        __syncthreads();
-#pragma unroll
-        for (int r = 0; r < R; ++r)
-#pragma unroll
-            for (int i = 0; i < 4; ++i) y[r][i] = 0.f;
-        if (lane * 4 < D) {
-            const float* row_inputs = input_lds + half * D * R;
-            for (int k = 0; k < D; ++k) {
-                const _Float16* rk = rotation_lds + k * D + lane * 4;
-                float rv[4];
-#pragma unroll
-                for (int i = 0; i < 4; ++i) rv[i] = (float)rk[i];
-#pragma unroll
-                for (int r = 0; r < R; ++r) {
-                    const float xv = row_inputs[k * R + r];
-#pragma unroll
-                    for (int i = 0; i < 4; ++i) y[r][i] = fmaf(xv, rv[i], y[r][i]);
-                }
-            }
-        }
-    } else {
-#pragma unroll
-        for (int r = 0; r < R; ++r) {
-            const uint16_t* src = nullptr;
-            if (valid)
-                src = (plane == 0 ? p.key_ptrs[r] + n * p.key_strides[r]
-                                  : p.value_ptrs[r] + n * p.value_strides[r]) +
-                      head * D;
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const int c = lane * 4 + i;
-                y[r][i] = (valid && c < D) ? bf16_f32(src[c]) : 0.f;
-            }
+            *reinterpret_cast<float4*>(&rotation_lds[8 * i]) = make_float4(f[0], f[1], f[2], f[3]);
+            *reinterpret_cast<float4*>(&rotation_lds[8 * i + 4]) = make_float4(f[4], f[5], f[6], f[7]);
         }
     }
-
-    uint8_t* page = nullptr;
-    int token = 0;
-    if (valid) {
-        const int64_t block = slot / p.page_tokens;
-        token = (int)(slot % p.page_tokens);
-        page = p.cache + plane * p.plane_stride +
-               (block * p.heads + head) * (int64_t)p.page_tokens * p.page_width;
-    }
-
-    uint32_t reference[4] = {0u, 0u, 0u, 0u};
     const bool has_mean = plane == 0 && p.key_mean != nullptr;
-    // Anchor first, then every other record ascending (kernel.cuh:321-329).
+    if (has_mean)
+        for (int i = threadIdx.x; i < R * D; i += kQuantizeThreads)
+            mean_lds[i] = p.key_mean[((int64_t)(i / D) * p.heads + head) * D + i % D];
+    if (threadIdx.x < 128) {
+        const uint32_t code = threadIdx.x;
+        inverse_scale[code] = (code == 0 || code == 0x7f) ? 0.0f : 1.0f / e4m3_value(code);
+    }
+    __syncthreads();
+
+    const int64_t block_first = (int64_t)blockIdx.x * block_tokens;
+    const int64_t block_end = block_first + block_tokens < p.tokens ? block_first + block_tokens : p.tokens;
+    // Stage loader role: token `load_token`, record `load_record`, 8-k segment `segment`.
+    const int load_token = lane64 >> 4;
+    const int load_record = (lane64 >> 2) & 3;
+    const int segment = lane64 & 3;
+
+    for (int64_t first = block_first + wave * kWaveTokens; first < block_end;
+         first += kQuantizeWaves * kWaveTokens) {
+        float x[R][2][4];
+
+        if (rotation != nullptr) {
+            const int64_t n_load = first + load_token < block_end ? first + load_token : block_end - 1;
+            const uint16_t* row = nullptr;
+            if (load_record < R)
+                row = (plane == 0 ? p.key_ptrs[load_record] + n_load * p.key_strides[load_record]
+                                  : p.value_ptrs[load_record] + n_load * p.value_strides[load_record]) +
+                      head * D + 8 * segment;
+            float (*buffers)[kWaveTokens][kChunk][kStageRecords] = stage[wave];
+            auto stage_chunk = [&](uint4 v, int buffer) {
+                if (load_record < R) {
+                    const uint32_t w[4] = {v.x, v.y, v.z, v.w};
 #pragma unroll
-    for (int step = 0; step < R; ++step) {
-        const int r = step == 0 ? A : (step - 1 < A ? step - 1 : step);
-        float mean[4] = {0.f, 0.f, 0.f, 0.f};
-        if (has_mean) {
+                    for (int e = 0; e < 4; ++e) {
+                        buffers[buffer][load_token][8 * segment + 2 * e][load_record] = bf16_f32(w[e] & 0xffffu);
+                        buffers[buffer][load_token][8 * segment + 2 * e + 1][load_record] = bf16_f32(w[e] >> 16);
+                    }
+                }
+            };
+            uint4 incoming = load_record < R ? *reinterpret_cast<const uint4*>(row) : make_uint4(0, 0, 0, 0);
+            stage_chunk(incoming, 0);
+
+            float acc[R][2][4];
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const int c = lane * 4 + i;
-                if (c < D) mean[i] = p.key_mean[((int64_t)r * p.heads + head) * D + c];
+            for (int r = 0; r < R; ++r)
+#pragma unroll
+                for (int h = 0; h < 2; ++h)
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) acc[r][h][i] = 0.f;
+
+#pragma unroll 1
+            for (int chunk = 0; chunk < D / kChunk; ++chunk) {
+                const bool more = chunk + 1 < D / kChunk;
+                if (more && load_record < R)
+                    incoming = *reinterpret_cast<const uint4*>(row + (chunk + 1) * kChunk);
+                // Operands of step k + 1 are read while step k computes.
+                const float4* xs_row = reinterpret_cast<const float4*>(&buffers[chunk & 1][group][0][0]);
+                const float* ra_row = rotation_lds + chunk * kChunk * D + column[0];
+                const float* rb_row = rotation_lds + chunk * kChunk * D + column[1];
+                float4 xv = xs_row[0];
+                float4 ra = *reinterpret_cast<const float4*>(ra_row);
+                float4 rb = *reinterpret_cast<const float4*>(rb_row);
+#pragma unroll 8
+                for (int k = 0; k < kChunk; ++k) {
+                    const int next = k + 1 < kChunk ? k + 1 : k;  // the last step re-reads its own row
+                    const float4 xn = xs_row[next];
+                    const float4 an = *reinterpret_cast<const float4*>(ra_row + next * D);
+                    const float4 bn = *reinterpret_cast<const float4*>(rb_row + next * D);
+                    __builtin_amdgcn_sched_barrier(0);  // keep the prefetch above this step's FMAs
+                    const float xs[4] = {xv.x, xv.y, xv.z, xv.w};
+                    const float rs[2][4] = {{ra.x, ra.y, ra.z, ra.w}, {rb.x, rb.y, rb.z, rb.w}};
+#pragma unroll
+                    for (int r = 0; r < R; ++r)
+#pragma unroll
+                        for (int h = 0; h < 2; ++h)
+#pragma unroll
+                            for (int i = 0; i < 4; ++i) acc[r][h][i] = fmaf(xs[r], rs[h][i], acc[r][h][i]);
+                    xv = xn;
+                    ra = an;
+                    rb = bn;
+                }
+                // The stage is private to this wave and one wave's LDS
+                // operations complete in order, so no barrier is needed.
+                if (more) stage_chunk(incoming, (chunk + 1) & 1);
+            }
+#pragma unroll
+            for (int r = 0; r < R; ++r)
+#pragma unroll
+                for (int h = 0; h < 2; ++h)
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) x[r][h][i] = active[h] ? acc[r][h][i] : 0.f;
+        } else {
+            const int64_t n = first + group < block_end ? first + group : block_end - 1;
+#pragma unroll
+            for (int r = 0; r < R; ++r) {
+                const uint16_t* src = (plane == 0 ? p.key_ptrs[r] + n * p.key_strides[r]
+                                                  : p.value_ptrs[r] + n * p.value_strides[r]) + head * D;
+#pragma unroll
+                for (int h = 0; h < 2; ++h) {
+                    uint2 v = make_uint2(0, 0);
+                    if (active[h]) v = *reinterpret_cast<const uint2*>(src + column[h]);
+                    x[r][h][0] = bf16_f32(v.x & 0xffffu);
+                    x[r][h][1] = bf16_f32(v.x >> 16);
+                    x[r][h][2] = bf16_f32(v.y & 0xffffu);
+                    x[r][h][3] = bf16_f32(v.y >> 16);
+                }
             }
         }
-        const bool is_anchor = r == A;
-        commit_record<D>(y[r], is_anchor, is_anchor || p.adjacent, p.coefficient, mean, has_mean,
-                         reference, p.region[r], page, token, p.page_tokens, lane, valid);
+
+        // Commit phase: lanes 16g..16g+15 own token first + g.
+        const int64_t n = first + group;
+        int64_t slot = -1;
+        if (n < block_end) slot = p.slots[n];
+        const bool valid = slot >= 0 && slot / p.page_tokens < p.num_blocks;
+        uint8_t* page = nullptr;
+        int token = 0;
+        if (valid) {
+            const int64_t block = slot / p.page_tokens;
+            token = (int)(slot % p.page_tokens);
+            page = p.cache + plane * p.plane_stride + (block * p.heads + head) * (int64_t)p.page_tokens * p.page_width;
+        }
+
+        uint32_t reference[2][4] = {{0u, 0u, 0u, 0u}, {0u, 0u, 0u, 0u}};
+        // Anchor first, then every other record ascending (kernel.cuh:321-329).
+#pragma unroll
+        for (int step = 0; step < R; ++step) {
+            const int r = step == 0 ? A : (step - 1 < A ? step - 1 : step);
+            const bool is_anchor = r == A;
+            float mean[2][4];
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                float4 m = make_float4(0.f, 0.f, 0.f, 0.f);
+                if (has_mean && active[h]) m = *reinterpret_cast<const float4*>(&mean_lds[r * D + column[h]]);
+                mean[h][0] = m.x; mean[h][1] = m.y; mean[h][2] = m.z; mean[h][3] = m.w;
+            }
+            commit_record(x[r], active, is_anchor, is_anchor || p.adjacent, p.coefficient, mean, has_mean,
+                          reference, p.region[r], page, token, p.page_tokens, j, valid, inverse_scale);
+        }
     }
 }
 
 template <int D, int R, int A>
 hipError_t launch_quantize_kernel(const QuantizeParams& p, hipStream_t stream) {
-    const dim3 grid((unsigned)((p.tokens + kTileTokens - 1) / kTileTokens), (unsigned)p.heads, 2);
-    hipLaunchKernelGGL((quantize_kernel<D, R, A>), grid, dim3(kQuantizeThreads), 0, stream, p);
+    // A workgroup pass covers 64 tokens of one (head, plane).  Long calls give
+    // each workgroup several passes so the rotation staging is amortised,
+    // keeping about two workgroups per CU; short calls (decode steps) use one.
+    const int64_t per_pass = kQuantizeWaves * kWaveTokens;
+    const int64_t work = (p.tokens + per_pass - 1) / per_pass * p.heads * 2;
+    int64_t passes = work / 512;
+    passes = passes < 1 ? 1 : (passes > 8 ? 8 : passes);
+    const int block_tokens = (int)(per_pass * passes);
+    const dim3 grid((unsigned)((p.tokens + block_tokens - 1) / block_tokens), (unsigned)p.heads, 2);
+    hipLaunchKernelGGL((quantize_kernel<D, R, A>), grid, dim3(kQuantizeThreads), 0, stream, p, block_tokens);
     return hipGetLastError();
 }
 

@@ -62,16 +62,17 @@ def test_page_width_known_answers_and_errors(lib):
 
 
 def _quantize_call(lib, records, *, head_dim=128, page_tokens=16, page_width=200, mode=0, anchor=3,
-                   coefficient=2, tokens=4, input_rows=4, width_override=None):
+                   coefficient=2, tokens=4, input_rows=4, width_override=None, input=0x10000,
+                   stride=None, rotation=None):
     count = len(records)
     fake = ctypes.c_void_p(0x10000)
-    ptrs = (ctypes.c_void_p * count)(*([fake.value] * count))
-    strides = (ctypes.c_int64 * count)(*([16 * head_dim] * count))
+    ptrs = (ctypes.c_void_p * count)(*([input] * count))
+    strides = (ctypes.c_int64 * count)(*([stride or 16 * head_dim] * count))
     bits, groups = _schedule(records)
     return lib.rq_quantize(count, ctypes.cast(ptrs, ctypes.c_void_p), ctypes.cast(strides, ctypes.c_void_p),
                            ctypes.cast(ptrs, ctypes.c_void_p), ctypes.cast(strides, ctypes.c_void_p), input_rows,
                            fake, 8, 16, page_tokens, width_override or page_width, fake, tokens, head_dim,
-                           None, None, None, ctypes.cast(bits, ctypes.c_void_p),
+                           rotation, rotation, None, ctypes.cast(bits, ctypes.c_void_p),
                            ctypes.cast(groups, ctypes.c_void_p), mode, anchor, coefficient, None)
 
 
@@ -90,6 +91,11 @@ def test_quantize_rejects_before_device_work(lib):
     assert _quantize_call(lib, G32, mode=1, anchor=3) == _lib.RQ_ENOKERNEL  # adjacent needs anchor 0
     assert _quantize_call(lib, [(3, 32)]) == _lib.RQ_ENOKERNEL
     assert _quantize_call(lib, G32, anchor=4) == _lib.RQ_ENOKERNEL
+    assert _quantize_call(lib, G32, input=0x10004) == _lib.RQ_EINVAL
+    assert lib.rq_last_error() == b"K/V addresses and token strides must be 8-byte aligned"
+    assert _quantize_call(lib, G32, stride=16 * 128 + 2) == _lib.RQ_EINVAL
+    assert _quantize_call(lib, G32, rotation=0x10008) == _lib.RQ_EINVAL
+    assert lib.rq_last_error() == b"Rotation addresses must be 16-byte aligned"
     assert _quantize_call(lib, G32, tokens=0, input_rows=0) == _lib.RQ_OK  # empty slot mapping: no launch
 
 
