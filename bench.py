@@ -8,6 +8,12 @@ Hadamard rotations on K and V.  One step = one decode step of the layer:
 the three residual-loop calls and the anchor-loop call.  The BF16 paged
 baseline runs the same four calls over a BF16 cache of the same shape.
 
+``--workload quantize`` instead times quantize-on-write at BASELINE config 1
+(C1): 4096 new tokens x 16 KV heads x D128 x 4 loops, schedule
+[2,16]x2+[2,32]+[4,32] (INT2 residuals at g16 and g32, INT4 anchor at g32),
+least-squares coefficients, seeded random-sign Hadamard rotations, scattered
+to random slots of a paged cache of 16-token blocks.
+
 Prints ONE JSON line on stdout; everything else goes to stderr.
 """
 
@@ -25,7 +31,9 @@ if ROOT not in sys.path:
     sys.path.insert(0, ROOT)
 
 PEAK_HBM_GBPS = 8000.0
+PEAK_FP32_TFLOPS = 157.3
 SCHEDULE = ((2, 32), (2, 32), (2, 32), (4, 32))
+QUANTIZE_SCHEDULE = ((2, 16), (2, 16), (2, 32), (4, 32))
 ANCHOR = 3
 
 
@@ -154,8 +162,129 @@ def cpu_baseline(torch, rq, workloads, cache, table, key_rotation, value_rotatio
     }
 
 
+def quantize_cpu_baseline(torch, workloads, pairs, slots, key_rotation, value_rotation, cache_shape, budget_s):
+    """The CPU oracle (single thread) quantizing a bounded prefix of the same tokens."""
+    import numpy as np
+    from oracle import oracle
+
+    oracle.lib()
+    bits = workloads.bf16_bits
+    keys = [bits(k) for k, _ in pairs]
+    values = [bits(v) for _, v in pairs]
+    kr, vr = bits(key_rotation), bits(value_rotation)
+    cache = np.zeros(cache_shape, dtype=np.uint8)
+    slot_array = slots.cpu().numpy()
+    done, elapsed, chunk = 0, 0.0, 16
+    while done < slot_array.size and elapsed < budget_s:
+        part = slice(done, min(done + chunk, slot_array.size))
+        start = time.perf_counter()
+        oracle.quantize([(k[part], v[part]) for k, v in zip(keys, values)], cache, slot_array[part], kr, vr,
+                        None, QUANTIZE_SCHEDULE, "anchor", ANCHOR, "ls")
+        elapsed += time.perf_counter() - start
+        done = part.stop
+    return {
+        "value": done / elapsed,
+        "unit": "tokens/s",
+        "cores": 1,
+        "kind": "port",
+        "sample": f"first {done} of {slot_array.size} tokens (all heads, both planes), oracle/rq_oracle.c "
+                  f"single-threaded; {elapsed:.2f} s; host {platform.processor() or 'cpu'}",
+    }
+
+
+def run_quantize(args):
+    """C1: one quantize-on-write call per step; kernel time from HIP events on torch's stream."""
+    import torch
+
+    import residualquant_amd as rq
+    from residualquant_amd import workloads
+
+    device = torch.device("cuda:0")
+    torch.cuda.set_device(device)
+    tokens, heads, dim, page_tokens, seed = args.tokens, 16, 128, 16, 2026
+    width = rq.page_width(dim, QUANTIZE_SCHEDULE)
+    blocks = 2 * ((tokens + page_tokens - 1) // page_tokens)
+    cache = torch.zeros((2, blocks, heads, page_tokens, width), dtype=torch.uint8, device=device)
+    generator = torch.Generator().manual_seed(seed)
+    slots = torch.randperm(blocks * page_tokens, generator=generator)[:tokens].to(device)
+    pairs = workloads.loop_kv(tokens, heads, dim, len(QUANTIZE_SCHEDULE), seed + 1, device=device)
+    key_rotation = workloads.random_sign_rotation(heads, dim, seed + 3, device=device)
+    value_rotation = workloads.random_sign_rotation(heads, dim, seed + 4, device=device)
+
+    def step():
+        rq.quantize(pairs, cache, slots, key_rotation, value_rotation, None, QUANTIZE_SCHEDULE, "anchor",
+                    ANCHOR, "ls")
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    begin, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start = time.perf_counter()
+    begin.record()
+    for _ in range(args.steps):
+        step()
+    end.record()
+    torch.cuda.synchronize()
+    wall_s = (time.perf_counter() - start) / args.steps
+    kernel_ms = begin.elapsed_time(end) / args.steps  # one launch per call
+    records = len(QUANTIZE_SCHEDULE)
+    flop = 2.0 * tokens * heads * 2 * records * dim * dim
+    input_bytes = tokens * heads * dim * 2 * records * 2
+    output_bytes = tokens * heads * 2 * width
+    achieved = flop / (kernel_ms * 1e-3) / 1e12
+    log(f"[bench] quantize {kernel_ms * 1e3:.1f} us/call ({achieved:.1f} TFLOP/s rotation), "
+        f"{(input_bytes + output_bytes) / (kernel_ms * 1e-3) / 1e9:.0f} GB/s")
+
+    cpu = None
+    if args.cpu_budget > 0:
+        log("[bench] cpu baseline (oracle quantize) ...")
+        cpu = quantize_cpu_baseline(torch, workloads, pairs, slots, key_rotation, value_rotation,
+                                    tuple(cache.shape), args.cpu_budget)
+        log(f"[bench] cpu {cpu['value']:.1f} tokens/s")
+
+    result = {
+        "metric": "quantize-on-write tokens/s (C1), 1 GPU",
+        "value": tokens / (kernel_ms * 1e-3),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": kernel_ms,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "fp32 rotation and fitting, int2/int4 codes, fp8 scales",
+        "data": "synthetic (seeded anchor N(0,1) with 4 outlier channels x8 + loop residuals N(0,0.15^2), "
+                "random-sign Hadamard rotations, random slots)",
+        "config": {
+            "workload": "C1 quantize-on-write micro-benchmark",
+            "tokens": tokens, "heads": heads, "head_dim": dim, "loops": records, "page_tokens": page_tokens,
+            "schedule": "[2,16]x2+[2,32]+[4,32] anchor 3 ls", "cache_blocks": blocks,
+        },
+        "us_per_call": kernel_ms * 1e3,
+        "us_per_call_wall": wall_s * 1e6,
+        "hbm_GBps": (input_bytes + output_bytes) / (kernel_ms * 1e-3) / 1e9,
+        "bytes_per_call": input_bytes + output_bytes,
+        "roofline": {
+            "bound": "mfma",
+            "achieved": achieved,
+            "peak": PEAK_FP32_TFLOPS,
+            "unit": "TFLOP/s",
+            "frac": achieved / PEAK_FP32_TFLOPS,
+            "traffic": None,
+            "kernel": "quantize_kernel<128,4,3>: FP32 rotation FMAs (VOP2 v_fmac_f32) against the "
+                      "published FP32 peak; HBM traffic is 6% of peak at this rate",
+        },
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(result), flush=True)
+
+
 def main():
     parser = argparse.ArgumentParser(description=__doc__)
+    parser.add_argument("--workload", choices=("decode", "quantize"), default="decode",
+                        help="decode: C2 paged decode attention (the headline); quantize: C1 quantize-on-write")
+    parser.add_argument("--tokens", type=int, default=4096, help="new tokens per quantize call (C1)")
     parser.add_argument("--gpus", type=int, default=1)
     parser.add_argument("--steps", type=int, default=20)
     parser.add_argument("--warmup", type=int, default=5)
@@ -177,6 +306,14 @@ def main():
               "(the reference forbids TP>1 and DCP>1); run with --gpus 1", file=sys.stderr)
         sys.exit(2)
 
+    if args.workload == "quantize":
+        run_quantize(args)
+        return
+    run_decode(args)
+
+
+def run_decode(args):
+    """C2: one decode step = the 3 residual-loop calls + the anchor-loop call."""
     import torch
 
     import residualquant_amd as rq

@@ -284,7 +284,13 @@ __global__ __launch_bounds__(kQuantizeThreads) void quantize_kernel(QuantizePara
                     }
                 }
             };
-            uint4 incoming = load_record < R ? *reinterpret_cast<const uint4*>(row) : make_uint4(0, 0, 0, 0);
+            // Rows are only guaranteed 8-byte aligned: two 8-byte loads per segment.
+            auto load_segment = [&](int chunk) {
+                const uint2* source = reinterpret_cast<const uint2*>(row + chunk * kChunk);
+                const uint2 a = source[0], b = source[1];
+                return make_uint4(a.x, a.y, b.x, b.y);
+            };
+            uint4 incoming = load_record < R ? load_segment(0) : make_uint4(0, 0, 0, 0);
             stage_chunk(incoming, 0);
 
             float acc[R][2][4];
@@ -298,8 +304,7 @@ __global__ __launch_bounds__(kQuantizeThreads) void quantize_kernel(QuantizePara
 #pragma unroll 1
             for (int chunk = 0; chunk < D / kChunk; ++chunk) {
                 const bool more = chunk + 1 < D / kChunk;
-                if (more && load_record < R)
-                    incoming = *reinterpret_cast<const uint4*>(row + (chunk + 1) * kChunk);
+                if (more && load_record < R) incoming = load_segment(chunk + 1);
                 // Operands of step k + 1 are read while step k computes.
                 const float4* xs_row = reinterpret_cast<const float4*>(&buffers[chunk & 1][group][0][0]);
                 const float* ra_row = rotation_lds + chunk * kChunk * D + column[0];

@@ -70,6 +70,27 @@ def test_quantize_strided_inputs(oracle, device):
     assert np.array_equal(cache.cpu().numpy(), expected)
 
 
+def test_quantize_rows_eight_byte_aligned(oracle, device):
+    """Rows that start 8 bytes past a 16-byte boundary, with a token stride of heads*D + 4."""
+    g = make_group(37, 2, 128, OURO_G16, seed=12)
+    expected = g.oracle_cache(oracle)
+    pairs = []
+    for k, v in g.pairs:
+        width = k.size(1) * k.size(2) + 4
+        flat_k = torch.zeros(k.size(0) * width + 8, dtype=torch.bfloat16, device=device)
+        flat_v = torch.zeros_like(flat_k)
+        view_k = flat_k[4:4 + k.size(0) * width].view(k.size(0), width)[:, : k.size(1) * k.size(2)]
+        view_v = flat_v[4:4 + k.size(0) * width].view(k.size(0), width)[:, : k.size(1) * k.size(2)]
+        view_k.copy_(k.reshape(k.size(0), -1).to(device))
+        view_v.copy_(v.reshape(v.size(0), -1).to(device))
+        pairs.append((view_k.view(k.shape), view_v.view(v.shape)))
+    assert pairs[0][0].data_ptr() % 16 == 8
+    cache = torch.zeros(g.cache_shape, dtype=torch.uint8, device=device)
+    kr, vr, km = g.device_args(device)
+    rq.quantize(pairs, cache, g.slots.to(device), kr, vr, km, g.records, g.mode, g.anchor, g.coefficient)
+    assert np.array_equal(cache.cpu().numpy(), expected)
+
+
 @pytest.mark.parametrize("case", QUANTIZE_CASES[:5], ids=lambda c: f"{c[2]}d-{len(c[3])}r-{c[5]}")
 def test_dequantize_bitexact(oracle, device, case):
     _print_case("dequantize", case)
