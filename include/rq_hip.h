@@ -135,6 +135,24 @@ int rq_paged_attention_bf16(const void* query, int64_t query_stride, const void*
                             size_t workspace_bytes, hipStream_t stream);
 
 /*
+ * Causal (or full) varlen prefill attention over raw BF16 Q/K/V:
+ * out[i] = softmax(softmax_scale * q_i K_j^T over keys j <= i + len_k - len_q) V
+ * per sequence s = [cu_seqlens[s], cu_seqlens[s + 1]) and head (query head h
+ * reads key/value head h / (heads_q / heads_k)).  Replaces the
+ * flash_attn_varlen_func(q, k, v, out, cu_seqlens_q, cu_seqlens_k,
+ * max_seqlen_q, max_seqlen_k, softmax_scale, causal) call of the full-prompt
+ * branch, src/residual_quantization/packed_backend.py:63-77 (vLLM 0.10.2).
+ * Q/K/V/output rows [tokens, heads, head_dim] with element strides per token,
+ * 8-byte aligned; cu_seqlens int32 [batch + 1] on the device; max_seqlen_q
+ * must be at least every sequence's query length.  head_dim 96 or 128.
+ */
+int rq_prefill_attention(const void* query, int64_t query_stride, const void* key, int64_t key_stride,
+                         const void* value, int64_t value_stride, void* output, int64_t output_stride,
+                         int heads_q, int heads_k, int head_dim, const int32_t* cu_seqlens_q,
+                         const int32_t* cu_seqlens_k, int64_t batch, int64_t max_seqlen_q,
+                         float softmax_scale, int causal, hipStream_t stream);
+
+/*
  * Kernel timing for measurement: when enabled, rq_attention and
  * rq_paged_attention_bf16 record HIP events around their split-K kernel on
  * the caller's stream; rq_timing_read() synchronizes the recorded events and

@@ -82,6 +82,10 @@ def _declare(l):
     l.rq_oracle_paged_attention_bf16.argtypes = [
         c_vp, c_i64, c_vp, c_i64, c_vp, c_i64, c_vp, c_i64, c_int, c_int, c_vp, c_i64, c_int,
         c_vp, c_vp, c_i64, c_vp, c_i64]
+    l.rq_oracle_prefill_attention.restype = c_int
+    l.rq_oracle_prefill_attention.argtypes = [
+        c_vp, c_i64, c_vp, c_i64, c_vp, c_i64, c_vp, c_int, c_int, c_int, c_vp, c_vp, c_i64,
+        ctypes.c_double, c_int]
 
 
 def _ptr(a):
@@ -233,3 +237,22 @@ def paged_attention_bf16(query, key, value, cache, query_start_loc, seq_lens, bl
     if rc != 0:
         raise RuntimeError("oracle bf16 attention rejected its arguments")
     return out
+
+
+def prefill_attention(query, key, value, cu_seqlens_q, cu_seqlens_k, scale, causal=True):
+    """FP64 varlen attention: query [Nq, Hq, D], key/value [Nk, Hk, D] as BF16 bits (uint16)."""
+    q = np.ascontiguousarray(query, dtype=np.uint16)
+    k = np.ascontiguousarray(key, dtype=np.uint16)
+    v = np.ascontiguousarray(value, dtype=np.uint16)
+    tokens_q, heads_q, head_dim = q.shape
+    heads_k = k.shape[1]
+    cq = np.ascontiguousarray(cu_seqlens_q, dtype=np.int32)
+    ck = np.ascontiguousarray(cu_seqlens_k, dtype=np.int32)
+    out = np.zeros((tokens_q, heads_q, head_dim), dtype=np.float64)
+    rc = lib().rq_oracle_prefill_attention(
+        _ptr(q), heads_q * head_dim, _ptr(k), heads_k * head_dim, _ptr(v), heads_k * head_dim, _ptr(out),
+        heads_q, heads_k, head_dim, _ptr(cq), _ptr(ck), cq.size - 1, ctypes.c_double(scale), 1 if causal else 0)
+    if rc != 0:
+        raise RuntimeError("oracle prefill attention rejected its arguments")
+    return out
+

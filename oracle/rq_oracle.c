@@ -14,6 +14,8 @@
  *   record restore            quantize/kernel.cuh:160-203, attention/compute.cuh:28-197
  *   decode attention          attention/prepare.cuh:13-230, compute.cuh:226-727,
  *                             merge.cuh:8-84, output.cuh:9-31, rotation.cuh:10-84
+ *   prefill attention         src/residual_quantization/packed_backend.py:63-77
+ *                             (vLLM flash_attn_varlen_func: textbook causal softmax)
  *
  * Canonical arithmetic (the reference binary's own order is not reproducible:
  * it uses TF32 mma.sync with a hardware-defined accumulation order and
@@ -703,6 +705,58 @@ int rq_oracle_paged_attention_bf16(
                 const double live_weight = exp(live - maximum);
                 for (int c = 0; c < head_dim; ++c)
                     out[c] = (hist[c] + live_weight * (double)rq_oracle_bf16_to_f32(vl[c])) / denominator;
+            }
+        }
+        free(scores);
+    }
+    return 0;
+}
+
+/* Varlen prefill attention in FP64: the flash_attn_varlen_func call of the
+ * full-prompt branch (src/residual_quantization/packed_backend.py:63-77).
+ * For sequence s (cu_q[s]..cu_q[s+1] queries, cu_k[s]..cu_k[s+1] keys), query
+ * head h reads key/value head h / (heads_q / heads_k); query i sees keys
+ * j <= i + len_k - len_q when causal (all keys otherwise); a query with no
+ * key gets a zero row.  out[i] = sum_j softmax_j(scale * q_i . k_j) v_j. */
+int rq_oracle_prefill_attention(const uint16_t* query, int64_t query_stride, const uint16_t* key,
+                                int64_t key_stride, const uint16_t* value, int64_t value_stride, double* output,
+                                int heads_q, int heads_k, int head_dim, const int32_t* cu_q, const int32_t* cu_k,
+                                int64_t batch, double scale, int causal) {
+    if (heads_q <= 0 || heads_k <= 0 || heads_q % heads_k || head_dim <= 0 || head_dim > RQ_ORACLE_MAX_DIM)
+        return -1;
+    const int group = heads_q / heads_k;
+    for (int64_t s = 0; s < batch; ++s) {
+        const int64_t q_begin = cu_q[s], q_len = cu_q[s + 1] - cu_q[s];
+        const int64_t k_begin = cu_k[s], k_len = cu_k[s + 1] - cu_k[s];
+        if (q_len < 0 || k_len < 0) return -1;
+        double* scores = (double*)malloc(sizeof(double) * (size_t)(k_len > 0 ? k_len : 1));
+        if (!scores) return -1;
+        for (int64_t i = 0; i < q_len; ++i) {
+            int64_t last = causal ? i + k_len - q_len : k_len - 1;
+            if (last > k_len - 1) last = k_len - 1;
+            for (int h = 0; h < heads_q; ++h) {
+                const int kh = h / group;
+                const uint16_t* q = query + (q_begin + i) * query_stride + (int64_t)h * head_dim;
+                double* out = output + ((q_begin + i) * heads_q + h) * (int64_t)head_dim;
+                for (int c = 0; c < head_dim; ++c) out[c] = 0.0;
+                if (last < 0) continue;
+                double maximum = -INFINITY;
+                for (int64_t j = 0; j <= last; ++j) {
+                    const uint16_t* k = key + (k_begin + j) * key_stride + (int64_t)kh * head_dim;
+                    double dot = 0.0;
+                    for (int c = 0; c < head_dim; ++c)
+                        dot += (double)rq_oracle_bf16_to_f32(q[c]) * (double)rq_oracle_bf16_to_f32(k[c]);
+                    scores[j] = scale * dot;
+                    if (scores[j] > maximum) maximum = scores[j];
+                }
+                double denominator = 0.0;
+                for (int64_t j = 0; j <= last; ++j) {
+                    const uint16_t* v = value + (k_begin + j) * value_stride + (int64_t)kh * head_dim;
+                    const double p = exp(scores[j] - maximum);
+                    denominator += p;
+                    for (int c = 0; c < head_dim; ++c) out[c] += p * (double)rq_oracle_bf16_to_f32(v[c]);
+                }
+                for (int c = 0; c < head_dim; ++c) out[c] /= denominator;
             }
         }
         free(scores);

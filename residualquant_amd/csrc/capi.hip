@@ -9,6 +9,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <cmath>
 #include <cstdarg>
 #include <cstdio>
 #include <mutex>
@@ -429,6 +430,52 @@ int rq_paged_attention_bf16(const void* query, int64_t query_stride, const void*
     hipEvent_t begin, end;
     timing_events(stream, &begin, &end);
     return check_launch(rq::launch_attention_bf16(p, stream, begin, end), "bf16 attention launch");
+}
+
+int rq_prefill_attention(const void* query, int64_t query_stride, const void* key, int64_t key_stride,
+                         const void* value, int64_t value_stride, void* output, int64_t output_stride,
+                         int heads_q, int heads_k, int head_dim, const int32_t* cu_seqlens_q,
+                         const int32_t* cu_seqlens_k, int64_t batch, int64_t max_seqlen_q,
+                         float softmax_scale, int causal, hipStream_t stream) {
+    if (head_dim != 96 && head_dim != 128)
+        return fail(RQ_ENOKERNEL, "No compiled prefill attention kernel for head_dim=%d", head_dim);
+    if (heads_q <= 0 || heads_k <= 0 || heads_q % heads_k != 0)
+        return fail(RQ_EINVAL, "Query heads must be a positive multiple of key/value heads");
+    if (batch < 0 || max_seqlen_q < 0 || max_seqlen_q > (int64_t)INT32_MAX || batch > 65535)
+        return fail(RQ_EINVAL, "Invalid batch or max_seqlen_q");
+    if (batch > 0 && (cu_seqlens_q == nullptr || cu_seqlens_k == nullptr))
+        return fail(RQ_EINVAL, "cu_seqlens_q and cu_seqlens_k required");
+    if (!(softmax_scale > 0.f) || !std::isfinite(softmax_scale)) return fail(RQ_EINVAL, "softmax_scale must be positive");
+    const int64_t q_row = (int64_t)heads_q * head_dim, k_row = (int64_t)heads_k * head_dim;
+    if (query_stride < q_row || output_stride < q_row || key_stride < k_row || value_stride < k_row)
+        return fail(RQ_EINVAL, "BF16 [tokens, heads, head_dim] with packed trailing strides required");
+    const void* rows[4] = {query, key, value, output};
+    const int64_t strides[4] = {query_stride, key_stride, value_stride, output_stride};
+    for (int i = 0; i < 4; ++i)
+        if ((reinterpret_cast<uintptr_t>(rows[i]) % 8) || strides[i] % 4)
+            return fail(RQ_EINVAL, "Q/K/V/output addresses and token strides must be 8-byte aligned");
+    if (batch == 0 || max_seqlen_q == 0) return ok();
+    if (query == nullptr || key == nullptr || value == nullptr || output == nullptr)
+        return fail(RQ_EINVAL, "Q/K/V/output required");
+    rq::PrefillParams p{};
+    p.query = static_cast<const uint16_t*>(query);
+    p.query_stride = query_stride;
+    p.key = static_cast<const uint16_t*>(key);
+    p.key_stride = key_stride;
+    p.value = static_cast<const uint16_t*>(value);
+    p.value_stride = value_stride;
+    p.output = static_cast<uint16_t*>(output);
+    p.output_stride = output_stride;
+    p.cu_seqlens_q = cu_seqlens_q;
+    p.cu_seqlens_k = cu_seqlens_k;
+    p.batch = (int)batch;
+    p.heads_q = heads_q;
+    p.group = heads_q / heads_k;
+    p.head_dim = head_dim;
+    p.max_seqlen_q = (int)max_seqlen_q;
+    p.causal = causal != 0;
+    p.softmax_scale = softmax_scale;
+    return check_launch(rq::launch_prefill(p, stream), "prefill attention launch");
 }
 
 void rq_timing_enable(int enabled) {

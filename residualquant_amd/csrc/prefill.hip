@@ -1,0 +1,240 @@
+// Causal varlen prefill attention over raw BF16 Q/K/V for gfx950.
+//
+// This is the full-prompt branch of the reference backend
+// (plugins/residual_quantization/src/residual_quantization/packed_backend.py:63-77),
+// which calls vLLM's flash_attn_varlen_func(q, k, v, out, cu_seqlens_q,
+// cu_seqlens_k, max_seqlen_q, max_seqlen_k, softmax_scale, causal=True):
+// out[i] = softmax(scale * q_i . K_j^T over keys j <= i + (len_k - len_q)) V.
+//
+// Work mapping: one workgroup = 128 queries of one (sequence, head), four
+// waves of 32 queries; key tiles of 64 are staged in LDS (K row-major, V
+// transposed) and shared by the waves.  Each wave computes S^T = K Q^T with
+// v_mfma_f32_32x32x16_bf16, so lane l owns query l % 32: the softmax row max
+// and sum are in-lane plus one exchange between the wave's halves, and the
+// probabilities P^T stay in the accumulator registers as the B operand of
+// O^T += V^T P^T.  The key order inside each P.V step is permuted to match
+// the accumulator layout (the A operand reads V^T at the same keys), so P
+// never moves between lanes.  Query blocks launch latest-first, since later
+// blocks see more keys.
+//
+// Lane layouts of v_mfma_f32_32x32x16_bf16 (checked on gfx950): A row l % 32,
+// k 8 (l / 32) + e; B column l % 32, k 8 (l / 32) + e; C register r holds row
+// 8 (r / 4) + 4 (l / 32) + r % 4, column l % 32.
+#include "rq_device.h"
+#include "rq_kernels.h"
+
+namespace rq {
+
+namespace {
+
+typedef __bf16 Bf16x8 __attribute__((ext_vector_type(8)));
+typedef float F32x16 __attribute__((ext_vector_type(16)));
+
+constexpr int kPrefillWaves = 4;
+constexpr int kPrefillThreads = 64 * kPrefillWaves;
+constexpr int kBlockQueries = 32 * kPrefillWaves;
+constexpr int kBlockKeys = 64;
+
+__device__ __forceinline__ F32x16 mfma(Bf16x8 a, Bf16x8 b, F32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+}
+
+// 8 BF16 from a row that is only 8-byte aligned.
+__device__ __forceinline__ Bf16x8 load8(const uint16_t* src) {
+    const uint2 a = reinterpret_cast<const uint2*>(src)[0];
+    const uint2 b = reinterpret_cast<const uint2*>(src)[1];
+    const uint4 v = make_uint4(a.x, a.y, b.x, b.y);
+    return __builtin_bit_cast(Bf16x8, v);
+}
+
+__device__ __forceinline__ uint4 load16(const uint16_t* src) {
+    const uint2 a = reinterpret_cast<const uint2*>(src)[0];
+    const uint2 b = reinterpret_cast<const uint2*>(src)[1];
+    return make_uint4(a.x, a.y, b.x, b.y);
+}
+
+template <int D>
+__global__ __launch_bounds__(kPrefillThreads) void prefill_kernel(PrefillParams p) {
+    // K tile [key][KS] and V^T tile [d][VS]; the pads put the 32 rows a wave
+    // reads at once on distinct banks.
+    constexpr int KS = D + 8;
+    constexpr int VS = kBlockKeys + 4;
+    __shared__ __attribute__((aligned(16))) uint16_t k_tile[kBlockKeys * KS];
+    __shared__ __attribute__((aligned(16))) uint16_t v_tile[D * VS];
+
+    const int sequence = blockIdx.z;
+    const int head = blockIdx.y;
+    const int q_block = gridDim.x - 1 - blockIdx.x;
+    const int q_begin = p.cu_seqlens_q[sequence];
+    const int q_len = p.cu_seqlens_q[sequence + 1] - q_begin;
+    const int k_begin = p.cu_seqlens_k[sequence];
+    const int k_len = p.cu_seqlens_k[sequence + 1] - k_begin;
+    const int q0 = q_block * kBlockQueries;
+    if (q0 >= q_len) return;  // uniform over the workgroup, before any barrier
+    const int shift = k_len - q_len;  // query i sees keys j <= i + shift (causal)
+    const int kv_head = head / p.group;
+
+    const int wave = threadIdx.x >> 6;
+    const int lane = threadIdx.x & 63;
+    const int column = lane & 31;
+    const int half = lane >> 5;
+    const int wave_q0 = q0 + 32 * wave;
+    const int my_q = wave_q0 + column;
+
+    int block_keys = k_len;
+    int wave_keys = k_len;
+    if (p.causal) {
+        const int block_limit = q0 + kBlockQueries + shift;
+        const int wave_limit = wave_q0 + 32 + shift;
+        block_keys = block_limit < k_len ? block_limit : k_len;
+        wave_keys = wave_limit < k_len ? wave_limit : k_len;
+    }
+    const int my_limit = p.causal ? my_q + shift : k_len - 1;  // last key this query sees
+
+    // Q^T operand (B of S^T = K Q^T): chunk m holds d = 16m + 8 half + e.
+    Bf16x8 q_operand[D / 16];
+    {
+        const int row = my_q < q_len ? my_q : q_len - 1;
+        const uint16_t* src = p.query + (int64_t)(q_begin + row) * p.query_stride + head * D + 8 * half;
+#pragma unroll
+        for (int m = 0; m < D / 16; ++m) q_operand[m] = load8(src + 16 * m);
+    }
+
+    F32x16 out[D / 32];
+#pragma unroll
+    for (int t = 0; t < D / 32; ++t)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) out[t][r] = 0.f;
+    float running_max = -__builtin_inff();
+    float running_sum = 0.f;
+    const float c = p.softmax_scale * 1.4426950408889634f;  // scores in log2 units
+
+    const uint16_t* k_base = p.key + (int64_t)k_begin * p.key_stride + kv_head * D;
+    const uint16_t* v_base = p.value + (int64_t)k_begin * p.value_stride + kv_head * D;
+
+    for (int kt = 0; kt < block_keys; kt += kBlockKeys) {
+        __syncthreads();  // the previous tile is consumed
+        // K tile: 64 rows of D/8 chunks of 8 BF16; rows past the sequence are zero.
+        for (int chunk = threadIdx.x; chunk < kBlockKeys * (D / 8); chunk += kPrefillThreads) {
+            const int row = chunk / (D / 8), segment = chunk % (D / 8);
+            uint4 v = make_uint4(0, 0, 0, 0);
+            if (kt + row < k_len) v = load16(k_base + (int64_t)(kt + row) * p.key_stride + 8 * segment);
+            *reinterpret_cast<uint4*>(&k_tile[row * KS + 8 * segment]) = v;
+        }
+        // V^T tile: units of (key pair, 8 channels) written as (key, key + 1) dwords.
+        for (int unit = threadIdx.x; unit < (kBlockKeys / 2) * (D / 8); unit += kPrefillThreads) {
+            const int pair = unit % (kBlockKeys / 2), group = unit / (kBlockKeys / 2);
+            const int key = kt + 2 * pair;
+            uint4 a = make_uint4(0, 0, 0, 0), b = make_uint4(0, 0, 0, 0);
+            if (key < k_len) a = load16(v_base + (int64_t)key * p.value_stride + 8 * group);
+            if (key + 1 < k_len) b = load16(v_base + (int64_t)(key + 1) * p.value_stride + 8 * group);
+            const uint32_t av[4] = {a.x, a.y, a.z, a.w}, bv[4] = {b.x, b.y, b.z, b.w};
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const uint32_t low = (av[i] & 0xffffu) | (bv[i] << 16);
+                const uint32_t high = (av[i] >> 16) | (bv[i] & 0xffff0000u);
+                *reinterpret_cast<uint32_t*>(&v_tile[(8 * group + 2 * i) * VS + 2 * pair]) = low;
+                *reinterpret_cast<uint32_t*>(&v_tile[(8 * group + 2 * i + 1) * VS + 2 * pair]) = high;
+            }
+        }
+        __syncthreads();
+        if (kt >= wave_keys) continue;  // wave-uniform: this wave's queries see none of these keys
+
+        // S^T for two sub-tiles of 32 keys: register r of lane l holds key
+        // kt + 32 sub + 8 (r / 4) + 4 half + r % 4 against query my_q.
+        F32x16 s[2];
+#pragma unroll
+        for (int sub = 0; sub < 2; ++sub) {
+#pragma unroll
+            for (int r = 0; r < 16; ++r) s[sub][r] = 0.f;
+            const uint16_t* k_row = &k_tile[(32 * sub + column) * KS + 8 * half];
+#pragma unroll
+            for (int m = 0; m < D / 16; ++m)
+                s[sub] = mfma(*reinterpret_cast<const Bf16x8*>(k_row + 16 * m), q_operand[m], s[sub]);
+        }
+        float tile_max = -__builtin_inff();
+#pragma unroll
+        for (int sub = 0; sub < 2; ++sub)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int key = kt + 32 * sub + 8 * (r >> 2) + 4 * half + (r & 3);
+                const float v = (key < k_len && key <= my_limit) ? s[sub][r] * c : -__builtin_inff();
+                s[sub][r] = v;
+                tile_max = fmaxf(tile_max, v);
+            }
+        tile_max = fmaxf(tile_max, __shfl_xor(tile_max, 32));
+        const float new_max = fmaxf(running_max, tile_max);
+        // A query with no visible key yet keeps zero weights (no -inf - -inf).
+        const float base = new_max == -__builtin_inff() ? 0.f : new_max;
+        const float rescale = __builtin_amdgcn_exp2f(running_max - base);
+        running_max = new_max;
+
+        // P^T in BF16 as the B operand of O^T += V^T P^T: step j of sub-tile
+        // `sub` takes registers 8j..8j+7, i.e. k-slot (half, e) is key
+        // 32 sub + 16 j + 4 half + e + (e >= 4 ? 4 : 0).
+        float tile_sum = 0.f;
+        Bf16x8 p_operand[2][2];
+#pragma unroll
+        for (int sub = 0; sub < 2; ++sub)
+#pragma unroll
+            for (int j = 0; j < 2; ++j)
+#pragma unroll
+                for (int e = 0; e < 8; ++e) {
+                    const __bf16 w = (__bf16)__builtin_amdgcn_exp2f(s[sub][8 * j + e] - base);
+                    p_operand[sub][j][e] = w;
+                    tile_sum += (float)w;
+                }
+        tile_sum += __shfl_xor(tile_sum, 32);
+        running_sum = running_sum * rescale + tile_sum;
+#pragma unroll
+        for (int t = 0; t < D / 32; ++t)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) out[t][r] *= rescale;
+
+#pragma unroll
+        for (int sub = 0; sub < 2; ++sub)
+#pragma unroll
+            for (int j = 0; j < 2; ++j) {
+                const int key_offset = 32 * sub + 16 * j + 4 * half;
+#pragma unroll
+                for (int t = 0; t < D / 32; ++t) {
+                    const uint16_t* v_row = &v_tile[(32 * t + column) * VS + key_offset];
+                    const uint2 lo = *reinterpret_cast<const uint2*>(v_row);
+                    const uint2 hi = *reinterpret_cast<const uint2*>(v_row + 8);
+                    const Bf16x8 a = __builtin_bit_cast(Bf16x8, make_uint4(lo.x, lo.y, hi.x, hi.y));
+                    out[t] = mfma(a, p_operand[sub][j], out[t]);
+                }
+            }
+    }
+
+    if (my_q < q_len) {
+        const float inverse = running_sum > 0.f ? 1.0f / running_sum : 0.f;
+        uint16_t* dst = p.output + (int64_t)(q_begin + my_q) * p.output_stride + head * D + 4 * half;
+#pragma unroll
+        for (int t = 0; t < D / 32; ++t)
+#pragma unroll
+            for (int g = 0; g < 4; ++g) {
+                const uint32_t b0 = bf16_rn(out[t][4 * g] * inverse), b1 = bf16_rn(out[t][4 * g + 1] * inverse);
+                const uint32_t b2 = bf16_rn(out[t][4 * g + 2] * inverse), b3 = bf16_rn(out[t][4 * g + 3] * inverse);
+                *reinterpret_cast<uint2*>(dst + 32 * t + 8 * g) = make_uint2(b0 | (b1 << 16), b2 | (b3 << 16));
+            }
+    }
+}
+
+}  // namespace
+
+hipError_t launch_prefill(const PrefillParams& p, hipStream_t stream) {
+    if (p.batch == 0 || p.max_seqlen_q == 0) return hipSuccess;
+    const dim3 grid((unsigned)((p.max_seqlen_q + kBlockQueries - 1) / kBlockQueries), (unsigned)p.heads_q,
+                    (unsigned)p.batch);
+    if (p.head_dim == 128) {
+        hipLaunchKernelGGL(prefill_kernel<128>, grid, dim3(kPrefillThreads), 0, stream, p);
+    } else if (p.head_dim == 96) {
+        hipLaunchKernelGGL(prefill_kernel<96>, grid, dim3(kPrefillThreads), 0, stream, p);
+    } else {
+        return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
+
+}  // namespace rq

@@ -48,6 +48,28 @@ struct RestoreParams {
 
 hipError_t launch_restore(const RestoreParams& p, hipStream_t stream);
 
+struct PrefillParams {
+    const uint16_t* query;   // BF16 [tokens_q, heads_q, D], token stride query_stride
+    int64_t query_stride;
+    const uint16_t* key;     // BF16 [tokens_k, heads_k, D]
+    int64_t key_stride;
+    const uint16_t* value;
+    int64_t value_stride;
+    uint16_t* output;        // BF16 [tokens_q, heads_q, D]
+    int64_t output_stride;
+    const int32_t* cu_seqlens_q;  // [batch + 1]
+    const int32_t* cu_seqlens_k;
+    int batch;
+    int heads_q;
+    int group;               // heads_q / heads_k
+    int head_dim;
+    int max_seqlen_q;
+    int causal;
+    float softmax_scale;
+};
+
+hipError_t launch_prefill(const PrefillParams& p, hipStream_t stream);
+
 // Per (row, head) prepared query block in the workspace (floats).
 constexpr int kPrepScalars = 16;   // [0] delta [1] live score [2] q'.mu_A [3..10] Q16 [11..14] Q32
 constexpr int kPrepQuery = 128;    // q' FP32 in log2 units

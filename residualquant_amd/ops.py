@@ -263,6 +263,57 @@ def paged_attention_bf16(query: torch.Tensor, key: torch.Tensor, value: torch.Te
     _lib.check(status)
 
 
+def flash_attn_varlen_func(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, max_seqlen_q: int,
+                           cu_seqlens_q: torch.Tensor, max_seqlen_k: int,
+                           cu_seqlens_k: Optional[torch.Tensor] = None, dropout_p: float = 0.0,
+                           softmax_scale: Optional[float] = None, causal: bool = False,
+                           window_size=None, softcap: float = 0.0, alibi_slopes=None,
+                           deterministic: bool = False, return_attn_probs: bool = False,
+                           block_table=None, return_softmax_lse: bool = False,
+                           out: Optional[torch.Tensor] = None, fa_version=None) -> torch.Tensor:
+    """Varlen (causal) attention over raw BF16 Q/K/V, the full-prompt branch.
+
+    Drop-in for the ``flash_attn_varlen_func`` call of the reference backend
+    (src/residual_quantization/packed_backend.py:63-77, vLLM 0.10.2): q
+    [tokens_q, heads_q, D], k/v [tokens_k, heads_k, D] BF16, sequence s spans
+    cu_seqlens[s]..cu_seqlens[s+1]; with ``causal`` query i of a sequence sees
+    keys j <= i + len_k - len_q.  The features that call does not use
+    (dropout, windows, softcap, ALiBi, paged K/V, returned LSE or
+    probabilities) raise.  ``fa_version`` is accepted and ignored.
+    """
+    _require(dropout_p == 0.0 and softcap == 0.0 and alibi_slopes is None and block_table is None
+             and not return_attn_probs and not return_softmax_lse
+             and (window_size is None or tuple(window_size) == (-1, -1)),
+             "Only dropout-free, unwindowed attention without ALiBi, softcap, paged K/V or returned "
+             "LSE is supported")
+    cu_seqlens_k = cu_seqlens_q if cu_seqlens_k is None else cu_seqlens_k
+    for tensor in (q, k, v):
+        _validate_bf16_token_tensor(tensor)
+    _require(k.device == q.device and v.device == q.device and k.shape == v.shape
+             and k.size(2) == q.size(2), "Q/K/V must share device and head_dim; K and V must match")
+    if out is None:
+        out = torch.empty_like(q)
+    _validate_bf16_token_tensor(out)
+    _require(out.device == q.device and out.shape == q.shape, "out must match q")
+    for seqlens in (cu_seqlens_q, cu_seqlens_k):
+        _require(seqlens.device == q.device and seqlens.dtype == torch.int32 and seqlens.dim() == 1
+                 and seqlens.is_contiguous(), "Contiguous INT32 cu_seqlens on the Q device required")
+    _require(cu_seqlens_q.numel() == cu_seqlens_k.numel() and cu_seqlens_q.numel() >= 1,
+             "cu_seqlens_q and cu_seqlens_k must describe the same sequences")
+    head_dim = q.size(2)
+    scale = head_dim ** -0.5 if softmax_scale is None else float(softmax_scale)
+    with torch.cuda.device(q.device):
+        status = _lib.lib().rq_prefill_attention(
+            q.data_ptr(), q.stride(0), k.data_ptr(), k.stride(0), v.data_ptr(), v.stride(0), out.data_ptr(),
+            out.stride(0), q.size(1), k.size(1), head_dim, cu_seqlens_q.data_ptr(), cu_seqlens_k.data_ptr(),
+            cu_seqlens_q.numel() - 1, int(max_seqlen_q), scale, 1 if causal else 0, _stream(q.device))
+    _lib.check(status)
+    return out
+
+
+prefill_attention = flash_attn_varlen_func
+
+
 def timing_enable(enabled: bool) -> None:
     """Record HIP events around every split-K decode launch (for measurement)."""
     _lib.lib().rq_timing_enable(1 if enabled else 0)

@@ -140,3 +140,20 @@ def test_python_ops_mirror_reference_messages():
         ops.attention(cpu, cpu, cpu, cache, cpu, torch.zeros(3, dtype=torch.int32),
                       torch.zeros(2, dtype=torch.int32), torch.zeros((2, 4), dtype=torch.int32), None, None, None,
                       G32, "anchor", 3, 0)
+
+
+def _prefill_call(lib, *, head_dim=128, heads_q=4, heads_k=2, query=0x10000, stride=None):
+    fake = 0x10000
+    row = stride or heads_q * head_dim
+    return lib.rq_prefill_attention(query, row, fake, heads_k * head_dim, fake, heads_k * head_dim, fake, row,
+                                    heads_q, heads_k, head_dim, fake, fake, 2, 64, 0.1, 1, None)
+
+
+def test_prefill_rejects_before_device_work(lib):
+    assert _prefill_call(lib, head_dim=64) == _lib.RQ_ENOKERNEL
+    assert lib.rq_last_error().startswith(b"No compiled prefill attention kernel")
+    assert _prefill_call(lib, heads_q=3) == _lib.RQ_EINVAL
+    assert _prefill_call(lib, query=0x10004) == _lib.RQ_EINVAL
+    assert lib.rq_last_error() == b"Q/K/V/output addresses and token strides must be 8-byte aligned"
+    assert _prefill_call(lib, stride=4 * 128 + 2) == _lib.RQ_EINVAL
+
