@@ -32,6 +32,7 @@ if ROOT not in sys.path:
 
 PEAK_HBM_GBPS = 8000.0
 PEAK_FP32_TFLOPS = 157.3
+PEAK_BF16_TFLOPS = 2500.0
 SCHEDULE = ((2, 32), (2, 32), (2, 32), (4, 32))
 QUANTIZE_SCHEDULE = ((2, 16), (2, 16), (2, 32), (4, 32))
 ANCHOR = 3
@@ -280,11 +281,86 @@ def run_quantize(args):
     print(json.dumps(result), flush=True)
 
 
+def run_prefill(args):
+    """A12: causal varlen prefill attention over one prompt; HIP events on torch's stream."""
+    import torch
+
+    import residualquant_amd as rq
+
+    device = torch.device("cuda:0")
+    torch.cuda.set_device(device)
+    tokens, heads, dim, seed = args.tokens, 16, 128, 2026
+    generator = torch.Generator(device=device).manual_seed(seed)
+    q, k, v = (torch.randn((tokens, heads, dim), generator=generator, device=device).to(torch.bfloat16)
+               for _ in range(3))
+    out = torch.empty_like(q)
+    cu = torch.tensor([0, tokens], dtype=torch.int32, device=device)
+    scale = dim ** -0.5
+
+    def step():
+        rq.flash_attn_varlen_func(q=q, k=k, v=v, out=out, cu_seqlens_q=cu, cu_seqlens_k=cu, max_seqlen_q=tokens,
+                                  max_seqlen_k=tokens, softmax_scale=scale, causal=True)
+
+    def event_ms(fn):
+        for _ in range(args.warmup):
+            fn()
+        torch.cuda.synchronize()
+        begin, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        begin.record()
+        for _ in range(args.steps):
+            fn()
+        end.record()
+        torch.cuda.synchronize()
+        return begin.elapsed_time(end) / args.steps
+
+    kernel_ms = event_ms(step)  # one launch per call
+    flop = 2.0 * 2.0 * heads * dim * tokens * (tokens + 1) / 2.0  # QK^T and PV over the causal half
+    achieved = flop / (kernel_ms * 1e-3) / 1e12
+    log(f"[bench] prefill {kernel_ms * 1e3:.1f} us/call ({achieved:.0f} TFLOP/s)")
+
+    qt, kt, vt = (t.transpose(0, 1).contiguous() for t in (q, k, v))  # [heads, tokens, D]
+    torch_ms = event_ms(lambda: torch.nn.functional.scaled_dot_product_attention(qt, kt, vt, is_causal=True,
+                                                                                   scale=scale))
+    log(f"[bench] torch scaled_dot_product_attention {torch_ms * 1e3:.1f} us/call")
+
+    result = {
+        "metric": "prefill attention TFLOP/s (causal, 1 GPU)",
+        "value": achieved,
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": kernel_ms,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16 in, fp32 accumulate",
+        "data": "synthetic N(0,1) Q/K/V",
+        "config": {"workload": "A12 causal prefill over one prompt", "tokens": tokens, "heads": heads,
+                   "head_dim": dim, "softmax_scale": scale},
+        "us_per_call": kernel_ms * 1e3,
+        "tokens_per_s": tokens / (kernel_ms * 1e-3),
+        "roofline": {
+            "bound": "mfma",
+            "achieved": achieved,
+            "peak": PEAK_BF16_TFLOPS,
+            "unit": "TFLOP/s",
+            "frac": achieved / PEAK_BF16_TFLOPS,
+            "traffic": None,
+            "kernel": "prefill_kernel<128>: causal-half QK^T + PV FLOPs against the dense BF16 MFMA peak",
+        },
+        "torch_sdpa": {"us_per_call": torch_ms * 1e3, "TFLOPs": flop / (torch_ms * 1e-3) / 1e12},
+        "cpu_baseline": None,
+    }
+    print(json.dumps(result), flush=True)
+
+
 def main():
     parser = argparse.ArgumentParser(description=__doc__)
-    parser.add_argument("--workload", choices=("decode", "quantize"), default="decode",
-                        help="decode: C2 paged decode attention (the headline); quantize: C1 quantize-on-write")
-    parser.add_argument("--tokens", type=int, default=4096, help="new tokens per quantize call (C1)")
+    parser.add_argument("--workload", choices=("decode", "quantize", "prefill"), default="decode",
+                        help="decode: C2 paged decode attention (the headline); quantize: C1 quantize-on-write; "
+                             "prefill: causal prompt attention")
+    parser.add_argument("--tokens", type=int, default=4096, help="tokens per quantize call or prompt")
     parser.add_argument("--gpus", type=int, default=1)
     parser.add_argument("--steps", type=int, default=20)
     parser.add_argument("--warmup", type=int, default=5)
@@ -308,6 +384,9 @@ def main():
 
     if args.workload == "quantize":
         run_quantize(args)
+        return
+    if args.workload == "prefill":
+        run_prefill(args)
         return
     run_decode(args)
 

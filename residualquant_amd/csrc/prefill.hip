@@ -54,13 +54,14 @@ __device__ __forceinline__ uint4 load16(const uint16_t* src) {
 }
 
 template <int D>
-__global__ __launch_bounds__(kPrefillThreads) void prefill_kernel(PrefillParams p) {
-    // K tile [key][KS] and V^T tile [d][VS]; the pads put the 32 rows a wave
-    // reads at once on distinct banks.
+__global__ __launch_bounds__(kPrefillThreads) __attribute__((amdgpu_waves_per_eu(2)))
+void prefill_kernel(PrefillParams p) {
+    // Double-buffered K tile [key][KS] and V^T tile [d][VS]; the pads put the
+    // 32 rows a wave reads at once on distinct banks.
     constexpr int KS = D + 8;
     constexpr int VS = kBlockKeys + 4;
-    __shared__ __attribute__((aligned(16))) uint16_t k_tile[kBlockKeys * KS];
-    __shared__ __attribute__((aligned(16))) uint16_t v_tile[D * VS];
+    __shared__ __attribute__((aligned(16))) uint16_t k_tiles[2][kBlockKeys * KS];
+    __shared__ __attribute__((aligned(16))) uint16_t v_tiles[2][D * VS];
 
     const int sequence = blockIdx.z;
     const int head = blockIdx.y;
@@ -112,33 +113,73 @@ __global__ __launch_bounds__(kPrefillThreads) void prefill_kernel(PrefillParams 
     const uint16_t* k_base = p.key + (int64_t)k_begin * p.key_stride + kv_head * D;
     const uint16_t* v_base = p.value + (int64_t)k_begin * p.value_stride + kv_head * D;
 
-    for (int kt = 0; kt < block_keys; kt += kBlockKeys) {
-        __syncthreads();  // the previous tile is consumed
-        // K tile: 64 rows of D/8 chunks of 8 BF16; rows past the sequence are zero.
-        for (int chunk = threadIdx.x; chunk < kBlockKeys * (D / 8); chunk += kPrefillThreads) {
+    // Tile loads: each thread fetches K chunks (row, 8 channels) and V units
+    // (key pair, 8 channels) of the next tile into registers while the current
+    // tile computes, then stages them (V transposed) into the other buffer.
+    constexpr int kKChunks = (kBlockKeys * (D / 8) + kPrefillThreads - 1) / kPrefillThreads;
+    constexpr int kVUnits = ((kBlockKeys / 2) * (D / 8) + kPrefillThreads - 1) / kPrefillThreads;
+    uint4 k_next[kKChunks], v_next[kVUnits][2];
+    auto fetch = [&](int kt) {
+#pragma unroll
+        for (int i = 0; i < kKChunks; ++i) {
+            const int chunk = threadIdx.x + i * kPrefillThreads;
             const int row = chunk / (D / 8), segment = chunk % (D / 8);
-            uint4 v = make_uint4(0, 0, 0, 0);
-            if (kt + row < k_len) v = load16(k_base + (int64_t)(kt + row) * p.key_stride + 8 * segment);
-            *reinterpret_cast<uint4*>(&k_tile[row * KS + 8 * segment]) = v;
+            k_next[i] = make_uint4(0, 0, 0, 0);
+            if (chunk < kBlockKeys * (D / 8) && kt + row < k_len)
+                k_next[i] = load16(k_base + (int64_t)(kt + row) * p.key_stride + 8 * segment);
         }
-        // V^T tile: units of (key pair, 8 channels) written as (key, key + 1) dwords.
-        for (int unit = threadIdx.x; unit < (kBlockKeys / 2) * (D / 8); unit += kPrefillThreads) {
+#pragma unroll
+        for (int i = 0; i < kVUnits; ++i) {
+            const int unit = threadIdx.x + i * kPrefillThreads;
             const int pair = unit % (kBlockKeys / 2), group = unit / (kBlockKeys / 2);
             const int key = kt + 2 * pair;
-            uint4 a = make_uint4(0, 0, 0, 0), b = make_uint4(0, 0, 0, 0);
-            if (key < k_len) a = load16(v_base + (int64_t)key * p.value_stride + 8 * group);
-            if (key + 1 < k_len) b = load16(v_base + (int64_t)(key + 1) * p.value_stride + 8 * group);
-            const uint32_t av[4] = {a.x, a.y, a.z, a.w}, bv[4] = {b.x, b.y, b.z, b.w};
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const uint32_t low = (av[i] & 0xffffu) | (bv[i] << 16);
-                const uint32_t high = (av[i] >> 16) | (bv[i] & 0xffff0000u);
-                *reinterpret_cast<uint32_t*>(&v_tile[(8 * group + 2 * i) * VS + 2 * pair]) = low;
-                *reinterpret_cast<uint32_t*>(&v_tile[(8 * group + 2 * i + 1) * VS + 2 * pair]) = high;
+            v_next[i][0] = v_next[i][1] = make_uint4(0, 0, 0, 0);
+            if (unit < (kBlockKeys / 2) * (D / 8)) {
+                if (key < k_len) v_next[i][0] = load16(v_base + (int64_t)key * p.value_stride + 8 * group);
+                if (key + 1 < k_len) v_next[i][1] = load16(v_base + (int64_t)(key + 1) * p.value_stride + 8 * group);
             }
         }
-        __syncthreads();
-        if (kt >= wave_keys) continue;  // wave-uniform: this wave's queries see none of these keys
+    };
+    auto stage = [&](int buffer) {
+#pragma unroll
+        for (int i = 0; i < kKChunks; ++i) {
+            const int chunk = threadIdx.x + i * kPrefillThreads;
+            const int row = chunk / (D / 8), segment = chunk % (D / 8);
+            if (chunk < kBlockKeys * (D / 8))
+                *reinterpret_cast<uint4*>(&k_tiles[buffer][row * KS + 8 * segment]) = k_next[i];
+        }
+#pragma unroll
+        for (int i = 0; i < kVUnits; ++i) {
+            const int unit = threadIdx.x + i * kPrefillThreads;
+            const int pair = unit % (kBlockKeys / 2), group = unit / (kBlockKeys / 2);
+            if (unit < (kBlockKeys / 2) * (D / 8)) {
+                const uint4 a = v_next[i][0], b = v_next[i][1];
+                const uint32_t av[4] = {a.x, a.y, a.z, a.w}, bv[4] = {b.x, b.y, b.z, b.w};
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const uint32_t low = (av[e] & 0xffffu) | (bv[e] << 16);
+                    const uint32_t high = (av[e] >> 16) | (bv[e] & 0xffff0000u);
+                    *reinterpret_cast<uint32_t*>(&v_tiles[buffer][(8 * group + 2 * e) * VS + 2 * pair]) = low;
+                    *reinterpret_cast<uint32_t*>(&v_tiles[buffer][(8 * group + 2 * e + 1) * VS + 2 * pair]) = high;
+                }
+            }
+        }
+    };
+
+    if (block_keys > 0) {
+        fetch(0);
+        stage(0);
+    }
+    __syncthreads();
+    int buffer = 0;
+    for (int kt = 0; kt < block_keys; kt += kBlockKeys, buffer ^= 1) {
+        // Buffer `buffer` holds this tile; every wave finished reading the
+        // other one before the barrier that ended the previous iteration.
+        const bool more = kt + kBlockKeys < block_keys;
+        if (more) fetch(kt + kBlockKeys);
+        const uint16_t* k_tile = k_tiles[buffer];
+        const uint16_t* v_tile = v_tiles[buffer];
+        if (kt < wave_keys) {  // wave-uniform: this wave's queries see some of these keys
 
         // S^T for two sub-tiles of 32 keys: register r of lane l holds key
         // kt + 32 sub + 8 (r / 4) + 4 half + r % 4 against query my_q.
@@ -153,15 +194,28 @@ __global__ __launch_bounds__(kPrefillThreads) void prefill_kernel(PrefillParams 
                 s[sub] = mfma(*reinterpret_cast<const Bf16x8*>(k_row + 16 * m), q_operand[m], s[sub]);
         }
         float tile_max = -__builtin_inff();
+        // Only tiles that cross the sequence end or this wave's causal
+        // diagonal need the per-key mask (wave-uniform branch).
+        const bool masked = kt + kBlockKeys > k_len || (p.causal && kt + kBlockKeys - 1 > wave_q0 + shift);
+        if (masked) {
 #pragma unroll
-        for (int sub = 0; sub < 2; ++sub)
+            for (int sub = 0; sub < 2; ++sub)
 #pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                const int key = kt + 32 * sub + 8 * (r >> 2) + 4 * half + (r & 3);
-                const float v = (key < k_len && key <= my_limit) ? s[sub][r] * c : -__builtin_inff();
-                s[sub][r] = v;
-                tile_max = fmaxf(tile_max, v);
-            }
+                for (int r = 0; r < 16; ++r) {
+                    const int key = kt + 32 * sub + 8 * (r >> 2) + 4 * half + (r & 3);
+                    const float v = (key < k_len && key <= my_limit) ? s[sub][r] * c : -__builtin_inff();
+                    s[sub][r] = v;
+                    tile_max = fmaxf(tile_max, v);
+                }
+        } else {
+#pragma unroll
+            for (int sub = 0; sub < 2; ++sub)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    s[sub][r] *= c;
+                    tile_max = fmaxf(tile_max, s[sub][r]);
+                }
+        }
         tile_max = fmaxf(tile_max, __shfl_xor(tile_max, 32));
         const float new_max = fmaxf(running_max, tile_max);
         // A query with no visible key yet keeps zero weights (no -inf - -inf).
@@ -205,6 +259,9 @@ __global__ __launch_bounds__(kPrefillThreads) void prefill_kernel(PrefillParams 
                     out[t] = mfma(a, p_operand[sub][j], out[t]);
                 }
             }
+        }
+        if (more) stage(buffer ^ 1);
+        __syncthreads();
     }
 
     if (my_q < q_len) {
