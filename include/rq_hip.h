@@ -144,13 +144,25 @@ int rq_paged_attention_bf16(const void* query, int64_t query_stride, const void*
  * branch, src/residual_quantization/packed_backend.py:63-77 (vLLM 0.10.2).
  * Q/K/V/output rows [tokens, heads, head_dim] with element strides per token,
  * 8-byte aligned; cu_seqlens int32 [batch + 1] on the device; max_seqlen_q
- * must be at least every sequence's query length.  head_dim 96 or 128.
+ * and max_seqlen_k must be at least every sequence's query and key length.
+ * head_dim 96 or 128.  `workspace` holds rq_prefill_workspace_bytes(...)
+ * bytes of device memory (may be null when that is 0).
  */
 int rq_prefill_attention(const void* query, int64_t query_stride, const void* key, int64_t key_stride,
                          const void* value, int64_t value_stride, void* output, int64_t output_stride,
                          int heads_q, int heads_k, int head_dim, const int32_t* cu_seqlens_q,
                          const int32_t* cu_seqlens_k, int64_t batch, int64_t max_seqlen_q,
-                         float softmax_scale, int causal, hipStream_t stream);
+                         int64_t max_seqlen_k, float softmax_scale, int causal, void* workspace,
+                         size_t workspace_bytes, hipStream_t stream);
+
+/*
+ * Workspace bytes rq_prefill_attention needs for these host shapes (the FP32
+ * partials of query blocks whose keys are split over several workgroups);
+ * same_lengths = 1 when cu_seqlens_q and cu_seqlens_k are the same array.
+ * No counterpart in the reference (flash-attn sizes its own scratch).
+ */
+size_t rq_prefill_workspace_bytes(int64_t batch, int heads_q, int head_dim, int64_t max_seqlen_q,
+                                  int64_t max_seqlen_k, int causal, int same_lengths);
 
 /*
  * Kernel timing for measurement: when enabled, rq_attention and

@@ -27,6 +27,7 @@ EXPORTED_SYMBOLS = (
     "rq_dequantize",
     "rq_paged_attention_bf16",
     "rq_prefill_attention",
+    "rq_prefill_workspace_bytes",
     "rq_timing_enable",
     "rq_timing_read",
     "rq_set_split_target",
@@ -80,7 +81,9 @@ def _declare(l: ctypes.CDLL) -> None:
     l.rq_timing_enable.restype = None
     l.rq_prefill_attention.restype = i32
     l.rq_prefill_attention.argtypes = [vp, i64, vp, i64, vp, i64, vp, i64, i32, i32, i32, vp, vp, i64, i64,
-                                       ctypes.c_float, i32, vp]
+                                       i64, ctypes.c_float, i32, vp, ctypes.c_size_t, vp]
+    l.rq_prefill_workspace_bytes.restype = ctypes.c_size_t
+    l.rq_prefill_workspace_bytes.argtypes = [i64, i32, i32, i64, i64, i32, i32]
     l.rq_timing_enable.argtypes = [i32]
     l.rq_timing_read.restype = i32
     l.rq_timing_read.argtypes = [ctypes.POINTER(ctypes.c_double), ctypes.POINTER(ctypes.c_int64)]

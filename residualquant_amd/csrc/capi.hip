@@ -436,13 +436,15 @@ int rq_prefill_attention(const void* query, int64_t query_stride, const void* ke
                          const void* value, int64_t value_stride, void* output, int64_t output_stride,
                          int heads_q, int heads_k, int head_dim, const int32_t* cu_seqlens_q,
                          const int32_t* cu_seqlens_k, int64_t batch, int64_t max_seqlen_q,
-                         float softmax_scale, int causal, hipStream_t stream) {
+                         int64_t max_seqlen_k, float softmax_scale, int causal, void* workspace,
+                         size_t workspace_bytes, hipStream_t stream) {
     if (head_dim != 96 && head_dim != 128)
         return fail(RQ_ENOKERNEL, "No compiled prefill attention kernel for head_dim=%d", head_dim);
     if (heads_q <= 0 || heads_k <= 0 || heads_q % heads_k != 0)
         return fail(RQ_EINVAL, "Query heads must be a positive multiple of key/value heads");
-    if (batch < 0 || max_seqlen_q < 0 || max_seqlen_q > (int64_t)INT32_MAX || batch > 65535)
-        return fail(RQ_EINVAL, "Invalid batch or max_seqlen_q");
+    if (batch < 0 || max_seqlen_q < 0 || max_seqlen_q > (int64_t)INT32_MAX || max_seqlen_k < 0 ||
+        max_seqlen_k > (int64_t)INT32_MAX || batch > 65535)
+        return fail(RQ_EINVAL, "Invalid batch, max_seqlen_q or max_seqlen_k");
     if (batch > 0 && (cu_seqlens_q == nullptr || cu_seqlens_k == nullptr))
         return fail(RQ_EINVAL, "cu_seqlens_q and cu_seqlens_k required");
     if (!(softmax_scale > 0.f) || !std::isfinite(softmax_scale)) return fail(RQ_EINVAL, "softmax_scale must be positive");
@@ -475,7 +477,27 @@ int rq_prefill_attention(const void* query, int64_t query_stride, const void* ke
     p.max_seqlen_q = (int)max_seqlen_q;
     p.causal = causal != 0;
     p.softmax_scale = softmax_scale;
+    p.causal_same = p.causal && cu_seqlens_q == cu_seqlens_k;
+    const size_t needed = rq::prefill_plan(p, max_seqlen_k);
+    if (needed > 0 && (workspace == nullptr || workspace_bytes < needed))
+        return fail(RQ_ENOSPACE, "Prefill workspace of %zu bytes required, %zu given", needed, workspace_bytes);
+    p.partials = static_cast<float*>(workspace);
     return check_launch(rq::launch_prefill(p, stream), "prefill attention launch");
+}
+
+size_t rq_prefill_workspace_bytes(int64_t batch, int heads_q, int head_dim, int64_t max_seqlen_q,
+                                  int64_t max_seqlen_k, int causal, int same_lengths) {
+    if (batch <= 0 || heads_q <= 0 || head_dim <= 0 || max_seqlen_q <= 0 || max_seqlen_k <= 0 ||
+        max_seqlen_q > (int64_t)INT32_MAX || max_seqlen_k > (int64_t)INT32_MAX)
+        return 0;
+    rq::PrefillParams p{};
+    p.batch = (int)batch;
+    p.heads_q = heads_q;
+    p.head_dim = head_dim;
+    p.max_seqlen_q = (int)max_seqlen_q;
+    p.causal = causal != 0;
+    p.causal_same = p.causal && same_lengths != 0;
+    return rq::prefill_plan(p, max_seqlen_k);
 }
 
 void rq_timing_enable(int enabled) {

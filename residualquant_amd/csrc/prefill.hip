@@ -32,8 +32,41 @@ typedef float F32x16 __attribute__((ext_vector_type(16)));
 
 constexpr int kPrefillWaves = 4;
 constexpr int kPrefillThreads = 64 * kPrefillWaves;
-constexpr int kBlockQueries = 32 * kPrefillWaves;
-constexpr int kBlockKeys = 64;
+constexpr int kBlockQueries = kPrefillBlockQueries;  // 32 per wave
+constexpr int kBlockKeys = kPrefillBlockKeys;
+constexpr int kSplitTiles = 16;  // key tiles per work item at most (1024 keys)
+static_assert(kBlockQueries == 32 * kPrefillWaves, "one 32-query MFMA column block per wave");
+
+// ---------------------------------------------------------------- plan
+
+// Key tiles query block qb may need: all of them, or 2 (qb + 1) when the
+// attention is causal over equal query and key lengths.
+__host__ __device__ inline int planned_tiles(const PrefillParams& p, int block) {
+    const int need = 2 * (block + 1);
+    return (p.causal_same && need < p.max_tiles) ? need : p.max_tiles;
+}
+
+__host__ __device__ inline int block_splits(const PrefillParams& p, int block) {
+    if (p.split_tiles <= 0) return 1;
+    const int n = (planned_tiles(p, block) + p.split_tiles - 1) / p.split_tiles;
+    return n < 1 ? 1 : (n > kMaxSplits ? kMaxSplits : n);
+}
+
+struct PrefillItem {
+    int block, split, splits, slot;  // slot: first partial slot of the block (split blocks only)
+};
+
+// Work items run heaviest first: query blocks from the last, their splits in order.
+__device__ inline PrefillItem decode_item(const PrefillParams& p, int item) {
+    int slot = 0;
+    for (int block = p.query_blocks - 1; block >= 0; --block) {
+        const int n = block_splits(p, block);
+        if (item < n) return {block, item, n, slot};
+        item -= n;
+        if (n > 1) slot += n;
+    }
+    return {-1, 0, 1, 0};
+}
 
 __device__ __forceinline__ F32x16 mfma(Bf16x8 a, Bf16x8 b, F32x16 c) {
     return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
@@ -65,7 +98,9 @@ void prefill_kernel(PrefillParams p) {
 
     const int sequence = blockIdx.z;
     const int head = blockIdx.y;
-    const int q_block = gridDim.x - 1 - blockIdx.x;
+    const PrefillItem work = decode_item(p, blockIdx.x);
+    if (work.block < 0) return;
+    const int q_block = work.block;
     const int q_begin = p.cu_seqlens_q[sequence];
     const int q_len = p.cu_seqlens_q[sequence + 1] - q_begin;
     const int k_begin = p.cu_seqlens_k[sequence];
@@ -166,16 +201,23 @@ void prefill_kernel(PrefillParams p) {
         }
     };
 
-    if (block_keys > 0) {
-        fetch(0);
+    // This item's share of the block's key tiles.
+    const int block_tiles = block_keys > 0 ? (block_keys + kBlockKeys - 1) / kBlockKeys : 0;
+    const int per_split = (block_tiles + work.splits - 1) / work.splits;
+    const int first_tile = work.split * per_split;
+    const int end_tile = first_tile + per_split < block_tiles ? first_tile + per_split : block_tiles;
+    const int key_end = end_tile * kBlockKeys < block_keys ? end_tile * kBlockKeys : block_keys;
+
+    if (first_tile * kBlockKeys < key_end) {
+        fetch(first_tile * kBlockKeys);
         stage(0);
     }
     __syncthreads();
     int buffer = 0;
-    for (int kt = 0; kt < block_keys; kt += kBlockKeys, buffer ^= 1) {
+    for (int kt = first_tile * kBlockKeys; kt < key_end; kt += kBlockKeys, buffer ^= 1) {
         // Buffer `buffer` holds this tile; every wave finished reading the
         // other one before the barrier that ended the previous iteration.
-        const bool more = kt + kBlockKeys < block_keys;
+        const bool more = kt + kBlockKeys < key_end;
         if (more) fetch(kt + kBlockKeys);
         const uint16_t* k_tile = k_tiles[buffer];
         const uint16_t* v_tile = v_tiles[buffer];
@@ -193,6 +235,8 @@ void prefill_kernel(PrefillParams p) {
             for (int m = 0; m < D / 16; ++m)
                 s[sub] = mfma(*reinterpret_cast<const Bf16x8*>(k_row + 16 * m), q_operand[m], s[sub]);
         }
+        // Raw scores: the scale is positive, so the row max of the scaled
+        // scores is the scaled row max and is folded into the exp2 argument.
         float tile_max = -__builtin_inff();
         // Only tiles that cross the sequence end or this wave's causal
         // diagonal need the per-key mask (wave-uniform branch).
@@ -203,20 +247,16 @@ void prefill_kernel(PrefillParams p) {
 #pragma unroll
                 for (int r = 0; r < 16; ++r) {
                     const int key = kt + 32 * sub + 8 * (r >> 2) + 4 * half + (r & 3);
-                    const float v = (key < k_len && key <= my_limit) ? s[sub][r] * c : -__builtin_inff();
-                    s[sub][r] = v;
-                    tile_max = fmaxf(tile_max, v);
+                    if (!(key < k_len && key <= my_limit)) s[sub][r] = -__builtin_inff();
+                    tile_max = fmaxf(tile_max, s[sub][r]);
                 }
         } else {
 #pragma unroll
             for (int sub = 0; sub < 2; ++sub)
 #pragma unroll
-                for (int r = 0; r < 16; ++r) {
-                    s[sub][r] *= c;
-                    tile_max = fmaxf(tile_max, s[sub][r]);
-                }
+                for (int r = 0; r < 16; ++r) tile_max = fmaxf(tile_max, s[sub][r]);
         }
-        tile_max = fmaxf(tile_max, __shfl_xor(tile_max, 32));
+        tile_max = fmaxf(tile_max, __shfl_xor(tile_max, 32)) * c;
         const float new_max = fmaxf(running_max, tile_max);
         // A query with no visible key yet keeps zero weights (no -inf - -inf).
         const float base = new_max == -__builtin_inff() ? 0.f : new_max;
@@ -234,16 +274,19 @@ void prefill_kernel(PrefillParams p) {
             for (int j = 0; j < 2; ++j)
 #pragma unroll
                 for (int e = 0; e < 8; ++e) {
-                    const __bf16 w = (__bf16)__builtin_amdgcn_exp2f(s[sub][8 * j + e] - base);
-                    p_operand[sub][j][e] = w;
-                    tile_sum += (float)w;
+                    const float w = __builtin_amdgcn_exp2f(fmaf(s[sub][8 * j + e], c, -base));
+                    p_operand[sub][j][e] = (__bf16)w;
+                    tile_sum += w;
                 }
         tile_sum += __shfl_xor(tile_sum, 32);
         running_sum = running_sum * rescale + tile_sum;
+        // Once the row maxima settle, most tiles leave every query's max in place.
+        if (!__all(rescale == 1.0f)) {
 #pragma unroll
-        for (int t = 0; t < D / 32; ++t)
+            for (int t = 0; t < D / 32; ++t)
 #pragma unroll
-            for (int r = 0; r < 16; ++r) out[t][r] *= rescale;
+                for (int r = 0; r < 16; ++r) out[t][r] *= rescale;
+        }
 
 #pragma unroll
         for (int sub = 0; sub < 2; ++sub)
@@ -264,6 +307,26 @@ void prefill_kernel(PrefillParams p) {
         __syncthreads();
     }
 
+    if (work.splits > 1) {
+        // Unnormalised partial [slot][row][query]: rows 0..D-1 the output,
+        // D the running max (log2 units), D + 1 the running sum.
+        if (my_q < q_len) {
+            const int query = 32 * wave + column;
+            float* partial = p.partials +
+                             ((((int64_t)sequence * p.heads_q + head) * p.partial_slots + work.slot + work.split) *
+                              (D + 2)) * kBlockQueries + query;
+#pragma unroll
+            for (int t = 0; t < D / 32; ++t)
+#pragma unroll
+                for (int r = 0; r < 16; ++r)
+                    partial[(32 * t + 8 * (r >> 2) + 4 * half + (r & 3)) * kBlockQueries] = out[t][r];
+            if (half == 0) {
+                partial[D * kBlockQueries] = running_max;
+                partial[(D + 1) * kBlockQueries] = running_sum;
+            }
+        }
+        return;
+    }
     if (my_q < q_len) {
         const float inverse = running_sum > 0.f ? 1.0f / running_sum : 0.f;
         uint16_t* dst = p.output + (int64_t)(q_begin + my_q) * p.output_stride + head * D + 4 * half;
@@ -278,16 +341,76 @@ void prefill_kernel(PrefillParams p) {
     }
 }
 
+// Combines the partials of split query blocks: the LSE merge of (max, sum,
+// output) triples in log2 units, then the BF16 row.  Thread = (query, 8
+// channels): grid.x = query_blocks * D / 8 chunk groups of 128 queries.
+template <int D>
+__global__ __launch_bounds__(kBlockQueries) void prefill_merge_kernel(PrefillParams p) {
+    const int block = blockIdx.x / (D / 8), chunk = blockIdx.x % (D / 8);
+    const int head = blockIdx.y, sequence = blockIdx.z;
+    const int splits = block_splits(p, block);
+    if (splits <= 1) return;
+    int slot = 0;
+    for (int b = p.query_blocks - 1; b > block; --b) {
+        const int n = block_splits(p, b);
+        if (n > 1) slot += n;
+    }
+    const int q_begin = p.cu_seqlens_q[sequence];
+    const int q_len = p.cu_seqlens_q[sequence + 1] - q_begin;
+    const int query = threadIdx.x;
+    const int q = block * kBlockQueries + query;
+    if (q >= q_len) return;
+    const float* base = p.partials + ((((int64_t)sequence * p.heads_q + head) * p.partial_slots + slot) * (D + 2)) *
+                                         kBlockQueries + query;
+    const int64_t stride = (int64_t)(D + 2) * kBlockQueries;
+    float maximum = -__builtin_inff();
+    for (int s = 0; s < splits; ++s) maximum = fmaxf(maximum, base[s * stride + D * kBlockQueries]);
+    float total = 0.f, acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    for (int s = 0; s < splits; ++s) {
+        const float* part = base + s * stride;
+        const float m = part[D * kBlockQueries];
+        const float w = m == -__builtin_inff() ? 0.f : __builtin_amdgcn_exp2f(m - maximum);
+        total += w * part[(D + 1) * kBlockQueries];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) acc[e] += w * part[(8 * chunk + e) * kBlockQueries];
+    }
+    const float inverse = total > 0.f ? 1.0f / total : 0.f;
+    uint32_t packed[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) packed[e] = bf16_rn(acc[2 * e] * inverse) | (bf16_rn(acc[2 * e + 1] * inverse) << 16);
+    uint16_t* dst = p.output + (int64_t)(q_begin + q) * p.output_stride + head * D + 8 * chunk;
+    reinterpret_cast<uint2*>(dst)[0] = make_uint2(packed[0], packed[1]);
+    reinterpret_cast<uint2*>(dst)[1] = make_uint2(packed[2], packed[3]);
+}
+
 }  // namespace
 
+size_t prefill_plan(PrefillParams& p, int64_t max_seqlen_k) {
+    p.query_blocks = (int)((p.max_seqlen_q + kBlockQueries - 1) / kBlockQueries);
+    p.max_tiles = (int)((max_seqlen_k + kBlockKeys - 1) / kBlockKeys);
+    p.split_tiles = kSplitTiles;
+    p.items = 0;
+    p.partial_slots = 0;
+    for (int block = 0; block < p.query_blocks; ++block) {
+        const int n = block_splits(p, block);
+        p.items += n;
+        if (n > 1) p.partial_slots += n;
+    }
+    return sizeof(float) * (size_t)p.batch * p.heads_q * p.partial_slots * (p.head_dim + 2) * kBlockQueries;
+}
+
 hipError_t launch_prefill(const PrefillParams& p, hipStream_t stream) {
-    if (p.batch == 0 || p.max_seqlen_q == 0) return hipSuccess;
-    const dim3 grid((unsigned)((p.max_seqlen_q + kBlockQueries - 1) / kBlockQueries), (unsigned)p.heads_q,
-                    (unsigned)p.batch);
+    if (p.batch == 0 || p.max_seqlen_q == 0 || p.items == 0) return hipSuccess;
+    const dim3 grid((unsigned)p.items, (unsigned)p.heads_q, (unsigned)p.batch);
+    const dim3 merge_grid((unsigned)(p.query_blocks * (p.head_dim / 8)), (unsigned)p.heads_q, (unsigned)p.batch);
     if (p.head_dim == 128) {
         hipLaunchKernelGGL(prefill_kernel<128>, grid, dim3(kPrefillThreads), 0, stream, p);
+        if (p.partial_slots > 0)
+            hipLaunchKernelGGL(prefill_merge_kernel<128>, merge_grid, dim3(kBlockQueries), 0, stream, p);
     } else if (p.head_dim == 96) {
         hipLaunchKernelGGL(prefill_kernel<96>, grid, dim3(kPrefillThreads), 0, stream, p);
+        if (p.partial_slots > 0)
+            hipLaunchKernelGGL(prefill_merge_kernel<96>, merge_grid, dim3(kBlockQueries), 0, stream, p);
     } else {
         return hipErrorInvalidValue;
     }

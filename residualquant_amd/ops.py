@@ -302,11 +302,17 @@ def flash_attn_varlen_func(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, ma
              "cu_seqlens_q and cu_seqlens_k must describe the same sequences")
     head_dim = q.size(2)
     scale = head_dim ** -0.5 if softmax_scale is None else float(softmax_scale)
+    batch = cu_seqlens_q.numel() - 1
+    same = cu_seqlens_q.data_ptr() == cu_seqlens_k.data_ptr()
+    needed = _lib.lib().rq_prefill_workspace_bytes(batch, q.size(1), head_dim, int(max_seqlen_q),
+                                                   int(max_seqlen_k), 1 if causal else 0, 1 if same else 0)
+    workspace = torch.empty(max(needed, 1), dtype=torch.uint8, device=q.device)
     with torch.cuda.device(q.device):
         status = _lib.lib().rq_prefill_attention(
             q.data_ptr(), q.stride(0), k.data_ptr(), k.stride(0), v.data_ptr(), v.stride(0), out.data_ptr(),
             out.stride(0), q.size(1), k.size(1), head_dim, cu_seqlens_q.data_ptr(), cu_seqlens_k.data_ptr(),
-            cu_seqlens_q.numel() - 1, int(max_seqlen_q), scale, 1 if causal else 0, _stream(q.device))
+            batch, int(max_seqlen_q), int(max_seqlen_k), scale, 1 if causal else 0, workspace.data_ptr(),
+            workspace.numel(), _stream(q.device))
     _lib.check(status)
     return out
 

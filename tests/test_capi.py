@@ -143,10 +143,11 @@ def test_python_ops_mirror_reference_messages():
 
 
 def _prefill_call(lib, *, head_dim=128, heads_q=4, heads_k=2, query=0x10000, stride=None):
+    # Every call below fails validation: the fake pointers never reach a kernel.
     fake = 0x10000
     row = stride or heads_q * head_dim
     return lib.rq_prefill_attention(query, row, fake, heads_k * head_dim, fake, heads_k * head_dim, fake, row,
-                                    heads_q, heads_k, head_dim, fake, fake, 2, 64, 0.1, 1, None)
+                                    heads_q, heads_k, head_dim, fake, fake, 2, 64, 64, 0.1, 1, None, 0, None)
 
 
 def test_prefill_rejects_before_device_work(lib):
@@ -156,4 +157,14 @@ def test_prefill_rejects_before_device_work(lib):
     assert _prefill_call(lib, query=0x10004) == _lib.RQ_EINVAL
     assert lib.rq_last_error() == b"Q/K/V/output addresses and token strides must be 8-byte aligned"
     assert _prefill_call(lib, stride=4 * 128 + 2) == _lib.RQ_EINVAL
+
+
+def test_prefill_workspace_plan(lib):
+    # 64-token prompts fit one work item per query block: no partials.
+    assert lib.rq_prefill_workspace_bytes(2, 4, 128, 64, 64, 1, 1) == 0
+    # A 4096-token causal prompt splits its later query blocks (16 key tiles per item).
+    big = lib.rq_prefill_workspace_bytes(1, 16, 128, 4096, 4096, 1, 1)
+    assert big > 0 and big % (4 * 130 * 128 * 16) == 0
+    # Without the same-lengths hint every block plans for all keys.
+    assert lib.rq_prefill_workspace_bytes(1, 16, 128, 4096, 4096, 1, 0) > big
 

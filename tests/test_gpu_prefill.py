@@ -39,6 +39,9 @@ CASES = [
     ([129, 64], None, 8, 2, 128, True),
     ([40, 90], [100, 90], 2, 2, 128, True),
     ([77, 5], [33, 140], 2, 1, 96, False),
+    # long enough for key splits and the partial merge
+    ([1500, 700], None, 2, 2, 128, True),
+    ([300, 200], [1300, 1250], 2, 1, 96, False),
 ]
 
 
@@ -59,6 +62,19 @@ def test_prefill_matches_oracle(oracle, device, case):
         cu_seqlens_q=torch.from_numpy(cu_q).to(device), cu_seqlens_k=torch.from_numpy(cu_k).to(device),
         max_seqlen_q=max(q_lens), max_seqlen_k=max(k_lens), softmax_scale=dim ** -0.5, causal=causal)
     _check(out, expected, "prefill")
+
+
+def test_prefill_separate_equal_seqlens(oracle, device):
+    """cu_seqlens_k a separate tensor with the same lengths: the general split plan."""
+    lens, heads, dim = [1200, 33], 2, 128
+    cu = np.concatenate([[0], np.cumsum(lens)]).astype(np.int32)
+    q, k, v = (_random((cu[-1], heads, dim), s) for s in (21, 22, 23))
+    expected = oracle.prefill_attention(_bits(q), _bits(k), _bits(v), cu, cu, dim ** -0.5, True)
+    out = rq.flash_attn_varlen_func(q.to(device), k.to(device), v.to(device), max(lens),
+                                    torch.from_numpy(cu).to(device), max(lens),
+                                    cu_seqlens_k=torch.from_numpy(cu.copy()).to(device), softmax_scale=dim ** -0.5,
+                                    causal=True)
+    _check(out, expected, "separate seqlens")
 
 
 def test_prefill_fused_qkv_views(oracle, device):
