@@ -151,37 +151,55 @@ void prefill_kernel(PrefillParams p) {
     // Tile loads: each thread fetches K chunks (row, 8 channels) and V units
     // (key pair, 8 channels) of the next tile into registers while the current
     // tile computes, then stages them (V transposed) into the other buffer.
+    // The loads are raw buffer loads from a wave-uniform resource rebased at
+    // each tile, so rows past the sequence read as zero without a branch and
+    // every per-thread offset is a loop-invariant 32-bit value.
     constexpr int kKChunks = (kBlockKeys * (D / 8) + kPrefillThreads - 1) / kPrefillThreads;
     constexpr int kVUnits = ((kBlockKeys / 2) * (D / 8) + kPrefillThreads - 1) / kPrefillThreads;
+    constexpr uint32_t kOutOfRange = 0x80000000u;  // beyond any tile's record count: loads zero
+    const uint32_t key_row_bytes = (uint32_t)p.key_stride * 2, value_row_bytes = (uint32_t)p.value_stride * 2;
+    uint32_t k_offset[kKChunks], v_offset[kVUnits];
+#pragma unroll
+    for (int i = 0; i < kKChunks; ++i) {
+        const int chunk = threadIdx.x + i * kPrefillThreads;
+        k_offset[i] = chunk < kBlockKeys * (D / 8) ? (uint32_t)(chunk / (D / 8)) * key_row_bytes + 16 * (chunk % (D / 8))
+                                                   : kOutOfRange;
+    }
+#pragma unroll
+    for (int i = 0; i < kVUnits; ++i) {
+        const int unit = threadIdx.x + i * kPrefillThreads;
+        v_offset[i] = unit < (kBlockKeys / 2) * (D / 8)
+                          ? (uint32_t)(2 * (unit % (kBlockKeys / 2))) * value_row_bytes + 16 * (unit / (kBlockKeys / 2))
+                          : kOutOfRange;
+    }
+    auto tile_resource = [&](const uint16_t* base, int64_t row_elements, int kt) {
+        // Bytes from row kt to the end of the tile's last valid row (its D
+        // channels); at most one tile of rows, so the count stays small.
+        const int64_t remaining = k_len - kt < kBlockKeys ? k_len - kt : kBlockKeys;
+        const uint32_t bytes = remaining > 0 ? (uint32_t)((remaining - 1) * row_elements * 2 + D * 2) : 0u;
+        return __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(base + (int64_t)kt * row_elements), (short)0,
+                                                 (int)bytes, 0x00020000);
+    };
     uint4 k_next[kKChunks], v_next[kVUnits][2];
     auto fetch = [&](int kt) {
+        const auto k_rsrc = tile_resource(k_base, p.key_stride, kt);
+        const auto v_rsrc = tile_resource(v_base, p.value_stride, kt);
 #pragma unroll
-        for (int i = 0; i < kKChunks; ++i) {
-            const int chunk = threadIdx.x + i * kPrefillThreads;
-            const int row = chunk / (D / 8), segment = chunk % (D / 8);
-            k_next[i] = make_uint4(0, 0, 0, 0);
-            if (chunk < kBlockKeys * (D / 8) && kt + row < k_len)
-                k_next[i] = load16(k_base + (int64_t)(kt + row) * p.key_stride + 8 * segment);
-        }
+        for (int i = 0; i < kKChunks; ++i)
+            k_next[i] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(k_rsrc, k_offset[i], 0, 0));
 #pragma unroll
         for (int i = 0; i < kVUnits; ++i) {
-            const int unit = threadIdx.x + i * kPrefillThreads;
-            const int pair = unit % (kBlockKeys / 2), group = unit / (kBlockKeys / 2);
-            const int key = kt + 2 * pair;
-            v_next[i][0] = v_next[i][1] = make_uint4(0, 0, 0, 0);
-            if (unit < (kBlockKeys / 2) * (D / 8)) {
-                if (key < k_len) v_next[i][0] = load16(v_base + (int64_t)key * p.value_stride + 8 * group);
-                if (key + 1 < k_len) v_next[i][1] = load16(v_base + (int64_t)(key + 1) * p.value_stride + 8 * group);
-            }
+            v_next[i][0] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(v_rsrc, v_offset[i], 0, 0));
+            v_next[i][1] = __builtin_bit_cast(
+                uint4, __builtin_amdgcn_raw_buffer_load_b128(v_rsrc, v_offset[i] + value_row_bytes, 0, 0));
         }
     };
     auto stage = [&](int buffer) {
 #pragma unroll
         for (int i = 0; i < kKChunks; ++i) {
             const int chunk = threadIdx.x + i * kPrefillThreads;
-            const int row = chunk / (D / 8), segment = chunk % (D / 8);
             if (chunk < kBlockKeys * (D / 8))
-                *reinterpret_cast<uint4*>(&k_tiles[buffer][row * KS + 8 * segment]) = k_next[i];
+                *reinterpret_cast<uint4*>(&k_tiles[buffer][(chunk / (D / 8)) * KS + 8 * (chunk % (D / 8))]) = k_next[i];
         }
 #pragma unroll
         for (int i = 0; i < kVUnits; ++i) {
@@ -190,12 +208,13 @@ void prefill_kernel(PrefillParams p) {
             if (unit < (kBlockKeys / 2) * (D / 8)) {
                 const uint4 a = v_next[i][0], b = v_next[i][1];
                 const uint32_t av[4] = {a.x, a.y, a.z, a.w}, bv[4] = {b.x, b.y, b.z, b.w};
+                uint16_t* column = &v_tiles[buffer][(8 * group) * VS + 2 * pair];
 #pragma unroll
                 for (int e = 0; e < 4; ++e) {
-                    const uint32_t low = (av[e] & 0xffffu) | (bv[e] << 16);
-                    const uint32_t high = (av[e] >> 16) | (bv[e] & 0xffff0000u);
-                    *reinterpret_cast<uint32_t*>(&v_tiles[buffer][(8 * group + 2 * e) * VS + 2 * pair]) = low;
-                    *reinterpret_cast<uint32_t*>(&v_tiles[buffer][(8 * group + 2 * e + 1) * VS + 2 * pair]) = high;
+                    // (key, key + 1) pairs of channels 2e and 2e + 1.
+                    *reinterpret_cast<uint32_t*>(column + (2 * e) * VS) = __builtin_amdgcn_perm(bv[e], av[e], 0x05040100u);
+                    *reinterpret_cast<uint32_t*>(column + (2 * e + 1) * VS) =
+                        __builtin_amdgcn_perm(bv[e], av[e], 0x07060302u);
                 }
             }
         }
