@@ -355,11 +355,86 @@ def run_prefill(args):
     print(json.dumps(result), flush=True)
 
 
+def run_step(args):
+    """C3: one graph replay = one decode step of all requests through 48 layers x 4 loops."""
+    import torch
+
+    from residualquant_amd import ops
+    from residualquant_amd.looped_decode import LoopedConfig, LoopedDecoder
+
+    device = torch.device("cuda:0")
+    torch.cuda.set_device(device)
+    config = LoopedConfig()
+    sweep = [(32, 8192)] if args.no_sweep else [(b, t) for t in (2048, 4096, 8192) for b in (1, 8, 32)]
+    new_tokens = args.steps
+    weights = None
+    results = []
+    for batch, context in sweep:
+        t0 = time.perf_counter()
+        model = LoopedDecoder(config, batch, context, new_tokens + args.warmup + 2, device, seed=2026,
+                              weights_from=weights)
+        weights = weights or model
+        model.build_history(seed=7)
+        torch.cuda.synchronize()
+        build_s = time.perf_counter() - t0
+        # Attention share: one eager step with the library's kernel timing.
+        ops.timing_read()
+        ops.timing_enable(True)
+        model.step()
+        torch.cuda.synchronize()
+        ops.timing_enable(False)
+        attention_ms, attention_calls = ops.timing_read()
+        graph = model.capture()
+        for _ in range(args.warmup):
+            graph.replay()
+        torch.cuda.synchronize()
+        begin, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        begin.record()
+        for _ in range(new_tokens):
+            graph.replay()
+        end.record()
+        torch.cuda.synchronize()
+        step_ms = begin.elapsed_time(end) / new_tokens
+        entry = {"batch": batch, "context": context, "ms_per_step": step_ms, "tokens_per_s": batch / step_ms * 1e3,
+                 "attention_kernel_ms_per_step": attention_ms, "attention_calls_per_step": attention_calls,
+                 "history_build_s": build_s}
+        log(f"[bench] step B={batch} ctx={context}: {step_ms:.2f} ms/step, {entry['tokens_per_s']:.0f} tokens/s, "
+            f"split-K attention kernels {attention_ms:.2f} ms in {attention_calls} calls")
+        results.append(entry)
+        del graph, model
+        torch.cuda.empty_cache()
+    head = next(r for r in results if (r["batch"], r["context"]) == (32, 8192)) if any(
+        (r["batch"], r["context"]) == (32, 8192) for r in results) else results[-1]
+    result = {
+        "metric": "looped-model decode tokens/s (C3, graph-captured step, 1 GPU)",
+        "value": head["tokens_per_s"],
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": new_tokens,
+        "warmup": args.warmup,
+        "ms_per_step": head["ms_per_step"],
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16 weights/activations, int2/int4 packed KV",
+        "data": "synthetic: random-init bf16 weights; history K/V quantized from seeded synthetic loops",
+        "config": {"workload": "C3 Ouro-2.6B-shaped looped decode step", "layers": config.layers,
+                   "loops": config.loops, "hidden": config.hidden, "heads": config.heads,
+                   "head_dim": config.head_dim, "intermediate_assumed": config.intermediate, "vocab": config.vocab,
+                   "batch": head["batch"], "context": head["context"], "generated_tokens": new_tokens,
+                   "schedule": "[2,32]x3+[4,32] anchor 3 ls"},
+        "sweep": results,
+        "cpu_baseline": None,
+    }
+    print(json.dumps(result), flush=True)
+
+
 def main():
     parser = argparse.ArgumentParser(description=__doc__)
-    parser.add_argument("--workload", choices=("decode", "quantize", "prefill"), default="decode",
+    parser.add_argument("--workload", choices=("decode", "quantize", "prefill", "step"), default="decode",
                         help="decode: C2 paged decode attention (the headline); quantize: C1 quantize-on-write; "
-                             "prefill: causal prompt attention")
+                             "prefill: causal prompt attention; step: C3 looped-model decode step")
+    parser.add_argument("--no-sweep", action="store_true", help="step workload: batch 32 x 8k only")
     parser.add_argument("--tokens", type=int, default=4096, help="tokens per quantize call or prompt")
     parser.add_argument("--gpus", type=int, default=1)
     parser.add_argument("--steps", type=int, default=20)
@@ -387,6 +462,9 @@ def main():
         return
     if args.workload == "prefill":
         run_prefill(args)
+        return
+    if args.workload == "step":
+        run_step(args)
         return
     run_decode(args)
 

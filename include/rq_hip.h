@@ -165,6 +165,45 @@ size_t rq_prefill_workspace_bytes(int64_t batch, int heads_q, int head_dim, int6
                                   int64_t max_seqlen_k, int causal, int same_lengths);
 
 /*
+ * Elementwise callers on either side of the packed attention in one layer of
+ * the looped (Ouro) decoder, plugins/looped_transformers/src/looped_transformers/ouro.py:101-157.
+ *
+ * rq_rms_norm replaces vLLM's RMSNorm (layernorm.py), used as
+ * input_layernorm / input_layernorm_2 / post_attention_layernorm(_2)
+ * (ouro.py:132-157) and the loop's final norm (ouro.py:240): with a residual,
+ * total = bf16(x + residual) is written to residual_out (which may alias
+ * residual) and normalized; without one, x is normalized.
+ * y = bf16(bf16(total * rsqrt(mean(total^2) + eps)) * weight), mean over the
+ * hidden channels in FP32.  BF16 rows, 16-byte aligned, strides multiples of
+ * 8 elements; hidden a multiple of 8 up to 2048.
+ */
+int rq_rms_norm(const void* x, int64_t x_stride, const void* residual, int64_t residual_stride,
+                void* residual_out, int64_t residual_out_stride, const void* weight, void* y, int64_t y_stride,
+                int64_t rows, int hidden, float eps, hipStream_t stream);
+
+/*
+ * Rotate-half rotary embedding of the Q and K of fused [q | k | v] BF16 rows
+ * (the rotary_emb(positions, query, key) call, ouro.py:93-99, :109, with
+ * rotary_dim = head_dim): for i < head_dim / 2,
+ * out[i] = x[i] cos - x[i + d/2] sin, out[i + d/2] = x[i + d/2] cos + x[i] sin,
+ * cos/sin FP32 tables [table_rows, head_dim / 2] indexed by the int64
+ * position of each row (clamped to the table).  Optionally also writes the
+ * rotated K and the raw V to key_stage / value_stage rows (the loop-group
+ * staging of the packed backend, src/residual_quantization/packed_backend.py:101-137).
+ */
+int rq_rope_qkv(const void* qkv, int64_t qkv_stride, const int64_t* positions, const float* cos_table,
+                const float* sin_table, int64_t table_rows, int heads, int head_dim, int64_t rows, void* query,
+                int64_t query_stride, void* key, int64_t key_stride, void* key_stage, void* value_stage,
+                int64_t stage_stride, hipStream_t stream);
+
+/*
+ * out = bf16(silu(gate) * up) over [gate | up] BF16 rows of 2 * width: the
+ * SiluAndMul activation of Qwen2MLP (ouro.py:125-131).
+ */
+int rq_silu_mul(const void* gate_up, int64_t gate_up_stride, void* out, int64_t out_stride, int64_t rows, int width,
+                hipStream_t stream);
+
+/*
  * Kernel timing for measurement: when enabled, rq_attention and
  * rq_paged_attention_bf16 record HIP events around their split-K kernel on
  * the caller's stream; rq_timing_read() synchronizes the recorded events and

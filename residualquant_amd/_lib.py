@@ -28,6 +28,9 @@ EXPORTED_SYMBOLS = (
     "rq_paged_attention_bf16",
     "rq_prefill_attention",
     "rq_prefill_workspace_bytes",
+    "rq_rms_norm",
+    "rq_rope_qkv",
+    "rq_silu_mul",
     "rq_timing_enable",
     "rq_timing_read",
     "rq_set_split_target",
@@ -84,6 +87,12 @@ def _declare(l: ctypes.CDLL) -> None:
                                        i64, ctypes.c_float, i32, vp, ctypes.c_size_t, vp]
     l.rq_prefill_workspace_bytes.restype = ctypes.c_size_t
     l.rq_prefill_workspace_bytes.argtypes = [i64, i32, i32, i64, i64, i32, i32]
+    l.rq_rms_norm.restype = i32
+    l.rq_rms_norm.argtypes = [vp, i64, vp, i64, vp, i64, vp, vp, i64, i64, i32, ctypes.c_float, vp]
+    l.rq_rope_qkv.restype = i32
+    l.rq_rope_qkv.argtypes = [vp, i64, vp, vp, vp, i64, i32, i32, i64, vp, i64, vp, i64, vp, vp, i64, vp]
+    l.rq_silu_mul.restype = i32
+    l.rq_silu_mul.argtypes = [vp, i64, vp, i64, i64, i32, vp]
     l.rq_timing_enable.argtypes = [i32]
     l.rq_timing_read.restype = i32
     l.rq_timing_read.argtypes = [ctypes.POINTER(ctypes.c_double), ctypes.POINTER(ctypes.c_int64)]

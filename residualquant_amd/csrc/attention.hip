@@ -860,14 +860,14 @@ hipError_t launch_all(const AttentionParams& p, hipStream_t stream, hipEvent_t b
                       bool bf16) {
     hipLaunchKernelGGL((prepare_kernel<D>), dim3((unsigned)p.rows, (unsigned)p.heads), dim3(128), 0,
                        stream, p);
-    if (begin) hipEventRecord(begin, stream);
+    if (begin) (void)hipEventRecord(begin, stream);
     if (bf16) {
         const unsigned blocks = (unsigned)(p.rows * p.heads * p.splits);
         hipLaunchKernelGGL((decode_bf16_kernel<D>), dim3(blocks), dim3(kDecodeThreads), 0, stream, p);
     } else if (!dispatch_anchor<D>(p, stream)) {
         return hipErrorInvalidValue;
     }
-    if (end) hipEventRecord(end, stream);
+    if (end) (void)hipEventRecord(end, stream);
     hipLaunchKernelGGL((merge_kernel<D>), dim3((unsigned)p.rows, (unsigned)p.heads), dim3(128), 0,
                        stream, p);
     return hipGetLastError();

@@ -160,7 +160,7 @@ bool timing_events(hipStream_t stream, hipEvent_t* begin, hipEvent_t* end) {
     } else {
         if (hipEventCreate(&pair.first) != hipSuccess) return false;
         if (hipEventCreate(&pair.second) != hipSuccess) {
-            hipEventDestroy(pair.first);
+            (void)hipEventDestroy(pair.first);
             return false;
         }
     }
@@ -483,6 +483,88 @@ int rq_prefill_attention(const void* query, int64_t query_stride, const void* ke
         return fail(RQ_ENOSPACE, "Prefill workspace of %zu bytes required, %zu given", needed, workspace_bytes);
     p.partials = static_cast<float*>(workspace);
     return check_launch(rq::launch_prefill(p, stream), "prefill attention launch");
+}
+
+int rq_rms_norm(const void* x, int64_t x_stride, const void* residual, int64_t residual_stride,
+                void* residual_out, int64_t residual_out_stride, const void* weight, void* y, int64_t y_stride,
+                int64_t rows, int hidden, float eps, hipStream_t stream) {
+    if (rows < 0 || rows > (int64_t)INT32_MAX || hidden <= 0 || hidden % 8 != 0 || hidden > 2048)
+        return fail(RQ_EINVAL, "RMSNorm needs rows >= 0 and a hidden size that is a multiple of 8 up to 2048");
+    if (!(eps >= 0.f) || !std::isfinite(eps)) return fail(RQ_EINVAL, "RMSNorm eps must be finite and non-negative");
+    if ((residual == nullptr) != (residual_out == nullptr))
+        return fail(RQ_EINVAL, "A residual input and a residual output go together");
+    if (rows == 0) return ok();
+    const void* pointers[5] = {x, weight, y, residual, residual_out};
+    const int64_t strides[5] = {x_stride, 0, y_stride, residual_stride, residual_out_stride};
+    for (int i = 0; i < 5; ++i) {
+        if (i < 3 && pointers[i] == nullptr) return fail(RQ_EINVAL, "RMSNorm input, weight and output required");
+        if (pointers[i] == nullptr) continue;
+        if ((reinterpret_cast<uintptr_t>(pointers[i]) % 16) || strides[i] % 8 || (i != 1 && strides[i] < hidden))
+            return fail(RQ_EINVAL, "RMSNorm rows must be 16-byte aligned BF16 rows of at least hidden elements");
+    }
+    rq::StepNormParams p{};
+    p.x = static_cast<const uint16_t*>(x);
+    p.x_stride = x_stride;
+    p.residual = static_cast<const uint16_t*>(residual);
+    p.residual_stride = residual_stride;
+    p.residual_out = static_cast<uint16_t*>(residual_out);
+    p.residual_out_stride = residual_out_stride;
+    p.weight = static_cast<const uint16_t*>(weight);
+    p.y = static_cast<uint16_t*>(y);
+    p.y_stride = y_stride;
+    p.rows = rows;
+    p.hidden = hidden;
+    p.eps = eps;
+    return check_launch(rq::launch_rms_norm(p, stream), "RMSNorm launch");
+}
+
+int rq_rope_qkv(const void* qkv, int64_t qkv_stride, const int64_t* positions, const float* cos_table,
+                const float* sin_table, int64_t table_rows, int heads, int head_dim, int64_t rows, void* query,
+                int64_t query_stride, void* key, int64_t key_stride, void* key_stage, void* value_stage,
+                int64_t stage_stride, hipStream_t stream) {
+    if (rows < 0 || rows > (int64_t)INT32_MAX || heads <= 0 || heads > 32768 || head_dim <= 0 || head_dim % 2 != 0)
+        return fail(RQ_EINVAL, "Rotary embedding needs rows >= 0, heads > 0 and an even head_dim");
+    const int64_t row = (int64_t)heads * head_dim;
+    if (qkv_stride < 3 * row || query_stride < row || key_stride < row ||
+        ((key_stage != nullptr || value_stage != nullptr) && stage_stride < row))
+        return fail(RQ_EINVAL, "Fused [q | k | v] rows and [heads, head_dim] outputs required");
+    if (rows == 0) return ok();
+    if (table_rows <= 0 || qkv == nullptr || positions == nullptr || cos_table == nullptr || sin_table == nullptr ||
+        query == nullptr || key == nullptr)
+        return fail(RQ_EINVAL, "QKV, positions, cos/sin tables and Q/K outputs required");
+    rq::StepRopeParams p{};
+    p.qkv = static_cast<const uint16_t*>(qkv);
+    p.qkv_stride = qkv_stride;
+    p.positions = positions;
+    p.cos_table = cos_table;
+    p.sin_table = sin_table;
+    p.table_rows = table_rows;
+    p.heads = heads;
+    p.head_dim = head_dim;
+    p.rows = rows;
+    p.q = static_cast<uint16_t*>(query);
+    p.q_stride = query_stride;
+    p.k = static_cast<uint16_t*>(key);
+    p.k_stride = key_stride;
+    p.k_stage = static_cast<uint16_t*>(key_stage);
+    p.v_stage = static_cast<uint16_t*>(value_stage);
+    p.stage_stride = stage_stride;
+    return check_launch(rq::launch_rope(p, stream), "rotary embedding launch");
+}
+
+int rq_silu_mul(const void* gate_up, int64_t gate_up_stride, void* out, int64_t out_stride, int64_t rows, int width,
+                hipStream_t stream) {
+    if (rows < 0 || rows > 65535 || width <= 0 || width % 2 != 0)
+        return fail(RQ_EINVAL, "SiLU-mul needs 0 <= rows <= 65535 and an even width");
+    if (gate_up_stride < 2 * (int64_t)width || out_stride < width || gate_up_stride % 2 || out_stride % 2)
+        return fail(RQ_EINVAL, "[gate | up] rows of 2 * width and output rows of width required (even strides)");
+    if (rows == 0) return ok();
+    if (gate_up == nullptr || out == nullptr || (reinterpret_cast<uintptr_t>(gate_up) % 4) ||
+        (reinterpret_cast<uintptr_t>(out) % 4))
+        return fail(RQ_EINVAL, "4-byte aligned gate/up input and output required");
+    return check_launch(rq::launch_silu_mul(static_cast<const uint16_t*>(gate_up), gate_up_stride,
+                                            static_cast<uint16_t*>(out), out_stride, rows, width, stream),
+                        "SiLU-mul launch");
 }
 
 size_t rq_prefill_workspace_bytes(int64_t batch, int heads_q, int head_dim, int64_t max_seqlen_q,

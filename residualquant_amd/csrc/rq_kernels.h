@@ -87,6 +87,45 @@ constexpr int kPrefillBlockKeys = 64;
 size_t prefill_plan(PrefillParams& p, int64_t max_seqlen_k);
 hipError_t launch_prefill(const PrefillParams& p, hipStream_t stream);
 
+// Fused elementwise kernels of the looped-model decode step (step_ops.hip).
+struct StepNormParams {
+    const uint16_t* x;          // BF16 [rows, hidden]
+    int64_t x_stride;
+    const uint16_t* residual;   // optional BF16 [rows, hidden] added to x first
+    int64_t residual_stride;
+    uint16_t* residual_out;     // optional: receives bf16(x + residual) (may alias residual)
+    int64_t residual_out_stride;
+    const uint16_t* weight;     // BF16 [hidden]
+    uint16_t* y;
+    int64_t y_stride;
+    int64_t rows;
+    int hidden;                 // multiple of 8, at most 2048
+    float eps;
+};
+
+struct StepRopeParams {
+    const uint16_t* qkv;        // BF16 [rows, 3 * heads * head_dim]
+    int64_t qkv_stride;
+    const int64_t* positions;   // [rows]
+    const float* cos_table;     // [positions, head_dim / 2]
+    const float* sin_table;
+    int64_t table_rows;         // positions are clamped to [0, table_rows - 1]
+    int heads, head_dim;
+    int64_t rows;
+    uint16_t* q;
+    int64_t q_stride;
+    uint16_t* k;
+    int64_t k_stride;
+    uint16_t* k_stage;          // optional copies of the rotated K and of V
+    uint16_t* v_stage;
+    int64_t stage_stride;
+};
+
+hipError_t launch_rms_norm(const StepNormParams& p, hipStream_t stream);
+hipError_t launch_rope(const StepRopeParams& p, hipStream_t stream);
+hipError_t launch_silu_mul(const uint16_t* gate_up, int64_t gate_up_stride, uint16_t* out, int64_t out_stride,
+                           int64_t rows, int width, hipStream_t stream);
+
 // Per (row, head) prepared query block in the workspace (floats).
 constexpr int kPrepScalars = 16;   // [0] delta [1] live score [2] q'.mu_A [3..10] Q16 [11..14] Q32
 constexpr int kPrepQuery = 128;    // q' FP32 in log2 units

@@ -1,0 +1,160 @@
+// Fused elementwise kernels of the looped-model decode step (the callers on
+// either side of the packed attention in one Ouro layer,
+// plugins/looped_transformers/src/looped_transformers/ouro.py:102-146):
+// residual add + RMSNorm, rotary embedding of Q/K with the K/V staging copy,
+// and SiLU(gate) * up.  One launch each instead of a dozen elementwise ops.
+#include "rq_device.h"
+#include "rq_kernels.h"
+
+namespace rq {
+
+namespace {
+
+constexpr int kNormThreads = 256;
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+    for (int distance = 32; distance; distance >>= 1) v += __shfl_xor(v, distance);
+    return v;
+}
+
+// One workgroup per row, 8 channels per thread (rows of at most 8 * 256
+// channels, a multiple of 8): total = bf16(x + residual) when a residual is
+// given (written to residual_out), y = bf16(bf16(total * rsqrt(mean(total^2) + eps)) * w).
+__global__ __launch_bounds__(kNormThreads) void rms_norm_kernel(const uint16_t* x, int64_t x_stride,
+                                                                const uint16_t* residual, int64_t residual_stride,
+                                                                uint16_t* residual_out, int64_t residual_out_stride,
+                                                                const uint16_t* weight, uint16_t* y, int64_t y_stride,
+                                                                int hidden, float eps) {
+    __shared__ float partial[kNormThreads / 64];
+    const int64_t row = blockIdx.x;
+    const int i = 8 * threadIdx.x;
+    const bool active = i < hidden;
+    float values[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    float sum = 0.f;
+    if (active) {
+        const uint4 raw = *reinterpret_cast<const uint4*>(x + row * x_stride + i);
+        const uint32_t w[4] = {raw.x, raw.y, raw.z, raw.w};
+        uint4 rres = make_uint4(0, 0, 0, 0);
+        if (residual != nullptr) rres = *reinterpret_cast<const uint4*>(residual + row * residual_stride + i);
+        const uint32_t r[4] = {rres.x, rres.y, rres.z, rres.w};
+        uint32_t packed[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            float lo = bf16_f32(w[e] & 0xffffu), hi = bf16_f32(w[e] >> 16);
+            if (residual != nullptr) {
+                lo = bf16_f32(bf16_rn(lo + bf16_f32(r[e] & 0xffffu)));
+                hi = bf16_f32(bf16_rn(hi + bf16_f32(r[e] >> 16)));
+            }
+            packed[e] = bf16_rn(lo) | (bf16_rn(hi) << 16);
+            values[2 * e] = lo;
+            values[2 * e + 1] = hi;
+            sum = fmaf(lo, lo, sum);
+            sum = fmaf(hi, hi, sum);
+        }
+        if (residual_out != nullptr)
+            *reinterpret_cast<uint4*>(residual_out + row * residual_out_stride + i) =
+                make_uint4(packed[0], packed[1], packed[2], packed[3]);
+    }
+    sum = wave_sum(sum);
+    if ((threadIdx.x & 63) == 0) partial[threadIdx.x >> 6] = sum;
+    __syncthreads();
+    float total = 0.f;
+#pragma unroll
+    for (int w = 0; w < kNormThreads / 64; ++w) total += partial[w];
+    const float scale = rsqrtf(total / (float)hidden + eps);
+    if (active) {
+        const uint4 wraw = *reinterpret_cast<const uint4*>(weight + i);
+        const uint32_t wv[4] = {wraw.x, wraw.y, wraw.z, wraw.w};
+        uint32_t out[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const float a = bf16_f32(bf16_rn(values[2 * e] * scale)) * bf16_f32(wv[e] & 0xffffu);
+            const float b = bf16_f32(bf16_rn(values[2 * e + 1] * scale)) * bf16_f32(wv[e] >> 16);
+            out[e] = bf16_rn(a) | (bf16_rn(b) << 16);
+        }
+        *reinterpret_cast<uint4*>(y + row * y_stride + i) = make_uint4(out[0], out[1], out[2], out[3]);
+    }
+}
+
+// Rotary embedding (rotate-half form) of the Q and K heads of a fused QKV row,
+// plus plain copies of K (rotated) and V into staging rows.  Grid (rows,
+// 2 * heads): y < heads rotates Q head y, else K head y - heads (and copies V).
+// Positions outside the cos/sin tables are clamped to them: the tables are
+// read from device-resident positions that the host cannot check.
+__global__ __launch_bounds__(64) void rope_kernel(const uint16_t* qkv, int64_t qkv_stride, const int64_t* positions,
+                                                  const float* cos_table, const float* sin_table,
+                                                  int64_t table_rows, int heads,
+                                                  int head_dim, uint16_t* q_out, int64_t q_stride, uint16_t* k_out,
+                                                  int64_t k_stride, uint16_t* k_stage, uint16_t* v_stage,
+                                                  int64_t stage_stride) {
+    const int64_t row = blockIdx.x;
+    const int which = blockIdx.y;
+    const bool is_key = which >= heads;
+    const int head = is_key ? which - heads : which;
+    const int half = head_dim / 2;
+    const int64_t position = min(max(positions[row], (int64_t)0), table_rows - 1);
+    const uint16_t* src = qkv + row * qkv_stride + (int64_t)(is_key ? heads + head : head) * head_dim;
+    for (int i = threadIdx.x; i < half; i += 64) {
+        const float c = cos_table[position * half + i], s = sin_table[position * half + i];
+        const float x1 = bf16_f32(src[i]), x2 = bf16_f32(src[i + half]);
+        const uint16_t a = (uint16_t)bf16_rn(x1 * c - x2 * s), b = (uint16_t)bf16_rn(x2 * c + x1 * s);
+        if (!is_key) {
+            q_out[row * q_stride + head * head_dim + i] = a;
+            q_out[row * q_stride + head * head_dim + i + half] = b;
+        } else {
+            k_out[row * k_stride + head * head_dim + i] = a;
+            k_out[row * k_stride + head * head_dim + i + half] = b;
+            if (k_stage != nullptr) {
+                k_stage[row * stage_stride + head * head_dim + i] = a;
+                k_stage[row * stage_stride + head * head_dim + i + half] = b;
+            }
+        }
+    }
+    if (is_key && v_stage != nullptr) {
+        const uint16_t* v = qkv + row * qkv_stride + (int64_t)(2 * heads + head) * head_dim;
+        for (int i = threadIdx.x; i < head_dim; i += 64) v_stage[row * stage_stride + head * head_dim + i] = v[i];
+    }
+}
+
+// act = bf16(silu(gate) * up) with gate/up the two halves of a [rows, 2 * width] row.
+__global__ __launch_bounds__(256) void silu_mul_kernel(const uint16_t* gate_up, int64_t gate_up_stride, uint16_t* out,
+                                                       int64_t out_stride, int width) {
+    const int64_t row = blockIdx.y;
+    const int i = 2 * (blockIdx.x * 256 + threadIdx.x);
+    if (i >= width) return;
+    const uint32_t g = *reinterpret_cast<const uint32_t*>(gate_up + row * gate_up_stride + i);
+    const uint32_t u = *reinterpret_cast<const uint32_t*>(gate_up + row * gate_up_stride + width + i);
+    const float g0 = bf16_f32(g & 0xffffu), g1 = bf16_f32(g >> 16);
+    const float a = g0 / (1.0f + __expf(-g0)) * bf16_f32(u & 0xffffu);
+    const float b = g1 / (1.0f + __expf(-g1)) * bf16_f32(u >> 16);
+    *reinterpret_cast<uint32_t*>(out + row * out_stride + i) = bf16_rn(a) | (bf16_rn(b) << 16);
+}
+
+}  // namespace
+
+hipError_t launch_rms_norm(const StepNormParams& p, hipStream_t stream) {
+    if (p.rows == 0) return hipSuccess;
+    hipLaunchKernelGGL(rms_norm_kernel, dim3((unsigned)p.rows), dim3(kNormThreads), 0, stream, p.x, p.x_stride,
+                       p.residual, p.residual_stride, p.residual_out, p.residual_out_stride, p.weight, p.y,
+                       p.y_stride, p.hidden, p.eps);
+    return hipGetLastError();
+}
+
+hipError_t launch_rope(const StepRopeParams& p, hipStream_t stream) {
+    if (p.rows == 0) return hipSuccess;
+    hipLaunchKernelGGL(rope_kernel, dim3((unsigned)p.rows, (unsigned)(2 * p.heads)), dim3(64), 0, stream, p.qkv,
+                       p.qkv_stride, p.positions, p.cos_table, p.sin_table, p.table_rows, p.heads, p.head_dim, p.q, p.q_stride, p.k,
+                       p.k_stride, p.k_stage, p.v_stage, p.stage_stride);
+    return hipGetLastError();
+}
+
+hipError_t launch_silu_mul(const uint16_t* gate_up, int64_t gate_up_stride, uint16_t* out, int64_t out_stride,
+                           int64_t rows, int width, hipStream_t stream) {
+    if (rows == 0) return hipSuccess;
+    hipLaunchKernelGGL(silu_mul_kernel, dim3((unsigned)((width / 2 + 255) / 256), (unsigned)rows), dim3(256), 0,
+                       stream, gate_up, gate_up_stride, out, out_stride, width);
+    return hipGetLastError();
+}
+
+}  // namespace rq

@@ -1,0 +1,217 @@
+"""A graph-captured decode step of an Ouro-shaped looped model over the packed cache.
+
+The model loop follows the reference's Ouro implementation
+(plugins/looped_transformers/src/looped_transformers/ouro.py:38-242): the
+physical layers are shared by every recurrent step ("loop"); each
+(loop, layer) pair owns an attention slot (``virtual_index = loop * layers +
+layer``, :48-52), and a layer is
+
+    x, residual = input_layernorm(h, residual)     (fused add + RMSNorm)
+    a = o_proj(attention(rope(q), rope(k), v))     (:102-110)
+    x, residual = post_attention_layernorm(input_layernorm_2(a), residual)
+    h = post_attention_layernorm_2(mlp(x))         (Qwen2MLP: SiLU(gate) * up)
+
+with the final ``norm(h, residual)`` after each loop (:240).  The packed
+backend stages the K/V of loops 0..2 of every layer and quantizes the whole
+loop group at the anchor loop (install_model.py:17-52,
+packed_backend.py:101-137), so one decode step runs 48 x 4 attention calls
+over the packed history plus 48 quantize calls.
+
+Weights are random BF16 (there are no checkpoints here), stored
+``[out, in]`` as vLLM's linear layers hold them.  Plain GEMMs go to torch
+(hipBLASLt); attention, quantize, the fused add + RMSNorm, the rotary
+embedding (which also writes the loop-group staging copies) and SiLU * up are
+this package's HIP kernels.  The whole step, including advancing positions,
+slots and the greedy next token, is captured once in a HIP graph and replayed
+per token.
+"""
+
+from __future__ import annotations
+
+import math
+from dataclasses import dataclass
+from typing import Optional, Tuple
+
+import torch
+
+import torch.nn.functional as F
+
+from . import ops, step_ops, workloads
+from .layout import page_width
+
+
+@dataclass
+class LoopedConfig:
+    """Ouro-2.6B-shaped decoder.
+
+    ``intermediate`` is not given by the benchmark configuration; 5632 (the
+    Ouro-1.4B MLP width at the same hidden size) is an assumption, as are
+    ``rope_theta`` and ``rms_eps``.
+    """
+
+    layers: int = 48
+    loops: int = 4
+    hidden: int = 2048
+    heads: int = 16
+    head_dim: int = 128
+    intermediate: int = 5632
+    vocab: int = 49152
+    rms_eps: float = 1e-6
+    rope_theta: float = 1_000_000.0
+    schedule: Tuple[Tuple[int, int], ...] = ((2, 32), (2, 32), (2, 32), (4, 32))
+    anchor: int = 3
+    coefficient: str = "ls"
+    page_tokens: int = 16
+
+
+class LoopedDecoder:
+    """Synthetic Ouro-shaped model with a packed paged cache for ``batch`` requests."""
+
+    def __init__(self, config: LoopedConfig, batch: int, context: int, max_new_tokens: int,
+                 device: torch.device, seed: int = 0, weights_from: Optional["LoopedDecoder"] = None):
+        if config.loops != len(config.schedule):
+            raise ValueError("one packed record per loop is required")
+        self.config = c = config
+        self.batch, self.context, self.device = batch, context, device
+        self.max_tokens = context + max_new_tokens
+        generator = torch.Generator(device=device).manual_seed(seed)
+
+        def weight(fan_out, fan_in):
+            scale = 1.0 / math.sqrt(fan_in)
+            return (torch.randn((fan_out, fan_in), generator=generator, device=device) * scale).to(torch.bfloat16)
+
+        q_size = c.heads * c.head_dim
+        if weights_from is not None:
+            if weights_from.config != c:
+                raise ValueError("shared weights need the same model configuration")
+            for name in ("embed", "qkv", "o", "gate_up", "down", "norms", "final_norm", "lm_head", "key_rotation",
+                         "value_rotation"):
+                setattr(self, name, getattr(weights_from, name))
+        else:
+            self.embed = (torch.randn((c.vocab, c.hidden), generator=generator, device=device) * 0.02).to(
+                torch.bfloat16)
+            self.qkv = [weight(3 * q_size, c.hidden) for _ in range(c.layers)]
+            self.o = [weight(c.hidden, q_size) for _ in range(c.layers)]
+            self.gate_up = [weight(2 * c.intermediate, c.hidden) for _ in range(c.layers)]
+            self.down = [weight(c.hidden, c.intermediate) for _ in range(c.layers)]
+            ones = torch.ones(c.hidden, dtype=torch.bfloat16, device=device)
+            self.norms = [[ones.clone() for _ in range(4)] for _ in range(c.layers)]
+            self.final_norm = ones.clone()
+            self.lm_head = weight(c.vocab, c.hidden)
+            self.key_rotation = [workloads.random_sign_rotation(c.heads, c.head_dim, seed + 11 + 2 * l, device=device)
+                                 for l in range(c.layers)]
+            self.value_rotation = [
+                workloads.random_sign_rotation(c.heads, c.head_dim, seed + 12 + 2 * l, device=device)
+                for l in range(c.layers)]
+
+        # Paged cache: every request owns ceil(max_tokens / PT) blocks, shuffled.
+        pages = (self.max_tokens + c.page_tokens - 1) // c.page_tokens
+        self.block_table = workloads.block_tables(batch, pages, seed + 5, device=device)
+        blocks = batch * pages
+        self.width = page_width(c.head_dim, c.schedule)
+        self.caches = [torch.zeros((2, blocks, c.heads, c.page_tokens, self.width), dtype=torch.uint8, device=device)
+                       for _ in range(c.layers)]
+
+        inv = 1.0 / (c.rope_theta ** (torch.arange(0, c.head_dim, 2, device=device, dtype=torch.float32) / c.head_dim))
+        angles = torch.arange(self.max_tokens, device=device, dtype=torch.float32)[:, None] * inv[None, :]
+        self.cos, self.sin = angles.cos(), angles.sin()
+
+        # Step state (static tensors for graph capture).
+        self.tokens = torch.randint(0, c.vocab, (batch,), generator=generator, device=device)
+        self.positions = torch.full((batch,), context, dtype=torch.int64, device=device)
+        self.seq_lens = torch.full((batch,), context + 1, dtype=torch.int32, device=device)
+        self.query_start_loc = torch.arange(batch + 1, dtype=torch.int32, device=device)
+        self.slots = torch.empty(batch, dtype=torch.int64, device=device)
+        self._update_slots()
+        self.attn_out = torch.empty((batch, c.heads, c.head_dim), dtype=torch.bfloat16, device=device)
+        self.residual = torch.empty((batch, c.hidden), dtype=torch.bfloat16, device=device)
+        self.staged = torch.empty((c.layers, c.loops, 2, batch, c.heads, c.head_dim), dtype=torch.bfloat16,
+                                  device=device)
+        self.workspace = torch.empty(ops.attention_workspace_bytes(batch, c.heads, c.head_dim, pages, c.page_tokens),
+                                     dtype=torch.uint8, device=device)
+        self.graph: Optional[torch.cuda.CUDAGraph] = None
+
+    # ------------------------------------------------------------ history
+
+    def build_history(self, seed: int = 0, chunk: int = 16384) -> None:
+        """Quantize synthetic K/V of tokens 0..context-1 into every layer's cache (the prefill stand-in)."""
+        c = self.config
+        if self.context == 0:
+            return
+        slots = workloads.history_slots(self.block_table, [self.context] * self.batch, c.page_tokens).to(self.device)
+        for layer in range(c.layers):
+            for start in range(0, slots.numel(), chunk):
+                part = slots[start:start + chunk]
+                pairs = workloads.loop_kv(part.numel(), c.heads, c.head_dim, c.loops, seed + 97 * layer + start,
+                                          device=self.device, anchor_index=c.anchor)
+                ops.quantize(pairs, self.caches[layer], part, self.key_rotation[layer], self.value_rotation[layer],
+                             None, c.schedule, "anchor", c.anchor, c.coefficient)
+
+    # ------------------------------------------------------------ the step
+
+    def _update_slots(self) -> None:
+        pt = self.config.page_tokens
+        page = torch.div(self.positions, pt, rounding_mode="floor")
+        block = self.block_table.long().gather(1, page[:, None])[:, 0]
+        self.slots.copy_(block * pt + self.positions % pt)
+
+    def step(self) -> torch.Tensor:
+        """One decode step for every request; returns the logits and advances the state in place."""
+        c = self.config
+        q_size = c.heads * c.head_dim
+        eps = c.rms_eps
+        h = self.embed[self.tokens]
+        for loop in range(c.loops):
+            for layer in range(c.layers):
+                norms = self.norms[layer]
+                # input_layernorm, ouro.py:148-152 (fused add from the second layer on).
+                if layer == 0:
+                    self.residual.copy_(h)
+                    x = step_ops.rms_norm(h, norms[0], eps)
+                else:
+                    x, _ = step_ops.rms_norm(h, norms[0], eps, residual=self.residual)
+                qkv = F.linear(x, self.qkv[layer])
+                key_stage, value_stage = self.staged[layer, loop, 0], self.staged[layer, loop, 1]
+                q, k = step_ops.rope_qkv(qkv, self.positions, self.cos, self.sin, c.heads, c.head_dim,
+                                         key_stage=key_stage, value_stage=value_stage)
+                ops.attention(q, k, value_stage, self.caches[layer], self.attn_out, self.query_start_loc,
+                              self.seq_lens, self.block_table, self.key_rotation[layer], self.value_rotation[layer],
+                              None, c.schedule, "anchor", c.anchor, loop, workspace=self.workspace)
+                # Loop group quantize at the anchor loop (install_model.py:40-52).
+                if loop == c.anchor:
+                    pairs = [(self.staged[layer, r, 0], self.staged[layer, r, 1]) for r in range(c.loops)]
+                    ops.quantize(pairs, self.caches[layer], self.slots, self.key_rotation[layer],
+                                 self.value_rotation[layer], None, c.schedule, "anchor", c.anchor, c.coefficient)
+                a = F.linear(self.attn_out.view(self.batch, q_size), self.o[layer])
+                a = step_ops.rms_norm(a, norms[1], eps)
+                x, _ = step_ops.rms_norm(a, norms[2], eps, residual=self.residual)
+                m = F.linear(step_ops.silu_mul(F.linear(x, self.gate_up[layer])), self.down[layer])
+                h = step_ops.rms_norm(m, norms[3], eps)
+            h, _ = step_ops.rms_norm(h, self.final_norm, eps, residual=self.residual)
+        logits = F.linear(h, self.lm_head)
+        # Greedy next token and the next position, slot and sequence length.
+        self.tokens.copy_(logits.argmax(dim=-1))
+        self.positions.add_(1)
+        self.seq_lens.add_(1)
+        self._update_slots()
+        return logits
+
+    def capture(self) -> torch.cuda.CUDAGraph:
+        """Capture one step as a HIP graph (the state tensors advance on every replay)."""
+        snapshot = (self.tokens.clone(), self.positions.clone(), self.seq_lens.clone(), self.slots.clone())
+        stream = torch.cuda.Stream(device=self.device)
+        stream.wait_stream(torch.cuda.current_stream(self.device))
+        with torch.cuda.stream(stream):
+            self.step()  # warm-up outside capture (allocator pools, library handles)
+        torch.cuda.current_stream(self.device).wait_stream(stream)
+        self._restore(snapshot)
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            self.logits = self.step()
+        self._restore(snapshot)
+        self.graph = graph
+        return graph
+
+    def _restore(self, snapshot) -> None:
+        for tensor, saved in zip((self.tokens, self.positions, self.seq_lens, self.slots), snapshot):
+            tensor.copy_(saved)
