@@ -7,7 +7,7 @@
 // against q' = (q . R_k) / sqrt(D); the live token is folded in at the merge;
 // the history value sum is inverse-rotated by R_v when given.
 //
-// Three launches per call, all with grids fixed by host shapes:
+// Two launches per call, both with grids fixed by host shapes:
 //   prepare  (rows x heads)          q' in log2 units, live score, group sums
 //                                    of q', q' as 16-bit integers split into
 //                                    four nibble planes for v_dot8_u32_u4;
@@ -17,8 +17,11 @@
 //                                    32-channel quarter; QK on integer dot8
 //                                    units, PV in FP32 registers, online
 //                                    softmax per wave, LDS merge of the waves;
-//   merge    (rows x heads)          log-sum-exp merge of the splits and the
-//                                    live token, V inverse rotation, BF16 out.
+//                                    the split that finishes last for its
+//                                    (row, head) does the log-sum-exp merge of
+//                                    the splits and the live token, the V
+//                                    inverse rotation and the BF16 output.
+// The BF16 baseline keeps a separate merge launch.
 #include "rq_device.h"
 #include "rq_kernels.h"
 
@@ -64,54 +67,92 @@ __device__ __forceinline__ float fp8_f32(uint32_t v) {
     return __builtin_amdgcn_cvt_f32_fp8((int)v, Sel);
 }
 
-__device__ __forceinline__ int find_request(const int32_t* qsl, int64_t requests, int64_t row) {
-    if (requests <= 0 || row < qsl[0] || row >= qsl[requests]) return -1;
-    int64_t lo = 0, hi = requests;
-    while (hi - lo > 1) {
-        const int64_t mid = (lo + hi) >> 1;
-        if (qsl[mid] <= row) lo = mid; else hi = mid;
-    }
-    return (int)lo;
-}
-
 // ------------------------------------------------------------------ prepare
 
+// Request of `row` for a 128-thread workgroup: the number of boundaries
+// qsl[1..requests] at or below the row (qsl is nondecreasing), -1 if the row
+// lies outside [qsl[0], qsl[requests]).  One round of parallel loads instead
+// of a dependent binary search.
+__device__ __forceinline__ int find_request_parallel(const int32_t* qsl, int64_t requests, int64_t row,
+                                                     int* lds_counts) {
+    const int c = threadIdx.x;
+    const int threads = blockDim.x;
+    int count = 0;
+    for (int64_t j = 1 + c; j <= requests; j += threads) count += qsl[j] <= row ? 1 : 0;
+#pragma unroll
+    for (int d = 32; d; d >>= 1) count += __shfl_xor(count, d);
+    if ((c & 63) == 0) lds_counts[c >> 6] = count;
+    __syncthreads();
+    if (requests <= 0 || row < qsl[0] || row >= qsl[requests]) return -1;
+    int total = 0;
+    for (int w = 0; w < threads / 64; ++w) total += lds_counts[w];
+    return total;
+}
+
+// The prepared query record of one (row, head), written to `record`
+// (kPrepFloats floats, global or LDS): [0] delta, [1] live score, [2] q'.mu_A,
+// [3..10] 16-channel and [11..14] 32-channel group sums of q', then q'
+// (FP32, log2 units) and its four nibble planes in the INT4 and INT2 word
+// orders (prepare.cuh:13-229).  Called by every thread of a workgroup of 128
+// or 256 threads (threads c >= D contribute nothing) after prepare_load and a
+// barrier; `rotation_lds` holds D * D halves.  Returns after a barrier with
+// `record` complete.
+// Loads of the prepare that do not depend on the request: q and the live key
+// of (row, head) into registers, R_k into LDS.  Issued before the request
+// lookup so both round trips overlap; the lookup's barrier publishes the LDS.
+struct PrepareInputs {
+    float q, k_live;
+};
+
 template <int D>
-__global__ __launch_bounds__(128) void prepare_kernel(AttentionParams p) {
-    const int64_t row = blockIdx.x;
-    const int head = blockIdx.y;
+__device__ __forceinline__ PrepareInputs prepare_load(const AttentionParams& p, int64_t row, int head,
+                                                      _Float16* rotation_lds) {
+    const int c = threadIdx.x;
+    const bool active = c < D;
+    PrepareInputs in;
+    in.q = active ? bf16_f32(p.query[row * p.query_stride + head * D + c]) : 0.f;
+    in.k_live = active ? bf16_f32(p.key[row * p.key_stride + head * D + c]) : 0.f;
+    if (p.key_rotation != nullptr) {
+        const uint4* src = reinterpret_cast<const uint4*>(p.key_rotation + (int64_t)head * D * D);
+        uint4* dst = reinterpret_cast<uint4*>(rotation_lds);
+        for (int i = c; i < D * D / 8; i += blockDim.x) dst[i] = src[i];
+    }
+    return in;
+}
+
+template <int D>
+__device__ __forceinline__ void prepare_record(const AttentionParams& p, int head, const PrepareInputs& in,
+                                               float* record, const _Float16* rotation_lds) {
+    __shared__ __attribute__((aligned(16))) float q_lds[128];
+    __shared__ float totals[4][kDecodeThreads / 64];
     const int c = threadIdx.x;
     const int lane = c & 63;
     const int wave = c >> 6;
-    __shared__ float q_lds[128];
-    __shared__ float totals[4][2];
-    __shared__ __attribute__((aligned(16))) _Float16 rotation_lds[D * D];
-
-    const int request = find_request(p.query_start_loc, p.requests, row);
-    if (head == 0 && c == 0) p.row_request[row] = request;
-    if (request < 0) return;
-
+    const int waves = blockDim.x >> 6;
     const bool active = c < D;
-    const float q = active ? bf16_f32(p.query[row * p.query_stride + head * D + c]) : 0.f;
-    q_lds[c] = q;
+    const float q = in.q, k_live = in.k_live;
+    if (c < 128) q_lds[c] = q;
     __syncthreads();
 
     float qr = q;
     if (p.key_rotation != nullptr) {
-        // Stage R_k of this head with 16-byte loads (32 KB at D = 128).
-        const uint4* src = reinterpret_cast<const uint4*>(p.key_rotation + (int64_t)head * D * D);
-        uint4* dst = reinterpret_cast<uint4*>(rotation_lds);
-        for (int i = c; i < D * D / 8; i += 128) dst[i] = src[i];
-        __syncthreads();
-        float acc = 0.f;
-        if (active)
-            for (int k = 0; k < D; ++k) acc = fmaf(q_lds[k], (float)rotation_lds[k * D + c], acc);
-        qr = acc;
+        // Four interleaved partial sums so the LDS reads pipeline.
+        float a[4] = {0.f, 0.f, 0.f, 0.f};
+        if (active) {
+#pragma unroll 8
+            for (int k = 0; k < D; k += 4) {
+                const float4 qv = *reinterpret_cast<const float4*>(q_lds + k);
+                a[0] = fmaf(qv.x, (float)rotation_lds[k * D + c], a[0]);
+                a[1] = fmaf(qv.y, (float)rotation_lds[(k + 1) * D + c], a[1]);
+                a[2] = fmaf(qv.z, (float)rotation_lds[(k + 2) * D + c], a[2]);
+                a[3] = fmaf(qv.w, (float)rotation_lds[(k + 3) * D + c], a[3]);
+            }
+        }
+        qr = (a[0] + a[1]) + (a[2] + a[3]);
     }
     const float scale = kLog2e / sqrtf((float)D);
     qr *= scale;
 
-    const float k_live = active ? bf16_f32(p.key[row * p.key_stride + head * D + c]) : 0.f;
     float parts[4];
     parts[0] = q * k_live;
     parts[1] = (active && p.key_mean_loop) ? qr * p.key_mean_loop[head * D + c] : 0.f;
@@ -137,22 +178,27 @@ __global__ __launch_bounds__(128) void prepare_kernel(AttentionParams p) {
     const float q32 = q16 + __shfl_xor(q16, 16);
     __syncthreads();
 
-    const float amax = fmaxf(totals[3][0], totals[3][1]);
-    const float delta = amax > 0.f ? amax / 32767.0f : 1.0f;
-    float* prep = p.prep + (row * p.heads + head) * (int64_t)kPrepFloats;
-    if (c == 0) {
-        prep[0] = delta;
-        prep[1] = scale * (totals[0][0] + totals[0][1]) - (totals[1][0] + totals[1][1]);
-        prep[2] = totals[2][0] + totals[2][1];
+    float sums[4] = {0.f, 0.f, 0.f, 0.f};
+    for (int w = 0; w < waves; ++w) {
+        sums[0] += totals[0][w];
+        sums[1] += totals[1][w];
+        sums[2] += totals[2][w];
+        sums[3] = fmaxf(sums[3], totals[3][w]);
     }
-    if (active && (c & 15) == 0) prep[3 + c / 16] = q16;
-    if (active && (c & 31) == 0) prep[11 + c / 32] = q32;
-    prep[kPrepScalars + c] = active ? qr : 0.f;
+    const float delta = sums[3] > 0.f ? sums[3] / 32767.0f : 1.0f;
+    if (c == 0) {
+        record[0] = delta;
+        record[1] = scale * sums[0] - sums[1];
+        record[2] = sums[2];
+    }
+    if (active && (c & 15) == 0) record[3 + c / 16] = q16;
+    if (active && (c & 31) == 0) record[11 + c / 32] = q32;
+    if (c < kPrepQuery) record[kPrepScalars + c] = active ? qr : 0.f;
 
     // 16-bit offset-binary integer of q', four nibble planes.
     const float scaled = fminf(fmaxf(rintf(qr / delta), -32767.f), 32767.f);
     const uint32_t qu = active ? (uint32_t)((int)scaled + 32768) : 32768u;
-    uint32_t* planes4 = reinterpret_cast<uint32_t*>(prep + kPrepScalars + kPrepQuery);
+    uint32_t* planes4 = reinterpret_cast<uint32_t*>(record + kPrepScalars + kPrepQuery);
     uint32_t* planes2 = planes4 + kPrepPlanes;
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
@@ -171,6 +217,24 @@ __global__ __launch_bounds__(128) void prepare_kernel(AttentionParams p) {
         if (active && (c & 7) == 0) planes4[j * 16 + c / 8] = w4;
         if (active && (c & 14) == 0) planes2[j * 16 + 2 * (c / 16) + (c & 1)] = w2;
     }
+    __syncthreads();
+}
+
+// Separate prepare pass (used when a (row, head) is split over several
+// workgroups, and by the BF16 baseline): one 128-thread workgroup per (row, head).
+template <int D>
+__global__ __launch_bounds__(128) void prepare_kernel(AttentionParams p) {
+    __shared__ int request_counts[2];
+    __shared__ __attribute__((aligned(16))) _Float16 rotation_lds[D * D];
+    const int64_t row = blockIdx.x;
+    const int head = blockIdx.y;
+    const int64_t rh = row * p.heads + head;
+    if (threadIdx.x == 0) p.arrivals[rh] = 0;
+    const PrepareInputs in = prepare_load<D>(p, row, head, rotation_lds);
+    const int request = find_request_parallel(p.query_start_loc, p.requests, row, request_counts);
+    if (head == 0 && threadIdx.x == 0) p.row_request[row] = request;
+    if (request < 0) return;
+    prepare_record<D>(p, head, in, p.prep + rh * (int64_t)kPrepFloats, rotation_lds);
 }
 
 // ------------------------------------------------------------------ packed decode
@@ -342,11 +406,17 @@ __device__ __forceinline__ void group_sums(const float* prep, int qd, float (&q_
 
 constexpr int kReduceBytes = kWaves * 16 * 128 * (int)sizeof(float);
 
-// Writes (m, l, acc[D]) of this split after merging the four waves in LDS.
+// The four waves' (m, l, acc) of one split merged in LDS: thread c < D gets
+// channel c of the unnormalized output; every thread gets m and l.
+struct SplitResult {
+    float sum, m, l;
+};
+
 template <int D>
-__device__ __forceinline__ void write_partial(float (&acc)[32], float m, float l_lane, int lane,
-                                              int wave, bool lane_active, float* partial) {
-    __shared__ __attribute__((aligned(16))) float red_acc[kWaves][16][128];
+__device__ __forceinline__ SplitResult merge_waves(float (&acc)[32], float m, float l_lane, int lane, int wave,
+                                                   bool lane_active, float* lds) {
+    // lds: kWaves * 16 * 128 floats, [wave][token][channel].
+    float (*red_acc)[16][128] = reinterpret_cast<float (*)[16][128]>(lds);
     __shared__ float red_m[kWaves], red_l[kWaves];
     const int t = lane >> 2, qd = lane & 3;
     const float l_wave = token_sum((lane_active && qd == 0) ? l_lane : 0.f);
@@ -370,23 +440,87 @@ __device__ __forceinline__ void write_partial(float (&acc)[32], float m, float l
         *reinterpret_cast<float4*>(dst + i) = v;
     }
     __syncthreads();
+    SplitResult r;
+    r.m = m_all;
+    r.l = 0.f;
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) r.l += red_m[w] == -INFINITY ? 0.f : red_l[w] * exp2f(red_m[w] - m_all);
+    r.sum = 0.f;
     const int c = threadIdx.x;
     if (c < D) {
-        float sum = 0.f;
 #pragma unroll
         for (int w = 0; w < kWaves; ++w)
 #pragma unroll
-            for (int tt = 0; tt < 16; ++tt) sum += red_acc[w][tt][c];
-        partial[2 + c] = sum;
+            for (int tt = 0; tt < 16; ++tt) r.sum += red_acc[w][tt][c];
     }
+    return r;
+}
+
+// Writes (m, l, acc[D]) of this split for the merge.
+template <int D>
+__device__ __forceinline__ void write_partial(float (&acc)[32], float m, float l_lane, int lane,
+                                              int wave, bool lane_active, float* partial, float* lds) {
+    const SplitResult r = merge_waves<D>(acc, m, l_lane, lane, wave, lane_active, lds);
+    const int c = threadIdx.x;
+    if (c < D) partial[2 + c] = r.sum;
     if (c == 0) {
-        float l_all = 0.f;
-#pragma unroll
-        for (int w = 0; w < kWaves; ++w)
-            l_all += red_m[w] == -INFINITY ? 0.f : red_l[w] * exp2f(red_m[w] - m_all);
-        partial[0] = m_all;
-        partial[1] = l_all;
+        partial[0] = r.m;
+        partial[1] = r.l;
     }
+}
+
+// One split covers the whole history of this (row, head): merge the waves,
+// fold in the live token, inverse-rotate V and write the BF16 output without
+// a round trip through the partials.  R_v row c, the live score and the live
+// value are loaded before the wave merge so their latency overlaps it.
+template <int D>
+__device__ __forceinline__ void finish_single(const AttentionParams& p, int64_t row, int head, float (&acc)[32],
+                                              float m, float l_lane, int lane, int wave, bool lane_active,
+                                              float live, float* lds) {
+    __shared__ float hist[128];
+    __shared__ float halves[2][128];
+    const int tid = threadIdx.x;
+    const int c = tid & 127, part = tid >> 7;
+    const bool rotate = p.value_rotation != nullptr;
+    uint4 rv[D / 16];
+    if (rotate && c < D) {
+        const uint4* r = reinterpret_cast<const uint4*>(p.value_rotation + ((int64_t)head * D + c) * D + part * (D / 2));
+#pragma unroll
+        for (int i = 0; i < D / 16; ++i) rv[i] = r[i];
+    }
+    const float v_live = tid < D ? bf16_f32(p.value[row * p.value_stride + head * D + tid]) : 0.f;
+
+    const SplitResult r = merge_waves<D>(acc, m, l_lane, lane, wave, lane_active, lds);
+    const float mx = fmaxf(r.m, live);
+    const float w_hist = r.m == -INFINITY ? 0.f : exp2f(r.m - mx);
+    const float w_live = exp2f(live - mx);
+    const float inv = 1.0f / fmaf(w_hist, r.l, w_live);
+    if (tid < 128) hist[c] = c < D ? r.sum * (w_hist * inv) : 0.f;
+    __syncthreads();
+    float o = 0.f;
+    if (c < D) {
+        if (rotate) {
+            float a[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int i = 0; i < D / 16; ++i) {
+                const float* hk = hist + part * (D / 2) + 8 * i;
+                const uint32_t w[4] = {rv[i].x, rv[i].y, rv[i].z, rv[i].w};
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    a[j] = fmaf(hk[2 * j], f16_f32((uint16_t)(w[j] & 0xffffu)), a[j]);
+                    a[j] = fmaf(hk[2 * j + 1], f16_f32((uint16_t)(w[j] >> 16)), a[j]);
+                }
+            }
+            o = (a[0] + a[1]) + (a[2] + a[3]);
+        } else if (part == 0) {
+            o = hist[c];
+        }
+    }
+    halves[part][c] = o;
+    __syncthreads();
+    if (tid < D)
+        p.output[row * p.output_stride + head * D + tid] =
+            (uint16_t)bf16_rn(fmaf(w_live * inv, v_live, halves[0][tid] + halves[1][tid]));
 }
 
 // Page range of one split (in 16-token units) for the request of `row`.
@@ -395,9 +529,9 @@ struct SplitRange {
     int64_t history, unit_begin, unit_end;
 };
 
-__device__ __forceinline__ SplitRange split_range(const AttentionParams& p, int64_t row, int split) {
+__device__ __forceinline__ SplitRange split_range(const AttentionParams& p, int request, int split) {
     SplitRange r;
-    r.request = p.row_request[row];
+    r.request = request;
     r.history = 0;
     r.unit_begin = r.unit_end = 0;
     if (r.request < 0) return r;
@@ -488,6 +622,119 @@ struct Unit {
     uint32_t alpha_k_bits, alpha_v_bits;
 };
 
+// ------------------------------------------------------------------ merge
+
+constexpr int kMergeThreads = 256;
+
+// Log-sum-exp merge of the splits of one (row, head) and the live token, the
+// inverse V rotation, and the BF16 output, by a 256-thread workgroup
+// (merge.cuh:8-84, output.cuh:9-31, rotation.cuh:10-84).  `lds` holds at
+// least kMergeLdsFloats floats; the caller has made every split's partial
+// visible to this workgroup.
+constexpr int kMergeLdsFloats = kMaxSplits + 4 + 128 + 2 * 128;
+
+template <int D>
+__device__ __forceinline__ void merge_output(const AttentionParams& p, int64_t row, int head, float* lds) {
+    const int tid = threadIdx.x;
+    const int64_t rh = row * p.heads + head;
+    float* weights = lds;                    // [kMaxSplits]
+    float* totals = lds + kMaxSplits;        // [2]: live weight, 1 / denominator
+    float* hist = totals + 4;                // [128]
+    float* halves = hist + 128;              // [2][128]
+    const float* parts = p.partials + rh * p.splits * (int64_t)(D + 2);
+    if (tid < 64) {
+        // One lane per split (splits <= 64).
+        const float live = p.prep[rh * kPrepFloats + 1];
+        const bool has = tid < p.splits;
+        const float ms = has ? parts[tid * (D + 2)] : -INFINITY;
+        const float ls = has ? parts[tid * (D + 2) + 1] : 0.f;
+        float m = fmaxf(ms, live);
+#pragma unroll
+        for (int d = 32; d; d >>= 1) m = fmaxf(m, __shfl_xor(m, d));
+        const float w = ms == -INFINITY ? 0.f : exp2f(ms - m);
+        float denominator = w * ls;
+#pragma unroll
+        for (int d = 32; d; d >>= 1) denominator += __shfl_xor(denominator, d);
+        const float live_weight = exp2f(live - m);
+        denominator += live_weight;
+        if (has) weights[tid] = w;
+        if (tid == 0) {
+            totals[0] = live_weight / denominator;
+            totals[1] = 1.0f / denominator;
+        }
+    }
+    __syncthreads();
+    // History sum: channel c, splits interleaved over the two thread halves.
+    const int c = tid & 127, part = tid >> 7;
+    float h = 0.f;
+    if (c < D) {
+#pragma unroll 4
+        for (int s = part; s < p.splits; s += 2) h = fmaf(weights[s], parts[s * (D + 2) + 2 + c], h);
+    }
+    halves[part * 128 + c] = h;
+    __syncthreads();
+    if (tid < 128) hist[c] = c < D ? (halves[c] + halves[128 + c]) * totals[1] : 0.f;
+    __syncthreads();
+    // out[c] = sum_k hist[k] R_v[c][k]: half `part` of the k range per thread,
+    // R_v row c read straight from global memory (L2) as 16-byte vectors.
+    float o = 0.f;
+    if (c < D) {
+        if (p.value_rotation != nullptr) {
+            const uint4* r = reinterpret_cast<const uint4*>(p.value_rotation + ((int64_t)head * D + c) * D +
+                                                            part * (D / 2));
+            float a[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int i = 0; i < D / 16; ++i) {
+                const uint4 v = r[i];
+                const float* hk = hist + part * (D / 2) + 8 * i;
+                const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    a[j] = fmaf(hk[2 * j], f16_f32((uint16_t)(w[j] & 0xffffu)), a[j]);
+                    a[j] = fmaf(hk[2 * j + 1], f16_f32((uint16_t)(w[j] >> 16)), a[j]);
+                }
+            }
+            o = (a[0] + a[1]) + (a[2] + a[3]);
+        } else if (part == 0) {
+            o = hist[c];
+        }
+    }
+    __syncthreads();
+    halves[part * 128 + c] = o;
+    __syncthreads();
+    if (tid < D) {
+        const float v = bf16_f32(p.value[row * p.value_stride + head * D + tid]);
+        p.output[row * p.output_stride + head * D + tid] =
+            (uint16_t)bf16_rn(fmaf(totals[0], v, halves[tid] + halves[128 + tid]));
+    }
+}
+
+// Separate merge pass (used by the BF16 baseline): one workgroup per (row, head).
+template <int D>
+__global__ __launch_bounds__(kMergeThreads) void merge_kernel(AttentionParams p) {
+    __shared__ float lds[kMergeLdsFloats];
+    const int64_t row = blockIdx.x;
+    if (p.row_request[row] < 0) return;
+    merge_output<D>(p, row, blockIdx.y, lds);
+}
+
+// The split that finishes last for its (row, head) merges: every split
+// publishes its partial, then counts itself in `arrivals` (zeroed by prepare);
+// the one that sees splits - 1 earlier arrivals reads them all.  Nothing
+// waits, so no workgroup depends on another being scheduled.
+template <int D>
+__device__ __forceinline__ void finish_split(const AttentionParams& p, int64_t row, int head) {
+    __shared__ float lds[kMergeLdsFloats];
+    __shared__ int last;
+    __threadfence();
+    __syncthreads();
+    if (threadIdx.x == 0) last = atomicAdd(&p.arrivals[row * p.heads + head], 1) == p.splits - 1;
+    __syncthreads();
+    if (!last) return;
+    __threadfence();
+    merge_output<D>(p, row, head, lds);
+}
+
 #ifndef RQ_DECODE_MIN_WAVES
 #define RQ_DECODE_MIN_WAVES 1
 #endif
@@ -511,12 +758,31 @@ void decode_kernel(AttentionParams p) {
     const int64_t row = rh / p.heads;
     // Nibble planes of q' per quarter: [quarter][anchor words 0..3 | loop words 0..3][plane]
     __shared__ __attribute__((aligned(16))) uint32_t planes_lds[4][8][4];
+    __shared__ __attribute__((aligned(16))) float prep_lds[kPrepFloats];
+    // R_k staging of the fused prepare, then the wave merge at the end.
+    __shared__ __attribute__((aligned(16))) float scratch_lds[kWaves * 16 * 128];
+    __shared__ int request_counts[kWaves];
 
-    const SplitRange range = split_range(p, row, split);
-    if (range.request < 0) return;
+    // With one split per (row, head) this workgroup prepares its own query;
+    // otherwise prepare_kernel has written the record.
+    int request;
+    if (p.fused_prepare) {
+        _Float16* rotation_lds = reinterpret_cast<_Float16*>(scratch_lds);
+        const PrepareInputs in = prepare_load<D>(p, row, head, rotation_lds);
+        request = find_request_parallel(p.query_start_loc, p.requests, row, request_counts);
+        if (request < 0) return;
+        prepare_record<D>(p, head, in, prep_lds, rotation_lds);
+    } else {
+        request = p.row_request[row];
+        if (request < 0) return;
+        const float* src = p.prep + rh * (int64_t)kPrepFloats;
+        for (int i = threadIdx.x; i < kPrepFloats; i += kDecodeThreads) prep_lds[i] = src[i];
+        __syncthreads();
+    }
+    const SplitRange range = split_range(p, request, split);
     float* partial = p.partials + (rh * p.splits + split) * (int64_t)(D + 2);
 
-    const float* prep = p.prep + rh * (int64_t)kPrepFloats;
+    const float* prep = prep_lds;
     if (threadIdx.x < 128) {
         // thread -> (quarter, record, word, plane); prep stores [plane][word] per order
         const int quarter = threadIdx.x >> 5, record = (threadIdx.x >> 4) & 1;
@@ -662,7 +928,12 @@ void decode_kernel(AttentionParams p) {
         acc[i] += cst0;
         acc[16 + i] += cst1;
     }
-    write_partial<D>(acc, m, l, lane, wave, lane_active, partial);
+    if (p.splits == 1) {
+        finish_single<D>(p, row, head, acc, m, l, lane, wave, lane_active, prep_lds[1], scratch_lds);
+    } else {
+        write_partial<D>(acc, m, l, lane, wave, lane_active, partial, scratch_lds);
+        finish_split<D>(p, row, head);
+    }
 }
 
 // ------------------------------------------------------------------ BF16 baseline decode
@@ -681,7 +952,7 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_bf16_kernel(AttentionPa
     const int head = (int)(rh % p.heads);
     const int64_t row = rh / p.heads;
 
-    const SplitRange range = split_range(p, row, split);
+    const SplitRange range = split_range(p, p.row_request[row], split);
     if (range.request < 0) return;
     float* partial = p.partials + (rh * p.splits + split) * (int64_t)(D + 2);
     const float* prep = p.prep + rh * (int64_t)kPrepFloats;
@@ -748,70 +1019,8 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_bf16_kernel(AttentionPa
             }
         }
     }
-    write_partial<D>(acc, m, l, lane, wave, lane_active, partial);
-}
-
-// ------------------------------------------------------------------ merge
-
-template <int D>
-__global__ __launch_bounds__(128) void merge_kernel(AttentionParams p) {
-    const int64_t row = blockIdx.x;
-    const int head = blockIdx.y;
-    const int c = threadIdx.x;
-    __shared__ float weights[kMaxSplits];
-    __shared__ float totals[2];
-    __shared__ float history[128];
-    // R_v rows padded by two halves so that lanes reading row c hit distinct banks.
-    constexpr int Stride = D + 2;
-    __shared__ __attribute__((aligned(16))) _Float16 rotation_lds[D * Stride];
-    const int request = p.row_request[row];
-    if (request < 0) return;
-    const int64_t rh = row * p.heads + head;
-    const float live = p.prep[rh * kPrepFloats + 1];
-    const float* parts = p.partials + rh * p.splits * (int64_t)(D + 2);
-    if (c == 0) {
-        float m = live;
-        for (int s = 0; s < p.splits; ++s) m = fmaxf(m, parts[s * (D + 2)]);
-        const float live_weight = exp2f(live - m);
-        float denominator = live_weight;
-        for (int s = 0; s < p.splits; ++s) {
-            const float ms = parts[s * (D + 2)];
-            const float w = ms == -INFINITY ? 0.f : exp2f(ms - m);
-            weights[s] = w;
-            denominator = fmaf(w, parts[s * (D + 2) + 1], denominator);
-        }
-        totals[0] = live_weight / denominator;
-        totals[1] = 1.0f / denominator;
-    }
-    __syncthreads();
-    float h = 0.f;
-    if (c < D) {
-        for (int s = 0; s < p.splits; ++s) h = fmaf(weights[s], parts[s * (D + 2) + 2 + c], h);
-        h *= totals[1];
-    }
-    if (p.value_rotation != nullptr) {
-        history[c] = h;
-        const uint4* src = reinterpret_cast<const uint4*>(p.value_rotation + (int64_t)head * D * D);
-        for (int i = c; i < D * D / 8; i += 128) {
-            const uint4 v = src[i];
-            uint32_t* dst = reinterpret_cast<uint32_t*>(rotation_lds + (i / (D / 8)) * Stride + (i % (D / 8)) * 8);
-            dst[0] = v.x;
-            dst[1] = v.y;
-            dst[2] = v.z;
-            dst[3] = v.w;
-        }
-        __syncthreads();
-        if (c < D) {
-            const _Float16* r = rotation_lds + c * Stride;
-            float acc = 0.f;
-            for (int k = 0; k < D; ++k) acc = fmaf(history[k], (float)r[k], acc);
-            h = acc;
-        }
-    }
-    if (c < D) {
-        const float v = bf16_f32(p.value[row * p.value_stride + head * D + c]);
-        p.output[row * p.output_stride + head * D + c] = (uint16_t)bf16_rn(fmaf(totals[0], v, h));
-    }
+    __shared__ __attribute__((aligned(16))) float scratch_lds[kWaves * 16 * 128];
+    write_partial<D>(acc, m, l, lane, wave, lane_active, partial, scratch_lds);
 }
 
 // ------------------------------------------------------------------ launch
@@ -858,8 +1067,9 @@ bool dispatch_anchor(const AttentionParams& p, hipStream_t stream) {
 template <int D>
 hipError_t launch_all(const AttentionParams& p, hipStream_t stream, hipEvent_t begin, hipEvent_t end,
                       bool bf16) {
-    hipLaunchKernelGGL((prepare_kernel<D>), dim3((unsigned)p.rows, (unsigned)p.heads), dim3(128), 0,
-                       stream, p);
+    if (bf16 || !p.fused_prepare)
+        hipLaunchKernelGGL((prepare_kernel<D>), dim3((unsigned)p.rows, (unsigned)p.heads), dim3(128), 0,
+                           stream, p);
     if (begin) (void)hipEventRecord(begin, stream);
     if (bf16) {
         const unsigned blocks = (unsigned)(p.rows * p.heads * p.splits);
@@ -868,8 +1078,9 @@ hipError_t launch_all(const AttentionParams& p, hipStream_t stream, hipEvent_t b
         return hipErrorInvalidValue;
     }
     if (end) (void)hipEventRecord(end, stream);
-    hipLaunchKernelGGL((merge_kernel<D>), dim3((unsigned)p.rows, (unsigned)p.heads), dim3(128), 0,
-                       stream, p);
+    if (bf16)
+        hipLaunchKernelGGL((merge_kernel<D>), dim3((unsigned)p.rows, (unsigned)p.heads), dim3(kMergeThreads), 0,
+                           stream, p);
     return hipGetLastError();
 }
 

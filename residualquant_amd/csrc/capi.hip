@@ -124,13 +124,14 @@ int split_count(int64_t rows, int heads, int64_t max_pages) {
 size_t align256(size_t bytes) { return (bytes + 255) & ~size_t(255); }
 
 struct WorkspaceLayout {
-    size_t row_request, prep, partials, total;
+    size_t row_request, arrivals, prep, partials, total;
 };
 
 WorkspaceLayout workspace_layout(int64_t rows, int heads, int head_dim, int splits) {
     WorkspaceLayout w;
     w.row_request = 0;
-    w.prep = align256(sizeof(int32_t) * (size_t)rows);
+    w.arrivals = align256(sizeof(int32_t) * (size_t)rows);
+    w.prep = w.arrivals + align256(sizeof(int32_t) * (size_t)rows * heads);
     w.partials = w.prep + align256(sizeof(float) * (size_t)rows * heads * rq::kPrepFloats);
     w.total = w.partials + align256(sizeof(float) * (size_t)rows * heads * splits * (head_dim + 2));
     return w;
@@ -306,6 +307,7 @@ static int attention_common(const void* query, int64_t query_stride, const void*
     p->block_table_stride = block_table_stride;
     p->max_pages = max_pages;
     p->row_request = reinterpret_cast<int32_t*>(ws + layout.row_request);
+    p->arrivals = reinterpret_cast<int32_t*>(ws + layout.arrivals);
     p->prep = reinterpret_cast<float*>(ws + layout.prep);
     p->partials = reinterpret_cast<float*>(ws + layout.partials);
     p->splits = splits;
@@ -332,6 +334,8 @@ int rq_attention(const void* query, int64_t query_stride, const void* key, int64
                     "16-byte aligned contiguous FP32 key mean with matching dimensions required");
     if (key_rotation != nullptr && (reinterpret_cast<uintptr_t>(key_rotation) % 16) != 0)
         return fail(RQ_EINVAL, "16-byte aligned key rotation required for asynchronous copies");
+    if (value_rotation != nullptr && (reinterpret_cast<uintptr_t>(value_rotation) % 16) != 0)
+        return fail(RQ_EINVAL, "16-byte aligned value rotation required");
     const int width = rq_page_width(head_dim, records, bits, groups);
     if (width != page_width) return fail(RQ_EINVAL, "Packed cache width differs from records");
     const bool adjacent = records > 1 && reference_mode == RQ_MODE_ADJACENT;
@@ -361,6 +365,7 @@ int rq_attention(const void* query, int64_t query_stride, const void* key, int64
     p.residual = regions[loop_index];
     p.key_mean_loop = key_mean ? key_mean + (int64_t)loop_index * heads * head_dim : nullptr;
     p.key_mean_anchor = (key_mean && p.has_residual) ? key_mean + (int64_t)anchor * heads * head_dim : nullptr;
+    p.fused_prepare = p.splits == 1 ? 1 : 0;
     hipEvent_t begin, end;
     timing_events(stream, &begin, &end);
     return check_launch(rq::launch_attention(p, stream, begin, end), "attention launch");

@@ -164,9 +164,11 @@ struct AttentionParams {
     RecordRegion residual;
     int has_residual;
     int32_t* row_request;  // workspace [rows]
+    int32_t* arrivals;     // workspace [rows, heads]: finished splits (zeroed by prepare)
     float* prep;           // workspace [rows, heads, kPrepFloats]
     float* partials;       // workspace [rows, heads, splits, D + 2]
     int splits;
+    int fused_prepare;     // 1: each decode workgroup prepares its own query (requires splits == 1)
 };
 
 hipError_t launch_attention(const AttentionParams& p, hipStream_t stream, hipEvent_t begin,
