@@ -593,7 +593,7 @@ def run_decode(args):
             "workload": "C2 paged decode attention, Ouro-1.4B-shaped layer",
             "batch": batch, "history_tokens": history, "heads": heads, "head_dim": dim, "loops": 4,
             "page_tokens": page_tokens, "schedule": "[2,32]x3+[4,32] anchor 3 ls",
-            "step": "3 residual-loop calls + 1 anchor-loop call (prepare + split-K decode + merge each)",
+            "step": "3 residual-loop calls + 1 anchor-loop call (one split-K decode launch each: query preparation, page streaming, live-token merge, V inverse rotation)",
         },
         "us_per_step": step_s * 1e6,
         "us_per_step_eager": eager_s * 1e6,
