@@ -462,10 +462,11 @@ __device__ __forceinline__ void write_partial(float (&acc)[32], float m, float l
                                               int wave, bool lane_active, float* partial, float* lds) {
     const SplitResult r = merge_waves<D>(acc, m, l_lane, lane, wave, lane_active, lds);
     const int c = threadIdx.x;
-    if (c < D) partial[2 + c] = r.sum;
+    const __amdgpu_buffer_rsrc_t out = handoff_resource(partial, (D + 2) * 4);
+    if (c < D) handoff_store(out, 8 + 4 * c, r.sum);
     if (c == 0) {
-        partial[0] = r.m;
-        partial[1] = r.l;
+        handoff_store(out, 0, r.m);
+        handoff_store(out, 4, r.l);
     }
 }
 
@@ -631,7 +632,7 @@ constexpr int kMergeThreads = 256;
 // (merge.cuh:8-84, output.cuh:9-31, rotation.cuh:10-84).  `lds` holds at
 // least kMergeLdsFloats floats; the caller has made every split's partial
 // visible to this workgroup.
-constexpr int kMergeLdsFloats = kMaxSplits + 4 + 128 + 2 * 128;
+constexpr int kMergeLdsFloats = kMaxSplits + 4 + 128 + 4 * 128;
 
 template <int D>
 __device__ __forceinline__ void merge_output(const AttentionParams& p, int64_t row, int head, float* lds) {
@@ -640,19 +641,21 @@ __device__ __forceinline__ void merge_output(const AttentionParams& p, int64_t r
     float* weights = lds;                    // [kMaxSplits]
     float* totals = lds + kMaxSplits;        // [2]: live weight, 1 / denominator
     float* hist = totals + 4;                // [128]
-    float* halves = hist + 128;              // [2][128]
-    const float* parts = p.partials + rh * p.splits * (int64_t)(D + 2);
+    float* halves = hist + 128;              // [4][128]
+    // Partials [split][D + 2] of this (row, head), read with coherent loads.
+    constexpr uint32_t kSplitBytes = (D + 2) * 4;
+    const __amdgpu_buffer_rsrc_t parts =
+        handoff_resource(p.partials + rh * p.splits * (int64_t)(D + 2), (uint32_t)(p.splits * kSplitBytes));
     if (tid < 64) {
-        // One lane per split (splits <= 64).
+        // One lane per split (splits <= 64): (m, l) of split tid.
         const float live = p.prep[rh * kPrepFloats + 1];
         const bool has = tid < p.splits;
-        const float ms = has ? parts[tid * (D + 2)] : -INFINITY;
-        const float ls = has ? parts[tid * (D + 2) + 1] : 0.f;
-        float m = fmaxf(ms, live);
+        const float2 ml = has ? handoff_load2(parts, tid * kSplitBytes) : make_float2(-INFINITY, 0.f);
+        float m = fmaxf(ml.x, live);
 #pragma unroll
         for (int d = 32; d; d >>= 1) m = fmaxf(m, __shfl_xor(m, d));
-        const float w = ms == -INFINITY ? 0.f : exp2f(ms - m);
-        float denominator = w * ls;
+        const float w = ml.x == -INFINITY ? 0.f : exp2f(ml.x - m);
+        float denominator = w * ml.y;
 #pragma unroll
         for (int d = 32; d; d >>= 1) denominator += __shfl_xor(denominator, d);
         const float live_weight = exp2f(live - m);
@@ -664,16 +667,26 @@ __device__ __forceinline__ void merge_output(const AttentionParams& p, int64_t r
         }
     }
     __syncthreads();
-    // History sum: channel c, splits interleaved over the two thread halves.
-    const int c = tid & 127, part = tid >> 7;
-    float h = 0.f;
-    if (c < D) {
-#pragma unroll 4
-        for (int s = part; s < p.splits; s += 2) h = fmaf(weights[s], parts[s * (D + 2) + 2 + c], h);
+    // History sum: thread = (channel pair, split group of four); every load of
+    // a thread is independent, so they are all in flight together.
+    {
+        const int pair = tid & 63, group = tid >> 6;
+        float2 h = make_float2(0.f, 0.f);
+        if (2 * pair < D) {
+#pragma unroll 8
+            for (int s = group; s < p.splits; s += 4) {
+                const float2 v = handoff_load2(parts, s * kSplitBytes + 8 + 8 * pair);
+                h.x = fmaf(weights[s], v.x, h.x);
+                h.y = fmaf(weights[s], v.y, h.y);
+            }
+        }
+        halves[group * 128 + 2 * pair] = h.x;
+        halves[group * 128 + 2 * pair + 1] = h.y;
     }
-    halves[part * 128 + c] = h;
     __syncthreads();
-    if (tid < 128) hist[c] = c < D ? (halves[c] + halves[128 + c]) * totals[1] : 0.f;
+    const int c = tid & 127, part = tid >> 7;
+    if (tid < 128)
+        hist[c] = c < D ? (((halves[c] + halves[128 + c]) + halves[256 + c]) + halves[384 + c]) * totals[1] : 0.f;
     __syncthreads();
     // out[c] = sum_k hist[k] R_v[c][k]: half `part` of the k range per thread,
     // R_v row c read straight from global memory (L2) as 16-byte vectors.
@@ -726,12 +739,7 @@ template <int D>
 __device__ __forceinline__ void finish_split(const AttentionParams& p, int64_t row, int head) {
     __shared__ float lds[kMergeLdsFloats];
     __shared__ int last;
-    __threadfence();
-    __syncthreads();
-    if (threadIdx.x == 0) last = atomicAdd(&p.arrivals[row * p.heads + head], 1) == p.splits - 1;
-    __syncthreads();
-    if (!last) return;
-    __threadfence();
+    if (!arrive_last(&p.arrivals[row * p.heads + head], p.splits, &last)) return;
     merge_output<D>(p, row, head, lds);
 }
 

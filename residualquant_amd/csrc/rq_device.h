@@ -97,6 +97,62 @@ __device__ __forceinline__ float max_z(float a, float b) {
     return (a > b || (a == b && !(__float_as_uint(a) >> 31))) ? a : b;
 }
 
+// ------------------------------------------------------------------ cross-workgroup hand-off
+//
+// A workgroup that hands data to another workgroup of the same launch (the
+// last-arriving split reads every split's partial) writes and reads it with
+// buffer stores and loads carrying the sc1 cache policy, which are coherent
+// across the XCDs' L2 caches (what agent-scope atomic loads and stores
+// compile to on gfx950), instead of an agent-scope fence (__threadfence: a
+// whole-L2 write-back and invalidate per workgroup).  Plain buffer
+// operations, unlike atomics, let the compiler keep many loads in flight.
+// The writer waits for its stores to be acknowledged (vmcnt counts stores on
+// gfx9) before the workgroup barrier and the arrival atomic; the reader
+// issues its loads after observing the final arrival.
+
+constexpr int kCoherentPolicy = 16;  // cache-policy operand: sc1
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t handoff_resource(const void* base, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
+}
+
+__device__ __forceinline__ void handoff_store(__amdgpu_buffer_rsrc_t r, uint32_t byte_offset, float v) {
+    __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(v), r, byte_offset, 0, kCoherentPolicy);
+}
+
+__device__ __forceinline__ void handoff_store4(__amdgpu_buffer_rsrc_t r, uint32_t byte_offset, float a, float b,
+                                               float c, float d) {
+    typedef uint32_t U32x4 __attribute__((ext_vector_type(4)));
+    const U32x4 v = {__float_as_uint(a), __float_as_uint(b), __float_as_uint(c), __float_as_uint(d)};
+    __builtin_amdgcn_raw_buffer_store_b128(v, r, byte_offset, 0, kCoherentPolicy);
+}
+
+__device__ __forceinline__ float2 handoff_load2(__amdgpu_buffer_rsrc_t r, uint32_t byte_offset) {
+    const auto v = __builtin_amdgcn_raw_buffer_load_b64(r, byte_offset, 0, kCoherentPolicy);
+    return make_float2(__uint_as_float(v[0]), __uint_as_float(v[1]));
+}
+
+__device__ __forceinline__ float4 handoff_load4(__amdgpu_buffer_rsrc_t r, uint32_t byte_offset) {
+    const auto v = __builtin_amdgcn_raw_buffer_load_b128(r, byte_offset, 0, kCoherentPolicy);
+    return make_float4(__uint_as_float(v[0]), __uint_as_float(v[1]), __uint_as_float(v[2]), __uint_as_float(v[3]));
+}
+
+// s_waitcnt vmcnt(0) expcnt(7) lgkmcnt(15): only outstanding vector memory
+// operations (loads and stores) are waited for.
+__device__ __forceinline__ void wait_vector_memory() { __builtin_amdgcn_s_waitcnt(0xF70); }
+
+// Counts this workgroup's arrival at `counter` (after every thread's shared
+// stores) and returns true in every thread of the workgroup that arrives last
+// of `expected`.  Nothing waits for other workgroups.
+__device__ __forceinline__ bool arrive_last(int* counter, int expected, int* lds_flag) {
+    wait_vector_memory();
+    __syncthreads();
+    if (threadIdx.x == 0)
+        *lds_flag = __hip_atomic_fetch_add(counter, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == expected - 1;
+    __syncthreads();
+    return *lds_flag != 0;
+}
+
 // ------------------------------------------------------------------ layout
 
 // Bytes of one token of record (bits, group) at head_dim D
