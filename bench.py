@@ -42,12 +42,12 @@ def log(*args):
     print(*args, file=sys.stderr, flush=True)
 
 
-def staged_call_bytes(batch, history, heads, dim, page_tokens, loop):
+def staged_call_bytes(batch, history, heads, dim, page_tokens, loop, schedule=SCHEDULE):
     """Algorithmic HBM bytes of one decode call (packed pages + Q/K/V/out + page table)."""
     from residualquant_amd.layout import staged_bytes
 
     pages = (history + page_tokens - 1) // page_tokens
-    per_page = staged_bytes(dim, SCHEDULE, page_tokens, "anchor", ANCHOR, loop)
+    per_page = staged_bytes(dim, schedule, page_tokens, "anchor", ANCHOR, loop)
     cache = batch * pages * heads * 2 * per_page
     live = 4 * batch * heads * dim * 2
     table = batch * pages * 4
@@ -58,12 +58,13 @@ def bf16_call_bytes(batch, history, heads, dim):
     return batch * history * heads * dim * 2 * 2 + 4 * batch * heads * dim * 2 + batch * (history // 16) * 4
 
 
-def build_packed_cache(torch, rq, workloads, batch, history, heads, dim, page_tokens, device, seed):
+def build_packed_cache(torch, rq, workloads, batch, history, heads, dim, page_tokens, device, seed,
+                       schedule=SCHEDULE):
     """Quantize synthetic K/V for every history token into a packed paged cache (on the GPU)."""
     pages = (history + page_tokens - 1) // page_tokens
     table = workloads.block_tables(batch, pages, seed + 5, device=device)
     num_blocks = batch * pages
-    width = rq.page_width(dim, SCHEDULE)
+    width = rq.page_width(dim, schedule)
     cache = torch.zeros((2, num_blocks, heads, page_tokens, width), dtype=torch.uint8, device=device)
     key_rotation = workloads.random_sign_rotation(heads, dim, seed + 3, device=device)
     value_rotation = workloads.random_sign_rotation(heads, dim, seed + 4, device=device)
@@ -71,8 +72,8 @@ def build_packed_cache(torch, rq, workloads, batch, history, heads, dim, page_to
     chunk = 16384
     for start in range(0, slots.numel(), chunk):
         part = slots[start:start + chunk]
-        pairs = workloads.loop_kv(part.numel(), heads, dim, len(SCHEDULE), seed + start, device=device)
-        rq.quantize(pairs, cache, part, key_rotation, value_rotation, None, SCHEDULE, "anchor", ANCHOR, "ls")
+        pairs = workloads.loop_kv(part.numel(), heads, dim, len(schedule), seed + start, device=device)
+        rq.quantize(pairs, cache, part, key_rotation, value_rotation, None, schedule, "anchor", ANCHOR, "ls")
         del pairs
     torch.cuda.synchronize()
     return cache, table, key_rotation, value_rotation
@@ -355,6 +356,123 @@ def run_prefill(args):
     print(json.dumps(result), flush=True)
 
 
+HUGINN_SCHEDULE = ((2, 16), (2, 16), (2, 16), (4, 32))
+
+
+def run_huginn(args):
+    """C4: Huginn-shaped deep-loop decode attention, 55 heads x D96, g16 residuals, B8 x T4096.
+
+    One step is the 4 calls of one loop group (3 residual loops + the anchor);
+    the recurrent core of 4 layers unrolled 32 loops runs 32 such groups per
+    generated token.
+    """
+    import torch
+
+    import residualquant_amd as rq
+    from residualquant_amd import ops, workloads
+
+    device = torch.device("cuda:0")
+    torch.cuda.set_device(device)
+    if args.split_target:
+        ops.set_split_target(args.split_target)
+    batch, history, heads, dim, page_tokens = 8, 4096, 55, 96, 16
+    schedule = HUGINN_SCHEDULE
+    seed = 4096
+    log(f"[bench] building packed cache B={batch} T={history} H={heads} D={dim} {schedule}")
+    cache, table, key_rotation, value_rotation = build_packed_cache(
+        torch, rq, workloads, batch, history, heads, dim, page_tokens, device, seed, schedule)
+    generator = torch.Generator(device=device).manual_seed(seed + 7)
+    query = torch.randn((batch, heads, dim), generator=generator, device=device).to(torch.bfloat16)
+    key = torch.randn((batch, heads, dim), generator=generator, device=device).to(torch.bfloat16)
+    value = torch.randn((batch, heads, dim), generator=generator, device=device).to(torch.bfloat16)
+    output = torch.empty_like(query)
+    qsl = torch.arange(batch + 1, dtype=torch.int32, device=device)
+    seq_lens = torch.full((batch,), history + 1, dtype=torch.int32, device=device)
+    workspace = torch.empty(ops.attention_workspace_bytes(batch, heads, dim, table.size(1), page_tokens),
+                            dtype=torch.uint8, device=device)
+
+    def call(loop):
+        rq.attention(query, key, value, cache, output, qsl, seq_lens, table, key_rotation, value_rotation,
+                     None, schedule, "anchor", ANCHOR, loop, workspace=workspace)
+
+    def step():
+        for loop in range(len(schedule)):
+            call(loop)
+
+    graph = capture(torch, step)
+    step_s = timed(torch, graph.replay, args.steps, args.warmup)
+    step_bytes = sum(staged_call_bytes(batch, history, heads, dim, page_tokens, loop, schedule) for loop in range(4))
+    residual_ms, launches = kernel_average_ms(torch, ops, lambda: call(0), max(10, args.steps))
+    anchor_ms, _ = kernel_average_ms(torch, ops, lambda: call(ANCHOR), max(10, args.steps))
+    residual_bytes = staged_call_bytes(batch, history, heads, dim, page_tokens, 0, schedule)
+    anchor_bytes = staged_call_bytes(batch, history, heads, dim, page_tokens, ANCHOR, schedule)
+    residual_gbps = residual_bytes / (residual_ms * 1e-3) / 1e9
+    log(f"[bench] C4 step {step_s * 1e6:.1f} us; residual call {residual_ms * 1e3:.1f} us ({residual_gbps:.0f} GB/s), "
+        f"anchor {anchor_ms * 1e3:.1f} us")
+
+    del workspace
+    bf16_cache = torch.randn((2, cache.size(1), heads, page_tokens, dim), device=device,
+                             generator=generator).to(torch.bfloat16)
+    bf16_ws = torch.empty(ops.attention_workspace_bytes(batch, heads, dim, table.size(1), page_tokens),
+                          dtype=torch.uint8, device=device)
+
+    def bf16_call():
+        rq.paged_attention_bf16(query, key, value, bf16_cache, output, qsl, seq_lens, table, workspace=bf16_ws)
+
+    bf16_ms, _ = kernel_average_ms(torch, ops, bf16_call, max(10, args.steps))
+    bytes_bf16 = bf16_call_bytes(batch, history, heads, dim)
+    log(f"[bench] C4 bf16 call {bf16_ms * 1e3:.1f} us ({bytes_bf16 / (bf16_ms * 1e-3) / 1e9:.0f} GB/s)")
+    result = {
+        "metric": "paged decode-attn µs/step + achieved HBM GB/s (% peak), INT2/INT4 vs bf16, 1 GPU",
+        "value": step_bytes / step_s / 1e9,
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": step_s * 1e3,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "int2/int4 packed codes, fp32 accumulate",
+        "data": "synthetic (seeded anchor N(0,1) + loop residuals N(0,0.15^2), random-sign Hadamard rotations, "
+                "Paley-12 x Sylvester-8 at D96)",
+        "config": {
+            "workload": "C4 Huginn-shaped deep-loop decode attention",
+            "batch": batch, "history_tokens": history, "heads": heads, "head_dim": dim, "loops": 4,
+            "page_tokens": page_tokens, "schedule": "[2,16]x3+[4,32] anchor 3 ls",
+            "step": "one loop group: 3 residual-loop calls + 1 anchor-loop call",
+        },
+        "us_per_step": step_s * 1e6,
+        "timing": "one HIP-graph replay of the 4 calls per step",
+        "pct_peak_step": 100.0 * step_bytes / step_s / 1e9 / PEAK_HBM_GBPS,
+        "bytes_per_step": step_bytes,
+        "decode_kernel": {
+            "residual_loop_us": residual_ms * 1e3,
+            "anchor_loop_us": anchor_ms * 1e3,
+            "residual_loop_bytes": residual_bytes,
+            "anchor_loop_bytes": anchor_bytes,
+            "anchor_loop_GBps": anchor_bytes / (anchor_ms * 1e-3) / 1e9,
+        },
+        "roofline": {
+            "bound": "hbm",
+            "achieved": residual_gbps,
+            "peak": PEAK_HBM_GBPS,
+            "unit": "GB/s",
+            "frac": residual_gbps / PEAK_HBM_GBPS,
+            "traffic": None,
+            "kernel": f"decode_kernel<96,16,4,32,2,16,true> (residual loop), {launches} HIP-event-timed launches",
+        },
+        "bf16_baseline": {
+            "us_per_call_kernel": bf16_ms * 1e3,
+            "kernel_GBps": bytes_bf16 / (bf16_ms * 1e-3) / 1e9,
+            "bytes_per_call": bytes_bf16,
+            "residual_call_speedup_packed_vs_bf16": bf16_ms / residual_ms,
+        },
+        "cpu_baseline": None,
+    }
+    print(json.dumps(result), flush=True)
+
+
 def run_step(args):
     """C3: one graph replay = one decode step of all requests through 48 layers x 4 loops."""
     import torch
@@ -431,9 +549,10 @@ def run_step(args):
 
 def main():
     parser = argparse.ArgumentParser(description=__doc__)
-    parser.add_argument("--workload", choices=("decode", "quantize", "prefill", "step"), default="decode",
+    parser.add_argument("--workload", choices=("decode", "quantize", "prefill", "step", "huginn"), default="decode",
                         help="decode: C2 paged decode attention (the headline); quantize: C1 quantize-on-write; "
-                             "prefill: causal prompt attention; step: C3 looped-model decode step")
+                             "prefill: causal prompt attention; step: C3 looped-model decode step; "
+                             "huginn: C4 deep-loop decode attention (55 heads x D96, g16)")
     parser.add_argument("--no-sweep", action="store_true", help="step workload: batch 32 x 8k only")
     parser.add_argument("--tokens", type=int, default=4096, help="tokens per quantize call or prompt")
     parser.add_argument("--gpus", type=int, default=1)
@@ -465,6 +584,9 @@ def main():
         return
     if args.workload == "step":
         run_step(args)
+        return
+    if args.workload == "huginn":
+        run_huginn(args)
         return
     run_decode(args)
 
