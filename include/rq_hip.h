@@ -174,12 +174,16 @@ size_t rq_prefill_workspace_bytes(int64_t batch, int heads_q, int head_dim, int6
  * total = bf16(x + residual) is written to residual_out (which may alias
  * residual) and normalized; without one, x is normalized.
  * y = bf16(bf16(total * rsqrt(mean(total^2) + eps)) * weight), mean over the
- * hidden channels in FP32.  BF16 rows, 16-byte aligned, strides multiples of
- * 8 elements; hidden a multiple of 8 up to 2048.
+ * hidden channels in FP32.  With pre_weight, x is first replaced by its own
+ * RMSNorm with pre_weight (same eps), which fuses a norm that feeds a fused
+ * add (input_layernorm_2 -> post_attention_layernorm, ouro.py:154-155, and
+ * post_attention_layernorm_2 -> the next layer's input_layernorm or the
+ * final norm) into one launch.  BF16 rows, 16-byte aligned, strides
+ * multiples of 8 elements; hidden a multiple of 8 up to 2048.
  */
-int rq_rms_norm(const void* x, int64_t x_stride, const void* residual, int64_t residual_stride,
-                void* residual_out, int64_t residual_out_stride, const void* weight, void* y, int64_t y_stride,
-                int64_t rows, int hidden, float eps, hipStream_t stream);
+int rq_rms_norm(const void* x, int64_t x_stride, const void* pre_weight, const void* residual,
+                int64_t residual_stride, void* residual_out, int64_t residual_out_stride, const void* weight, void* y,
+                int64_t y_stride, int64_t rows, int hidden, float eps, hipStream_t stream);
 
 /*
  * Rotate-half rotary embedding of the Q and K of fused [q | k | v] BF16 rows

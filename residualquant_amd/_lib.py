@@ -88,7 +88,7 @@ def _declare(l: ctypes.CDLL) -> None:
     l.rq_prefill_workspace_bytes.restype = ctypes.c_size_t
     l.rq_prefill_workspace_bytes.argtypes = [i64, i32, i32, i64, i64, i32, i32]
     l.rq_rms_norm.restype = i32
-    l.rq_rms_norm.argtypes = [vp, i64, vp, i64, vp, i64, vp, vp, i64, i64, i32, ctypes.c_float, vp]
+    l.rq_rms_norm.argtypes = [vp, i64, vp, vp, i64, vp, i64, vp, vp, i64, i64, i32, ctypes.c_float, vp]
     l.rq_rope_qkv.restype = i32
     l.rq_rope_qkv.argtypes = [vp, i64, vp, vp, vp, i64, i32, i32, i64, vp, i64, vp, i64, vp, vp, i64, vp]
     l.rq_silu_mul.restype = i32

@@ -490,26 +490,28 @@ int rq_prefill_attention(const void* query, int64_t query_stride, const void* ke
     return check_launch(rq::launch_prefill(p, stream), "prefill attention launch");
 }
 
-int rq_rms_norm(const void* x, int64_t x_stride, const void* residual, int64_t residual_stride,
-                void* residual_out, int64_t residual_out_stride, const void* weight, void* y, int64_t y_stride,
-                int64_t rows, int hidden, float eps, hipStream_t stream) {
+int rq_rms_norm(const void* x, int64_t x_stride, const void* pre_weight, const void* residual,
+                int64_t residual_stride, void* residual_out, int64_t residual_out_stride, const void* weight, void* y,
+                int64_t y_stride, int64_t rows, int hidden, float eps, hipStream_t stream) {
     if (rows < 0 || rows > (int64_t)INT32_MAX || hidden <= 0 || hidden % 8 != 0 || hidden > 2048)
         return fail(RQ_EINVAL, "RMSNorm needs rows >= 0 and a hidden size that is a multiple of 8 up to 2048");
     if (!(eps >= 0.f) || !std::isfinite(eps)) return fail(RQ_EINVAL, "RMSNorm eps must be finite and non-negative");
     if ((residual == nullptr) != (residual_out == nullptr))
         return fail(RQ_EINVAL, "A residual input and a residual output go together");
     if (rows == 0) return ok();
-    const void* pointers[5] = {x, weight, y, residual, residual_out};
-    const int64_t strides[5] = {x_stride, 0, y_stride, residual_stride, residual_out_stride};
-    for (int i = 0; i < 5; ++i) {
+    const void* pointers[6] = {x, weight, y, residual, residual_out, pre_weight};
+    const int64_t strides[6] = {x_stride, 0, y_stride, residual_stride, residual_out_stride, 0};
+    for (int i = 0; i < 6; ++i) {
         if (i < 3 && pointers[i] == nullptr) return fail(RQ_EINVAL, "RMSNorm input, weight and output required");
         if (pointers[i] == nullptr) continue;
-        if ((reinterpret_cast<uintptr_t>(pointers[i]) % 16) || strides[i] % 8 || (i != 1 && strides[i] < hidden))
+        if ((reinterpret_cast<uintptr_t>(pointers[i]) % 16) || strides[i] % 8 ||
+            (i != 1 && i != 5 && strides[i] < hidden))
             return fail(RQ_EINVAL, "RMSNorm rows must be 16-byte aligned BF16 rows of at least hidden elements");
     }
     rq::StepNormParams p{};
     p.x = static_cast<const uint16_t*>(x);
     p.x_stride = x_stride;
+    p.pre_weight = static_cast<const uint16_t*>(pre_weight);
     p.residual = static_cast<const uint16_t*>(residual);
     p.residual_stride = residual_stride;
     p.residual_out = static_cast<uint16_t*>(residual_out);

@@ -91,6 +91,7 @@ hipError_t launch_prefill(const PrefillParams& p, hipStream_t stream);
 struct StepNormParams {
     const uint16_t* x;          // BF16 [rows, hidden]
     int64_t x_stride;
+    const uint16_t* pre_weight; // optional: x is first RMS-normalized with this weight
     const uint16_t* residual;   // optional BF16 [rows, hidden] added to x first
     int64_t residual_stride;
     uint16_t* residual_out;     // optional: receives bf16(x + residual) (may alias residual)

@@ -18,10 +18,45 @@ __device__ __forceinline__ float wave_sum(float v) {
     return v;
 }
 
+// Sum of one float per thread over the 256-thread workgroup (`partial` holds
+// one float per wave; the trailing barrier lets the caller reuse it).
+__device__ __forceinline__ float block_sum(float v, float* partial) {
+    v = wave_sum(v);
+    if ((threadIdx.x & 63) == 0) partial[threadIdx.x >> 6] = v;
+    __syncthreads();
+    float total = 0.f;
+#pragma unroll
+    for (int w = 0; w < kNormThreads / 64; ++w) total += partial[w];
+    __syncthreads();
+    return total;
+}
+
+// values[e] = bf16(bf16(values[e] * rsqrt(mean(values^2) + eps)) * w[e]) over the row.
+__device__ __forceinline__ void normalize_row(float (&values)[8], const uint16_t* weight, int i, bool active,
+                                              int hidden, float eps, float* partial) {
+    float sum = 0.f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) sum = fmaf(values[e], values[e], sum);
+    const float scale = rsqrtf(block_sum(sum, partial) / (float)hidden + eps);
+    if (!active) return;
+    const uint4 wraw = *reinterpret_cast<const uint4*>(weight + i);
+    const uint32_t wv[4] = {wraw.x, wraw.y, wraw.z, wraw.w};
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        values[2 * e] = bf16_f32(bf16_rn(bf16_f32(bf16_rn(values[2 * e] * scale)) * bf16_f32(wv[e] & 0xffffu)));
+        values[2 * e + 1] =
+            bf16_f32(bf16_rn(bf16_f32(bf16_rn(values[2 * e + 1] * scale)) * bf16_f32(wv[e] >> 16)));
+    }
+}
+
 // One workgroup per row, 8 channels per thread (rows of at most 8 * 256
-// channels, a multiple of 8): total = bf16(x + residual) when a residual is
-// given (written to residual_out), y = bf16(bf16(total * rsqrt(mean(total^2) + eps)) * w).
+// channels, a multiple of 8).  Optionally x is first normalized with
+// pre_weight (a norm whose output feeds a fused add, as input_layernorm_2
+// feeds post_attention_layernorm, ouro.py:154-155); then, with a residual,
+// total = bf16(x + residual) is written to residual_out and normalized:
+// y = bf16(bf16(total * rsqrt(mean(total^2) + eps)) * weight).
 __global__ __launch_bounds__(kNormThreads) void rms_norm_kernel(const uint16_t* x, int64_t x_stride,
+                                                                const uint16_t* pre_weight,
                                                                 const uint16_t* residual, int64_t residual_stride,
                                                                 uint16_t* residual_out, int64_t residual_out_stride,
                                                                 const uint16_t* weight, uint16_t* y, int64_t y_stride,
@@ -31,48 +66,37 @@ __global__ __launch_bounds__(kNormThreads) void rms_norm_kernel(const uint16_t* 
     const int i = 8 * threadIdx.x;
     const bool active = i < hidden;
     float values[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-    float sum = 0.f;
+    uint4 rres = make_uint4(0, 0, 0, 0);
     if (active) {
         const uint4 raw = *reinterpret_cast<const uint4*>(x + row * x_stride + i);
-        const uint32_t w[4] = {raw.x, raw.y, raw.z, raw.w};
-        uint4 rres = make_uint4(0, 0, 0, 0);
         if (residual != nullptr) rres = *reinterpret_cast<const uint4*>(residual + row * residual_stride + i);
+        const uint32_t w[4] = {raw.x, raw.y, raw.z, raw.w};
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            values[2 * e] = bf16_f32(w[e] & 0xffffu);
+            values[2 * e + 1] = bf16_f32(w[e] >> 16);
+        }
+    }
+    if (pre_weight != nullptr) normalize_row(values, pre_weight, i, active, hidden, eps, partial);
+    if (residual != nullptr && active) {
         const uint32_t r[4] = {rres.x, rres.y, rres.z, rres.w};
         uint32_t packed[4];
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-            float lo = bf16_f32(w[e] & 0xffffu), hi = bf16_f32(w[e] >> 16);
-            if (residual != nullptr) {
-                lo = bf16_f32(bf16_rn(lo + bf16_f32(r[e] & 0xffffu)));
-                hi = bf16_f32(bf16_rn(hi + bf16_f32(r[e] >> 16)));
-            }
-            packed[e] = bf16_rn(lo) | (bf16_rn(hi) << 16);
-            values[2 * e] = lo;
-            values[2 * e + 1] = hi;
-            sum = fmaf(lo, lo, sum);
-            sum = fmaf(hi, hi, sum);
+            const uint32_t lo = bf16_rn(values[2 * e] + bf16_f32(r[e] & 0xffffu));
+            const uint32_t hi = bf16_rn(values[2 * e + 1] + bf16_f32(r[e] >> 16));
+            values[2 * e] = bf16_f32(lo);
+            values[2 * e + 1] = bf16_f32(hi);
+            packed[e] = lo | (hi << 16);
         }
-        if (residual_out != nullptr)
-            *reinterpret_cast<uint4*>(residual_out + row * residual_out_stride + i) =
-                make_uint4(packed[0], packed[1], packed[2], packed[3]);
+        *reinterpret_cast<uint4*>(residual_out + row * residual_out_stride + i) =
+            make_uint4(packed[0], packed[1], packed[2], packed[3]);
     }
-    sum = wave_sum(sum);
-    if ((threadIdx.x & 63) == 0) partial[threadIdx.x >> 6] = sum;
-    __syncthreads();
-    float total = 0.f;
-#pragma unroll
-    for (int w = 0; w < kNormThreads / 64; ++w) total += partial[w];
-    const float scale = rsqrtf(total / (float)hidden + eps);
+    normalize_row(values, weight, i, active, hidden, eps, partial);
     if (active) {
-        const uint4 wraw = *reinterpret_cast<const uint4*>(weight + i);
-        const uint32_t wv[4] = {wraw.x, wraw.y, wraw.z, wraw.w};
         uint32_t out[4];
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-            const float a = bf16_f32(bf16_rn(values[2 * e] * scale)) * bf16_f32(wv[e] & 0xffffu);
-            const float b = bf16_f32(bf16_rn(values[2 * e + 1] * scale)) * bf16_f32(wv[e] >> 16);
-            out[e] = bf16_rn(a) | (bf16_rn(b) << 16);
-        }
+        for (int e = 0; e < 4; ++e) out[e] = bf16_rn(values[2 * e]) | (bf16_rn(values[2 * e + 1]) << 16);
         *reinterpret_cast<uint4*>(y + row * y_stride + i) = make_uint4(out[0], out[1], out[2], out[3]);
     }
 }
@@ -136,7 +160,7 @@ __global__ __launch_bounds__(256) void silu_mul_kernel(const uint16_t* gate_up, 
 hipError_t launch_rms_norm(const StepNormParams& p, hipStream_t stream) {
     if (p.rows == 0) return hipSuccess;
     hipLaunchKernelGGL(rms_norm_kernel, dim3((unsigned)p.rows), dim3(kNormThreads), 0, stream, p.x, p.x_stride,
-                       p.residual, p.residual_stride, p.residual_out, p.residual_out_stride, p.weight, p.y,
+                       p.pre_weight, p.residual, p.residual_stride, p.residual_out, p.residual_out_stride, p.weight, p.y,
                        p.y_stride, p.hidden, p.eps);
     return hipGetLastError();
 }

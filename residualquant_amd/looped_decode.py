@@ -162,14 +162,11 @@ class LoopedDecoder:
         eps = c.rms_eps
         h = self.embed[self.tokens]
         for loop in range(c.loops):
+            # input_layernorm of layer 0, ouro.py:148-150 (the residual starts as the loop input).
+            self.residual.copy_(h)
+            x = step_ops.rms_norm(h, self.norms[0][0], eps)
             for layer in range(c.layers):
                 norms = self.norms[layer]
-                # input_layernorm, ouro.py:148-152 (fused add from the second layer on).
-                if layer == 0:
-                    self.residual.copy_(h)
-                    x = step_ops.rms_norm(h, norms[0], eps)
-                else:
-                    x, _ = step_ops.rms_norm(h, norms[0], eps, residual=self.residual)
                 qkv = F.linear(x, self.qkv[layer])
                 key_stage, value_stage = self.staged[layer, loop, 0], self.staged[layer, loop, 1]
                 q, k = step_ops.rope_qkv(qkv, self.positions, self.cos, self.sin, c.heads, c.head_dim,
@@ -183,11 +180,14 @@ class LoopedDecoder:
                     ops.quantize(pairs, self.caches[layer], self.slots, self.key_rotation[layer],
                                  self.value_rotation[layer], None, c.schedule, "anchor", c.anchor, c.coefficient)
                 a = F.linear(self.attn_out.view(self.batch, q_size), self.o[layer])
-                a = step_ops.rms_norm(a, norms[1], eps)
-                x, _ = step_ops.rms_norm(a, norms[2], eps, residual=self.residual)
+                # input_layernorm_2 then post_attention_layernorm with the fused add (ouro.py:154-155), one launch.
+                x, _ = step_ops.rms_norm(a, norms[2], eps, residual=self.residual, pre_weight=norms[1])
                 m = F.linear(step_ops.silu_mul(F.linear(x, self.gate_up[layer])), self.down[layer])
-                h = step_ops.rms_norm(m, norms[3], eps)
-            h, _ = step_ops.rms_norm(h, self.final_norm, eps, residual=self.residual)
+                # post_attention_layernorm_2 (ouro.py:157), then the next layer's input_layernorm
+                # with the fused add (:151-152) or the loop's final norm (:240), one launch.
+                following = self.norms[layer + 1][0] if layer + 1 < c.layers else self.final_norm
+                x, _ = step_ops.rms_norm(m, following, eps, residual=self.residual, pre_weight=norms[3])
+            h = x
         logits = F.linear(h, self.lm_head)
         # Greedy next token and the next position, slot and sequence length.
         self.tokens.copy_(logits.argmax(dim=-1))

@@ -32,18 +32,21 @@ def _rows(tensor: torch.Tensor, name: str) -> None:
 
 
 def rms_norm(x: torch.Tensor, weight: torch.Tensor, eps: float, residual: Optional[torch.Tensor] = None,
-             out: Optional[torch.Tensor] = None):
+             out: Optional[torch.Tensor] = None, pre_weight: Optional[torch.Tensor] = None):
     """RMSNorm of ``x`` (vLLM RMSNorm.forward); with ``residual``, the fused form.
 
     Without a residual returns ``y = bf16(bf16(x * rsqrt(mean(x^2) + eps)) * weight)``.
     With one, ``residual`` is updated in place to ``bf16(x + residual)`` and
     ``(y, residual)`` is returned, y normalizing the updated residual
-    (vLLM's fused_add_rms_norm contract).
+    (vLLM's fused_add_rms_norm contract).  With ``pre_weight``, ``x`` is
+    first replaced by ``rms_norm(x, pre_weight, eps)`` in the same launch.
     """
     _rows(x, "x")
     rows, hidden = x.shape
-    _require(weight.is_cuda and weight.dtype == torch.bfloat16 and weight.shape == (hidden,)
-             and weight.is_contiguous(), "RMSNorm weight must be a contiguous BF16 [hidden] vector")
+    for w in (weight, pre_weight):
+        if w is not None:
+            _require(w.is_cuda and w.dtype == torch.bfloat16 and w.shape == (hidden,) and w.is_contiguous(),
+                     "RMSNorm weight must be a contiguous BF16 [hidden] vector")
     if residual is not None:
         _rows(residual, "residual")
         _require(residual.shape == x.shape and residual.device == x.device, "residual must match x")
@@ -53,7 +56,8 @@ def rms_norm(x: torch.Tensor, weight: torch.Tensor, eps: float, residual: Option
     _require(out.shape == x.shape and out.device == x.device, "out must match x")
     with torch.cuda.device(x.device):
         status = _lib.lib().rq_rms_norm(
-            x.data_ptr(), x.stride(0), residual.data_ptr() if residual is not None else None,
+            x.data_ptr(), x.stride(0), pre_weight.data_ptr() if pre_weight is not None else None,
+            residual.data_ptr() if residual is not None else None,
             residual.stride(0) if residual is not None else 0,
             residual.data_ptr() if residual is not None else None,
             residual.stride(0) if residual is not None else 0, weight.data_ptr(), out.data_ptr(), out.stride(0),

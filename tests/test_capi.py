@@ -173,12 +173,14 @@ def test_prefill_workspace_plan(lib):
 def test_step_ops_reject_before_device_work(lib):
     # Every call below fails validation before any launch (fake pointers never reach a kernel).
     fake = 0x10000
-    assert lib.rq_rms_norm(fake, 4096, None, 0, None, 0, fake, fake, 4096, 2, 4096, 1e-6, None) == _lib.RQ_EINVAL
+    assert lib.rq_rms_norm(fake, 4096, None, None, 0, None, 0, fake, fake, 4096, 2, 4096, 1e-6, None) == _lib.RQ_EINVAL
     assert b"multiple of 8 up to 2048" in lib.rq_last_error()
-    assert lib.rq_rms_norm(fake, 256, fake, 256, None, 0, fake, fake, 256, 2, 256, 1e-6, None) == _lib.RQ_EINVAL
-    assert lib.rq_rms_norm(fake + 8, 256, None, 0, None, 0, fake, fake, 256, 2, 256, 1e-6, None) == _lib.RQ_EINVAL
+    assert lib.rq_rms_norm(fake, 256, None, fake, 256, None, 0, fake, fake, 256, 2, 256, 1e-6, None) == _lib.RQ_EINVAL
+    assert lib.rq_rms_norm(fake + 8, 256, None, None, 0, None, 0, fake, fake, 256, 2, 256, 1e-6, None) == _lib.RQ_EINVAL
     assert b"16-byte aligned" in lib.rq_last_error()
-    assert lib.rq_rms_norm(fake, 256, None, 0, None, 0, fake, fake, 256, 0, 256, 1e-6, None) == _lib.RQ_OK
+    assert lib.rq_rms_norm(fake, 256, fake + 8, None, 0, None, 0, fake, fake, 256, 2, 256, 1e-6, None) == _lib.RQ_EINVAL
+    assert b"16-byte aligned" in lib.rq_last_error()
+    assert lib.rq_rms_norm(fake, 256, None, None, 0, None, 0, fake, fake, 256, 0, 256, 1e-6, None) == _lib.RQ_OK
     assert lib.rq_rope_qkv(fake, 3 * 256, fake, fake, fake, 16, 2, 127, 1, fake, 256, fake, 256, None, None, 0,
                            None) == _lib.RQ_EINVAL
     assert lib.rq_rope_qkv(fake, 2 * 256, fake, fake, fake, 16, 2, 128, 1, fake, 256, fake, 256, None, None, 0,

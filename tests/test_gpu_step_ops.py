@@ -56,6 +56,26 @@ def test_fused_add_rms_norm(device, rows, hidden):
     _close(y, want)
 
 
+@pytest.mark.parametrize("rows,hidden", [(3, 2048), (32, 256)])
+def test_two_norms_fused(device, rows, hidden):
+    """rms_norm(x, w2, residual, pre_weight=w1) == fused_add(rms_norm(x, w1), residual) then norm with w2."""
+    print(f"two fused norms rows={rows} hidden={hidden}", flush=True)
+    g = torch.Generator(device=device).manual_seed(3 * rows + hidden)
+    x = (torch.randn((rows, hidden), generator=g, device=device) * 5).to(torch.bfloat16)
+    residual = torch.randn((rows, hidden), generator=g, device=device).to(torch.bfloat16)
+    w1 = (torch.rand(hidden, generator=g, device=device) + 0.5).to(torch.bfloat16)
+    w2 = (torch.rand(hidden, generator=g, device=device) + 0.5).to(torch.bfloat16)
+    first, _ = _rms_reference(x, w1, 1e-6)
+    want, want_total = _rms_reference(first, w2, 1e-6, residual)
+    staged = residual.clone()
+    y, _ = step_ops.rms_norm(x, w2, 1e-6, residual=staged, pre_weight=w1)
+    chained = residual.clone()
+    y2, _ = step_ops.rms_norm(step_ops.rms_norm(x, w1, 1e-6), w2, 1e-6, residual=chained)
+    assert torch.equal(staged, chained) and torch.equal(y, y2)
+    _close(y, want)
+    _close(staged, want_total)
+
+
 def test_rms_norm_strided_rows(device):
     base = torch.randn((6, 3 * 256), device=device).to(torch.bfloat16)
     x = base[:, 256:512]
