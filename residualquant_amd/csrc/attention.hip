@@ -30,8 +30,12 @@ namespace rq {
 namespace {
 
 constexpr float kLog2e = 1.4426950408889634f;
-constexpr int kDecodeThreads = 256;
-constexpr int kWaves = kDecodeThreads / 64;
+#ifndef RQ_DECODE_WAVES
+#define RQ_DECODE_WAVES 4
+#endif
+constexpr int kWaves = RQ_DECODE_WAVES;
+constexpr int kDecodeThreads = 64 * kWaves;
+static_assert(kWaves >= 4, "the finish and merge use at least 256 threads");
 constexpr int kUnitTokens = 16;
 
 __device__ __forceinline__ float quad_xor1(float x) {
@@ -482,9 +486,10 @@ __device__ __forceinline__ void finish_single(const AttentionParams& p, int64_t 
     __shared__ float halves[2][128];
     const int tid = threadIdx.x;
     const int c = tid & 127, part = tid >> 7;
+    const bool in_halves = tid < 256;  // two threads per channel, half of k each
     const bool rotate = p.value_rotation != nullptr;
     uint4 rv[D / 16];
-    if (rotate && c < D) {
+    if (rotate && c < D && in_halves) {
         const uint4* r = reinterpret_cast<const uint4*>(p.value_rotation + ((int64_t)head * D + c) * D + part * (D / 2));
 #pragma unroll
         for (int i = 0; i < D / 16; ++i) rv[i] = r[i];
@@ -499,7 +504,7 @@ __device__ __forceinline__ void finish_single(const AttentionParams& p, int64_t 
     if (tid < 128) hist[c] = c < D ? r.sum * (w_hist * inv) : 0.f;
     __syncthreads();
     float o = 0.f;
-    if (c < D) {
+    if (c < D && in_halves) {
         if (rotate) {
             float a[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -517,7 +522,7 @@ __device__ __forceinline__ void finish_single(const AttentionParams& p, int64_t 
             o = hist[c];
         }
     }
-    halves[part][c] = o;
+    if (in_halves) halves[part][c] = o;
     __syncthreads();
     if (tid < D)
         p.output[row * p.output_stride + head * D + tid] =
@@ -632,7 +637,7 @@ constexpr int kMergeThreads = 256;
 // (merge.cuh:8-84, output.cuh:9-31, rotation.cuh:10-84).  `lds` holds at
 // least kMergeLdsFloats floats; the caller has made every split's partial
 // visible to this workgroup.
-constexpr int kMergeLdsFloats = kMaxSplits + 4 + 128 + 4 * 128;
+constexpr int kMergeLdsFloats = kMaxSplits + 4 + 128 + kWaves * 128;
 
 template <int D>
 __device__ __forceinline__ void merge_output(const AttentionParams& p, int64_t row, int head, float* lds) {
@@ -641,7 +646,7 @@ __device__ __forceinline__ void merge_output(const AttentionParams& p, int64_t r
     float* weights = lds;                    // [kMaxSplits]
     float* totals = lds + kMaxSplits;        // [2]: live weight, 1 / denominator
     float* hist = totals + 4;                // [128]
-    float* halves = hist + 128;              // [4][128]
+    float* halves = hist + 128;              // [waves][128]
     // Partials [split][D + 2] of this (row, head), read with coherent loads.
     constexpr uint32_t kSplitBytes = (D + 2) * 4;
     const __amdgpu_buffer_rsrc_t parts =
@@ -667,14 +672,15 @@ __device__ __forceinline__ void merge_output(const AttentionParams& p, int64_t r
         }
     }
     __syncthreads();
-    // History sum: thread = (channel pair, split group of four); every load of
-    // a thread is independent, so they are all in flight together.
+    // History sum: thread = (channel pair, split group); every load of a
+    // thread is independent, so they are all in flight together.
+    const int groups = blockDim.x >> 6;
     {
         const int pair = tid & 63, group = tid >> 6;
         float2 h = make_float2(0.f, 0.f);
         if (2 * pair < D) {
 #pragma unroll 8
-            for (int s = group; s < p.splits; s += 4) {
+            for (int s = group; s < p.splits; s += groups) {
                 const float2 v = handoff_load2(parts, s * kSplitBytes + 8 + 8 * pair);
                 h.x = fmaf(weights[s], v.x, h.x);
                 h.y = fmaf(weights[s], v.y, h.y);
@@ -685,13 +691,18 @@ __device__ __forceinline__ void merge_output(const AttentionParams& p, int64_t r
     }
     __syncthreads();
     const int c = tid & 127, part = tid >> 7;
-    if (tid < 128)
-        hist[c] = c < D ? (((halves[c] + halves[128 + c]) + halves[256 + c]) + halves[384 + c]) * totals[1] : 0.f;
+    if (tid < 128) {
+        float sum = 0.f;
+        for (int g = 0; g < groups; ++g) sum += halves[g * 128 + c];
+        hist[c] = c < D ? sum * totals[1] : 0.f;
+    }
     __syncthreads();
-    // out[c] = sum_k hist[k] R_v[c][k]: half `part` of the k range per thread,
-    // R_v row c read straight from global memory (L2) as 16-byte vectors.
+    // out[c] = sum_k hist[k] R_v[c][k]: half `part` of the k range per thread
+    // (the first 256 threads), R_v row c read straight from global memory (L2)
+    // as 16-byte vectors.
+    const bool in_halves = tid < 256;
     float o = 0.f;
-    if (c < D) {
+    if (c < D && in_halves) {
         if (p.value_rotation != nullptr) {
             const uint4* r = reinterpret_cast<const uint4*>(p.value_rotation + ((int64_t)head * D + c) * D +
                                                             part * (D / 2));
@@ -713,7 +724,7 @@ __device__ __forceinline__ void merge_output(const AttentionParams& p, int64_t r
         }
     }
     __syncthreads();
-    halves[part * 128 + c] = o;
+    if (in_halves) halves[part * 128 + c] = o;
     __syncthreads();
     if (tid < D) {
         const float v = bf16_f32(p.value[row * p.value_stride + head * D + tid]);
