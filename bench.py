@@ -274,8 +274,8 @@ def run_quantize(args):
             "unit": "TFLOP/s",
             "frac": achieved / PEAK_FP32_TFLOPS,
             "traffic": None,
-            "kernel": "quantize_kernel<128,4,3>: FP32 rotation FMAs (VOP2 v_fmac_f32) against the "
-                      "published FP32 peak; HBM traffic is 6% of peak at this rate",
+            "kernel": "quantize_mfma_kernel<128,4,3>: FP32 rotation FMAs (K=1 v_mfma_f32_16x16x1_4b_f32 "
+                      "chains) against the published FP32 peak; HBM traffic is 6% of peak at this rate",
         },
         "cpu_baseline": cpu,
     }

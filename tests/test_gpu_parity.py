@@ -31,6 +31,11 @@ QUANTIZE_CASES = [
     (25, 3, 96, ((2, 32),) * 4, 32, "anchor", 0, "ls", True, False, 4),
     (64, 2, 128, ((4, 16), (2, 16)), 16, "adjacent", 0, "ls", True, True, 0),
     (300, 4, 128, OURO_G32, 16, "anchor", 3, "norm", True, True, 7),
+    # 2048 tokens and more run the matrix-core rotation kernel.
+    (2100, 2, 128, OURO_G32, 16, "anchor", 3, "ls", True, True, 5),
+    (2048, 2, 96, OURO_G16, 16, "anchor", 3, "ls", True, True, 3),
+    (2053, 1, 128, ((4, 32), (2, 32), (2, 32), (2, 32)), 32, "adjacent", 0, "norm", True, False, 1),
+    (2049, 1, 128, ((4, 32), (2, 16)), 16, "anchor", 0, "unit", False, True, 2),
 ]
 
 
