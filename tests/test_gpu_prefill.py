@@ -109,6 +109,23 @@ def test_prefill_long_prompt_edges(oracle, device):
     _check(out[-edge:], last, "last rows")
 
 
+def test_prefill_split_merge_repeats_exactly(device):
+    """Blocks whose keys are split over several work items are merged from
+    FP32 partials; repeated calls, and calls of other shapes in between, give
+    bit-identical outputs."""
+    n, heads, dim = 3000, 4, 128
+    q, k, v = (_random((n, heads, dim), s).to(device) for s in (11, 12, 13))
+    cu = torch.tensor([0, n], dtype=torch.int32, device=device)
+    first = rq.flash_attn_varlen_func(q, k, v, n, cu, n, causal=True)
+    for _ in range(3):
+        again = rq.flash_attn_varlen_func(q, k, v, n, cu, n, causal=True)
+        assert torch.equal(first, again)
+    # A different shape in between, then the first again.
+    rq.flash_attn_varlen_func(q[:1500], k[:2500], v[:2500], 1500, cu.new_tensor([0, 1500]), 2500,
+                              cu_seqlens_k=cu.new_tensor([0, 2500]), causal=True)
+    assert torch.equal(first, rq.flash_attn_varlen_func(q, k, v, n, cu, n, causal=True))
+
+
 def test_prefill_rejects_unsupported(device):
     q = torch.zeros((4, 2, 64), dtype=torch.bfloat16, device=device)
     cu = torch.tensor([0, 4], dtype=torch.int32, device=device)
