@@ -81,16 +81,69 @@ __device__ __forceinline__ int find_request_parallel(const int32_t* qsl, int64_t
                                                      int* lds_counts) {
     const int c = threadIdx.x;
     const int threads = blockDim.x;
+    // The range bounds are loaded with the counts, before the barrier.
+    const int32_t lo = requests > 0 ? qsl[0] : 0;
+    const int32_t hi = requests > 0 ? qsl[requests] : 0;
     int count = 0;
     for (int64_t j = 1 + c; j <= requests; j += threads) count += qsl[j] <= row ? 1 : 0;
 #pragma unroll
     for (int d = 32; d; d >>= 1) count += __shfl_xor(count, d);
     if ((c & 63) == 0) lds_counts[c >> 6] = count;
     __syncthreads();
-    if (requests <= 0 || row < qsl[0] || row >= qsl[requests]) return -1;
+    if (requests <= 0 || row < lo || row >= hi) return -1;
     int total = 0;
     for (int w = 0; w < threads / 64; ++w) total += lds_counts[w];
     return total;
+}
+
+// Loads of the prepare that do not depend on the request: q, the live key and
+// the two key means of (row, head), and R_k, all into registers.  Issued
+// before the request lookup so their round trips overlap; prepare_stage then
+// writes R_k to LDS, which the lookup's barrier or prepare_record's first
+// barrier publishes.  prepare_record reads no global memory, so loads issued
+// after prepare_stage are not waited on before it ends.
+typedef uint32_t Chunk16 __attribute__((ext_vector_type(4)));
+
+template <int D, int Threads>
+struct PrepareInputs {
+    static constexpr int kChunks = D * D / 8;  // 16-byte pieces of R_k
+    static constexpr int kPerThread = (kChunks + Threads - 1) / Threads;
+    Chunk16 chunk[kPerThread];
+    float mean_loop, mean_anchor;  // FP32 key means of channel min(c, D - 1) (0 without)
+    uint32_t q_bits, k_bits;       // BF16 q and live key of that channel
+};
+
+template <int D, int Threads>
+__device__ __forceinline__ void prepare_load(const AttentionParams& p, int64_t row, int head,
+                                             PrepareInputs<D, Threads>& in) {
+    using In = PrepareInputs<D, Threads>;
+    // Unconditional loads (threads past D read channel D - 1; prepare_record
+    // masks them), converted where they are used so nothing waits here.
+    const int c = threadIdx.x;
+    const int channel = c < D ? c : D - 1;
+    in.q_bits = p.query[row * p.query_stride + head * D + channel];
+    in.k_bits = p.key[row * p.key_stride + head * D + channel];
+    in.mean_loop = p.key_mean_loop ? p.key_mean_loop[head * D + channel] : 0.f;
+    in.mean_anchor = p.key_mean_anchor ? p.key_mean_anchor[head * D + channel] : 0.f;
+    if (p.key_rotation != nullptr) {
+        const Chunk16* src = reinterpret_cast<const Chunk16*>(p.key_rotation + (int64_t)head * D * D);
+#pragma unroll
+        for (int j = 0; j < In::kPerThread; ++j)
+            if (In::kChunks % Threads == 0 || c + j * Threads < In::kChunks) in.chunk[j] = src[c + j * Threads];
+    }
+}
+
+template <int D, int Threads>
+__device__ __forceinline__ void prepare_stage(const AttentionParams& p, const PrepareInputs<D, Threads>& in,
+                                              _Float16* rotation_lds) {
+    using In = PrepareInputs<D, Threads>;
+    const int c = threadIdx.x;
+    if (p.key_rotation != nullptr) {
+        Chunk16* dst = reinterpret_cast<Chunk16*>(rotation_lds);
+#pragma unroll
+        for (int j = 0; j < In::kPerThread; ++j)
+            if (In::kChunks % Threads == 0 || c + j * Threads < In::kChunks) dst[c + j * Threads] = in.chunk[j];
+    }
 }
 
 // The prepared query record of one (row, head), written to `record`
@@ -98,35 +151,13 @@ __device__ __forceinline__ int find_request_parallel(const int32_t* qsl, int64_t
 // [3..10] 16-channel and [11..14] 32-channel group sums of q', then q'
 // (FP32, log2 units) and its four nibble planes in the INT4 and INT2 word
 // orders (prepare.cuh:13-229).  Called by every thread of a workgroup of 128
-// or 256 threads (threads c >= D contribute nothing) after prepare_load and a
-// barrier; `rotation_lds` holds D * D halves.  Returns after a barrier with
-// `record` complete.
-// Loads of the prepare that do not depend on the request: q and the live key
-// of (row, head) into registers, R_k into LDS.  Issued before the request
-// lookup so both round trips overlap; the lookup's barrier publishes the LDS.
-struct PrepareInputs {
-    float q, k_live;
-};
-
-template <int D>
-__device__ __forceinline__ PrepareInputs prepare_load(const AttentionParams& p, int64_t row, int head,
-                                                      _Float16* rotation_lds) {
-    const int c = threadIdx.x;
-    const bool active = c < D;
-    PrepareInputs in;
-    in.q = active ? bf16_f32(p.query[row * p.query_stride + head * D + c]) : 0.f;
-    in.k_live = active ? bf16_f32(p.key[row * p.key_stride + head * D + c]) : 0.f;
-    if (p.key_rotation != nullptr) {
-        const uint4* src = reinterpret_cast<const uint4*>(p.key_rotation + (int64_t)head * D * D);
-        uint4* dst = reinterpret_cast<uint4*>(rotation_lds);
-        for (int i = c; i < D * D / 8; i += blockDim.x) dst[i] = src[i];
-    }
-    return in;
-}
-
-template <int D>
-__device__ __forceinline__ void prepare_record(const AttentionParams& p, int head, const PrepareInputs& in,
-                                               float* record, const _Float16* rotation_lds) {
+// or 256 threads (threads c >= D contribute nothing) after prepare_stage;
+// `rotation_lds` holds D * D halves.  Returns after a barrier with `record`
+// complete.
+template <int D, int Threads>
+__device__ __forceinline__ void prepare_record(const AttentionParams& p, int head,
+                                               const PrepareInputs<D, Threads>& in, float* record,
+                                               const _Float16* rotation_lds) {
     __shared__ __attribute__((aligned(16))) float q_lds[128];
     __shared__ float totals[4][kDecodeThreads / 64];
     const int c = threadIdx.x;
@@ -134,22 +165,34 @@ __device__ __forceinline__ void prepare_record(const AttentionParams& p, int hea
     const int wave = c >> 6;
     const int waves = blockDim.x >> 6;
     const bool active = c < D;
-    const float q = in.q, k_live = in.k_live;
+    const float q = active ? bf16_f32(in.q_bits) : 0.f;
+    const float k_live = active ? bf16_f32(in.k_bits) : 0.f;
     if (c < 128) q_lds[c] = q;
     __syncthreads();
 
     float qr = q;
     if (p.key_rotation != nullptr) {
-        // Four interleaved partial sums so the LDS reads pipeline.
+        // Four interleaved partial sums (a[j] takes k = j mod 4, ascending).
+        // Sixteen column reads are issued before their FMAs (sched_barrier),
+        // so the LDS round trips overlap instead of one per k.
         float a[4] = {0.f, 0.f, 0.f, 0.f};
         if (active) {
-#pragma unroll 8
-            for (int k = 0; k < D; k += 4) {
-                const float4 qv = *reinterpret_cast<const float4*>(q_lds + k);
-                a[0] = fmaf(qv.x, (float)rotation_lds[k * D + c], a[0]);
-                a[1] = fmaf(qv.y, (float)rotation_lds[(k + 1) * D + c], a[1]);
-                a[2] = fmaf(qv.z, (float)rotation_lds[(k + 2) * D + c], a[2]);
-                a[3] = fmaf(qv.w, (float)rotation_lds[(k + 3) * D + c], a[3]);
+#pragma unroll 2
+            for (int k = 0; k < D; k += 16) {
+                _Float16 r[16];
+#pragma unroll
+                for (int j = 0; j < 16; ++j) r[j] = rotation_lds[(k + j) * D + c];
+                float4 qv[4];
+#pragma unroll
+                for (int j = 0; j < 4; ++j) qv[j] = *reinterpret_cast<const float4*>(q_lds + k + 4 * j);
+                __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    a[0] = fmaf(qv[j].x, (float)r[4 * j], a[0]);
+                    a[1] = fmaf(qv[j].y, (float)r[4 * j + 1], a[1]);
+                    a[2] = fmaf(qv[j].z, (float)r[4 * j + 2], a[2]);
+                    a[3] = fmaf(qv[j].w, (float)r[4 * j + 3], a[3]);
+                }
             }
         }
         qr = (a[0] + a[1]) + (a[2] + a[3]);
@@ -159,9 +202,9 @@ __device__ __forceinline__ void prepare_record(const AttentionParams& p, int hea
 
     float parts[4];
     parts[0] = q * k_live;
-    parts[1] = (active && p.key_mean_loop) ? qr * p.key_mean_loop[head * D + c] : 0.f;
+    parts[1] = (active && p.key_mean_loop) ? qr * in.mean_loop : 0.f;
     // The anchor term of residual loops uses the BF16 mean (compute.cuh:327-336).
-    parts[2] = (active && p.key_mean_anchor) ? qr * bf16_f32(bf16_rn(p.key_mean_anchor[head * D + c])) : 0.f;
+    parts[2] = (active && p.key_mean_anchor) ? qr * bf16_f32(bf16_rn(in.mean_anchor)) : 0.f;
     parts[3] = fabsf(qr);
 #pragma unroll
     for (int d = 32; d; d >>= 1) {
@@ -234,11 +277,13 @@ __global__ __launch_bounds__(128) void prepare_kernel(AttentionParams p) {
     const int head = blockIdx.y;
     const int64_t rh = row * p.heads + head;
     if (threadIdx.x == 0) p.arrivals[rh] = 0;
-    const PrepareInputs in = prepare_load<D>(p, row, head, rotation_lds);
+    PrepareInputs<D, 128> in;
+    prepare_load<D, 128>(p, row, head, in);
     const int request = find_request_parallel(p.query_start_loc, p.requests, row, request_counts);
     if (head == 0 && threadIdx.x == 0) p.row_request[row] = request;
     if (request < 0) return;
-    prepare_record<D>(p, head, in, p.prep + rh * (int64_t)kPrepFloats, rotation_lds);
+    prepare_stage<D, 128>(p, in, rotation_lds);
+    prepare_record<D, 128>(p, head, in, p.prep + rh * (int64_t)kPrepFloats, rotation_lds);
 }
 
 // ------------------------------------------------------------------ packed decode
@@ -783,43 +828,28 @@ void decode_kernel(AttentionParams p) {
     __shared__ int request_counts[kWaves];
 
     // With one split per (row, head) this workgroup prepares its own query;
-    // otherwise prepare_kernel has written the record.
+    // otherwise prepare_kernel has written the record.  The request lookup
+    // comes first either way, so the first units' page loads are in flight
+    // while the query record is computed (the loop's first iteration uses them).
     int request;
+    PrepareInputs<D, kDecodeThreads> in;
+    _Float16* rotation_lds = reinterpret_cast<_Float16*>(scratch_lds);
     if (p.fused_prepare) {
-        _Float16* rotation_lds = reinterpret_cast<_Float16*>(scratch_lds);
-        const PrepareInputs in = prepare_load<D>(p, row, head, rotation_lds);
+        prepare_load<D, kDecodeThreads>(p, row, head, in);
         request = find_request_parallel(p.query_start_loc, p.requests, row, request_counts);
-        if (request < 0) return;
-        prepare_record<D>(p, head, in, prep_lds, rotation_lds);
+        if (request >= 0) prepare_stage<D, kDecodeThreads>(p, in, rotation_lds);
     } else {
         request = p.row_request[row];
-        if (request < 0) return;
-        const float* src = p.prep + rh * (int64_t)kPrepFloats;
-        for (int i = threadIdx.x; i < kPrepFloats; i += kDecodeThreads) prep_lds[i] = src[i];
-        __syncthreads();
     }
-    const SplitRange range = split_range(p, request, split);
+    if (request < 0) return;
+    // The range is the same in every lane; kept in scalar registers so the
+    // block table below is read with scalar loads.
+    request = __builtin_amdgcn_readfirstlane(request);
+    SplitRange range = split_range(p, request, split);
+    range.history = uniform64(range.history);
+    range.unit_begin = uniform64(range.unit_begin);
+    range.unit_end = uniform64(range.unit_end);
     float* partial = p.partials + (rh * p.splits + split) * (int64_t)(D + 2);
-
-    const float* prep = prep_lds;
-    if (threadIdx.x < 128) {
-        // thread -> (quarter, record, word, plane); prep stores [plane][word] per order
-        const int quarter = threadIdx.x >> 5, record = (threadIdx.x >> 4) & 1;
-        const int word = (threadIdx.x >> 2) & 3, plane = threadIdx.x & 3;
-        const int bits = record == 0 ? BA : BL;
-        const uint32_t* base = reinterpret_cast<const uint32_t*>(prep + kPrepScalars + kPrepQuery) +
-                               (bits == 2 ? kPrepPlanes : 0);
-        planes_lds[quarter][record * 4 + word][plane] =
-            quarter < Quarters ? base[plane * 16 + 4 * quarter + word] : 0u;
-    }
-    const float delta = prep[0];
-    const float q_mean_anchor = prep[2];
-    float q_sum_a[2], q_sum_l[2];
-    group_sums<GA>(prep, lq, q_sum_a);
-    group_sums<GL>(prep, lq, q_sum_l);
-    __syncthreads();
-    const uint32_t* planes_a = &planes_lds[lq][0][0];
-    const uint32_t* planes_l = &planes_lds[lq][4][0];
 
     // Per-lane byte offsets inside a page (first 16-token half); the second
     // half of a 32-token page adds a wave-uniform step per region.
@@ -831,20 +861,33 @@ void decode_kernel(AttentionParams p) {
     const uint32_t off_offs_l = off_scale_l + PT * GroupsL;
     const uint32_t off_alpha = p.residual.offset + PT * (CodeL + 2 * GroupsL) + 2 * t;
 
-    float acc[32];
-#pragma unroll
-    for (int i = 0; i < 32; ++i) acc[i] = 0.f;
-    float cst0 = 0.f, cst1 = 0.f;
-    float m = -INFINITY, l = 0.f;
-
-    const int32_t* table = p.block_table + (int64_t)range.request * p.block_table_stride;
+    // Block table entries are read through the scalar cache: their waits
+    // (lgkmcnt) are not ordered behind the page loads in flight (vmcnt counts
+    // vector loads in issue order, so a vector read of the next entry would
+    // wait for every page load issued before it).
+    const ConstantInt32* table =
+        (const ConstantInt32*)(p.block_table + (int64_t)range.request * p.block_table_stride);
     const int64_t page_bytes = (int64_t)PT * p.page_width;
     const int64_t history = range.history;
+    // Units u (even) and u + 1 share a page when a page holds an even number of units.
+    constexpr bool kPairSharesPage = UnitsPerPage % 2 == 0;
+    struct PairBlocks {
+        int first, second;
+    };
+    auto pair_blocks = [&](int64_t u) -> PairBlocks {
+        PairBlocks b{-1, -1};
+        if (u < range.unit_end) {
+            b.first = table[u / UnitsPerPage];
+            if (kPairSharesPage)
+                b.second = b.first;
+            else if (u + 1 < range.unit_end)
+                b.second = table[(u + 1) / UnitsPerPage];
+        }
+        return b;
+    };
 
-    auto load_unit = [&](int64_t u, Unit<BA, GA, BL, GL, HasL>& d) -> bool {
-        const int64_t page_index = u / UnitsPerPage;
+    auto load_unit = [&](int block, int64_t u, Unit<BA, GA, BL, GL, HasL>& d) -> bool {
         const int half = (int)(u % UnitsPerPage);
-        const int block = __builtin_amdgcn_readfirstlane(table[page_index]);
         if (block < 0 || block >= p.num_blocks) return false;
         const uint8_t* kbase = p.cache + ((int64_t)block * p.heads + head) * page_bytes;
         const __amdgpu_buffer_rsrc_t kpage = page_resource(kbase, (uint32_t)page_bytes);
@@ -868,6 +911,52 @@ void decode_kernel(AttentionParams p) {
         }
         return true;
     };
+
+    const int64_t first = range.unit_begin + 2 * wave;
+    Unit<BA, GA, BL, GL, HasL> d0, d1;
+    bool ok0 = false, ok1 = false;
+    // The prologue's own loads have all been consumed or are due now; with
+    // nothing older outstanding, the record's arithmetic below waits for none
+    // of the page loads.
+    wait_vector_memory();
+    PairBlocks blocks = pair_blocks(first);
+    ok0 = first < range.unit_end && load_unit(blocks.first, first, d0);
+    ok1 = first + 1 < range.unit_end && load_unit(blocks.second, first + 1, d1);
+    // Table entries of the next iteration, read while this one computes.
+    blocks = pair_blocks(first + 2 * kWaves);
+
+    if (p.fused_prepare) {
+        prepare_record<D, kDecodeThreads>(p, head, in, prep_lds, rotation_lds);
+    } else {
+        const float* src = p.prep + rh * (int64_t)kPrepFloats;
+        for (int i = threadIdx.x; i < kPrepFloats; i += kDecodeThreads) prep_lds[i] = src[i];
+        __syncthreads();
+    }
+    const float* prep = prep_lds;
+    if (threadIdx.x < 128) {
+        // thread -> (quarter, record, word, plane); prep stores [plane][word] per order
+        const int quarter = threadIdx.x >> 5, record = (threadIdx.x >> 4) & 1;
+        const int word = (threadIdx.x >> 2) & 3, plane = threadIdx.x & 3;
+        const int bits = record == 0 ? BA : BL;
+        const uint32_t* base = reinterpret_cast<const uint32_t*>(prep + kPrepScalars + kPrepQuery) +
+                               (bits == 2 ? kPrepPlanes : 0);
+        planes_lds[quarter][record * 4 + word][plane] =
+            quarter < Quarters ? base[plane * 16 + 4 * quarter + word] : 0u;
+    }
+    const float delta = prep[0];
+    const float q_mean_anchor = prep[2];
+    float q_sum_a[2], q_sum_l[2];
+    group_sums<GA>(prep, lq, q_sum_a);
+    group_sums<GL>(prep, lq, q_sum_l);
+    __syncthreads();
+    const uint32_t* planes_a = &planes_lds[lq][0][0];
+    const uint32_t* planes_l = &planes_lds[lq][4][0];
+
+    float acc[32];
+#pragma unroll
+    for (int i = 0; i < 32; ++i) acc[i] = 0.f;
+    float cst0 = 0.f, cst1 = 0.f;
+    float m = -INFINITY, l = 0.f;
 
     // Values of one unit: acc += p * (alpha_v * deq_A + deq_L); offsets go to cst.
     auto accumulate = [&](const Unit<BA, GA, BL, GL, HasL>& d, float prob) {
@@ -894,13 +983,14 @@ void decode_kernel(AttentionParams p) {
         accumulate_codes<BA>(d.vca, w_a, acc);
     };
 
-    // Each iteration streams two consecutive 16-token units of the split.
-    const int64_t first = range.unit_begin + 2 * wave;
+    // Each iteration streams two consecutive 16-token units of the split
+    // (the first iteration's were loaded before the query preparation).
     for (int64_t u = first; u < range.unit_end; u += 2 * kWaves) {
-        Unit<BA, GA, BL, GL, HasL> d0, d1;
-        const bool ok0 = load_unit(u, d0);
-        const bool has1 = u + 1 < range.unit_end;
-        const bool ok1 = has1 && load_unit(u + 1, d1);
+        if (u != first) {
+            ok0 = load_unit(blocks.first, u, d0);
+            ok1 = u + 1 < range.unit_end && load_unit(blocks.second, u + 1, d1);
+            blocks = pair_blocks(u + 2 * kWaves);
+        }
         const int64_t pos0 = (u / UnitsPerPage) * PT + (u % UnitsPerPage) * kUnitTokens + t;
         const int64_t pos1 = ((u + 1) / UnitsPerPage) * PT + ((u + 1) % UnitsPerPage) * kUnitTokens + t;
         const bool valid0 = ok0 && lane_active && pos0 < history;

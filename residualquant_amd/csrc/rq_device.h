@@ -137,6 +137,18 @@ __device__ __forceinline__ float4 handoff_load4(__amdgpu_buffer_rsrc_t r, uint32
     return make_float4(__uint_as_float(v[0]), __uint_as_float(v[1]), __uint_as_float(v[2]), __uint_as_float(v[3]));
 }
 
+// A value known to be equal in every lane, moved to scalar registers.
+__device__ __forceinline__ int64_t uniform64(int64_t x) {
+    const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)x);
+    const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)((uint64_t)x >> 32));
+    return (int64_t)(((uint64_t)hi << 32) | lo);
+}
+
+// Global memory read through the scalar cache (constant address space):
+// loads from a wave-uniform address compile to s_load.  Only for data no
+// kernel writes while the reading kernel runs.
+typedef const int32_t __attribute__((address_space(4))) ConstantInt32;
+
 // s_waitcnt vmcnt(0) expcnt(7) lgkmcnt(15): only outstanding vector memory
 // operations (loads and stores) are waited for.
 __device__ __forceinline__ void wait_vector_memory() { __builtin_amdgcn_s_waitcnt(0xF70); }

@@ -40,6 +40,19 @@ from . import ops, step_ops, workloads
 from .layout import page_width
 
 
+def _project(x: torch.Tensor, weight: torch.Tensor) -> torch.Tensor:
+    """``x @ weight.T`` for a linear weight held ``[out, in]``.
+
+    With one row the product is issued as ``weight @ x.T`` ([out, 1], the same
+    bytes as [1, out]): hipBLASLt streams the weights through its matrix-vector
+    kernels that way, 37.7 µs instead of 47.8 µs for the four projections of
+    one layer at hidden 2048.  Larger batches keep ``F.linear``, which is as
+    fast or faster there."""
+    if x.shape[0] == 1:
+        return torch.mm(weight, x.t()).view(1, -1)
+    return F.linear(x, weight)
+
+
 @dataclass
 class LoopedConfig:
     """Ouro-2.6B-shaped decoder.
@@ -167,7 +180,7 @@ class LoopedDecoder:
             x = step_ops.rms_norm(h, self.norms[0][0], eps)
             for layer in range(c.layers):
                 norms = self.norms[layer]
-                qkv = F.linear(x, self.qkv[layer])
+                qkv = _project(x, self.qkv[layer])
                 key_stage, value_stage = self.staged[layer, loop, 0], self.staged[layer, loop, 1]
                 q, k = step_ops.rope_qkv(qkv, self.positions, self.cos, self.sin, c.heads, c.head_dim,
                                          key_stage=key_stage, value_stage=value_stage)
@@ -179,16 +192,16 @@ class LoopedDecoder:
                     pairs = [(self.staged[layer, r, 0], self.staged[layer, r, 1]) for r in range(c.loops)]
                     ops.quantize(pairs, self.caches[layer], self.slots, self.key_rotation[layer],
                                  self.value_rotation[layer], None, c.schedule, "anchor", c.anchor, c.coefficient)
-                a = F.linear(self.attn_out.view(self.batch, q_size), self.o[layer])
+                a = _project(self.attn_out.view(self.batch, q_size), self.o[layer])
                 # input_layernorm_2 then post_attention_layernorm with the fused add (ouro.py:154-155), one launch.
                 x, _ = step_ops.rms_norm(a, norms[2], eps, residual=self.residual, pre_weight=norms[1])
-                m = F.linear(step_ops.silu_mul(F.linear(x, self.gate_up[layer])), self.down[layer])
+                m = _project(step_ops.silu_mul(_project(x, self.gate_up[layer])), self.down[layer])
                 # post_attention_layernorm_2 (ouro.py:157), then the next layer's input_layernorm
                 # with the fused add (:151-152) or the loop's final norm (:240), one launch.
                 following = self.norms[layer + 1][0] if layer + 1 < c.layers else self.final_norm
                 x, _ = step_ops.rms_norm(m, following, eps, residual=self.residual, pre_weight=norms[3])
             h = x
-        logits = F.linear(h, self.lm_head)
+        logits = _project(h, self.lm_head)
         # Greedy next token and the next position, slot and sequence length.
         self.tokens.copy_(logits.argmax(dim=-1))
         self.positions.add_(1)

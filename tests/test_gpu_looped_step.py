@@ -18,19 +18,21 @@ pytestmark = pytest.mark.gpu
 TINY = LoopedConfig(layers=2, loops=4, hidden=256, heads=2, head_dim=128, intermediate=512, vocab=1000)
 
 
-def _model(device):
-    model = LoopedDecoder(TINY, batch=3, context=37, max_new_tokens=8, device=device, seed=3)
+def _model(device, batch=3):
+    model = LoopedDecoder(TINY, batch=batch, context=37, max_new_tokens=8, device=device, seed=3)
     model.build_history(seed=5)
     return model
 
 
-def test_graph_replay_matches_eager_steps(device):
-    eager, graphed = _model(device), _model(device)
+@pytest.mark.parametrize("batch", [3, 1])
+def test_graph_replay_matches_eager_steps(device, batch):
+    """Batch 1 takes the matrix-vector form of the projections."""
+    eager, graphed = _model(device, batch), _model(device, batch)
     for a, b in zip(eager.caches, graphed.caches):
         assert torch.equal(a, b)
     graphed.capture()
     for step in range(4):
-        print(f"looped step {step}", flush=True)
+        print(f"looped step {step} batch {batch}", flush=True)
         logits = eager.step()
         graphed.graph.replay()
         torch.cuda.synchronize()
@@ -58,3 +60,15 @@ def test_step_writes_the_new_token_of_every_layer(device):
         # token's bytes are spread over the page).
         touched = {int(b) for b in changed[:, 1]}
         assert touched <= {int(s) // pt for s in slots}, layer
+
+
+def test_single_row_projection_matches_linear(device):
+    from residualquant_amd.looped_decode import _project
+
+    g = torch.Generator(device=device).manual_seed(11)
+    weight = (torch.randn((3072, 2048), generator=g, device=device) * 0.02).to(torch.bfloat16)
+    x = torch.randn((1, 2048), generator=g, device=device).to(torch.bfloat16)
+    got = _project(x, weight)
+    assert got.shape == (1, 3072) and got.is_contiguous()
+    want = x.float() @ weight.float().t()
+    assert ((got.float() - want).abs() <= want.abs() * 2.0 ** -7 + 1e-3).all()
