@@ -7,20 +7,26 @@
 // against q' = (q . R_k) / sqrt(D); the live token is folded in at the merge;
 // the history value sum is inverse-rotated by R_v when given.
 //
-// Two launches per call, both with grids fixed by host shapes:
+// Launches, with grids fixed by host shapes:
 //   prepare  (rows x heads)          q' in log2 units, live score, group sums
 //                                    of q', q' as 16-bit integers split into
-//                                    four nibble planes for v_dot8_u32_u4;
+//                                    four nibble planes for v_dot8_u32_u4
+//                                    (with one split per (row, head) the
+//                                    decode workgroup does this itself and
+//                                    the call is one launch);
 //   decode   (rows x heads x splits) one workgroup = 4 waves streaming the
-//                                    pages of one split; each wave owns one
-//                                    16-token unit at a time, lane = token x
-//                                    32-channel quarter; QK on integer dot8
-//                                    units, PV in FP32 registers, online
-//                                    softmax per wave, LDS merge of the waves;
-//                                    the split that finishes last for its
-//                                    (row, head) does the log-sum-exp merge of
-//                                    the splits and the live token, the V
-//                                    inverse rotation and the BF16 output.
+//                                    pages of one split, two 16-token units
+//                                    per wave iteration; lane = token x
+//                                    32-channel quarter (decode_kernel), or
+//                                    token x 48-channel half for D = 96
+//                                    residual loops (decode96_kernel); QK on
+//                                    integer dot8 units, PV in FP32 registers,
+//                                    online softmax per wave, LDS merge of the
+//                                    waves; the split that finishes last for
+//                                    its (row, head) does the log-sum-exp
+//                                    merge of the splits and the live token,
+//                                    the V inverse rotation and the BF16
+//                                    output.
 // The BF16 baseline keeps a separate merge launch.
 #include "rq_device.h"
 #include "rq_kernels.h"
@@ -507,9 +513,7 @@ __device__ __forceinline__ SplitResult merge_waves(float (&acc)[32], float m, fl
 
 // Writes (m, l, acc[D]) of this split for the merge.
 template <int D>
-__device__ __forceinline__ void write_partial(float (&acc)[32], float m, float l_lane, int lane,
-                                              int wave, bool lane_active, float* partial, float* lds) {
-    const SplitResult r = merge_waves<D>(acc, m, l_lane, lane, wave, lane_active, lds);
+__device__ __forceinline__ void write_partial(const SplitResult& r, float* partial) {
     const int c = threadIdx.x;
     const __amdgpu_buffer_rsrc_t out = handoff_resource(partial, (D + 2) * 4);
     if (c < D) handoff_store(out, 8 + 4 * c, r.sum);
@@ -519,14 +523,14 @@ __device__ __forceinline__ void write_partial(float (&acc)[32], float m, float l
     }
 }
 
-// One split covers the whole history of this (row, head): merge the waves,
-// fold in the live token, inverse-rotate V and write the BF16 output without
-// a round trip through the partials.  R_v row c, the live score and the live
-// value are loaded before the wave merge so their latency overlaps it.
-template <int D>
-__device__ __forceinline__ void finish_single(const AttentionParams& p, int64_t row, int head, float (&acc)[32],
-                                              float m, float l_lane, int lane, int wave, bool lane_active,
-                                              float live, float* lds) {
+// One split covers the whole history of this (row, head): merge the waves
+// (`merge_waves()` returns this split's SplitResult), fold in the live token,
+// inverse-rotate V and write the BF16 output without a round trip through the
+// partials.  R_v row c and the live value are loaded before the wave merge so
+// their latency overlaps it.
+template <int D, typename MergeWaves>
+__device__ __forceinline__ void finish_single(const AttentionParams& p, int64_t row, int head, float live,
+                                              MergeWaves merge_waves) {
     __shared__ float hist[128];
     __shared__ float halves[2][128];
     const int tid = threadIdx.x;
@@ -541,7 +545,7 @@ __device__ __forceinline__ void finish_single(const AttentionParams& p, int64_t 
     }
     const float v_live = tid < D ? bf16_f32(p.value[row * p.value_stride + head * D + tid]) : 0.f;
 
-    const SplitResult r = merge_waves<D>(acc, m, l_lane, lane, wave, lane_active, lds);
+    const SplitResult r = merge_waves();
     const float mx = fmaxf(r.m, live);
     const float w_hist = r.m == -INFINITY ? 0.f : exp2f(r.m - mx);
     const float w_live = exp2f(live - mx);
@@ -1038,9 +1042,451 @@ void decode_kernel(AttentionParams p) {
         acc[16 + i] += cst1;
     }
     if (p.splits == 1) {
-        finish_single<D>(p, row, head, acc, m, l, lane, wave, lane_active, prep_lds[1], scratch_lds);
+        finish_single<D>(p, row, head, prep_lds[1],
+                         [&] { return merge_waves<D>(acc, m, l, lane, wave, lane_active, scratch_lds); });
     } else {
-        write_partial<D>(acc, m, l, lane, wave, lane_active, partial, scratch_lds);
+        write_partial<D>(merge_waves<D>(acc, m, l, lane, wave, lane_active, scratch_lds), partial);
+        finish_split<D>(p, row, head);
+    }
+}
+
+// ------------------------------------------------------------------ D = 96 packed decode
+//
+// decode_kernel maps lane = token x 32-channel quarter, which leaves one lane
+// in four idle at D = 96.  decode96_kernel gives every lane one token's
+// 48-channel half instead: lane = 2 * slot + half, and a wave iteration covers
+// two 16-token units (slots 0..15: unit u, slots 16..31: unit u + 1).  A half
+// is three 16-channel blocks: six INT4 or three INT2 code words; block b of
+// half h belongs to group (3h + b) * 16 / G.  The two units of an iteration
+// can lie in different pages, so each lane addresses its own page through a
+// buffer resource over the whole K (or V) plane; launch_decode uses this
+// kernel when a plane fits in 4 GiB of buffer offsets.
+
+template <int Bits>
+struct HalfCodes {
+    static constexpr int kWords = Bits == 4 ? 6 : 3;
+    uint32_t w[kWords];
+};
+
+template <int Bits>
+__device__ __forceinline__ void load_half_codes(__amdgpu_buffer_rsrc_t plane, uint32_t offset, HalfCodes<Bits>& c) {
+    const auto a = __builtin_amdgcn_raw_buffer_load_b96(plane, offset, 0, 0);
+    c.w[0] = a[0]; c.w[1] = a[1]; c.w[2] = a[2];
+    if constexpr (Bits == 4) {
+        const auto b = __builtin_amdgcn_raw_buffer_load_b96(plane, offset + 12, 0, 0);
+        c.w[3] = b[0]; c.w[4] = b[1]; c.w[5] = b[2];
+    }
+}
+
+// Raw FP8 scale/offset bytes of a half's groups, first group in byte 0:
+// three groups for G16 (one per block), two for G32 (groups h and h + 1).
+// Each is one 8-byte load from the 4-byte-aligned address at or below the
+// first byte, shifted into place (v_alignbyte): fewer, wider loads than one
+// per byte.
+template <int G>
+struct HalfParams {
+    uint32_t s, o;
+    __device__ __forceinline__ void load(__amdgpu_buffer_rsrc_t plane, uint32_t scale_word, uint32_t offset_word,
+                                         uint32_t shift) {
+        const auto sv = __builtin_amdgcn_raw_buffer_load_b64(plane, scale_word, 0, 0);
+        const auto ov = __builtin_amdgcn_raw_buffer_load_b64(plane, offset_word, 0, 0);
+        s = __builtin_amdgcn_alignbyte(sv[1], sv[0], shift);
+        o = __builtin_amdgcn_alignbyte(ov[1], ov[0], shift);
+    }
+    // Scale and offset of each of the three blocks of half `upper`.
+    __device__ __forceinline__ void decode(bool upper, float (&scale)[3], float (&offset)[3]) const {
+        if constexpr (G == 16) {
+            scale[0] = fp8_f32<0>(s); scale[1] = fp8_f32<1>(s); scale[2] = fp8_f32<2>(s);
+            offset[0] = fp8_f32<0>(o); offset[1] = fp8_f32<1>(o); offset[2] = fp8_f32<2>(o);
+        } else {
+            const float s0 = fp8_f32<0>(s), s1 = fp8_f32<1>(s);
+            const float o0 = fp8_f32<0>(o), o1 = fp8_f32<1>(o);
+            scale[0] = s0; scale[1] = upper ? s1 : s0; scale[2] = s1;
+            offset[0] = o0; offset[1] = upper ? o1 : o0; offset[2] = o1;
+        }
+    }
+};
+
+// Integer q'.codes of the half's three blocks.  planes[i][j] (LDS): nibble
+// plane j of the half's i-th plane word (INT4: code word i; INT2: even (2b) /
+// odd (2b + 1) channels of code word b), one 16-byte read per word.
+template <int Bits>
+__device__ __forceinline__ void half_dots(const HalfCodes<Bits>& c, const uint32_t (*planes)[4], int (&dot)[3]) {
+    uint32_t d[3][4] = {};
+    uint32_t n[3] = {0u, 0u, 0u};
+    constexpr uint32_t kOnes = 0x11111111u;
+    if constexpr (Bits == 4) {
+#pragma unroll
+        for (int i = 0; i < 6; ++i) {
+            const int b = i >> 1;
+            const uint4 q = *reinterpret_cast<const uint4*>(planes[i]);
+            const uint32_t qj[4] = {q.x, q.y, q.z, q.w};
+#pragma unroll
+            for (int j = 0; j < 4; ++j) d[b][j] = __builtin_amdgcn_udot8(qj[j], c.w[i], d[b][j], false);
+            n[b] = __builtin_amdgcn_udot8(kOnes, c.w[i], n[b], false);
+        }
+    } else {
+#pragma unroll
+        for (int b = 0; b < 3; ++b) {
+            const uint32_t even = c.w[b] & 0x33333333u, odd = (c.w[b] >> 2) & 0x33333333u;
+            const uint4 qe = *reinterpret_cast<const uint4*>(planes[2 * b]);
+            const uint4 qo = *reinterpret_cast<const uint4*>(planes[2 * b + 1]);
+            const uint32_t ej[4] = {qe.x, qe.y, qe.z, qe.w};
+            const uint32_t oj[4] = {qo.x, qo.y, qo.z, qo.w};
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                d[b][j] = __builtin_amdgcn_udot8(ej[j], even, d[b][j], false);
+                d[b][j] = __builtin_amdgcn_udot8(oj[j], odd, d[b][j], false);
+            }
+            n[b] = __builtin_amdgcn_udot8(kOnes, even, __builtin_amdgcn_udot8(kOnes, odd, n[b], false), false);
+        }
+    }
+#pragma unroll
+    for (int b = 0; b < 3; ++b)
+        dot[b] = (int)(d[b][0] + 16u * d[b][1] + 256u * d[b][2] + 4096u * d[b][3]) - 32768 * (int)n[b];
+}
+
+// Lane part of one record's score: sum over the half's blocks of
+// scale * delta * (q_int . codes) + offset * sum(q').
+__device__ __forceinline__ float half_score(const float (&scale)[3], const float (&offset)[3], const int (&dot)[3],
+                                            float delta, const float (&q_sum)[3]) {
+    float s = 0.f;
+#pragma unroll
+    for (int b = 0; b < 3; ++b) s += scale[b] * (delta * (float)dot[b]) + offset[b] * q_sum[b];
+    return s;
+}
+
+// acc[16b + i] += weight[b] * code over the half's 48 channels (codes are
+// FP8 E4M3 values c * 2^-9 when held in a byte, as in accumulate_codes).
+template <int Bits>
+__device__ __forceinline__ void accumulate_half(const HalfCodes<Bits>& c, const float (&weight)[3],
+                                                float (&acc)[48]) {
+    if constexpr (Bits == 4) {
+#pragma unroll
+        for (int i = 0; i < 6; ++i) {
+            const float w = weight[i >> 1];
+            const int lo = (int)(c.w[i] & 0x0f0f0f0fu);
+            const int hi = (int)((c.w[i] >> 4) & 0x0f0f0f0fu);
+            const auto l01 = __builtin_amdgcn_cvt_pk_f32_fp8(lo, false);
+            const auto l23 = __builtin_amdgcn_cvt_pk_f32_fp8(lo, true);
+            const auto h01 = __builtin_amdgcn_cvt_pk_f32_fp8(hi, false);
+            const auto h23 = __builtin_amdgcn_cvt_pk_f32_fp8(hi, true);
+            float* a = acc + 8 * i;
+            a[0] = fmaf(w, l01[0], a[0]);
+            a[2] = fmaf(w, l01[1], a[2]);
+            a[4] = fmaf(w, l23[0], a[4]);
+            a[6] = fmaf(w, l23[1], a[6]);
+            a[1] = fmaf(w, h01[0], a[1]);
+            a[3] = fmaf(w, h01[1], a[3]);
+            a[5] = fmaf(w, h23[0], a[5]);
+            a[7] = fmaf(w, h23[1], a[7]);
+        }
+    } else {
+#pragma unroll
+        for (int b = 0; b < 3; ++b) {
+            const float w = weight[b];
+            float* a = acc + 16 * b;
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                const int part = (int)((c.w[b] >> (2 * k)) & 0x03030303u);  // byte j: channel 4j + k
+                const auto c01 = __builtin_amdgcn_cvt_pk_f32_fp8(part, false);
+                const auto c23 = __builtin_amdgcn_cvt_pk_f32_fp8(part, true);
+                a[k] = fmaf(w, c01[0], a[k]);
+                a[4 + k] = fmaf(w, c01[1], a[4 + k]);
+                a[8 + k] = fmaf(w, c23[0], a[8 + k]);
+                a[12 + k] = fmaf(w, c23[1], a[12 + k]);
+            }
+        }
+    }
+}
+
+// Max over the wave of one value per token slot (the two lanes of a slot
+// agree), broadcast to every lane.
+__device__ __forceinline__ float slot_wave_max(float x) {
+    x = fmaxf(x, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(x), 0x122, 0xF, 0xF, true)));  // row_ror:2
+    x = fmaxf(x, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(x), 0x124, 0xF, 0xF, true)));  // row_ror:4
+    x = fmaxf(x, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(x), 0x128, 0xF, 0xF, true)));  // row_ror:8
+    const float r0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), 0));
+    const float r1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), 16));
+    const float r2 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), 32));
+    const float r3 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), 48));
+    return fmaxf(fmaxf(r0, r1), fmaxf(r2, r3));
+}
+
+// The four waves' (m, l, acc) of one split in decode96_kernel's layout, merged
+// in LDS: thread c < 96 gets channel c of the unnormalized output, every
+// thread gets m and l.  Slot pairs are added with DPP first, so the LDS holds
+// [wave][slot pair][96] (kWaves * 16 * 96 floats of `lds`).
+__device__ __forceinline__ SplitResult merge_waves_half(float (&acc)[48], float m, float l_lane, int lane,
+                                                        int wave, float* lds) {
+    constexpr int D = 96;
+    float (*red_acc)[16][D] = reinterpret_cast<float (*)[16][D]>(lds);
+    __shared__ float red_m[kWaves], red_l[kWaves];
+    float l_wave = l_lane;  // carried by the half-0 lanes only
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) l_wave += __shfl_xor(l_wave, d);
+    if (lane == 0) {
+        red_m[wave] = m;
+        red_l[wave] = l_wave;
+    }
+    __syncthreads();
+    float m_all = red_m[0];
+#pragma unroll
+    for (int w = 1; w < kWaves; ++w) m_all = fmaxf(m_all, red_m[w]);
+    const float wave_scale = m == -INFINITY ? 0.f : exp2f(m - m_all);
+    float pair[48];
+#pragma unroll
+    for (int i = 0; i < 48; ++i) pair[i] = (acc[i] + quad_xor2(acc[i])) * wave_scale;  // slots 2k, 2k + 1
+    if ((lane & 2) == 0) {
+        float* dst = &red_acc[wave][lane >> 2][48 * (lane & 1)];
+#pragma unroll
+        for (int i = 0; i < 48; i += 4) *reinterpret_cast<float4*>(dst + i) = make_float4(pair[i], pair[i + 1], pair[i + 2], pair[i + 3]);
+    }
+    __syncthreads();
+    SplitResult r;
+    r.m = m_all;
+    r.l = 0.f;
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) r.l += red_m[w] == -INFINITY ? 0.f : red_l[w] * exp2f(red_m[w] - m_all);
+    r.sum = 0.f;
+    const int c = threadIdx.x;
+    if (c < D) {
+#pragma unroll
+        for (int w = 0; w < kWaves; ++w)
+#pragma unroll
+            for (int k = 0; k < 16; ++k) r.sum += red_acc[w][k][c];
+    }
+    return r;
+}
+
+// Registers of one lane's token: K/V codes, raw FP8 parameters, alphas.
+template <int BA, int GA, int BL, int GL, bool HasL>
+struct HalfUnit {
+    HalfCodes<BA> kca, vca;
+    HalfParams<GA> kpa, vpa;
+    HalfCodes<BL> kcl, vcl;
+    HalfParams<GL> kpl, vpl;
+    uint32_t alpha_k_bits, alpha_v_bits;
+};
+
+template <int PT, int BA, int GA, int BL, int GL, bool HasL>
+__global__ __launch_bounds__(kDecodeThreads) __attribute__((amdgpu_waves_per_eu(RQ_DECODE_MIN_WAVES)))
+void decode96_kernel(AttentionParams p) {
+    constexpr int D = 96;
+    constexpr int UnitsPerPage = PT / kUnitTokens;
+    constexpr int CodeA = D * BA / 8, GroupsA = D / GA;
+    constexpr int CodeL = D * BL / 8, GroupsL = D / GL;
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int slot = lane >> 1;          // token slot of the iteration, 0..31
+    const int h = lane & 1;              // channel half
+    const bool upper = slot >= 16;       // slot on the iteration's second unit
+    const int tok = PT == 32 ? slot : (slot & 15);  // token row inside the slot's page
+    const int split = blockIdx.x % p.splits;
+    const int64_t rh = blockIdx.x / p.splits;
+    const int head = (int)(rh % p.heads);
+    const int64_t row = rh / p.heads;
+    __shared__ __attribute__((aligned(16))) float prep_lds[kPrepFloats];
+    __shared__ __attribute__((aligned(16))) uint32_t half_planes[2][2][6][4];
+    // R_k staging of the fused prepare, then the wave merge at the end.
+    __shared__ __attribute__((aligned(16))) float scratch_lds[kWaves * 16 * 128];
+    __shared__ int request_counts[kWaves];
+
+    // Query record and request lookup as in decode_kernel: the lookup first,
+    // so the first iteration's page loads overlap the record's arithmetic.
+    int request;
+    PrepareInputs<D, kDecodeThreads> in;
+    _Float16* rotation_lds = reinterpret_cast<_Float16*>(scratch_lds);
+    if (p.fused_prepare) {
+        prepare_load<D, kDecodeThreads>(p, row, head, in);
+        request = find_request_parallel(p.query_start_loc, p.requests, row, request_counts);
+        if (request >= 0) prepare_stage<D, kDecodeThreads>(p, in, rotation_lds);
+    } else {
+        request = p.row_request[row];
+    }
+    if (request < 0) return;
+    request = __builtin_amdgcn_readfirstlane(request);
+    SplitRange range = split_range(p, request, split);
+    range.history = uniform64(range.history);
+    range.unit_begin = uniform64(range.unit_begin);
+    range.unit_end = uniform64(range.unit_end);
+    float* partial = p.partials + (rh * p.splits + split) * (int64_t)(D + 2);
+
+    // Lane offsets inside a page (the page offset is added per iteration).
+    // Parameter regions start 16-byte aligned (pages and record regions are
+    // multiples of 16 bytes), so the 4-byte alignment of a lane's first group
+    // byte is fixed per lane.
+    const uint32_t first_a = tok * GroupsA + (GA == 16 ? 3 * h : h);
+    const uint32_t first_l = tok * GroupsL + (GL == 16 ? 3 * h : h);
+    const uint32_t shift_a = first_a & 3u, shift_l = first_l & 3u;
+    const uint32_t off_codes_a = p.anchor.offset + tok * CodeA + h * (CodeA / 2);
+    const uint32_t off_scale_a = p.anchor.offset + PT * CodeA + (first_a & ~3u);
+    const uint32_t off_offs_a = off_scale_a + PT * GroupsA;
+    const uint32_t off_codes_l = p.residual.offset + tok * CodeL + h * (CodeL / 2);
+    const uint32_t off_scale_l = p.residual.offset + PT * CodeL + (first_l & ~3u);
+    const uint32_t off_offs_l = off_scale_l + PT * GroupsL;
+    const uint32_t off_alpha = p.residual.offset + PT * (CodeL + 2 * GroupsL) + 2 * tok;
+
+    const ConstantInt32* table =
+        (const ConstantInt32*)(p.block_table + (int64_t)range.request * p.block_table_stride);
+    const uint32_t page_bytes = (uint32_t)PT * (uint32_t)p.page_width;
+    const __amdgpu_buffer_rsrc_t kplane = page_resource(p.cache, (uint32_t)p.plane_stride);
+    const __amdgpu_buffer_rsrc_t vplane = page_resource(p.cache + p.plane_stride, (uint32_t)p.plane_stride);
+    constexpr bool kPairSharesPage = UnitsPerPage % 2 == 0;
+    struct PairBlocks {
+        int first, second;
+    };
+    auto pair_blocks = [&](int64_t u) -> PairBlocks {
+        PairBlocks b{-1, -1};
+        if (u < range.unit_end) {
+            b.first = table[u / UnitsPerPage];
+            if (kPairSharesPage)
+                b.second = b.first;
+            else if (u + 1 < range.unit_end)
+                b.second = table[(u + 1) / UnitsPerPage];
+        }
+        return b;
+    };
+
+    // Loads of the lane's token of units (u, u + 1); false if its page is
+    // missing (the lane then reads page 0 and is masked).
+    auto load_slot = [&](const PairBlocks& blocks, HalfUnit<BA, GA, BL, GL, HasL>& d) -> bool {
+        const int block = upper ? blocks.second : blocks.first;
+        const bool ok = block >= 0 && block < p.num_blocks;
+        const uint32_t page = ok ? ((uint32_t)block * (uint32_t)p.heads + (uint32_t)head) * page_bytes : 0u;
+        load_half_codes<BA>(kplane, page + off_codes_a, d.kca);
+        d.kpa.load(kplane, page + off_scale_a, page + off_offs_a, shift_a);
+        load_half_codes<BA>(vplane, page + off_codes_a, d.vca);
+        d.vpa.load(vplane, page + off_scale_a, page + off_offs_a, shift_a);
+        if constexpr (HasL) {
+            load_half_codes<BL>(kplane, page + off_codes_l, d.kcl);
+            d.kpl.load(kplane, page + off_scale_l, page + off_offs_l, shift_l);
+            load_half_codes<BL>(vplane, page + off_codes_l, d.vcl);
+            d.vpl.load(vplane, page + off_scale_l, page + off_offs_l, shift_l);
+            d.alpha_k_bits = __builtin_amdgcn_raw_buffer_load_b16(kplane, page + off_alpha, 0, 0);
+            d.alpha_v_bits = __builtin_amdgcn_raw_buffer_load_b16(vplane, page + off_alpha, 0, 0);
+        }
+        return ok;
+    };
+
+    const int64_t first = range.unit_begin + 2 * wave;
+    HalfUnit<BA, GA, BL, GL, HasL> d;
+    wait_vector_memory();
+    PairBlocks blocks = pair_blocks(first);
+    bool ok = load_slot(blocks, d);
+    blocks = pair_blocks(first + 2 * kWaves);
+
+    if (p.fused_prepare) {
+        prepare_record<D, kDecodeThreads>(p, head, in, prep_lds, rotation_lds);
+    } else {
+        const float* src = p.prep + rh * (int64_t)kPrepFloats;
+        for (int i = threadIdx.x; i < kPrepFloats; i += kDecodeThreads) prep_lds[i] = src[i];
+        __syncthreads();
+    }
+    const float* prep = prep_lds;
+    const float delta = prep[0];
+    const float q_mean_anchor = h == 0 ? prep[2] : 0.f;  // added once per token
+    float q_sum[3];
+#pragma unroll
+    for (int b = 0; b < 3; ++b) q_sum[b] = prep[3 + 3 * h + b];
+    // Nibble planes per half, [record (anchor, loop)][half][word][plane]: the
+    // loop reads one word's four planes with one 16-byte LDS read instead of
+    // holding all 48 in registers (which would cost a wave per SIMD).
+    if (threadIdx.x < 96) {
+        const int record = threadIdx.x / 48, half = (threadIdx.x / 24) & 1;
+        const int word = (threadIdx.x >> 2) % 6, plane = threadIdx.x & 3;
+        const int bits = record == 0 ? BA : BL;
+        const uint32_t* base = reinterpret_cast<const uint32_t*>(prep + kPrepScalars + kPrepQuery) +
+                               (bits == 2 ? kPrepPlanes : 0);
+        half_planes[record][half][word][plane] = base[plane * 16 + 6 * half + word];
+    }
+    __syncthreads();
+    const uint32_t (*planes_a)[4] = half_planes[0][h];
+    const uint32_t (*planes_l)[4] = half_planes[1][h];
+
+    float acc[48];
+#pragma unroll
+    for (int i = 0; i < 48; ++i) acc[i] = 0.f;
+    float cst[3] = {0.f, 0.f, 0.f};
+    float m = -INFINITY, l = 0.f;
+
+    // Each iteration streams units (u, u + 1), one token per lane pair.
+    for (int64_t u = first; u < range.unit_end; u += 2 * kWaves) {
+        // Keeps the plane reads in the loop (nothing in LDS changes here).
+        asm volatile("" ::: "memory");
+        if (u != first) {
+            ok = load_slot(blocks, d);
+            blocks = pair_blocks(u + 2 * kWaves);
+        }
+        const int64_t unit = u + (upper ? 1 : 0);
+        const bool valid = ok && unit < range.unit_end && 16 * unit + (slot & 15) < range.history;
+
+        float sa[3], oa[3];
+        d.kpa.decode(h != 0, sa, oa);
+        int da[3];
+        half_dots<BA>(d.kca, planes_a, da);
+        float s = half_score(sa, oa, da, delta, q_sum);
+        if constexpr (HasL) {
+            float sl[3], ol[3];
+            d.kpl.decode(h != 0, sl, ol);
+            int dl[3];
+            half_dots<BL>(d.kcl, planes_l, dl);
+            s = __uint_as_float(d.alpha_k_bits << 16) * (s + q_mean_anchor) + half_score(sl, ol, dl, delta, q_sum);
+        }
+        float score = s + quad_xor1(s);  // the token's two halves
+        score = valid ? score : -INFINITY;
+
+        const float unit_max = slot_wave_max(score);
+        if (unit_max > m) {
+            const float factor = m == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m - unit_max);
+#pragma unroll
+            for (int i = 0; i < 48; ++i) acc[i] *= factor;
+#pragma unroll
+            for (int b = 0; b < 3; ++b) cst[b] *= factor;
+            l *= factor;
+            m = unit_max;
+        }
+        const float prob = valid ? __builtin_amdgcn_exp2f(score - m) : 0.f;
+        l += h == 0 ? prob : 0.f;
+
+        // Values: acc += p * (alpha_v * deq_A + deq_L); offsets go to cst.
+        const float p512 = prob * 512.0f;
+        float sva[3], ova[3];
+        d.vpa.decode(h != 0, sva, ova);
+        float w_a[3];
+        if constexpr (HasL) {
+            const float alpha_v = __uint_as_float(d.alpha_v_bits << 16);
+            const float pa = prob * alpha_v;
+            const float pa512 = p512 * alpha_v;
+            float svl[3], ovl[3];
+            d.vpl.decode(h != 0, svl, ovl);
+            float w_l[3];
+#pragma unroll
+            for (int b = 0; b < 3; ++b) {
+                w_a[b] = pa512 * sva[b];
+                w_l[b] = p512 * svl[b];
+                cst[b] = fmaf(pa, ova[b], fmaf(prob, ovl[b], cst[b]));
+            }
+            accumulate_half<BL>(d.vcl, w_l, acc);
+        } else {
+#pragma unroll
+            for (int b = 0; b < 3; ++b) {
+                w_a[b] = p512 * sva[b];
+                cst[b] = fmaf(prob, ova[b], cst[b]);
+            }
+        }
+        accumulate_half<BA>(d.vca, w_a, acc);
+    }
+
+#pragma unroll
+    for (int b = 0; b < 3; ++b)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) acc[16 * b + i] += cst[b];
+    if (p.splits == 1) {
+        finish_single<D>(p, row, head, prep_lds[1],
+                         [&] { return merge_waves_half(acc, m, l, lane, wave, scratch_lds); });
+    } else {
+        write_partial<D>(merge_waves_half(acc, m, l, lane, wave, scratch_lds), partial);
         finish_split<D>(p, row, head);
     }
 }
@@ -1129,7 +1575,7 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_bf16_kernel(AttentionPa
         }
     }
     __shared__ __attribute__((aligned(16))) float scratch_lds[kWaves * 16 * 128];
-    write_partial<D>(acc, m, l, lane, wave, lane_active, partial, scratch_lds);
+    write_partial<D>(merge_waves<D>(acc, m, l, lane, wave, lane_active, scratch_lds), partial);
 }
 
 // ------------------------------------------------------------------ launch
@@ -1137,6 +1583,16 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_bf16_kernel(AttentionPa
 template <int D, int PT, int BA, int GA, int BL, int GL, bool HasL>
 void launch_decode(const AttentionParams& p, hipStream_t stream) {
     const unsigned blocks = (unsigned)(p.rows * p.heads * p.splits);
+    if constexpr (D == 96 && HasL) {
+        // Residual loops (the anchor-only loop streams half the bytes per
+        // token and measured faster on decode_kernel).  Per-lane page offsets
+        // are 32-bit buffer offsets into one plane.
+        if (p.plane_stride > 0 && p.plane_stride <= (int64_t)UINT32_MAX) {
+            hipLaunchKernelGGL((decode96_kernel<PT, BA, GA, BL, GL, HasL>), dim3(blocks), dim3(kDecodeThreads), 0,
+                               stream, p);
+            return;
+        }
+    }
     hipLaunchKernelGGL((decode_kernel<D, PT, BA, GA, BL, GL, HasL>), dim3(blocks), dim3(kDecodeThreads), 0,
                        stream, p);
 }

@@ -107,13 +107,16 @@ int compute_units() {
 // Splits per (row, head): about two workgroups per compute unit (long page
 // streams per workgroup measured best at batch 32 x 8k), at least 4 pages per
 // split, at most rq::kMaxSplits.
-int split_count(int64_t rows, int heads, int64_t max_pages) {
+// Splits per (row, head): enough workgroups for `target` (default two per
+// compute unit, or one per compute unit with `one_per_cu`), at least 4 pages
+// per split.
+int split_count(int64_t rows, int heads, int64_t max_pages, bool one_per_cu = false) {
     int64_t target;
     {
         std::lock_guard<std::mutex> lock(g_device_mutex);
         target = g_split_target;
     }
-    if (target <= 0) target = 2LL * compute_units();
+    if (target <= 0) target = (one_per_cu ? 1LL : 2LL) * compute_units();
     const int64_t pairs = std::max<int64_t>(1, rows * heads);
     int64_t splits = (target + pairs - 1) / pairs;
     const int64_t by_pages = std::max<int64_t>(1, (max_pages + 3) / 4);
@@ -267,7 +270,7 @@ static int attention_common(const void* query, int64_t query_stride, const void*
                             int64_t rows, int heads, int head_dim, const int32_t* query_start_loc,
                             const int32_t* seq_lens, int64_t requests, const int32_t* block_table,
                             int64_t block_table_stride, int64_t max_pages, void* workspace,
-                            size_t workspace_bytes, rq::AttentionParams* p) {
+                            size_t workspace_bytes, int splits, rq::AttentionParams* p) {
     if (rows < 0 || heads <= 0) return fail(RQ_EINVAL, "Q/K/V/output must have matching shapes and devices");
     if (rows > 0 && (query == nullptr || key == nullptr || value == nullptr || output == nullptr))
         return fail(RQ_EINVAL, "Q/K/V/output must have matching shapes and devices");
@@ -282,7 +285,6 @@ static int attention_common(const void* query, int64_t query_stride, const void*
         return fail(RQ_EINVAL, "Contiguous INT32 query starts with one final boundary required");
     if (block_table == nullptr || max_pages < 0 || block_table_stride < max_pages)
         return fail(RQ_EINVAL, "INT32 page table with packed rows required");
-    const int splits = split_count(rows, heads, max_pages);
     const WorkspaceLayout layout = workspace_layout(rows, heads, head_dim, splits);
     if (rows > 0 && (workspace == nullptr || workspace_bytes < layout.total))
         return fail(RQ_ENOSPACE, "Attention workspace of %zu bytes required (got %zu)", layout.total,
@@ -345,14 +347,20 @@ int rq_attention(const void* query, int64_t query_stride, const void* key, int64
                     "reference_mode=adjacent, loop_index=%d (adjacent decode covers loop 0)",
                     heads, head_dim, records, loop_index);
     rq::AttentionParams p;
+    // Residual loops at D = 96 run on decode96_kernel (one token half per
+    // lane), which is fastest with one workgroup per (row, head) once those
+    // fill the compute units.  Never more splits than
+    // rq_attention_workspace_bytes() provides for.
+    const int anchor_record = adjacent ? 0 : anchor_index;
+    const int splits = split_count(rows, heads, max_pages, head_dim == 96 && loop_index != anchor_record);
     status = attention_common(query, query_stride, key, key_stride, value, value_stride, output,
                               output_stride, rows, heads, head_dim, query_start_loc, seq_lens, requests,
-                              block_table, block_table_stride, max_pages, workspace, workspace_bytes, &p);
+                              block_table, block_table_stride, max_pages, workspace, workspace_bytes, splits, &p);
     if (status != RQ_OK) return status;
     if (rows == 0) return ok();
     rq::RecordRegion regions[rq::kMaxRecords];
     fill_regions(head_dim, records, bits, groups, page_tokens, regions);
-    const int anchor = adjacent ? 0 : anchor_index;
+    const int anchor = anchor_record;
     p.cache = static_cast<const uint8_t*>(kv_cache);
     p.plane_stride = num_blocks * heads * (int64_t)page_tokens * page_width;
     p.num_blocks = num_blocks;
@@ -424,7 +432,8 @@ int rq_paged_attention_bf16(const void* query, int64_t query_stride, const void*
     rq::AttentionParams p;
     int status = attention_common(query, query_stride, key, key_stride, value, value_stride, output,
                                   output_stride, rows, heads, head_dim, query_start_loc, seq_lens, requests,
-                                  block_table, block_table_stride, max_pages, workspace, workspace_bytes, &p);
+                                  block_table, block_table_stride, max_pages, workspace, workspace_bytes,
+                                  split_count(rows, heads, max_pages), &p);
     if (status != RQ_OK) return status;
     if (rows == 0) return ok();
     p.cache = static_cast<const uint8_t*>(cache);

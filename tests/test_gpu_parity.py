@@ -160,29 +160,41 @@ def test_attention_history_zero_is_live_value(device):
         assert torch.equal(out.cpu(), d.value)
 
 
-def test_attention_split_invariance(oracle, device):
-    """Different split-K counts give outputs within rounding of each other and the oracle."""
-    d = make_decode([700, 129], 2, 128, OURO_G32, seed=9)
+# Residual loops of every (bits, group) the D = 96 decode kernel compiles,
+# INT4 g32 anchor.
+MIXED_D96 = ((2, 16), (4, 16), (2, 32), (4, 32))
+
+
+@pytest.mark.parametrize("dim,records,loops", [(128, OURO_G32, (1,)), (96, MIXED_D96, (0, 1, 2, 3))],
+                         ids=["128d", "96d"])
+def test_attention_split_invariance(oracle, device, dim, records, loops):
+    """Different split-K counts give outputs within rounding of each other and the oracle.
+
+    A target of one workgroup gives one split per (row, head): the decode
+    launch then prepares its own query and finishes without partials."""
+    print(f"split invariance dim={dim}", flush=True)
+    d = make_decode([700, 129], 2, dim, records, seed=9 + dim)
     g = d.group
     cache_np = g.oracle_cache(oracle)
     cache = torch.from_numpy(cache_np).to(device)
     kr, vr, km = g.device_args(device)
-    expected = oracle_attention(oracle, d, cache_np, 1)
-    outs = []
-    try:
-        for target in (1, 8, 64, 4096):
-            rq.ops.set_split_target(target)
-            out = torch.zeros_like(d.query, device=device)
-            rq.attention(d.query.to(device), d.key.to(device), d.value.to(device), cache, out,
-                         d.query_start_loc.to(device), d.seq_lens.to(device), d.table.to(device), kr, vr,
-                         km, g.records, g.mode, g.anchor, 1)
-            outs.append(out.float().cpu().numpy())
-    finally:
-        rq.ops.set_split_target(0)
-    for out in outs:
-        err = np.abs(out - expected)
-        assert err.max() <= MAX_ABS and err.mean() <= MEAN_ABS
-        assert np.abs(out - outs[0]).max() <= 2 * MAX_ABS
+    for loop in loops:
+        expected = oracle_attention(oracle, d, cache_np, loop)
+        outs = []
+        try:
+            for target in (1, 8, 64, 4096):
+                rq.ops.set_split_target(target)
+                out = torch.zeros_like(d.query, device=device)
+                rq.attention(d.query.to(device), d.key.to(device), d.value.to(device), cache, out,
+                             d.query_start_loc.to(device), d.seq_lens.to(device), d.table.to(device), kr, vr,
+                             km, g.records, g.mode, g.anchor, loop)
+                outs.append(out.float().cpu().numpy())
+        finally:
+            rq.ops.set_split_target(0)
+        for out in outs:
+            err = np.abs(out - expected)
+            assert err.max() <= MAX_ABS and err.mean() <= MEAN_ABS, (loop, err.max(), err.mean())
+            assert np.abs(out - outs[0]).max() <= 2 * MAX_ABS
 
 
 def test_paged_attention_bf16_matches_oracle(oracle, device):
