@@ -890,12 +890,17 @@ void decode_kernel(AttentionParams p) {
         return b;
     };
 
+    // Issues the loads of unit u of `block` whether or not the block is valid
+    // (a missing block, or -1 past the range, gets an empty buffer: its loads
+    // read zeros and touch no memory), so no branch sits between the loads of
+    // consecutive units and the compiler can count them (vmcnt) exactly.
     auto load_unit = [&](int block, int64_t u, Unit<BA, GA, BL, GL, HasL>& d) -> bool {
         const int half = (int)(u % UnitsPerPage);
-        if (block < 0 || block >= p.num_blocks) return false;
-        const uint8_t* kbase = p.cache + ((int64_t)block * p.heads + head) * page_bytes;
-        const __amdgpu_buffer_rsrc_t kpage = page_resource(kbase, (uint32_t)page_bytes);
-        const __amdgpu_buffer_rsrc_t vpage = page_resource(kbase + p.plane_stride, (uint32_t)page_bytes);
+        const bool valid = block >= 0 && block < p.num_blocks;
+        const uint8_t* kbase = p.cache + (valid ? ((int64_t)block * p.heads + head) * page_bytes : 0);
+        const uint32_t bytes = valid ? (uint32_t)page_bytes : 0u;
+        const __amdgpu_buffer_rsrc_t kpage = page_resource(kbase, bytes);
+        const __amdgpu_buffer_rsrc_t vpage = page_resource(kbase + (valid ? p.plane_stride : 0), bytes);
         const uint32_t step_codes_a = half * (kUnitTokens * CodeA);
         const uint32_t step_par_a = half * (kUnitTokens * GroupsA);
         load_codes<BA>(kpage, off_codes_a, step_codes_a, d.kca);
@@ -913,7 +918,7 @@ void decode_kernel(AttentionParams p) {
             d.alpha_k_bits = __builtin_amdgcn_raw_buffer_load_b16(kpage, off_alpha, step_alpha, 0);
             d.alpha_v_bits = __builtin_amdgcn_raw_buffer_load_b16(vpage, off_alpha, step_alpha, 0);
         }
-        return true;
+        return valid;
     };
 
     const int64_t first = range.unit_begin + 2 * wave;
@@ -924,8 +929,8 @@ void decode_kernel(AttentionParams p) {
     // of the page loads.
     wait_vector_memory();
     PairBlocks blocks = pair_blocks(first);
-    ok0 = first < range.unit_end && load_unit(blocks.first, first, d0);
-    ok1 = first + 1 < range.unit_end && load_unit(blocks.second, first + 1, d1);
+    ok0 = load_unit(blocks.first, first, d0);
+    ok1 = load_unit(blocks.second, first + 1, d1);
     // Table entries of the next iteration, read while this one computes.
     blocks = pair_blocks(first + 2 * kWaves);
 
@@ -987,19 +992,13 @@ void decode_kernel(AttentionParams p) {
         accumulate_codes<BA>(d.vca, w_a, acc);
     };
 
-    // Each iteration streams two consecutive 16-token units of the split
-    // (the first iteration's were loaded before the query preparation).
-    for (int64_t u = first; u < range.unit_end; u += 2 * kWaves) {
-        if (u != first) {
-            ok0 = load_unit(blocks.first, u, d0);
-            ok1 = u + 1 < range.unit_end && load_unit(blocks.second, u + 1, d1);
-            blocks = pair_blocks(u + 2 * kWaves);
-        }
+    // Scores, softmax and values of the unit pair (u, u + 1) held in (d0, d1).
+    auto process = [&](Unit<BA, GA, BL, GL, HasL>& d0, Unit<BA, GA, BL, GL, HasL>& d1, bool ok0, bool ok1,
+                       int64_t u) {
         const int64_t pos0 = (u / UnitsPerPage) * PT + (u % UnitsPerPage) * kUnitTokens + t;
         const int64_t pos1 = ((u + 1) / UnitsPerPage) * PT + ((u + 1) % UnitsPerPage) * kUnitTokens + t;
         const bool valid0 = ok0 && lane_active && pos0 < history;
         const bool valid1 = ok1 && lane_active && pos1 < history;
-        if (!ok1) d1 = d0;  // keep the registers defined; unit 1 is masked
 
         int da0[2], da1[2];
         code_dots2<BA>(d0.kca, d1.kca, planes_a, da0, da1);
@@ -1034,6 +1033,17 @@ void decode_kernel(AttentionParams p) {
         l += prob0 + prob1;
         accumulate(d0, prob0);
         accumulate(d1, prob1);
+    };
+
+    // Each iteration streams two consecutive 16-token units of the split
+    // (the first iteration's were loaded before the query preparation).
+    for (int64_t u = first; u < range.unit_end; u += 2 * kWaves) {
+        if (u != first) {
+            ok0 = load_unit(blocks.first, u, d0);
+            ok1 = load_unit(blocks.second, u + 1, d1);
+            blocks = pair_blocks(u + 2 * kWaves);
+        }
+        process(d0, d1, ok0, ok1, u);
     }
 
 #pragma unroll
