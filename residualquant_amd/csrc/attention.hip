@@ -1501,6 +1501,214 @@ void decode96_kernel(AttentionParams p) {
     }
 }
 
+// ------------------------------------------------------------------ adjacent mode, loops > 0
+//
+// Adjacent mode stores each loop as a residual of the previous loop, so the
+// key and value of loop L are the BF16 restore chain over records 0..L
+// (compute.cuh:120-197, :506-528): X_0 = bf16(c s + o), X_r = bf16(alpha_r
+// X_{r-1} + bf16(c s + o)), the K plane adding bf16(mu_r) to each record's
+// value except the current loop's (the live score carries -q'.mu_L).  The
+// chain is not linear in the codes, so decode_chain_kernel rebuilds each
+// token's K and V (lane = token x 32-channel quarter, one 16-token unit per
+// wave iteration) and scores and accumulates them in FP32.  Each BF16 step is
+// an FP32 operation rounded once to BF16; the reference rounds the exact
+// value once, and the two differ only when the FP32 result sits on a BF16
+// midpoint it did not reach exactly (within the attention tolerance).
+
+// RNE to BF16 of a finite FP32 value, returned as FP32.
+__device__ __forceinline__ float bf16_round_finite(float f) {
+    uint32_t u = __float_as_uint(f);
+    u += 0x7fffu + ((u >> 16) & 1u);
+    return __uint_as_float(u & 0xffff0000u);
+}
+
+// BF16 values (as FP32) of the lane's 32 channels [32 lq, 32 lq + 32) of one
+// record at token row `tok` of the page: bf16(code * scale + offset).
+template <int PT>
+__device__ __forceinline__ void chain_record(__amdgpu_buffer_rsrc_t page, const RecordRegion& reg, int tok,
+                                             int lq, float (&out)[32]) {
+    const uint32_t params = reg.offset + PT * reg.code_bytes + tok * reg.groups;
+    float scale[2], offset[2];
+    if (reg.group == 32) {
+        const uint32_t s = __builtin_amdgcn_raw_buffer_load_b8(page, params + lq, 0, 0);
+        const uint32_t o = __builtin_amdgcn_raw_buffer_load_b8(page, params + PT * reg.groups + lq, 0, 0);
+        scale[0] = scale[1] = fp8_f32<0>(s) * 512.0f;
+        offset[0] = offset[1] = fp8_f32<0>(o);
+    } else {
+        const uint32_t s = __builtin_amdgcn_raw_buffer_load_b16(page, params + 2 * lq, 0, 0);
+        const uint32_t o = __builtin_amdgcn_raw_buffer_load_b16(page, params + PT * reg.groups + 2 * lq, 0, 0);
+        scale[0] = fp8_f32<0>(s) * 512.0f;
+        scale[1] = fp8_f32<1>(s) * 512.0f;
+        offset[0] = fp8_f32<0>(o);
+        offset[1] = fp8_f32<1>(o);
+    }
+    // A code c held in a byte is the FP8 E4M3 value c * 2^-9 (scale carries 2^9).
+    const uint32_t codes = reg.offset + tok * reg.code_bytes;
+    if (reg.bits == 4) {
+        const auto v = __builtin_amdgcn_raw_buffer_load_b128(page, codes + 16 * lq, 0, 0);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int h = i >> 1;
+            const int lo = (int)(v[i] & 0x0f0f0f0fu), hi = (int)((v[i] >> 4) & 0x0f0f0f0fu);
+            const auto l01 = __builtin_amdgcn_cvt_pk_f32_fp8(lo, false);
+            const auto l23 = __builtin_amdgcn_cvt_pk_f32_fp8(lo, true);
+            const auto h01 = __builtin_amdgcn_cvt_pk_f32_fp8(hi, false);
+            const auto h23 = __builtin_amdgcn_cvt_pk_f32_fp8(hi, true);
+            const float c[8] = {l01[0], h01[0], l01[1], h01[1], l23[0], h23[0], l23[1], h23[1]};
+#pragma unroll
+            for (int k = 0; k < 8; ++k) out[8 * i + k] = bf16_round_finite(fmaf(c[k], scale[h], offset[h]));
+        }
+    } else {
+        const auto v = __builtin_amdgcn_raw_buffer_load_b64(page, codes + 8 * lq, 0, 0);
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                const int part = (int)((v[i] >> (2 * k)) & 0x03030303u);  // byte j: channel 4j + k
+                const auto c01 = __builtin_amdgcn_cvt_pk_f32_fp8(part, false);
+                const auto c23 = __builtin_amdgcn_cvt_pk_f32_fp8(part, true);
+                out[16 * i + k] = bf16_round_finite(fmaf(c01[0], scale[i], offset[i]));
+                out[16 * i + 4 + k] = bf16_round_finite(fmaf(c01[1], scale[i], offset[i]));
+                out[16 * i + 8 + k] = bf16_round_finite(fmaf(c23[0], scale[i], offset[i]));
+                out[16 * i + 12 + k] = bf16_round_finite(fmaf(c23[1], scale[i], offset[i]));
+            }
+    }
+}
+
+template <int D, int PT>
+__global__ __launch_bounds__(kDecodeThreads) void decode_chain_kernel(AttentionParams p) {
+    constexpr int Quarters = D / 32;
+    constexpr int UnitsPerPage = PT / kUnitTokens;
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int t = lane >> 2;
+    const int qd = lane & 3;
+    const bool lane_active = qd < Quarters;
+    const int lq = lane_active ? qd : 0;
+    const int split = blockIdx.x % p.splits;
+    const int64_t rh = blockIdx.x / p.splits;
+    const int head = (int)(rh % p.heads);
+    const int64_t row = rh / p.heads;
+    const int links = p.chain_length;  // records 0 .. L
+    __shared__ __attribute__((aligned(16))) float prep_lds[kPrepFloats];
+    // bf16(mu_r) of records 0 .. L - 1 (the K plane's chain), FP32.
+    __shared__ __attribute__((aligned(16))) float mean_lds[kMaxRecords][128];
+    __shared__ __attribute__((aligned(16))) float scratch_lds[kWaves * 16 * 128];
+    __shared__ int request_counts[kWaves];
+
+    int request;
+    PrepareInputs<D, kDecodeThreads> in;
+    _Float16* rotation_lds = reinterpret_cast<_Float16*>(scratch_lds);
+    if (p.fused_prepare) {
+        prepare_load<D, kDecodeThreads>(p, row, head, in);
+        request = find_request_parallel(p.query_start_loc, p.requests, row, request_counts);
+        if (request >= 0) prepare_stage<D, kDecodeThreads>(p, in, rotation_lds);
+    } else {
+        request = p.row_request[row];
+    }
+    if (request < 0) return;
+    request = __builtin_amdgcn_readfirstlane(request);
+    SplitRange range = split_range(p, request, split);
+    range.history = uniform64(range.history);
+    range.unit_begin = uniform64(range.unit_begin);
+    range.unit_end = uniform64(range.unit_end);
+    float* partial = p.partials + (rh * p.splits + split) * (int64_t)(D + 2);
+
+    for (int i = threadIdx.x; i < (links - 1) * 128; i += kDecodeThreads) {
+        const int r = i / 128, c = i % 128;
+        mean_lds[r][c] = (p.key_mean_all != nullptr && c < D)
+                             ? bf16_f32(bf16_rn(p.key_mean_all[((int64_t)r * p.heads + head) * D + c]))
+                             : 0.f;
+    }
+    if (p.fused_prepare) {
+        prepare_record<D, kDecodeThreads>(p, head, in, prep_lds, rotation_lds);
+    } else {
+        const float* src = p.prep + rh * (int64_t)kPrepFloats;
+        for (int i = threadIdx.x; i < kPrepFloats; i += kDecodeThreads) prep_lds[i] = src[i];
+        __syncthreads();
+    }
+    // q' of the lane's channels (FP32, log2 units, scale folded in).
+    float qv[32];
+#pragma unroll
+    for (int i = 0; i < 32; ++i) qv[i] = prep_lds[kPrepScalars + 32 * lq + i];
+
+    const ConstantInt32* table =
+        (const ConstantInt32*)(p.block_table + (int64_t)range.request * p.block_table_stride);
+    const int64_t page_bytes = (int64_t)PT * p.page_width;
+    const bool has_mean = p.key_mean_all != nullptr;
+
+    float acc[32];
+#pragma unroll
+    for (int i = 0; i < 32; ++i) acc[i] = 0.f;
+    float m = -INFINITY, l = 0.f;
+
+    for (int64_t u = range.unit_begin + wave; u < range.unit_end; u += kWaves) {
+        const int block = table[u / UnitsPerPage];
+        const bool ok = block >= 0 && block < p.num_blocks;
+        const uint8_t* kbase = p.cache + (ok ? ((int64_t)block * p.heads + head) * page_bytes : 0);
+        const uint32_t bytes = ok ? (uint32_t)page_bytes : 0u;
+        const __amdgpu_buffer_rsrc_t kpage = page_resource(kbase, bytes);
+        const __amdgpu_buffer_rsrc_t vpage = page_resource(kbase + (ok ? p.plane_stride : 0), bytes);
+        const int tok = (int)(u % UnitsPerPage) * kUnitTokens + t;
+        const int64_t pos = u * kUnitTokens + t;
+        const bool valid = ok && lane_active && pos < range.history;
+
+        float kx[32], vx[32];
+        for (int r = 0; r < links; ++r) {
+            const RecordRegion reg = p.chain[r];
+            float kr[32], vr[32];
+            chain_record<PT>(kpage, reg, tok, lq, kr);
+            chain_record<PT>(vpage, reg, tok, lq, vr);
+            if (has_mean && r + 1 < links) {
+#pragma unroll
+                for (int i = 0; i < 32; ++i) kr[i] = bf16_round_finite(kr[i] + mean_lds[r][32 * lq + i]);
+            }
+            if (r == 0) {
+#pragma unroll
+                for (int i = 0; i < 32; ++i) {
+                    kx[i] = kr[i];
+                    vx[i] = vr[i];
+                }
+            } else {
+                const uint32_t alpha_offset = reg.offset + PT * (reg.code_bytes + 2 * reg.groups) + 2 * tok;
+                const float ak = bf16_f32(__builtin_amdgcn_raw_buffer_load_b16(kpage, alpha_offset, 0, 0));
+                const float av = bf16_f32(__builtin_amdgcn_raw_buffer_load_b16(vpage, alpha_offset, 0, 0));
+#pragma unroll
+                for (int i = 0; i < 32; ++i) {
+                    kx[i] = bf16_round_finite(fmaf(kx[i], ak, kr[i]));
+                    vx[i] = bf16_round_finite(fmaf(vx[i], av, vr[i]));
+                }
+            }
+        }
+
+        float s[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int i = 0; i < 32; ++i) s[i & 3] = fmaf(qv[i], kx[i], s[i & 3]);
+        float score = quad_sum_fast(lane_active ? (s[0] + s[1]) + (s[2] + s[3]) : 0.f);
+        score = valid ? score : -INFINITY;
+        const float unit_max = wave_max(score);
+        if (unit_max > m) {
+            const float factor = m == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m - unit_max);
+#pragma unroll
+            for (int i = 0; i < 32; ++i) acc[i] *= factor;
+            l *= factor;
+            m = unit_max;
+        }
+        const float prob = valid ? __builtin_amdgcn_exp2f(score - m) : 0.f;
+        l += prob;
+#pragma unroll
+        for (int i = 0; i < 32; ++i) acc[i] = fmaf(prob, vx[i], acc[i]);
+    }
+
+    if (p.splits == 1) {
+        finish_single<D>(p, row, head, prep_lds[1],
+                         [&] { return merge_waves<D>(acc, m, l, lane, wave, lane_active, scratch_lds); });
+    } else {
+        write_partial<D>(merge_waves<D>(acc, m, l, lane, wave, lane_active, scratch_lds), partial);
+        finish_split<D>(p, row, head);
+    }
+}
+
 // ------------------------------------------------------------------ BF16 baseline decode
 
 template <int D>
@@ -1649,6 +1857,14 @@ hipError_t launch_all(const AttentionParams& p, hipStream_t stream, hipEvent_t b
     if (bf16) {
         const unsigned blocks = (unsigned)(p.rows * p.heads * p.splits);
         hipLaunchKernelGGL((decode_bf16_kernel<D>), dim3(blocks), dim3(kDecodeThreads), 0, stream, p);
+    } else if (p.chain_length > 1) {
+        const unsigned blocks = (unsigned)(p.rows * p.heads * p.splits);
+        if (p.page_tokens == 16)
+            hipLaunchKernelGGL((decode_chain_kernel<D, 16>), dim3(blocks), dim3(kDecodeThreads), 0, stream, p);
+        else if (p.page_tokens == 32)
+            hipLaunchKernelGGL((decode_chain_kernel<D, 32>), dim3(blocks), dim3(kDecodeThreads), 0, stream, p);
+        else
+            return hipErrorInvalidValue;
     } else if (!dispatch_anchor<D>(p, stream)) {
         return hipErrorInvalidValue;
     }

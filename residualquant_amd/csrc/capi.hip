@@ -341,11 +341,6 @@ int rq_attention(const void* query, int64_t query_stride, const void* key, int64
     const int width = rq_page_width(head_dim, records, bits, groups);
     if (width != page_width) return fail(RQ_EINVAL, "Packed cache width differs from records");
     const bool adjacent = records > 1 && reference_mode == RQ_MODE_ADJACENT;
-    if (adjacent && loop_index > 0)
-        return fail(RQ_ENOKERNEL,
-                    "No compiled packed HIP kernel for heads=%d, head_dim=%d, record count=%d, "
-                    "reference_mode=adjacent, loop_index=%d (adjacent decode covers loop 0)",
-                    heads, head_dim, records, loop_index);
     rq::AttentionParams p;
     // Residual loops at D = 96 run on decode96_kernel (one token half per
     // lane), which is fastest with one workgroup per (row, head) once those
@@ -374,6 +369,10 @@ int rq_attention(const void* query, int64_t query_stride, const void* key, int64
     p.key_mean_loop = key_mean ? key_mean + (int64_t)loop_index * heads * head_dim : nullptr;
     p.key_mean_anchor = (key_mean && p.has_residual) ? key_mean + (int64_t)anchor * heads * head_dim : nullptr;
     p.fused_prepare = p.splits == 1 ? 1 : 0;
+    // Adjacent mode past loop 0 decodes the restore chain of records 0..loop.
+    p.chain_length = adjacent && loop_index > 0 ? loop_index + 1 : 0;
+    for (int r = 0; r < p.chain_length; ++r) p.chain[r] = regions[r];
+    p.key_mean_all = key_mean;
     hipEvent_t begin, end;
     timing_events(stream, &begin, &end);
     return check_launch(rq::launch_attention(p, stream, begin, end), "attention launch");

@@ -170,6 +170,11 @@ struct AttentionParams {
     float* partials;       // workspace [rows, heads, splits, D + 2]
     int splits;
     int fused_prepare;     // 1: each decode workgroup prepares its own query (requires splits == 1)
+    // Adjacent mode, loop L > 0: records 0..L of the restore chain (chain_length = L + 1, else 0)
+    // and the key means of every record [records, heads, D] (or null).
+    RecordRegion chain[kMaxRecords];
+    int chain_length;
+    const float* key_mean_all;
 };
 
 hipError_t launch_attention(const AttentionParams& p, hipStream_t stream, hipEvent_t begin,

@@ -146,6 +146,40 @@ def test_attention_matches_oracle(oracle, device, case):
         assert err.max() <= MAX_ABS and err.mean() <= MEAN_ABS, (loop, err.max(), err.mean())
 
 
+ADJACENT_CASES = [
+    # lengths, heads, dim, records, page_tokens, rotation, mean, split target (0: default)
+    ([130, 1, 77, 300], 2, 128, ((4, 32), (2, 32), (2, 32), (2, 32)), 16, True, True, 0),
+    ([97, 33], 3, 96, ((4, 16), (2, 16), (4, 32), (2, 32)), 32, True, False, 0),
+    ([250, 65], 2, 128, ((4, 32), (4, 16), (2, 16)), 16, False, True, 1),
+]
+
+
+@pytest.mark.parametrize("case", ADJACENT_CASES, ids=lambda c: f"{c[2]}d-pt{c[4]}-r{len(c[3])}-t{c[7]}")
+def test_adjacent_attention_matches_oracle(oracle, device, case):
+    """Adjacent mode: loop L scores and sums the BF16 restore chain of records
+    0..L (compute.cuh:120-197, :506-528); loop 0 is the anchor record alone."""
+    _print_case("adjacent attention", case)
+    lengths, heads, dim, records, pt, rotation, mean, target = case
+    d = make_decode(lengths, heads, dim, records, seed=sum(lengths) + 3 * dim, page_tokens=pt, mode="adjacent",
+                    anchor=0, rotation=rotation, mean=mean)
+    g = d.group
+    cache_np = g.oracle_cache(oracle)
+    cache = torch.from_numpy(cache_np).to(device)
+    kr, vr, km = g.device_args(device)
+    try:
+        rq.ops.set_split_target(target)
+        for loop in range(len(records)):
+            expected = oracle_attention(oracle, d, cache_np, loop)
+            out = torch.zeros_like(d.query, device=device)
+            rq.attention(d.query.to(device), d.key.to(device), d.value.to(device), cache, out,
+                         d.query_start_loc.to(device), d.seq_lens.to(device), d.table.to(device), kr, vr, km,
+                         g.records, g.mode, g.anchor, loop)
+            err = np.abs(out.float().cpu().numpy().astype(np.float64) - expected)
+            assert err.max() <= MAX_ABS and err.mean() <= MEAN_ABS, (loop, err.max(), err.mean())
+    finally:
+        rq.ops.set_split_target(0)
+
+
 def test_attention_history_zero_is_live_value(device):
     """With no history the output is the current token's value exactly (merge.cuh:19-83)."""
     d = make_decode([1, 1, 1], 4, 128, OURO_G32, seed=3)
