@@ -1515,11 +1515,15 @@ void decode96_kernel(AttentionParams p) {
 // value once, and the two differ only when the FP32 result sits on a BF16
 // midpoint it did not reach exactly (within the attention tolerance).
 
-// RNE to BF16 of a finite FP32 value, returned as FP32.
-__device__ __forceinline__ float bf16_round_finite(float f) {
-    uint32_t u = __float_as_uint(f);
-    u += 0x7fffu + ((u >> 16) & 1u);
-    return __uint_as_float(u & 0xffff0000u);
+// RNE to BF16 of two FP32 values, returned as FP32: one v_cvt_pk_bf16_f32
+// and two bit operations.
+typedef __bf16 Bf16x2 __attribute__((ext_vector_type(2)));
+typedef float F32x2 __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ void bf16_round2(float& a, float& b) {
+    const F32x2 f = {a, b};
+    const uint32_t u = __builtin_bit_cast(uint32_t, __builtin_convertvector(f, Bf16x2));
+    a = __uint_as_float(u << 16);
+    b = __uint_as_float(u & 0xffff0000u);
 }
 
 // BF16 values (as FP32) of the lane's 32 channels [32 lq, 32 lq + 32) of one
@@ -1556,7 +1560,7 @@ __device__ __forceinline__ void chain_record(__amdgpu_buffer_rsrc_t page, const 
             const auto h23 = __builtin_amdgcn_cvt_pk_f32_fp8(hi, true);
             const float c[8] = {l01[0], h01[0], l01[1], h01[1], l23[0], h23[0], l23[1], h23[1]};
 #pragma unroll
-            for (int k = 0; k < 8; ++k) out[8 * i + k] = bf16_round_finite(fmaf(c[k], scale[h], offset[h]));
+            for (int k = 0; k < 8; ++k) out[8 * i + k] = fmaf(c[k], scale[h], offset[h]);
         }
     } else {
         const auto v = __builtin_amdgcn_raw_buffer_load_b64(page, codes + 8 * lq, 0, 0);
@@ -1567,12 +1571,14 @@ __device__ __forceinline__ void chain_record(__amdgpu_buffer_rsrc_t page, const 
                 const int part = (int)((v[i] >> (2 * k)) & 0x03030303u);  // byte j: channel 4j + k
                 const auto c01 = __builtin_amdgcn_cvt_pk_f32_fp8(part, false);
                 const auto c23 = __builtin_amdgcn_cvt_pk_f32_fp8(part, true);
-                out[16 * i + k] = bf16_round_finite(fmaf(c01[0], scale[i], offset[i]));
-                out[16 * i + 4 + k] = bf16_round_finite(fmaf(c01[1], scale[i], offset[i]));
-                out[16 * i + 8 + k] = bf16_round_finite(fmaf(c23[0], scale[i], offset[i]));
-                out[16 * i + 12 + k] = bf16_round_finite(fmaf(c23[1], scale[i], offset[i]));
+                out[16 * i + k] = fmaf(c01[0], scale[i], offset[i]);
+                out[16 * i + 4 + k] = fmaf(c01[1], scale[i], offset[i]);
+                out[16 * i + 8 + k] = fmaf(c23[0], scale[i], offset[i]);
+                out[16 * i + 12 + k] = fmaf(c23[1], scale[i], offset[i]);
             }
     }
+#pragma unroll
+    for (int i = 0; i < 32; i += 2) bf16_round2(out[i], out[i + 1]);
 }
 
 template <int D, int PT>
@@ -1661,7 +1667,11 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_chain_kernel(AttentionP
             chain_record<PT>(vpage, reg, tok, lq, vr);
             if (has_mean && r + 1 < links) {
 #pragma unroll
-                for (int i = 0; i < 32; ++i) kr[i] = bf16_round_finite(kr[i] + mean_lds[r][32 * lq + i]);
+                for (int i = 0; i < 32; i += 2) {
+                    kr[i] += mean_lds[r][32 * lq + i];
+                    kr[i + 1] += mean_lds[r][32 * lq + i + 1];
+                    bf16_round2(kr[i], kr[i + 1]);
+                }
             }
             if (r == 0) {
 #pragma unroll
@@ -1674,9 +1684,13 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_chain_kernel(AttentionP
                 const float ak = bf16_f32(__builtin_amdgcn_raw_buffer_load_b16(kpage, alpha_offset, 0, 0));
                 const float av = bf16_f32(__builtin_amdgcn_raw_buffer_load_b16(vpage, alpha_offset, 0, 0));
 #pragma unroll
-                for (int i = 0; i < 32; ++i) {
-                    kx[i] = bf16_round_finite(fmaf(kx[i], ak, kr[i]));
-                    vx[i] = bf16_round_finite(fmaf(vx[i], av, vr[i]));
+                for (int i = 0; i < 32; i += 2) {
+                    kx[i] = fmaf(kx[i], ak, kr[i]);
+                    kx[i + 1] = fmaf(kx[i + 1], ak, kr[i + 1]);
+                    vx[i] = fmaf(vx[i], av, vr[i]);
+                    vx[i + 1] = fmaf(vx[i + 1], av, vr[i + 1]);
+                    bf16_round2(kx[i], kx[i + 1]);
+                    bf16_round2(vx[i], vx[i + 1]);
                 }
             }
         }
