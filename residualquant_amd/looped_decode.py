@@ -36,6 +36,7 @@ import torch
 
 import torch.nn.functional as F
 
+from . import artifact as artifact_module
 from . import ops, step_ops, workloads
 from .layout import page_width
 
@@ -116,6 +117,10 @@ class LoopedDecoder:
             self.value_rotation = [
                 workloads.random_sign_rotation(c.heads, c.head_dim, seed + 12 + 2 * l, device=device)
                 for l in range(c.layers)]
+        self.key_mean: list = [None] * c.layers
+        # V rotations folded into the projection weights (use_artifact), used
+        # only to rotate the synthetic history the way those weights would.
+        self.folded_value_rotation: list = [None] * c.layers
 
         # Paged cache: every request owns ceil(max_tokens / PT) blocks, shuffled.
         pages = (self.max_tokens + c.page_tokens - 1) // c.page_tokens
@@ -144,6 +149,31 @@ class LoopedDecoder:
                                      dtype=torch.uint8, device=device)
         self.graph: Optional[torch.cuda.CUDAGraph] = None
 
+    # ------------------------------------------------------------ artifact
+
+    def use_artifact(self, artifact: dict) -> None:
+        """Take the K/V rotations and key means of a rotation artifact
+        (``artifact.load_rotation_artifact``), one packed group covering the
+        model's loops, as the reference binds them (install_model.py:154-196).
+        4-D value rotations are folded into this decoder's QKV and O weights
+        (weights.py:8-37), in place: call before building the history, and
+        before sharing the weights with another decoder."""
+        c = self.config
+        q_size = c.heads * c.head_dim
+        prepared, folded = artifact_module.prepare_value_rotation(artifact)
+        slots = artifact_module.bind_slots(prepared, [c.schedule], c.layers, self.device)[0]
+        # Own lists (a decoder built with weights_from shares the originals).
+        self.key_rotation, self.value_rotation = list(self.key_rotation), list(self.value_rotation)
+        for layer, slot in enumerate(slots):
+            self.key_rotation[layer] = slot.key_rotation
+            self.value_rotation[layer] = slot.value_rotation
+            self.key_mean[layer] = slot.key_mean
+            if folded is not None:
+                rotation = folded[layer].to(self.device)
+                artifact_module.absorb_value_rotation(self.qkv[layer], self.o[layer], rotation, c.heads, c.head_dim,
+                                                      q_size, q_size)
+                self.folded_value_rotation[layer] = rotation
+
     # ------------------------------------------------------------ history
 
     def build_history(self, seed: int = 0, chunk: int = 16384) -> None:
@@ -157,8 +187,11 @@ class LoopedDecoder:
                 part = slots[start:start + chunk]
                 pairs = workloads.loop_kv(part.numel(), c.heads, c.head_dim, c.loops, seed + 97 * layer + start,
                                           device=self.device, anchor_index=c.anchor)
-                ops.quantize(pairs, self.caches[layer], part, self.key_rotation[layer], self.value_rotation[layer],
-                             None, c.schedule, "anchor", c.anchor, c.coefficient)
+                value_rotation = self.value_rotation[layer]
+                if value_rotation is None:
+                    value_rotation = self.folded_value_rotation[layer]
+                ops.quantize(pairs, self.caches[layer], part, self.key_rotation[layer], value_rotation,
+                             self.key_mean[layer], c.schedule, "anchor", c.anchor, c.coefficient)
 
     # ------------------------------------------------------------ the step
 
@@ -186,12 +219,13 @@ class LoopedDecoder:
                                          key_stage=key_stage, value_stage=value_stage)
                 ops.attention(q, k, value_stage, self.caches[layer], self.attn_out, self.query_start_loc,
                               self.seq_lens, self.block_table, self.key_rotation[layer], self.value_rotation[layer],
-                              None, c.schedule, "anchor", c.anchor, loop, workspace=self.workspace)
+                              self.key_mean[layer], c.schedule, "anchor", c.anchor, loop, workspace=self.workspace)
                 # Loop group quantize at the anchor loop (install_model.py:40-52).
                 if loop == c.anchor:
                     pairs = [(self.staged[layer, r, 0], self.staged[layer, r, 1]) for r in range(c.loops)]
                     ops.quantize(pairs, self.caches[layer], self.slots, self.key_rotation[layer],
-                                 self.value_rotation[layer], None, c.schedule, "anchor", c.anchor, c.coefficient)
+                                 self.value_rotation[layer], self.key_mean[layer], c.schedule, "anchor", c.anchor,
+                                 c.coefficient)
                 a = _project(self.attn_out.view(self.batch, q_size), self.o[layer])
                 # input_layernorm_2 then post_attention_layernorm with the fused add (ouro.py:154-155), one launch.
                 x, _ = step_ops.rms_norm(a, norms[2], eps, residual=self.residual, pre_weight=norms[1])

@@ -72,3 +72,55 @@ def test_single_row_projection_matches_linear(device):
     assert got.shape == (1, 3072) and got.is_contiguous()
     want = x.float() @ weight.float().t()
     assert ((got.float() - want).abs() <= want.abs() * 2.0 ** -7 + 1e-3).all()
+
+
+def _tiny_artifact(value_dims, seed=21):
+    import torch as t
+    from residualquant_amd import workloads
+    c = TINY
+    key = t.stack([workloads.random_sign_rotation(c.heads, c.head_dim, seed + l) for l in range(c.layers)])
+    value = t.stack([workloads.random_sign_rotation(c.heads, c.head_dim, seed + 50 + l) for l in range(c.layers)])
+    if value_dims == 5:
+        value = value[None]
+    g = t.Generator().manual_seed(seed)
+    return {"format_version": 2, "model": "tiny", "schedule": [b for b, _ in c.schedule],
+            "groups": [s for _, s in c.schedule], "key_rotations": key, "value_rotations": value,
+            "key_means": t.randn((c.loops, c.layers, c.heads, c.head_dim), generator=g) * 0.5}
+
+
+def test_artifact_folded_value_rotation_matches_kernel_rotation(device):
+    """With the V rotation folded into the QKV/O weights (4-D artifact,
+    weights.py:8-37) the step computes what the kernels' own V rotation (5-D
+    artifact) computes: the same logits up to BF16 and quantization rounding.
+    Key means and K rotations come from the artifact in both."""
+    kernel_side = LoopedDecoder(TINY, batch=2, context=40, max_new_tokens=4, device=device, seed=7)
+    folded = LoopedDecoder(TINY, batch=2, context=40, max_new_tokens=4, device=device, seed=7)
+    kernel_side.use_artifact(_tiny_artifact(5))
+    folded.use_artifact(_tiny_artifact(4))
+    assert all(v is None for v in folded.value_rotation) and all(m is not None for m in folded.key_mean)
+    for model in (kernel_side, folded):
+        model.build_history(seed=5)
+    a = kernel_side.step().float()
+    b = folded.step().float()
+    torch.cuda.synchronize()
+    cosine = torch.nn.functional.cosine_similarity(a, b, dim=-1)
+    print(f"artifact folded vs kernel rotation: cosine {cosine.tolist()}", flush=True)
+    assert bool((cosine > 0.995).all())
+
+
+def test_graph_replay_with_artifact_means(device):
+    eager = _model(device)
+    graphed = _model(device)
+    for model in (eager, graphed):
+        model.use_artifact(_tiny_artifact(5))
+    # Rebuild the history with the artifact's rotations and means.
+    for model in (eager, graphed):
+        for cache in model.caches:
+            cache.zero_()
+        model.build_history(seed=5)
+    graphed.capture()
+    for step in range(2):
+        logits = eager.step()
+        graphed.graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(logits, graphed.logits), step
