@@ -460,7 +460,7 @@ def run_huginn(args):
             "unit": "GB/s",
             "frac": residual_gbps / PEAK_HBM_GBPS,
             "traffic": None,
-            "kernel": f"decode_kernel<96,16,4,32,2,16,true> (residual loop), {launches} HIP-event-timed launches",
+            "kernel": f"decode96_kernel<16,4,32,2,16,true> (residual loop), {launches} HIP-event-timed launches",
         },
         "bf16_baseline": {
             "us_per_call_kernel": bf16_ms * 1e3,
@@ -737,7 +737,7 @@ def run_decode(args):
             "unit": "GB/s",
             "frac": residual_gbps / PEAK_HBM_GBPS,
             "traffic": measured_traffic(),
-            "kernel": "decode_kernel<128,4,32,2,32,true> (residual loop), "
+            "kernel": "decode_kernel<128,16,4,32,2,32,true> (residual loop), "
                       f"{residual_launches} HIP-event-timed launches",
         },
         "bf16_baseline": bf16,
