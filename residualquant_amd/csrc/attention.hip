@@ -315,10 +315,10 @@ template <int Bits>
 __device__ __forceinline__ void load_codes(__amdgpu_buffer_rsrc_t page, uint32_t offset, uint32_t uniform,
                                            Codes<Bits>& c) {
     if constexpr (Bits == 4) {
-        const auto v = __builtin_amdgcn_raw_buffer_load_b128(page, offset, uniform, 0);
+        const auto v = __builtin_amdgcn_raw_buffer_load_b128(page, offset, uniform, kStreamPolicy);
         c.w[0] = v[0]; c.w[1] = v[1]; c.w[2] = v[2]; c.w[3] = v[3];
     } else {
-        const auto v = __builtin_amdgcn_raw_buffer_load_b64(page, offset, uniform, 0);
+        const auto v = __builtin_amdgcn_raw_buffer_load_b64(page, offset, uniform, kStreamPolicy);
         c.w[0] = v[0]; c.w[1] = v[1];
     }
 }
@@ -331,11 +331,11 @@ struct GroupParams {
     __device__ __forceinline__ void load(__amdgpu_buffer_rsrc_t page, uint32_t scale_offset,
                                          uint32_t offset_offset, uint32_t uniform) {
         if constexpr (G == 32) {
-            scales = __builtin_amdgcn_raw_buffer_load_b8(page, scale_offset, uniform, 0);
-            offsets = __builtin_amdgcn_raw_buffer_load_b8(page, offset_offset, uniform, 0);
+            scales = __builtin_amdgcn_raw_buffer_load_b8(page, scale_offset, uniform, kStreamPolicy);
+            offsets = __builtin_amdgcn_raw_buffer_load_b8(page, offset_offset, uniform, kStreamPolicy);
         } else {
-            scales = __builtin_amdgcn_raw_buffer_load_b16(page, scale_offset, uniform, 0);
-            offsets = __builtin_amdgcn_raw_buffer_load_b16(page, offset_offset, uniform, 0);
+            scales = __builtin_amdgcn_raw_buffer_load_b16(page, scale_offset, uniform, kStreamPolicy);
+            offsets = __builtin_amdgcn_raw_buffer_load_b16(page, offset_offset, uniform, kStreamPolicy);
         }
     }
     // Scale / offset of the lane's 16-channel half H.
@@ -915,8 +915,8 @@ void decode_kernel(AttentionParams p) {
             d.kpl.load(kpage, off_scale_l, off_offs_l, step_par_l);
             load_codes<BL>(vpage, off_codes_l, step_codes_l, d.vcl);
             d.vpl.load(vpage, off_scale_l, off_offs_l, step_par_l);
-            d.alpha_k_bits = __builtin_amdgcn_raw_buffer_load_b16(kpage, off_alpha, step_alpha, 0);
-            d.alpha_v_bits = __builtin_amdgcn_raw_buffer_load_b16(vpage, off_alpha, step_alpha, 0);
+            d.alpha_k_bits = __builtin_amdgcn_raw_buffer_load_b16(kpage, off_alpha, step_alpha, kStreamPolicy);
+            d.alpha_v_bits = __builtin_amdgcn_raw_buffer_load_b16(vpage, off_alpha, step_alpha, kStreamPolicy);
         }
         return valid;
     };
@@ -1080,10 +1080,10 @@ struct HalfCodes {
 
 template <int Bits>
 __device__ __forceinline__ void load_half_codes(__amdgpu_buffer_rsrc_t plane, uint32_t offset, HalfCodes<Bits>& c) {
-    const auto a = __builtin_amdgcn_raw_buffer_load_b96(plane, offset, 0, 0);
+    const auto a = __builtin_amdgcn_raw_buffer_load_b96(plane, offset, 0, kStreamPolicy);
     c.w[0] = a[0]; c.w[1] = a[1]; c.w[2] = a[2];
     if constexpr (Bits == 4) {
-        const auto b = __builtin_amdgcn_raw_buffer_load_b96(plane, offset + 12, 0, 0);
+        const auto b = __builtin_amdgcn_raw_buffer_load_b96(plane, offset + 12, 0, kStreamPolicy);
         c.w[3] = b[0]; c.w[4] = b[1]; c.w[5] = b[2];
     }
 }
@@ -1098,8 +1098,8 @@ struct HalfParams {
     uint32_t s, o;
     __device__ __forceinline__ void load(__amdgpu_buffer_rsrc_t plane, uint32_t scale_word, uint32_t offset_word,
                                          uint32_t shift) {
-        const auto sv = __builtin_amdgcn_raw_buffer_load_b64(plane, scale_word, 0, 0);
-        const auto ov = __builtin_amdgcn_raw_buffer_load_b64(plane, offset_word, 0, 0);
+        const auto sv = __builtin_amdgcn_raw_buffer_load_b64(plane, scale_word, 0, kStreamPolicy);
+        const auto ov = __builtin_amdgcn_raw_buffer_load_b64(plane, offset_word, 0, kStreamPolicy);
         s = __builtin_amdgcn_alignbyte(sv[1], sv[0], shift);
         o = __builtin_amdgcn_alignbyte(ov[1], ov[0], shift);
     }
@@ -1373,8 +1373,8 @@ void decode96_kernel(AttentionParams p) {
             d.kpl.load(kplane, page + off_scale_l, page + off_offs_l, shift_l);
             load_half_codes<BL>(vplane, page + off_codes_l, d.vcl);
             d.vpl.load(vplane, page + off_scale_l, page + off_offs_l, shift_l);
-            d.alpha_k_bits = __builtin_amdgcn_raw_buffer_load_b16(kplane, page + off_alpha, 0, 0);
-            d.alpha_v_bits = __builtin_amdgcn_raw_buffer_load_b16(vplane, page + off_alpha, 0, 0);
+            d.alpha_k_bits = __builtin_amdgcn_raw_buffer_load_b16(kplane, page + off_alpha, 0, kStreamPolicy);
+            d.alpha_v_bits = __builtin_amdgcn_raw_buffer_load_b16(vplane, page + off_alpha, 0, kStreamPolicy);
         }
         return ok;
     };
@@ -1534,13 +1534,13 @@ __device__ __forceinline__ void chain_record(__amdgpu_buffer_rsrc_t page, const 
     const uint32_t params = reg.offset + PT * reg.code_bytes + tok * reg.groups;
     float scale[2], offset[2];
     if (reg.group == 32) {
-        const uint32_t s = __builtin_amdgcn_raw_buffer_load_b8(page, params + lq, 0, 0);
-        const uint32_t o = __builtin_amdgcn_raw_buffer_load_b8(page, params + PT * reg.groups + lq, 0, 0);
+        const uint32_t s = __builtin_amdgcn_raw_buffer_load_b8(page, params + lq, 0, kStreamPolicy);
+        const uint32_t o = __builtin_amdgcn_raw_buffer_load_b8(page, params + PT * reg.groups + lq, 0, kStreamPolicy);
         scale[0] = scale[1] = fp8_f32<0>(s) * 512.0f;
         offset[0] = offset[1] = fp8_f32<0>(o);
     } else {
-        const uint32_t s = __builtin_amdgcn_raw_buffer_load_b16(page, params + 2 * lq, 0, 0);
-        const uint32_t o = __builtin_amdgcn_raw_buffer_load_b16(page, params + PT * reg.groups + 2 * lq, 0, 0);
+        const uint32_t s = __builtin_amdgcn_raw_buffer_load_b16(page, params + 2 * lq, 0, kStreamPolicy);
+        const uint32_t o = __builtin_amdgcn_raw_buffer_load_b16(page, params + PT * reg.groups + 2 * lq, 0, kStreamPolicy);
         scale[0] = fp8_f32<0>(s) * 512.0f;
         scale[1] = fp8_f32<1>(s) * 512.0f;
         offset[0] = fp8_f32<0>(o);
@@ -1549,7 +1549,7 @@ __device__ __forceinline__ void chain_record(__amdgpu_buffer_rsrc_t page, const 
     // A code c held in a byte is the FP8 E4M3 value c * 2^-9 (scale carries 2^9).
     const uint32_t codes = reg.offset + tok * reg.code_bytes;
     if (reg.bits == 4) {
-        const auto v = __builtin_amdgcn_raw_buffer_load_b128(page, codes + 16 * lq, 0, 0);
+        const auto v = __builtin_amdgcn_raw_buffer_load_b128(page, codes + 16 * lq, 0, kStreamPolicy);
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             const int h = i >> 1;
@@ -1563,7 +1563,7 @@ __device__ __forceinline__ void chain_record(__amdgpu_buffer_rsrc_t page, const 
             for (int k = 0; k < 8; ++k) out[8 * i + k] = fmaf(c[k], scale[h], offset[h]);
         }
     } else {
-        const auto v = __builtin_amdgcn_raw_buffer_load_b64(page, codes + 8 * lq, 0, 0);
+        const auto v = __builtin_amdgcn_raw_buffer_load_b64(page, codes + 8 * lq, 0, kStreamPolicy);
 #pragma unroll
         for (int i = 0; i < 2; ++i)
 #pragma unroll
@@ -1681,8 +1681,8 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_chain_kernel(AttentionP
                 }
             } else {
                 const uint32_t alpha_offset = reg.offset + PT * (reg.code_bytes + 2 * reg.groups) + 2 * tok;
-                const float ak = bf16_f32(__builtin_amdgcn_raw_buffer_load_b16(kpage, alpha_offset, 0, 0));
-                const float av = bf16_f32(__builtin_amdgcn_raw_buffer_load_b16(vpage, alpha_offset, 0, 0));
+                const float ak = bf16_f32(__builtin_amdgcn_raw_buffer_load_b16(kpage, alpha_offset, 0, kStreamPolicy));
+                const float av = bf16_f32(__builtin_amdgcn_raw_buffer_load_b16(vpage, alpha_offset, 0, kStreamPolicy));
 #pragma unroll
                 for (int i = 0; i < 32; i += 2) {
                     kx[i] = fmaf(kx[i], ak, kr[i]);

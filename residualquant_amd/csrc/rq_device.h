@@ -112,6 +112,13 @@ __device__ __forceinline__ float max_z(float a, float b) {
 
 constexpr int kCoherentPolicy = 16;  // cache-policy operand: sc1
 
+// Cache-policy operand of the decode kernels' page loads: nt (non-temporal).
+// A decode call reads each page span once, so its loads stream past the
+// caches instead of displacing lines that are reused (rotations, queries,
+// block tables).  A no-arithmetic gather of one B32 x 8192-token residual-loop
+// call measured 163 us with nt against 177 us without.
+constexpr int kStreamPolicy = 2;
+
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t handoff_resource(const void* base, uint32_t bytes) {
     return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
 }
