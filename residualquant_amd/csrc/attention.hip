@@ -311,14 +311,31 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t page_resource(const uint8_t* p
     return __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(page), (short)0, (int)bytes, 0x00020000);
 }
 
-template <int Bits>
+// Cache policy of the page loads by head dimension: non-temporal (nt) or the
+// default, for the code words and for the FP8 scale/offset and alpha bytes.
+// Chosen by measurement (A/B on one box, eager calls timed by HIP events):
+//   D = 128 (16 query heads, B32 x 8192): nt codes with default parameters
+//     173 us per residual-loop call; nt everywhere 184 us; nt parameters with
+//     default codes 192 us; default everywhere 203 us;
+//   D = 96 (55 heads, B8 x 4096): default codes with nt parameters 88 us per
+//     residual-loop call (the D96 kernel reads each token's codes with two
+//     loads that interleave within every line, so a line streamed past L2
+//     after the first is fetched again by the second); default everywhere
+//     91 us; nt everywhere 97 us.
+template <int D>
+struct PagePolicy {
+    static constexpr int kCodes = D == 128 ? kStreamPolicy : 0;
+    static constexpr int kParams = D == 128 ? 0 : kStreamPolicy;
+};
+
+template <int Bits, int Policy>
 __device__ __forceinline__ void load_codes(__amdgpu_buffer_rsrc_t page, uint32_t offset, uint32_t uniform,
                                            Codes<Bits>& c) {
     if constexpr (Bits == 4) {
-        const auto v = __builtin_amdgcn_raw_buffer_load_b128(page, offset, uniform, kStreamPolicy);
+        const auto v = __builtin_amdgcn_raw_buffer_load_b128(page, offset, uniform, Policy);
         c.w[0] = v[0]; c.w[1] = v[1]; c.w[2] = v[2]; c.w[3] = v[3];
     } else {
-        const auto v = __builtin_amdgcn_raw_buffer_load_b64(page, offset, uniform, kStreamPolicy);
+        const auto v = __builtin_amdgcn_raw_buffer_load_b64(page, offset, uniform, Policy);
         c.w[0] = v[0]; c.w[1] = v[1];
     }
 }
@@ -328,14 +345,15 @@ __device__ __forceinline__ void load_codes(__amdgpu_buffer_rsrc_t page, uint32_t
 template <int G>
 struct GroupParams {
     uint32_t scales, offsets;
+    template <int Policy>
     __device__ __forceinline__ void load(__amdgpu_buffer_rsrc_t page, uint32_t scale_offset,
                                          uint32_t offset_offset, uint32_t uniform) {
         if constexpr (G == 32) {
-            scales = __builtin_amdgcn_raw_buffer_load_b8(page, scale_offset, uniform, kStreamPolicy);
-            offsets = __builtin_amdgcn_raw_buffer_load_b8(page, offset_offset, uniform, kStreamPolicy);
+            scales = __builtin_amdgcn_raw_buffer_load_b8(page, scale_offset, uniform, Policy);
+            offsets = __builtin_amdgcn_raw_buffer_load_b8(page, offset_offset, uniform, Policy);
         } else {
-            scales = __builtin_amdgcn_raw_buffer_load_b16(page, scale_offset, uniform, kStreamPolicy);
-            offsets = __builtin_amdgcn_raw_buffer_load_b16(page, offset_offset, uniform, kStreamPolicy);
+            scales = __builtin_amdgcn_raw_buffer_load_b16(page, scale_offset, uniform, Policy);
+            offsets = __builtin_amdgcn_raw_buffer_load_b16(page, offset_offset, uniform, Policy);
         }
     }
     // Scale / offset of the lane's 16-channel half H.
@@ -903,20 +921,21 @@ void decode_kernel(AttentionParams p) {
         const __amdgpu_buffer_rsrc_t vpage = page_resource(kbase + (valid ? p.plane_stride : 0), bytes);
         const uint32_t step_codes_a = half * (kUnitTokens * CodeA);
         const uint32_t step_par_a = half * (kUnitTokens * GroupsA);
-        load_codes<BA>(kpage, off_codes_a, step_codes_a, d.kca);
-        d.kpa.load(kpage, off_scale_a, off_offs_a, step_par_a);
-        load_codes<BA>(vpage, off_codes_a, step_codes_a, d.vca);
-        d.vpa.load(vpage, off_scale_a, off_offs_a, step_par_a);
+        using Policy = PagePolicy<D>;
+        load_codes<BA, Policy::kCodes>(kpage, off_codes_a, step_codes_a, d.kca);
+        d.kpa.template load<Policy::kParams>(kpage, off_scale_a, off_offs_a, step_par_a);
+        load_codes<BA, Policy::kCodes>(vpage, off_codes_a, step_codes_a, d.vca);
+        d.vpa.template load<Policy::kParams>(vpage, off_scale_a, off_offs_a, step_par_a);
         if constexpr (HasL) {
             const uint32_t step_codes_l = half * (kUnitTokens * CodeL);
             const uint32_t step_par_l = half * (kUnitTokens * GroupsL);
             const uint32_t step_alpha = half * (2 * kUnitTokens);
-            load_codes<BL>(kpage, off_codes_l, step_codes_l, d.kcl);
-            d.kpl.load(kpage, off_scale_l, off_offs_l, step_par_l);
-            load_codes<BL>(vpage, off_codes_l, step_codes_l, d.vcl);
-            d.vpl.load(vpage, off_scale_l, off_offs_l, step_par_l);
-            d.alpha_k_bits = __builtin_amdgcn_raw_buffer_load_b16(kpage, off_alpha, step_alpha, kStreamPolicy);
-            d.alpha_v_bits = __builtin_amdgcn_raw_buffer_load_b16(vpage, off_alpha, step_alpha, kStreamPolicy);
+            load_codes<BL, Policy::kCodes>(kpage, off_codes_l, step_codes_l, d.kcl);
+            d.kpl.template load<Policy::kParams>(kpage, off_scale_l, off_offs_l, step_par_l);
+            load_codes<BL, Policy::kCodes>(vpage, off_codes_l, step_codes_l, d.vcl);
+            d.vpl.template load<Policy::kParams>(vpage, off_scale_l, off_offs_l, step_par_l);
+            d.alpha_k_bits = __builtin_amdgcn_raw_buffer_load_b16(kpage, off_alpha, step_alpha, Policy::kParams);
+            d.alpha_v_bits = __builtin_amdgcn_raw_buffer_load_b16(vpage, off_alpha, step_alpha, Policy::kParams);
         }
         return valid;
     };
@@ -1080,10 +1099,10 @@ struct HalfCodes {
 
 template <int Bits>
 __device__ __forceinline__ void load_half_codes(__amdgpu_buffer_rsrc_t plane, uint32_t offset, HalfCodes<Bits>& c) {
-    const auto a = __builtin_amdgcn_raw_buffer_load_b96(plane, offset, 0, kStreamPolicy);
+    const auto a = __builtin_amdgcn_raw_buffer_load_b96(plane, offset, 0, PagePolicy<96>::kCodes);
     c.w[0] = a[0]; c.w[1] = a[1]; c.w[2] = a[2];
     if constexpr (Bits == 4) {
-        const auto b = __builtin_amdgcn_raw_buffer_load_b96(plane, offset + 12, 0, kStreamPolicy);
+        const auto b = __builtin_amdgcn_raw_buffer_load_b96(plane, offset + 12, 0, PagePolicy<96>::kCodes);
         c.w[3] = b[0]; c.w[4] = b[1]; c.w[5] = b[2];
     }
 }
@@ -1098,8 +1117,8 @@ struct HalfParams {
     uint32_t s, o;
     __device__ __forceinline__ void load(__amdgpu_buffer_rsrc_t plane, uint32_t scale_word, uint32_t offset_word,
                                          uint32_t shift) {
-        const auto sv = __builtin_amdgcn_raw_buffer_load_b64(plane, scale_word, 0, kStreamPolicy);
-        const auto ov = __builtin_amdgcn_raw_buffer_load_b64(plane, offset_word, 0, kStreamPolicy);
+        const auto sv = __builtin_amdgcn_raw_buffer_load_b64(plane, scale_word, 0, PagePolicy<96>::kParams);
+        const auto ov = __builtin_amdgcn_raw_buffer_load_b64(plane, offset_word, 0, PagePolicy<96>::kParams);
         s = __builtin_amdgcn_alignbyte(sv[1], sv[0], shift);
         o = __builtin_amdgcn_alignbyte(ov[1], ov[0], shift);
     }
@@ -1373,8 +1392,8 @@ void decode96_kernel(AttentionParams p) {
             d.kpl.load(kplane, page + off_scale_l, page + off_offs_l, shift_l);
             load_half_codes<BL>(vplane, page + off_codes_l, d.vcl);
             d.vpl.load(vplane, page + off_scale_l, page + off_offs_l, shift_l);
-            d.alpha_k_bits = __builtin_amdgcn_raw_buffer_load_b16(kplane, page + off_alpha, 0, kStreamPolicy);
-            d.alpha_v_bits = __builtin_amdgcn_raw_buffer_load_b16(vplane, page + off_alpha, 0, kStreamPolicy);
+            d.alpha_k_bits = __builtin_amdgcn_raw_buffer_load_b16(kplane, page + off_alpha, 0, PagePolicy<96>::kParams);
+            d.alpha_v_bits = __builtin_amdgcn_raw_buffer_load_b16(vplane, page + off_alpha, 0, PagePolicy<96>::kParams);
         }
         return ok;
     };
@@ -1528,19 +1547,20 @@ __device__ __forceinline__ void bf16_round2(float& a, float& b) {
 
 // BF16 values (as FP32) of the lane's 32 channels [32 lq, 32 lq + 32) of one
 // record at token row `tok` of the page: bf16(code * scale + offset).
-template <int PT>
+template <int D, int PT>
 __device__ __forceinline__ void chain_record(__amdgpu_buffer_rsrc_t page, const RecordRegion& reg, int tok,
                                              int lq, float (&out)[32]) {
+    using Policy = PagePolicy<D>;
     const uint32_t params = reg.offset + PT * reg.code_bytes + tok * reg.groups;
     float scale[2], offset[2];
     if (reg.group == 32) {
-        const uint32_t s = __builtin_amdgcn_raw_buffer_load_b8(page, params + lq, 0, kStreamPolicy);
-        const uint32_t o = __builtin_amdgcn_raw_buffer_load_b8(page, params + PT * reg.groups + lq, 0, kStreamPolicy);
+        const uint32_t s = __builtin_amdgcn_raw_buffer_load_b8(page, params + lq, 0, Policy::kParams);
+        const uint32_t o = __builtin_amdgcn_raw_buffer_load_b8(page, params + PT * reg.groups + lq, 0, Policy::kParams);
         scale[0] = scale[1] = fp8_f32<0>(s) * 512.0f;
         offset[0] = offset[1] = fp8_f32<0>(o);
     } else {
-        const uint32_t s = __builtin_amdgcn_raw_buffer_load_b16(page, params + 2 * lq, 0, kStreamPolicy);
-        const uint32_t o = __builtin_amdgcn_raw_buffer_load_b16(page, params + PT * reg.groups + 2 * lq, 0, kStreamPolicy);
+        const uint32_t s = __builtin_amdgcn_raw_buffer_load_b16(page, params + 2 * lq, 0, Policy::kParams);
+        const uint32_t o = __builtin_amdgcn_raw_buffer_load_b16(page, params + PT * reg.groups + 2 * lq, 0, Policy::kParams);
         scale[0] = fp8_f32<0>(s) * 512.0f;
         scale[1] = fp8_f32<1>(s) * 512.0f;
         offset[0] = fp8_f32<0>(o);
@@ -1549,7 +1569,7 @@ __device__ __forceinline__ void chain_record(__amdgpu_buffer_rsrc_t page, const 
     // A code c held in a byte is the FP8 E4M3 value c * 2^-9 (scale carries 2^9).
     const uint32_t codes = reg.offset + tok * reg.code_bytes;
     if (reg.bits == 4) {
-        const auto v = __builtin_amdgcn_raw_buffer_load_b128(page, codes + 16 * lq, 0, kStreamPolicy);
+        const auto v = __builtin_amdgcn_raw_buffer_load_b128(page, codes + 16 * lq, 0, Policy::kCodes);
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             const int h = i >> 1;
@@ -1563,7 +1583,7 @@ __device__ __forceinline__ void chain_record(__amdgpu_buffer_rsrc_t page, const 
             for (int k = 0; k < 8; ++k) out[8 * i + k] = fmaf(c[k], scale[h], offset[h]);
         }
     } else {
-        const auto v = __builtin_amdgcn_raw_buffer_load_b64(page, codes + 8 * lq, 0, kStreamPolicy);
+        const auto v = __builtin_amdgcn_raw_buffer_load_b64(page, codes + 8 * lq, 0, Policy::kCodes);
 #pragma unroll
         for (int i = 0; i < 2; ++i)
 #pragma unroll
@@ -1663,8 +1683,8 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_chain_kernel(AttentionP
         for (int r = 0; r < links; ++r) {
             const RecordRegion reg = p.chain[r];
             float kr[32], vr[32];
-            chain_record<PT>(kpage, reg, tok, lq, kr);
-            chain_record<PT>(vpage, reg, tok, lq, vr);
+            chain_record<D, PT>(kpage, reg, tok, lq, kr);
+            chain_record<D, PT>(vpage, reg, tok, lq, vr);
             if (has_mean && r + 1 < links) {
 #pragma unroll
                 for (int i = 0; i < 32; i += 2) {
@@ -1681,8 +1701,8 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_chain_kernel(AttentionP
                 }
             } else {
                 const uint32_t alpha_offset = reg.offset + PT * (reg.code_bytes + 2 * reg.groups) + 2 * tok;
-                const float ak = bf16_f32(__builtin_amdgcn_raw_buffer_load_b16(kpage, alpha_offset, 0, kStreamPolicy));
-                const float av = bf16_f32(__builtin_amdgcn_raw_buffer_load_b16(vpage, alpha_offset, 0, kStreamPolicy));
+                const float ak = bf16_f32(__builtin_amdgcn_raw_buffer_load_b16(kpage, alpha_offset, 0, PagePolicy<D>::kParams));
+                const float av = bf16_f32(__builtin_amdgcn_raw_buffer_load_b16(vpage, alpha_offset, 0, PagePolicy<D>::kParams));
 #pragma unroll
                 for (int i = 0; i < 32; i += 2) {
                     kx[i] = fmaf(kx[i], ak, kr[i]);

@@ -112,11 +112,12 @@ __device__ __forceinline__ float max_z(float a, float b) {
 
 constexpr int kCoherentPolicy = 16;  // cache-policy operand: sc1
 
-// Cache-policy operand of the decode kernels' page loads: nt (non-temporal).
-// A decode call reads each page span once, so its loads stream past the
-// caches instead of displacing lines that are reused (rotations, queries,
-// block tables).  A no-arithmetic gather of one B32 x 8192-token residual-loop
-// call measured 163 us with nt against 177 us without.
+// Cache-policy operand nt (non-temporal) for page loads that stream: a
+// decode call reads each page span once, so such loads pass the caches
+// instead of displacing lines that are reused (rotations, queries, block
+// tables).  A no-arithmetic gather of one B32 x 8192-token residual-loop call
+// measured 163 us with nt against 177 us without.  Which page loads carry it
+// is chosen per head dimension (PagePolicy in attention.hip).
 constexpr int kStreamPolicy = 2;
 
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t handoff_resource(const void* base, uint32_t bytes) {
