@@ -64,20 +64,29 @@ class DeferredKVGroup:
             self.pending.append((key.clone(), value.clone()))
         return None
 
+    def wants_lookahead(self, prefill: bool) -> bool:
+        """Whether this call completes the group from the lookahead ring
+        (the ``lookahead`` flag of packed_backend.py:47-54)."""
+        return (self.prefill_offload is not None and prefill and len(self.records) > 1
+                and len(self.pending) + 1 == len(self.records) and self.prefill_offload.lookahead_enabled)
+
     def store(self, key: torch.Tensor, value: torch.Tensor, kv_cache: torch.Tensor,
               slot_mapping: torch.Tensor, key_rotation: Optional[torch.Tensor],
               value_rotation: Optional[torch.Tensor], key_mean: Optional[torch.Tensor],
-              prefill: bool = False) -> bool:
+              prefill: bool = False, lookahead: Optional[bool] = None) -> bool:
         """One loop's write: stage, and quantize the whole group on its last loop.
 
         ``prefill`` marks a call with more than one query token per request
-        (the only calls that use the offload, packed_backend.py:47)."""
+        (the only calls that use the offload, packed_backend.py:47).  A caller
+        that has already taken ``wants_lookahead`` and called the offload's
+        ``prepare`` before its attention (as ``PackedImpl.forward`` does,
+        packed_backend.py:47-55) passes that flag as ``lookahead``."""
         tokens = slot_mapping.numel()
         offload = self.prefill_offload is not None and prefill
-        lookahead = (offload and len(self.records) > 1 and len(self.pending) + 1 == len(self.records)
-                     and self.prefill_offload.lookahead_enabled)
-        if lookahead:
-            self.prefill_offload.prepare(self, tokens)
+        if lookahead is None:
+            lookahead = self.wants_lookahead(prefill)
+            if lookahead:
+                self.prefill_offload.prepare(self, tokens)
         records = self.stage(key[:tokens], value[:tokens], offload=offload)
         if (offload and records is None and len(self.pending) + 1 == len(self.records)
                 and self.prefill_offload.lookahead_enabled):
