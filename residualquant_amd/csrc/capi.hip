@@ -104,12 +104,10 @@ int compute_units() {
     return g_compute_units[device];
 }
 
-// Splits per (row, head): about two workgroups per compute unit (long page
-// streams per workgroup measured best at batch 32 x 8k), at least 4 pages per
-// split, at most rq::kMaxSplits.
 // Splits per (row, head): enough workgroups for `target` (default two per
-// compute unit, or one per compute unit with `one_per_cu`), at least 4 pages
-// per split.
+// compute unit, or one per compute unit with `one_per_cu`; long page streams
+// per workgroup measured best at batch 32 x 8k), at least 4 pages per split,
+// at most rq::kMaxSplits.
 int split_count(int64_t rows, int heads, int64_t max_pages, bool one_per_cu = false) {
     int64_t target;
     {
@@ -342,12 +340,15 @@ int rq_attention(const void* query, int64_t query_stride, const void* key, int64
     if (width != page_width) return fail(RQ_EINVAL, "Packed cache width differs from records");
     const bool adjacent = records > 1 && reference_mode == RQ_MODE_ADJACENT;
     rq::AttentionParams p;
-    // Residual loops at D = 96 run on decode96_kernel (one token half per
-    // lane), which is fastest with one workgroup per (row, head) once those
-    // fill the compute units.  Never more splits than
-    // rq_attention_workspace_bytes() provides for.
+    // At D = 96 a call takes one workgroup per (row, head) once those fill
+    // the compute units: the residual loops run decode96_kernel (one token
+    // half per lane), fastest that way, and the anchor-only loop then also
+    // prepares its query inside the decode launch (one launch per call; at
+    // 55 heads x B8 x 4096 the anchor call's two splits plus the separate
+    // prepare launch measured 1-2% slower per loop-group step).  Never more
+    // splits than rq_attention_workspace_bytes() provides for.
+    const int splits = split_count(rows, heads, max_pages, head_dim == 96);
     const int anchor_record = adjacent ? 0 : anchor_index;
-    const int splits = split_count(rows, heads, max_pages, head_dim == 96 && loop_index != anchor_record);
     status = attention_common(query, query_stride, key, key_stride, value, value_stride, output,
                               output_stride, rows, heads, head_dim, query_start_loc, seq_lens, requests,
                               block_table, block_table_stride, max_pages, workspace, workspace_bytes, splits, &p);
