@@ -216,8 +216,8 @@ int rq_quantize(int records, const void* const* key_ptrs, const int64_t* key_str
     const int width = rq_page_width(head_dim, records, bits, groups);
     if (width != page_width) return fail(RQ_EINVAL, "Packed cache width differs from records");
     for (int r = 0; r < records; ++r)
-        if (key_ptrs[r] == nullptr || value_ptrs[r] == nullptr || key_strides[r] < (int64_t)heads * head_dim ||
-            value_strides[r] < (int64_t)heads * head_dim)
+        if ((tokens > 0 && (key_ptrs[r] == nullptr || value_ptrs[r] == nullptr)) ||
+            key_strides[r] < (int64_t)heads * head_dim || value_strides[r] < (int64_t)heads * head_dim)
             return fail(RQ_EINVAL, "BF16 [tokens, heads, channels] with packed trailing strides required");
     // The rotation phase reads input rows with 8-byte scalar loads and stages
     // each FP16 rotation with 16-byte loads.
@@ -281,7 +281,7 @@ static int attention_common(const void* query, int64_t query_stride, const void*
         return fail(RQ_EINVAL, "Q/K addresses and token strides must be 8-byte aligned");
     if (requests < 0 || (requests > 0 && (query_start_loc == nullptr || seq_lens == nullptr)))
         return fail(RQ_EINVAL, "Contiguous INT32 query starts with one final boundary required");
-    if (block_table == nullptr || max_pages < 0 || block_table_stride < max_pages)
+    if ((rows > 0 && block_table == nullptr) || max_pages < 0 || block_table_stride < max_pages)
         return fail(RQ_EINVAL, "INT32 page table with packed rows required");
     const WorkspaceLayout layout = workspace_layout(rows, heads, head_dim, splits);
     if (rows > 0 && (workspace == nullptr || workspace_bytes < layout.total))

@@ -307,3 +307,27 @@ def test_attention_graph_replay(oracle, device):
         graph.replay()
         torch.cuda.synchronize()
         assert torch.equal(out, eager)
+
+
+def test_empty_calls_are_noops(device):
+    """Zero tokens / rows through every op: nothing is launched or written."""
+    g = make_group(20, 2, 128, OURO_G32, seed=77)
+    kr, vr, km = g.device_args(device)
+    cache = torch.full(g.cache_shape, 7, dtype=torch.uint8, device=device)
+    empty = torch.empty((0, 2, 128), dtype=torch.bfloat16, device=device)
+    pairs = [(empty, empty) for _ in g.records]
+    rq.quantize(pairs, cache, torch.empty(0, dtype=torch.int64, device=device), kr, vr, km, g.records, "anchor",
+                3, "ls")
+    assert bool((cache == 7).all())
+    qsl = torch.zeros(1, dtype=torch.int32, device=device)
+    lens = torch.empty(0, dtype=torch.int32, device=device)
+    table = torch.empty((0, 4), dtype=torch.int32, device=device)
+    out = torch.empty_like(empty)
+    rq.attention(empty, empty, empty, cache, out, qsl, lens, table, kr, vr, km, g.records, "anchor", 3, 1)
+    k, v = rq.dequantize(cache, torch.empty(0, dtype=torch.int64, device=device), 128, km, g.records, "anchor", 3, 0)
+    assert k.shape == (0, 2, 128) and v.shape == (0, 2, 128)
+    cu = torch.zeros(2, dtype=torch.int32, device=device)
+    res = rq.flash_attn_varlen_func(empty, empty, empty, 0, cu, 0, causal=True)
+    assert res.shape == (0, 2, 128)
+    torch.cuda.synchronize()
+    assert bool((cache == 7).all())
