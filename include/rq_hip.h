@@ -208,6 +208,18 @@ int rq_silu_mul(const void* gate_up, int64_t gate_up_stride, void* out, int64_t 
                 hipStream_t stream);
 
 /*
+ * y = bf16(x . weight^T) for 1-8 BF16 rows x [rows, in_features] and a
+ * contiguous BF16 weight [out_features, in_features] (a linear layer's
+ * weight as nn.Linear holds it), FP32 accumulation: the QKV, O, gate/up and
+ * down projections of a decode step at small batch (ouro.py:101-131 runs
+ * them through vLLM's linear layers), where the product is a stream of the
+ * weights.  in_features a multiple of 8 up to 6144; x and weight 16-byte
+ * aligned, x_stride a multiple of 8.  More rows return RQ_ENOKERNEL.
+ */
+int rq_linear_rows(const void* x, int64_t x_stride, const void* weight, void* y, int64_t y_stride, int64_t rows,
+                   int64_t out_features, int64_t in_features, hipStream_t stream);
+
+/*
  * Kernel timing for measurement: when enabled, rq_attention and
  * rq_paged_attention_bf16 record HIP events around their split-K kernel on
  * the caller's stream; rq_timing_read() synchronizes the recorded events and

@@ -31,6 +31,7 @@ EXPORTED_SYMBOLS = (
     "rq_rms_norm",
     "rq_rope_qkv",
     "rq_silu_mul",
+    "rq_linear_rows",
     "rq_timing_enable",
     "rq_timing_read",
     "rq_set_split_target",
@@ -93,6 +94,8 @@ def _declare(l: ctypes.CDLL) -> None:
     l.rq_rope_qkv.argtypes = [vp, i64, vp, vp, vp, i64, i32, i32, i64, vp, i64, vp, i64, vp, vp, i64, vp]
     l.rq_silu_mul.restype = i32
     l.rq_silu_mul.argtypes = [vp, i64, vp, i64, i64, i32, vp]
+    l.rq_linear_rows.restype = i32
+    l.rq_linear_rows.argtypes = [vp, i64, vp, vp, i64, i64, i64, i64, vp]
     l.rq_timing_enable.argtypes = [i32]
     l.rq_timing_read.restype = i32
     l.rq_timing_read.argtypes = [ctypes.POINTER(ctypes.c_double), ctypes.POINTER(ctypes.c_int64)]

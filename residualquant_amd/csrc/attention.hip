@@ -108,7 +108,6 @@ __device__ __forceinline__ int find_request_parallel(const int32_t* qsl, int64_t
 // writes R_k to LDS, which the lookup's barrier or prepare_record's first
 // barrier publishes.  prepare_record reads no global memory, so loads issued
 // after prepare_stage are not waited on before it ends.
-typedef uint32_t Chunk16 __attribute__((ext_vector_type(4)));
 
 template <int D, int Threads>
 struct PrepareInputs {

@@ -583,6 +583,26 @@ int rq_silu_mul(const void* gate_up, int64_t gate_up_stride, void* out, int64_t 
                         "SiLU-mul launch");
 }
 
+int rq_linear_rows(const void* x, int64_t x_stride, const void* weight, void* y, int64_t y_stride, int64_t rows,
+                   int64_t out_features, int64_t in_features, hipStream_t stream) {
+    if (rows < 0 || rows > rq::kLinearMaxRows)
+        return fail(RQ_ENOKERNEL, "No compiled row-projection kernel for %lld rows (at most %d)", (long long)rows,
+                    rq::kLinearMaxRows);
+    if (out_features <= 0 || out_features > (int64_t)INT32_MAX || in_features <= 0 || in_features % 8 != 0 ||
+        in_features > 6144)
+        return fail(RQ_EINVAL, "Projection needs out_features > 0 and in_features a multiple of 8 up to 6144");
+    if (x_stride < in_features || x_stride % 8 != 0 || y_stride < out_features)
+        return fail(RQ_EINVAL, "x rows of in_features (stride a multiple of 8) and y rows of out_features required");
+    if (rows == 0) return ok();
+    if (x == nullptr || weight == nullptr || y == nullptr || (reinterpret_cast<uintptr_t>(x) % 16) ||
+        (reinterpret_cast<uintptr_t>(weight) % 16) || (reinterpret_cast<uintptr_t>(y) % 2))
+        return fail(RQ_EINVAL, "16-byte aligned x and weight and a BF16 output required");
+    return check_launch(rq::launch_linear_rows(static_cast<const uint16_t*>(x), x_stride,
+                                               static_cast<const uint16_t*>(weight), static_cast<uint16_t*>(y),
+                                               y_stride, (int)rows, (int)out_features, (int)in_features, stream),
+                        "row projection launch");
+}
+
 size_t rq_prefill_workspace_bytes(int64_t batch, int heads_q, int head_dim, int64_t max_seqlen_q,
                                   int64_t max_seqlen_k, int causal, int same_lengths) {
     if (batch <= 0 || heads_q <= 0 || head_dim <= 0 || max_seqlen_q <= 0 || max_seqlen_k <= 0 ||

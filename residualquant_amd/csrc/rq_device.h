@@ -97,6 +97,11 @@ __device__ __forceinline__ float max_z(float a, float b) {
     return (a > b || (a == b && !(__float_as_uint(a) >> 31))) ? a : b;
 }
 
+// Sixteen bytes as four 32-bit words in one vector register group (a vector
+// type, unlike HIP's uint4 struct, stays in registers inside structs and
+// arrays).
+typedef uint32_t Chunk16 __attribute__((ext_vector_type(4)));
+
 // ------------------------------------------------------------------ cross-workgroup hand-off
 //
 // A workgroup that hands data to another workgroup of the same launch (the

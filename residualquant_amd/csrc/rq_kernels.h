@@ -124,6 +124,11 @@ struct StepRopeParams {
 
 hipError_t launch_rms_norm(const StepNormParams& p, hipStream_t stream);
 hipError_t launch_rope(const StepRopeParams& p, hipStream_t stream);
+// y = bf16(x . w^T) for 1 <= rows <= kLinearMaxRows rows of x [rows, in],
+// w [out, in] contiguous; in_features a multiple of 8 up to 6144.
+constexpr int kLinearMaxRows = 8;
+hipError_t launch_linear_rows(const uint16_t* x, int64_t x_stride, const uint16_t* w, uint16_t* y, int64_t y_stride,
+                              int rows, int out_features, int in_features, hipStream_t stream);
 hipError_t launch_silu_mul(const uint16_t* gate_up, int64_t gate_up_stride, uint16_t* out, int64_t out_stride,
                            int64_t rows, int width, hipStream_t stream);
 

@@ -155,6 +155,84 @@ __global__ __launch_bounds__(256) void silu_mul_kernel(const uint16_t* gate_up, 
     *reinterpret_cast<uint32_t*>(out + row * out_stride + i) = bf16_rn(a) | (bf16_rn(b) << 16);
 }
 
+
+// y[m, n] = bf16(sum_k x[m, k] * w[n, k]) for a few rows m: the decode step's
+// projections at small batch, where a GEMM is a weight stream.  One
+// workgroup computes Cols output columns for every row.  Thread t takes the
+// 16-byte chunks t, t + 256, ... of each weight row (one load instruction
+// covers 4 KB of a row, so the weights are read once, non-temporal) and the
+// same chunks of the x rows (kept in registers); FP32 partial sums meet in a
+// wave reduction and then across the 4 waves through LDS.
+constexpr int kLinearThreads = 256;
+
+__device__ __forceinline__ float dot8_bf16(const Chunk16& a, const Chunk16& b, float acc) {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        acc = fmaf(__uint_as_float(a[e] << 16), __uint_as_float(b[e] << 16), acc);
+        acc = fmaf(__uint_as_float(a[e] & 0xffff0000u), __uint_as_float(b[e] & 0xffff0000u), acc);
+    }
+    return acc;
+}
+
+// Chunks: 16-byte chunks per thread and row (in_features up to 2048 * Chunks).
+template <int M, int Cols, int Chunks>
+__global__ __launch_bounds__(kLinearThreads) void linear_rows_kernel(const uint16_t* x, int64_t x_stride,
+                                                                     const uint16_t* w, uint16_t* y, int64_t y_stride,
+                                                                     int out_features, int in_features) {
+    __shared__ float partial[kLinearThreads / 64][M * Cols];
+    const int t = threadIdx.x;
+    const int chunks = in_features / 8;
+    const int n0 = blockIdx.x * Cols;
+    const Chunk16 zero = {0u, 0u, 0u, 0u};
+    Chunk16 wv[Cols][Chunks];
+#pragma unroll
+    for (int col = 0; col < Cols; ++col) {
+        const bool row_ok = n0 + col < out_features;
+        const Chunk16* row = reinterpret_cast<const Chunk16*>(w + (int64_t)(row_ok ? n0 + col : 0) * in_features);
+#pragma unroll
+        for (int j = 0; j < Chunks; ++j) {
+            const int c = t + kLinearThreads * j;
+            wv[col][j] = (row_ok && c < chunks) ? __builtin_nontemporal_load(row + c) : zero;
+        }
+    }
+    Chunk16 xv[M][Chunks];
+#pragma unroll
+    for (int m = 0; m < M; ++m) {
+        const Chunk16* row = reinterpret_cast<const Chunk16*>(x + m * x_stride);
+#pragma unroll
+        for (int j = 0; j < Chunks; ++j) {
+            const int c = t + kLinearThreads * j;
+            xv[m][j] = c < chunks ? row[c] : zero;
+        }
+    }
+    float acc[M][Cols];
+#pragma unroll
+    for (int m = 0; m < M; ++m)
+#pragma unroll
+        for (int col = 0; col < Cols; ++col) {
+            float a = 0.f;
+#pragma unroll
+            for (int j = 0; j < Chunks; ++j) a = dot8_bf16(wv[col][j], xv[m][j], a);
+            acc[m][col] = wave_sum(a);
+        }
+    if ((t & 63) == 0) {
+#pragma unroll
+        for (int m = 0; m < M; ++m)
+#pragma unroll
+            for (int col = 0; col < Cols; ++col) partial[t >> 6][m * Cols + col] = acc[m][col];
+    }
+    __syncthreads();
+    if (t < M * Cols) {
+        const int m = t / Cols, col = t % Cols;
+        if (n0 + col < out_features) {
+            float sum = 0.f;
+#pragma unroll
+            for (int wave = 0; wave < kLinearThreads / 64; ++wave) sum += partial[wave][t];
+            y[m * y_stride + n0 + col] = (uint16_t)bf16_rn(sum);
+        }
+    }
+}
+
 }  // namespace
 
 hipError_t launch_rms_norm(const StepNormParams& p, hipStream_t stream) {
@@ -178,6 +256,43 @@ hipError_t launch_silu_mul(const uint16_t* gate_up, int64_t gate_up_stride, uint
     if (rows == 0) return hipSuccess;
     hipLaunchKernelGGL(silu_mul_kernel, dim3((unsigned)((width / 2 + 255) / 256), (unsigned)rows), dim3(256), 0,
                        stream, gate_up, gate_up_stride, out, out_stride, width);
+    return hipGetLastError();
+}
+
+hipError_t launch_linear_rows(const uint16_t* x, int64_t x_stride, const uint16_t* w, uint16_t* y, int64_t y_stride,
+                              int rows, int out_features, int in_features, hipStream_t stream) {
+    if (rows == 0 || out_features == 0) return hipSuccess;
+    // Chunks per thread from in_features; columns per workgroup so that the
+    // weight, x and accumulator registers stay near 128 per lane.
+    const int chunks = (in_features / 8 + kLinearThreads - 1) / kLinearThreads;
+    const int cols = chunks == 1 ? 8 : (chunks == 2 || rows <= 4 ? 4 : 2);
+    const dim3 grid((unsigned)((out_features + cols - 1) / cols));
+#define RQ_LINEAR_CASE(M)                                                                                         \
+    case M:                                                                                                       \
+        if (chunks == 1)                                                                                          \
+            hipLaunchKernelGGL((linear_rows_kernel<M, 8, 1>), grid, dim3(kLinearThreads), 0, stream, x, x_stride, \
+                               w, y, y_stride, out_features, in_features);                                        \
+        else if (chunks == 2)                                                                                     \
+            hipLaunchKernelGGL((linear_rows_kernel<M, 4, 2>), grid, dim3(kLinearThreads), 0, stream, x, x_stride, \
+                               w, y, y_stride, out_features, in_features);                                        \
+        else                                                                                                      \
+            hipLaunchKernelGGL((linear_rows_kernel<M, (M <= 4 ? 4 : 2), 3>), grid, dim3(kLinearThreads), 0, stream, \
+                               x, x_stride,                                                                       \
+                               w, y, y_stride, out_features, in_features);                                        \
+        break;
+    switch (rows) {
+        RQ_LINEAR_CASE(1)
+        RQ_LINEAR_CASE(2)
+        RQ_LINEAR_CASE(3)
+        RQ_LINEAR_CASE(4)
+        RQ_LINEAR_CASE(5)
+        RQ_LINEAR_CASE(6)
+        RQ_LINEAR_CASE(7)
+        RQ_LINEAR_CASE(8)
+        default:
+            return hipErrorInvalidValue;
+    }
+#undef RQ_LINEAR_CASE
     return hipGetLastError();
 }
 

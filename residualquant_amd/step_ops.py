@@ -121,3 +121,28 @@ def silu_mul(gate_up: torch.Tensor, out: Optional[torch.Tensor] = None) -> torch
                                         width, _stream(gate_up.device))
     _lib.check(status)
     return out
+
+
+LINEAR_MAX_ROWS = 8
+
+
+def linear_rows(x: torch.Tensor, weight: torch.Tensor, out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """``bf16(x @ weight.T)`` for 1-8 BF16 rows (rq_linear_rows), FP32 accumulation.
+
+    ``weight`` is a contiguous BF16 ``[out_features, in_features]`` linear
+    weight; ``in_features`` a multiple of 8 up to 6144.  The projections of a
+    decode step at small batch, streamed as matrix-vector products."""
+    _rows(x, "x")
+    rows, in_features = x.shape
+    _require(weight.is_cuda and weight.dtype == torch.bfloat16 and weight.dim() == 2 and weight.is_contiguous()
+             and weight.size(1) == in_features and weight.device == x.device,
+             "weight must be a contiguous BF16 [out_features, in_features] tensor on x's device")
+    if out is None:
+        out = torch.empty((rows, weight.size(0)), dtype=torch.bfloat16, device=x.device)
+    _rows(out, "out")
+    _require(out.shape == (rows, weight.size(0)) and out.device == x.device, "out must be [rows, out_features]")
+    with torch.cuda.device(x.device):
+        status = _lib.lib().rq_linear_rows(x.data_ptr(), x.stride(0), weight.data_ptr(), out.data_ptr(), out.stride(0),
+                                          rows, weight.size(0), in_features, _stream(x.device))
+    _lib.check(status)
+    return out

@@ -136,3 +136,34 @@ def test_rejects_unsupported_shapes(device):
                           torch.ones(4096, dtype=torch.bfloat16, device=device), 1e-6)
     with pytest.raises(RuntimeError, match="even width"):
         step_ops.silu_mul(torch.zeros((2, 6), dtype=torch.bfloat16, device=device))
+
+
+@pytest.mark.parametrize("rows", [1, 2, 3, 4, 5, 8])
+@pytest.mark.parametrize("out_features,in_features", [(6144, 2048), (2048, 5632), (100, 2048), (20, 8)])
+def test_linear_rows_matches_fp32_product(device, rows, out_features, in_features):
+    """bf16(x @ w^T) with FP32 accumulation: within one BF16 rounding of the
+    FP32 product (the summation order differs from torch's)."""
+    g = torch.Generator(device=device).manual_seed(rows * 7919 + out_features + in_features)
+    weight = (torch.randn((out_features, in_features), generator=g, device=device) * 0.02).to(torch.bfloat16)
+    x = torch.randn((rows, in_features), generator=g, device=device).to(torch.bfloat16)
+    got = step_ops.linear_rows(x, weight)
+    want = x.float() @ weight.float().t()
+    assert got.shape == (rows, out_features)
+    err = (got.float() - want).abs()
+    assert bool((err <= want.abs() * 2.0 ** -8 + 1e-4).all()), float(err.max())
+
+
+def test_linear_rows_strided_rows_and_rejections(device):
+    g = torch.Generator(device=device).manual_seed(3)
+    weight = (torch.randn((64, 256), generator=g, device=device) * 0.05).to(torch.bfloat16)
+    wide = torch.randn((3, 512), generator=g, device=device).to(torch.bfloat16)
+    x = wide[:, 128:384]  # row stride 512, 16-byte aligned
+    out = torch.empty((3, 96), dtype=torch.bfloat16, device=device)[:, 16:80]
+    step_ops.linear_rows(x, weight, out=out)
+    want = x.float() @ weight.float().t()
+    assert bool(((out.float() - want).abs() <= want.abs() * 2.0 ** -8 + 1e-4).all())
+    with pytest.raises(RuntimeError, match="No compiled row-projection kernel"):
+        step_ops.linear_rows(torch.zeros((9, 256), dtype=torch.bfloat16, device=device), weight)
+    with pytest.raises(RuntimeError, match="multiple of 8"):
+        step_ops.linear_rows(torch.zeros((1, 12), dtype=torch.bfloat16, device=device),
+                             torch.zeros((4, 12), dtype=torch.bfloat16, device=device))
