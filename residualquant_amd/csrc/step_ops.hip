@@ -165,16 +165,6 @@ __global__ __launch_bounds__(256) void silu_mul_kernel(const uint16_t* gate_up, 
 // wave reduction and then across the 4 waves through LDS.
 constexpr int kLinearThreads = 256;
 
-__device__ __forceinline__ float dot8_bf16(const Chunk16& a, const Chunk16& b, float acc) {
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-        acc = fmaf(__uint_as_float(a[e] << 16), __uint_as_float(b[e] << 16), acc);
-        acc = fmaf(__uint_as_float(a[e] & 0xffff0000u), __uint_as_float(b[e] & 0xffff0000u), acc);
-    }
-    return acc;
-}
-
-// Chunks: 16-byte chunks per thread and row (in_features up to 2048 * Chunks).
 template <int M, int Cols, int Chunks>
 __global__ __launch_bounds__(kLinearThreads) void linear_rows_kernel(const uint16_t* x, int64_t x_stride,
                                                                      const uint16_t* w, uint16_t* y, int64_t y_stride,
@@ -205,16 +195,40 @@ __global__ __launch_bounds__(kLinearThreads) void linear_rows_kernel(const uint1
             xv[m][j] = c < chunks ? row[c] : zero;
         }
     }
+    // Each chunk's x values are widened once and shared by every column.
     float acc[M][Cols];
 #pragma unroll
     for (int m = 0; m < M; ++m)
 #pragma unroll
-        for (int col = 0; col < Cols; ++col) {
-            float a = 0.f;
+        for (int col = 0; col < Cols; ++col) acc[m][col] = 0.f;
 #pragma unroll
-            for (int j = 0; j < Chunks; ++j) a = dot8_bf16(wv[col][j], xv[m][j], a);
-            acc[m][col] = wave_sum(a);
+    for (int j = 0; j < Chunks; ++j) {
+        float xf[M][8];
+#pragma unroll
+        for (int m = 0; m < M; ++m)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                xf[m][2 * e] = __uint_as_float(xv[m][j][e] << 16);
+                xf[m][2 * e + 1] = __uint_as_float(xv[m][j][e] & 0xffff0000u);
+            }
+#pragma unroll
+        for (int col = 0; col < Cols; ++col) {
+            float wf[8];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                wf[2 * e] = __uint_as_float(wv[col][j][e] << 16);
+                wf[2 * e + 1] = __uint_as_float(wv[col][j][e] & 0xffff0000u);
+            }
+#pragma unroll
+            for (int m = 0; m < M; ++m)
+#pragma unroll
+                for (int e = 0; e < 8; ++e) acc[m][col] = fmaf(wf[e], xf[m][e], acc[m][col]);
         }
+    }
+#pragma unroll
+    for (int m = 0; m < M; ++m)
+#pragma unroll
+        for (int col = 0; col < Cols; ++col) acc[m][col] = wave_sum(acc[m][col]);
     if ((t & 63) == 0) {
 #pragma unroll
         for (int m = 0; m < M; ++m)

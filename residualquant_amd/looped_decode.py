@@ -43,7 +43,7 @@ from .layout import page_width
 
 # Rows up to which the projections run on rq_linear_rows (measured per layer
 # at hidden 2048, graph replay over 48 layers' weights: 26.8 vs 37.7 us at
-# one row, 33.0 vs 48.0 at two, 46.7 vs 48.0 at four, 74.6 vs 48.1 at eight).
+# one row, 30.9 vs 48.0 at two, 47.3 vs 48.4 at four, 72.8 vs 48.5 at eight).
 LINEAR_ROWS_MAX = 2
 
 
