@@ -225,16 +225,40 @@ __global__ __launch_bounds__(kLinearThreads) void linear_rows_kernel(const uint1
                 for (int e = 0; e < 8; ++e) acc[m][col] = fmaf(wf[e], xf[m][e], acc[m][col]);
         }
     }
+    // Reduce-scatter over the wave: each exchange at distance d halves the
+    // values a lane keeps (lanes with bit d set keep the upper half and add
+    // the partner's copy of it), so after log2(V) exchanges lane l holds the
+    // wave total of value l / (64 / V), summed over the remaining lane bits.
+    constexpr int V = M * Cols;
+    static_assert(V <= 64, "at most 64 values per lane");
+    float v[64];
 #pragma unroll
     for (int m = 0; m < M; ++m)
 #pragma unroll
-        for (int col = 0; col < Cols; ++col) acc[m][col] = wave_sum(acc[m][col]);
-    if ((t & 63) == 0) {
+        for (int col = 0; col < Cols; ++col) v[m * Cols + col] = acc[m][col];
+    constexpr int P = V <= 1 ? 1 : V <= 2 ? 2 : V <= 4 ? 4 : V <= 8 ? 8 : V <= 16 ? 16 : V <= 32 ? 32 : 64;
 #pragma unroll
-        for (int m = 0; m < M; ++m)
+    for (int i = V; i < P; ++i) v[i] = 0.f;
+    const int lane = t & 63;
+    int n = P;
 #pragma unroll
-            for (int col = 0; col < Cols; ++col) partial[t >> 6][m * Cols + col] = acc[m][col];
+    for (int d = 32; d >= 64 / P; d >>= 1) {
+        const bool upper = (lane & d) != 0;
+        n >>= 1;
+#pragma unroll
+        for (int i = 0; i < 32; ++i) {
+            if (i < n) {
+                const float send = upper ? v[i] : v[i + n];
+                const float keep = upper ? v[i + n] : v[i];
+                v[i] = keep + __shfl_xor(send, d);
+            }
+        }
     }
+    float total = v[0];
+#pragma unroll
+    for (int d = 64 / P / 2; d >= 1; d >>= 1) total += __shfl_xor(total, d);
+    const int index = lane / (64 / P);
+    if ((lane & (64 / P - 1)) == 0 && index < V) partial[t >> 6][index] = total;
     __syncthreads();
     if (t < M * Cols) {
         const int m = t / Cols, col = t % Cols;

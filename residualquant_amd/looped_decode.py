@@ -42,15 +42,16 @@ from .layout import page_width
 
 
 # Rows up to which the projections run on rq_linear_rows (measured per layer
-# at hidden 2048, graph replay over 48 layers' weights: 26.8 vs 37.7 us at
-# one row, 30.9 vs 48.0 at two, 47.3 vs 48.4 at four, 72.8 vs 48.5 at eight).
-LINEAR_ROWS_MAX = 2
+# at hidden 2048, graph replay over 48 layers' weights, against hipBLASLt:
+# 25.6 vs 37.7 us at one row, 26.0 vs 48.0 at two, 31.3 vs 48.1 at four,
+# 42.8 vs 48.0 at eight).
+LINEAR_ROWS_MAX = 8
 
 
 def _project(x: torch.Tensor, weight: torch.Tensor) -> torch.Tensor:
     """``x @ weight.T`` for a linear weight held ``[out, in]``.
 
-    At one or two rows the product is a weight stream: ``step_ops.linear_rows``
+    At up to eight rows the product is a weight stream: ``step_ops.linear_rows``
     reads every weight row once with 16-byte loads and FP32 accumulation.
     Larger batches take hipBLASLt through ``F.linear``."""
     rows, in_features = x.shape
