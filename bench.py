@@ -104,9 +104,9 @@ def capture(torch, fn):
     return graph
 
 
-def measured_traffic():
-    """HBM bytes per residual-loop decode launch from the committed rocprofv3 counter summary."""
-    path = os.path.join(ROOT, "profiles", "decode_c2_counters.json")
+def measured_traffic(summary="decode_c2_counters.json"):
+    """HBM bytes per residual-loop decode launch from a committed rocprofv3 counter summary."""
+    path = os.path.join(ROOT, "profiles", summary)
     if not os.path.exists(path):
         return None
     with open(path) as handle:
@@ -459,7 +459,7 @@ def run_huginn(args):
             "peak": PEAK_HBM_GBPS,
             "unit": "GB/s",
             "frac": residual_gbps / PEAK_HBM_GBPS,
-            "traffic": None,
+            "traffic": measured_traffic("decode_c4_counters.json"),
             "kernel": f"decode96_kernel<16,4,32,2,16,true> (residual loop), {launches} HIP-event-timed launches",
         },
         "bf16_baseline": {
