@@ -103,3 +103,54 @@ def test_forward_routes_prompts_and_decode_like_the_reference(device):
     expected_cache = cache_before.clone()
     rq.quantize(kv_b, expected_cache, slots_b, kr, vr, mean, RECORDS, "anchor", 3, "ls")
     assert torch.equal(cache, expected_cache), "cache after the mixed batch"
+
+
+@pytest.mark.parametrize("lookahead", [False, True], ids=["chunks", "lookahead"])
+def test_forward_with_prefill_offload(device, lookahead):
+    """Two layers' groups with the pinned-host prefill offload driven through
+    ``backend.forward`` in model order (every layer of loop 0, then loop 1,
+    ...): the forward prepares the lookahead before its attention calls, and
+    the caches hold the bytes of one quantize of every record."""
+    from residualquant_amd.prefill_offload import PrefillCPUOffload
+
+    layers, lens = 2, [150, 90]
+    tokens = sum(lens)
+    offload = PrefillCPUOffload(64, len(RECORDS) - 1, HEADS, DIM)
+    offload.lookahead_enabled = lookahead
+    offload.reserve(tokens)
+    table = workloads.block_tables(2, PAGES * 4, 51, device=device)
+    slots = _slots(table, [(0, (0, lens[0])), (1, (0, lens[1]))]).to(device)
+    meta = backend.build_metadata(torch.tensor([0, lens[0], tokens], dtype=torch.int32),
+                                  torch.tensor(lens, dtype=torch.int32), table, slots)
+    chain, states, caches, data = [], [], [], []
+    for i in range(layers):
+        group = rq.DeferredKVGroup(CONFIG, RECORDS, PT, prefill_offload=offload)
+        if lookahead:
+            group.offload_chain, group.offload_index = chain, i
+            chain.append(group)
+        kr = workloads.random_sign_rotation(HEADS, DIM, 60 + i, device=device)
+        vr = workloads.random_sign_rotation(HEADS, DIM, 70 + i, device=device)
+        states.append(backend.PackedLayer(group=group, loop_index=0, key_rotation=kr, value_rotation=vr))
+        shape = backend.kv_cache_shape(table.numel(), PT, HEADS, rq.page_width(DIM, RECORDS))
+        caches.append(torch.zeros(shape, dtype=torch.uint8, device=device))
+        data.append(workloads.loop_kv(tokens, HEADS, DIM, len(RECORDS), 80 + i, device=device, anchor_index=3))
+    generator = torch.Generator(device=device).manual_seed(90)
+    cu = torch.tensor([0, lens[0], tokens], dtype=torch.int32, device=device)
+    for loop in range(len(RECORDS)):
+        for i in range(layers):
+            print(f"offload forward lookahead={lookahead} loop {loop} layer {i}", flush=True)
+            states[i].loop_index = loop
+            key, value = data[i][loop]
+            q = torch.randn((tokens, HEADS, DIM), generator=generator, device=device).to(torch.bfloat16)
+            out = torch.empty_like(q)
+            backend.forward(states[i], q, key.clone(), value.clone(), caches[i], meta, out)
+            expected = rq.flash_attn_varlen_func(q, key, value, max(lens), cu, max(lens),
+                                                 softmax_scale=DIM ** -0.5, causal=True)
+            assert torch.equal(out, expected)
+    for i in range(layers):
+        direct = torch.zeros_like(caches[i])
+        rq.quantize(data[i], direct, slots, states[i].key_rotation, states[i].value_rotation, None, RECORDS,
+                    "anchor", 3, "ls")
+        assert torch.equal(caches[i], direct), i
+    if lookahead:
+        assert offload.prefetched == {}
