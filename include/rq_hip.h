@@ -106,6 +106,30 @@ int rq_attention(const void* query, int64_t query_stride, const void* key, int64
                  int loop_index, void* workspace, size_t workspace_bytes, hipStream_t stream);
 
 /*
+ * rq_attention without a workspace argument, for callers that cannot
+ * allocate device memory (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc).  No counterpart in the reference, whose
+ * attention() allocates its temporaries per call (attention/launch.cuh:85-98).
+ * Same arguments, semantics, kernels and results as rq_attention; the
+ * workspace is a static device array of RQ_ATTENTION_NOALLOC_MAX_BYTES per
+ * GPU, held until the process ends, so a call whose
+ * rq_attention_workspace_bytes(...) exceeds that size returns RQ_ENOSPACE.
+ * Every noalloc call on one GPU shares that array: calls that overlap on one
+ * GPU (concurrent streams or threads) race and must be serialized by the
+ * caller.  Calls no hipMalloc/hipFree and records no timing events.
+ */
+#define RQ_ATTENTION_NOALLOC_MAX_BYTES ((size_t)8 << 20)
+int rq_attention_noalloc(const void* query, int64_t query_stride, const void* key, int64_t key_stride,
+                         const void* value, int64_t value_stride, void* output, int64_t output_stride,
+                         int64_t rows, int heads, int head_dim, const void* kv_cache, int64_t num_blocks,
+                         int page_tokens, int page_width, const int32_t* query_start_loc,
+                         const int32_t* seq_lens, int64_t requests, const int32_t* block_table,
+                         int64_t block_table_stride, int64_t max_pages, const void* key_rotation,
+                         const void* value_rotation, const float* key_mean, int records, const int* bits,
+                         const int* groups, int reference_mode, int anchor_index, int loop_index,
+                         hipStream_t stream);
+
+/*
  * Restore the BF16 K/V of `loop_index` at the given slots (rotated space,
  * K including its mean): the record value the quantizer keeps as its
  * reference (quantize/kernel.cuh:160-203; attention/compute.cuh:28-197).

@@ -15,6 +15,7 @@ LIB_PATH = os.environ.get("RQ_HIP_LIBRARY") or os.path.join(PACKAGE_DIR, "librq_
 CSRC_DIR = os.path.join(PACKAGE_DIR, "csrc")
 
 RQ_OK, RQ_EINVAL, RQ_ENOKERNEL, RQ_ELAUNCH, RQ_ENOSPACE = 0, -1, -2, -3, -4
+RQ_ATTENTION_NOALLOC_MAX_BYTES = 8 << 20
 
 # Every symbol include/rq_hip.h declares.
 EXPORTED_SYMBOLS = (
@@ -24,6 +25,7 @@ EXPORTED_SYMBOLS = (
     "rq_quantize",
     "rq_attention_workspace_bytes",
     "rq_attention",
+    "rq_attention_noalloc",
     "rq_dequantize",
     "rq_paged_attention_bf16",
     "rq_prefill_attention",
@@ -76,6 +78,9 @@ def _declare(l: ctypes.CDLL) -> None:
     l.rq_attention.argtypes = [vp, i64, vp, i64, vp, i64, vp, i64, i64, i32, i32, vp, i64, i32, i32,
                                vp, vp, i64, vp, i64, i64, vp, vp, vp, i32, vp, vp, i32, i32, i32, vp,
                                sz, vp]
+    l.rq_attention_noalloc.restype = i32
+    l.rq_attention_noalloc.argtypes = [vp, i64, vp, i64, vp, i64, vp, i64, i64, i32, i32, vp, i64, i32, i32,
+                                       vp, vp, i64, vp, i64, i64, vp, vp, vp, i32, vp, vp, i32, i32, i32, vp]
     l.rq_dequantize.restype = i32
     l.rq_dequantize.argtypes = [vp, i64, i32, i32, i32, vp, i64, i32, vp, i32, vp, vp, i32, i32, i32,
                                 vp, vp, vp]

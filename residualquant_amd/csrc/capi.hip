@@ -314,15 +314,26 @@ static int attention_common(const void* query, int64_t query_stride, const void*
     return RQ_OK;
 }
 
-int rq_attention(const void* query, int64_t query_stride, const void* key, int64_t key_stride,
-                 const void* value, int64_t value_stride, void* output, int64_t output_stride,
-                 int64_t rows, int heads, int head_dim, const void* kv_cache, int64_t num_blocks,
-                 int page_tokens, int page_width, const int32_t* query_start_loc, const int32_t* seq_lens,
-                 int64_t requests, const int32_t* block_table, int64_t block_table_stride,
-                 int64_t max_pages, const void* key_rotation, const void* value_rotation,
-                 const float* key_mean, int records, const int* bits, const int* groups,
-                 int reference_mode, int anchor_index, int loop_index, void* workspace,
-                 size_t workspace_bytes, hipStream_t stream) {
+// Splits per (row, head) of a packed attention call.  At D = 96 a call takes
+// one workgroup per (row, head) once those fill the compute units: the
+// residual loops run decode96_kernel (one token half per lane), fastest that
+// way, and the anchor-only loop then also prepares its query inside the
+// decode launch (one launch per call; at 55 heads x B8 x 4096 the anchor
+// call's two splits plus the separate prepare launch measured 1-2% slower per
+// loop-group step).
+static int packed_splits(int64_t rows, int heads, int head_dim, int64_t max_pages) {
+    return split_count(rows, heads, max_pages, head_dim == 96);
+}
+
+static int attention_packed(const void* query, int64_t query_stride, const void* key, int64_t key_stride,
+                            const void* value, int64_t value_stride, void* output, int64_t output_stride,
+                            int64_t rows, int heads, int head_dim, const void* kv_cache, int64_t num_blocks,
+                            int page_tokens, int page_width, const int32_t* query_start_loc,
+                            const int32_t* seq_lens, int64_t requests, const int32_t* block_table,
+                            int64_t block_table_stride, int64_t max_pages, const void* key_rotation,
+                            const void* value_rotation, const float* key_mean, int records, const int* bits,
+                            const int* groups, int reference_mode, int anchor_index, int loop_index,
+                            void* workspace, size_t workspace_bytes, hipStream_t stream, bool timed) {
     int status = validate_schedule(head_dim, records, bits, groups, page_tokens, reference_mode,
                                    anchor_index, heads);
     if (status != RQ_OK) return status;
@@ -340,14 +351,8 @@ int rq_attention(const void* query, int64_t query_stride, const void* key, int64
     if (width != page_width) return fail(RQ_EINVAL, "Packed cache width differs from records");
     const bool adjacent = records > 1 && reference_mode == RQ_MODE_ADJACENT;
     rq::AttentionParams p;
-    // At D = 96 a call takes one workgroup per (row, head) once those fill
-    // the compute units: the residual loops run decode96_kernel (one token
-    // half per lane), fastest that way, and the anchor-only loop then also
-    // prepares its query inside the decode launch (one launch per call; at
-    // 55 heads x B8 x 4096 the anchor call's two splits plus the separate
-    // prepare launch measured 1-2% slower per loop-group step).  Never more
-    // splits than rq_attention_workspace_bytes() provides for.
-    const int splits = split_count(rows, heads, max_pages, head_dim == 96);
+    // Never more splits than rq_attention_workspace_bytes() provides for.
+    const int splits = packed_splits(rows, heads, head_dim, max_pages);
     const int anchor_record = adjacent ? 0 : anchor_index;
     status = attention_common(query, query_stride, key, key_stride, value, value_stride, output,
                               output_stride, rows, heads, head_dim, query_start_loc, seq_lens, requests,
@@ -374,9 +379,88 @@ int rq_attention(const void* query, int64_t query_stride, const void* key, int64
     p.chain_length = adjacent && loop_index > 0 ? loop_index + 1 : 0;
     for (int r = 0; r < p.chain_length; ++r) p.chain[r] = regions[r];
     p.key_mean_all = key_mean;
-    hipEvent_t begin, end;
-    timing_events(stream, &begin, &end);
+    hipEvent_t begin = nullptr, end = nullptr;
+    if (timed) timing_events(stream, &begin, &end);
     return check_launch(rq::launch_attention(p, stream, begin, end), "attention launch");
+}
+
+// ------------------------------------------------- attention without a workspace
+
+// Device scratch of rq_attention_noalloc: the attention workspace (request of
+// each row, split arrival counters, query records, split partials) for
+// callers that cannot allocate.  Each GPU holds its own copy for the life of
+// the process; host code reaches it only through the address that
+// hipGetSymbolAddress returns on that device (scratch_address), never
+// through the name.  Every noalloc call on a GPU shares it, so calls that
+// overlap on one GPU race; what must start at zero (the arrival counters) is
+// cleared by the call's own kernels.
+constexpr size_t kAttentionScratchBytes = RQ_ATTENTION_NOALLOC_MAX_BYTES;
+static __device__ __align__(256) uint8_t scratch[kAttentionScratchBytes];
+
+static std::mutex g_scratch_mutex;
+static std::vector<void*> g_scratch_address;  // per device; null until looked up
+
+// The current device's address of `scratch`, looked up once per device with
+// that device current.
+static int scratch_address(void** address) {
+    int device = 0;
+    hipError_t status = hipGetDevice(&device);
+    if (status != hipSuccess) return fail(RQ_ELAUNCH, "hipGetDevice: %s", hipGetErrorString(status));
+    std::lock_guard<std::mutex> lock(g_scratch_mutex);
+    if ((int)g_scratch_address.size() <= device) g_scratch_address.resize(device + 1, nullptr);
+    if (g_scratch_address[device] == nullptr) {
+        void* ptr = nullptr;
+        status = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+        if (status != hipSuccess || ptr == nullptr)
+            return fail(RQ_ELAUNCH, "hipGetSymbolAddress(scratch): %s", hipGetErrorString(status));
+        g_scratch_address[device] = ptr;
+    }
+    *address = g_scratch_address[device];
+    return RQ_OK;
+}
+
+int rq_attention(const void* query, int64_t query_stride, const void* key, int64_t key_stride,
+                 const void* value, int64_t value_stride, void* output, int64_t output_stride,
+                 int64_t rows, int heads, int head_dim, const void* kv_cache, int64_t num_blocks,
+                 int page_tokens, int page_width, const int32_t* query_start_loc, const int32_t* seq_lens,
+                 int64_t requests, const int32_t* block_table, int64_t block_table_stride,
+                 int64_t max_pages, const void* key_rotation, const void* value_rotation,
+                 const float* key_mean, int records, const int* bits, const int* groups,
+                 int reference_mode, int anchor_index, int loop_index, void* workspace,
+                 size_t workspace_bytes, hipStream_t stream) {
+    return attention_packed(query, query_stride, key, key_stride, value, value_stride, output, output_stride,
+                            rows, heads, head_dim, kv_cache, num_blocks, page_tokens, page_width,
+                            query_start_loc, seq_lens, requests, block_table, block_table_stride, max_pages,
+                            key_rotation, value_rotation, key_mean, records, bits, groups, reference_mode,
+                            anchor_index, loop_index, workspace, workspace_bytes, stream, true);
+}
+
+int rq_attention_noalloc(const void* query, int64_t query_stride, const void* key, int64_t key_stride,
+                         const void* value, int64_t value_stride, void* output, int64_t output_stride,
+                         int64_t rows, int heads, int head_dim, const void* kv_cache, int64_t num_blocks,
+                         int page_tokens, int page_width, const int32_t* query_start_loc,
+                         const int32_t* seq_lens, int64_t requests, const int32_t* block_table,
+                         int64_t block_table_stride, int64_t max_pages, const void* key_rotation,
+                         const void* value_rotation, const float* key_mean, int records, const int* bits,
+                         const int* groups, int reference_mode, int anchor_index, int loop_index,
+                         hipStream_t stream) {
+    if (rows > 0 && heads > 0 && head_dim > 0) {
+        const size_t needed =
+            workspace_layout(rows, heads, head_dim, packed_splits(rows, heads, head_dim, max_pages)).total;
+        if (needed > kAttentionScratchBytes)
+            return fail(RQ_ENOSPACE,
+                        "rq_attention_noalloc: this call needs %zu bytes of scratch, the static scratch holds "
+                        "%zu; call rq_attention with a workspace instead",
+                        needed, kAttentionScratchBytes);
+    }
+    void* workspace = nullptr;
+    const int status = scratch_address(&workspace);
+    if (status != RQ_OK) return status;
+    return attention_packed(query, query_stride, key, key_stride, value, value_stride, output, output_stride,
+                            rows, heads, head_dim, kv_cache, num_blocks, page_tokens, page_width,
+                            query_start_loc, seq_lens, requests, block_table, block_table_stride, max_pages,
+                            key_rotation, value_rotation, key_mean, records, bits, groups, reference_mode,
+                            anchor_index, loop_index, workspace, kAttentionScratchBytes, stream, false);
 }
 
 int rq_dequantize(const void* kv_cache, int64_t num_blocks, int heads, int page_tokens, int page_width,

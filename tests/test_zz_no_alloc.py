@@ -1,0 +1,86 @@
+"""rq_attention_noalloc (workspace in a static device array) against
+rq_attention (caller workspace), both called through the C ABI on the same
+inputs: the outputs must be identical, on two calls in a row with the second
+one smaller, and sizes beyond the static scratch are rejected on the host."""
+
+from __future__ import annotations
+
+import ctypes
+
+import numpy as np
+import pytest
+import torch
+
+from residualquant_amd import _lib
+
+from .cases import OURO_G32, make_decode, oracle_attention
+
+pytestmark = pytest.mark.gpu
+
+_MODES = {"anchor": 0, "adjacent": 1}
+
+
+def _schedule(records):
+    bits = (ctypes.c_int * len(records))(*[r[0] for r in records])
+    groups = (ctypes.c_int * len(records))(*[r[1] for r in records])
+    return bits, groups
+
+
+def _call(lib, d, device, cache, loop, noalloc):
+    g = d.group
+    q, k, v = (t.to(device) for t in (d.query, d.key, d.value))
+    out = torch.full_like(q, float("nan"))
+    starts, lens, table = (t.to(device) for t in (d.query_start_loc, d.seq_lens, d.table))
+    kr, vr, km = g.device_args(device)
+    rows, heads, dim = q.shape
+    bits, groups = _schedule(g.records)
+    ptr = (lambda t: None if t is None else t.data_ptr())
+    stream = torch.cuda.current_stream(device).cuda_stream
+    common = [q.data_ptr(), q.stride(0), k.data_ptr(), k.stride(0), v.data_ptr(), v.stride(0),
+              out.data_ptr(), out.stride(0), rows, heads, dim, cache.data_ptr(), cache.size(1),
+              cache.size(3), cache.size(4), starts.data_ptr(), lens.data_ptr(), len(d.lengths),
+              table.data_ptr(), table.stride(0), table.size(1), ptr(kr), ptr(vr), ptr(km),
+              len(g.records), bits, groups, _MODES[g.mode], g.anchor, loop]
+    if noalloc:
+        status = lib.rq_attention_noalloc(*common, stream)
+    else:
+        size = lib.rq_attention_workspace_bytes(rows, heads, dim, table.size(1), cache.size(3))
+        workspace = torch.empty(size, dtype=torch.uint8, device=device)
+        status = lib.rq_attention(*common, workspace.data_ptr(), size, stream)
+    _lib.check(status)
+    torch.cuda.synchronize(device)
+    return out
+
+
+def test_noalloc_matches_workspace_entry_point(oracle, device):
+    lib = _lib.lib()
+    # The first call splits each (row, head) over several workgroups (arrival
+    # counters and partials in the scratch); the second is smaller and
+    # reuses the scratch the first one left behind.
+    cases = [([700, 300, 129, 50], 4, 61), ([90, 33], 4, 62)]
+    for lengths, heads, seed in cases:
+        print(f"[case] noalloc lengths={lengths} heads={heads} seed={seed}", flush=True)
+        d = make_decode(lengths, heads, 128, OURO_G32, seed=seed)
+        expected_cache = d.group.oracle_cache(oracle)
+        cache = torch.from_numpy(expected_cache).to(device)
+        for loop in (0, 3):
+            want = _call(lib, d, device, cache, loop, noalloc=False)
+            got = _call(lib, d, device, cache, loop, noalloc=True)
+            assert torch.equal(got.view(torch.int16), want.view(torch.int16)), f"loop {loop}"
+            err = np.abs(got.float().cpu().numpy() - oracle_attention(oracle, d, expected_cache, loop))
+            assert err.max() <= 2e-2 and err.mean() <= 1e-3, (err.max(), err.mean())
+
+
+def test_noalloc_rejects_calls_beyond_the_scratch(device):
+    lib = _lib.lib()
+    heads, dim, rows = 16, 128, 8192
+    needed = lib.rq_attention_workspace_bytes(rows, heads, dim, 8, 16)
+    assert needed > _lib.RQ_ATTENTION_NOALLOC_MAX_BYTES
+    bits, groups = _schedule(OURO_G32)
+    dummy = torch.zeros(16, dtype=torch.uint8, device=device).data_ptr()
+    status = lib.rq_attention_noalloc(dummy, heads * dim, dummy, heads * dim, dummy, heads * dim, dummy,
+                                      heads * dim, rows, heads, dim, dummy, 1, 16, 200, dummy, dummy, rows,
+                                      dummy, 8, 8, None, None, None, 4, bits, groups, 0, 3, 0,
+                                      torch.cuda.current_stream(device).cuda_stream)
+    assert status == _lib.RQ_ENOSPACE
+    assert b"static scratch" in lib.rq_last_error()
