@@ -4,7 +4,8 @@
   torch FP8 scales) rebuilt into keys as the reference decode kernel scores
   them (compute.cuh:397-505: alpha_L * (c.s+o + bf16(mu_A))_A + (c.s+o)_L,
   shift-invariant mean of the current loop) and values as its BF16 restore
-  (compute.cuh:28-107), then a textbook float64 softmax.
+  (compute.cuh:28-107), then a textbook float64 softmax.  Adjacent mode is
+  pinned the same way in test_oracle_restore_pins.py.
 - Closed forms: no history -> the live value exactly (merge.cuh:19-83);
   q = 0 -> uniform weights over history and live token.
 - Moving a request's pages to other block ids (and the table with them)
@@ -20,6 +21,7 @@ from residualquant_amd import workloads
 from residualquant_amd.layout import record_offsets
 
 from .cases import OURO_G16, OURO_G32, make_decode, oracle_attention
+from .test_oracle_restore_pins import rne_bf16
 
 
 def _fp8(b):
@@ -27,7 +29,7 @@ def _fp8(b):
 
 
 def _bf(x):
-    return torch.tensor(np.asarray(x, dtype=np.float64)).to(torch.bfloat16).double().numpy()
+    return rne_bf16(x)
 
 
 def _record(cache, plane, block, head, token, r, records, dim, pt):
