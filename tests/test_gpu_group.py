@@ -1,9 +1,10 @@
 """The write path on the GPU: a loop group staged loop by loop
 (residualquant_amd/group.py, install_model.py:17-52, packed_backend.py:101-137)
 writes the same cache bytes as one quantize of every record, with the earlier
-loops kept on the device or, during prefill, in pinned host memory
-(prefill_offload.py, the reference's prefill_offload.py:10-200) returned in
-chunks or through the lookahead ring."""
+loops kept on the device or, during prefill, spilled to pinned host memory
+(residualquant_amd/prefill_offload.py, whose contract is the reference's
+prefill_offload.py:10-200) and recalled in windows or through the lookahead
+ring of layer slots."""
 
 from __future__ import annotations
 
@@ -11,7 +12,7 @@ import pytest
 import torch
 
 import residualquant_amd as rq
-from residualquant_amd import workloads
+from residualquant_amd import prefill_offload, workloads
 from residualquant_amd.prefill_offload import PrefillCPUOffload
 
 pytestmark = pytest.mark.gpu
@@ -50,9 +51,13 @@ def test_group_store_matches_one_quantize(device):
     assert torch.equal(cache, _direct(layer, device))
 
 
-@pytest.mark.parametrize("lookahead", [False, True], ids=["chunks", "lookahead"])
-def test_prefill_offload_matches_device_staging(device, lookahead):
-    layers, tokens = 3, 250  # 250 tokens in chunks of 96: 96, 96, 58
+@pytest.mark.parametrize("lookahead,layers,ring", [(False, 3, 8), (True, 3, 8), (True, 5, 2)],
+                         ids=["chunks", "lookahead", "lookahead-2-slots"])
+def test_prefill_offload_matches_device_staging(device, monkeypatch, lookahead, layers, ring):
+    # With 2 layer slots for 5 layers, later layers are recalled as earlier
+    # ones free their slot (chain order), and none waits for a slot.
+    monkeypatch.setattr(prefill_offload, "RING_MAX_LAYERS", ring)
+    tokens = 250  # 250 tokens in windows of 96: 96, 96, 58
     offload = PrefillCPUOffload(96, len(RECORDS) - 1, HEADS, DIM)
     offload.lookahead_enabled = lookahead
     offload.reserve(tokens)
@@ -78,18 +83,37 @@ def test_prefill_offload_matches_device_staging(device, lookahead):
             assert torch.equal(caches[i], _direct(d, device)), (call, i)
     if lookahead:
         assert offload.prefetched == {}
+        assert offload.layers.slots == ring and sorted(offload.layers.free) == list(range(ring))
+    assert sorted(offload.windows.free) == [0, 1]
 
 
 def test_offload_store_round_trip(device):
     offload = PrefillCPUOffload(64, 1, HEADS, DIM)
     key = torch.randn((100, HEADS, DIM), device=device).to(torch.bfloat16)
     value = torch.randn((100, HEADS, DIM), device=device).to(torch.bfloat16)
-    buffer = offload.store(key, value, None)
-    assert buffer.is_pinned() and buffer.shape == (2, 100, HEADS, DIM)
+    spill = offload.store(key, value, None)
+    assert spill.block.is_pinned() and spill.block.shape == (2, 100, HEADS, DIM)
     key_copy, value_copy = key.clone(), value.clone()
     key.zero_()  # the caller may reuse its tensors right away
     torch.cuda.synchronize()
-    assert torch.equal(buffer[0], key_copy.cpu()) and torch.equal(buffer[1], value_copy.cpu())
-    again = offload.store(value_copy, key_copy, buffer)
+    k, v = spill.views()
+    assert torch.equal(k, key_copy.cpu()) and torch.equal(v, value_copy.cpu())
+    again = offload.store(value_copy[:60], key_copy[:60], spill)
     torch.cuda.synchronize()
-    assert again is buffer and torch.equal(buffer[0], value_copy.cpu())
+    assert again is spill and spill.rows == 60 and torch.equal(spill.views()[0], value_copy[:60].cpu())
+    longer = torch.cat([key_copy, key_copy])
+    bigger = offload.store(longer, longer, spill)
+    torch.cuda.synchronize()
+    assert bigger is not spill and bigger.rows == 200 and torch.equal(bigger.views()[1], longer.cpu())
+
+
+def test_recall_windows_returned_when_the_consumer_stops_early(device):
+    offload = PrefillCPUOffload(32, 1, HEADS, DIM)
+    key = torch.randn((100, HEADS, DIM), device=device).to(torch.bfloat16)
+    spill = offload.store(key, key, None)
+    slots = torch.arange(100, dtype=torch.int64, device=device)
+    pieces = offload.chunks([spill.views(), (key, key)], slots)
+    first, first_slots = next(pieces)
+    assert first_slots.numel() == 32 and torch.equal(first[0][0], key[:32])
+    pieces.close()
+    assert sorted(offload.windows.free) == [0, 1]
