@@ -143,7 +143,9 @@ class LoopedDecoder:
         self.cos, self.sin = angles.cos(), angles.sin()
 
         # Step state (static tensors for graph capture).
-        self.tokens = torch.randint(0, c.vocab, (batch,), generator=generator, device=device)
+        # Own generator: the first tokens do not depend on whether the weights were drawn or shared.
+        token_generator = torch.Generator(device=device).manual_seed(seed + 3)
+        self.tokens = torch.randint(0, c.vocab, (batch,), generator=token_generator, device=device)
         self.positions = torch.full((batch,), context, dtype=torch.int64, device=device)
         self.seq_lens = torch.full((batch,), context + 1, dtype=torch.int32, device=device)
         self.query_start_loc = torch.arange(batch + 1, dtype=torch.int32, device=device)
@@ -156,6 +158,14 @@ class LoopedDecoder:
         self.workspace = torch.empty(ops.attention_workspace_bytes(batch, c.heads, c.head_dim, pages, c.page_tokens),
                                      dtype=torch.uint8, device=device)
         self.graph: Optional[torch.cuda.CUDAGraph] = None
+        # Host mirror of the next position (the same for every request).
+        self.next_position = context
+        # (loop, layer) pairs whose inputs and attention an eager step()
+        # keeps in ``tapped`` (for tests; never inside a capture): the layer
+        # input x and residual, the roped q and k, v, the attention output;
+        # and ("h", loop) the loop's final hidden state.
+        self.taps: set = set()
+        self.tapped: dict = {}
 
     # ------------------------------------------------------------ artifact
 
@@ -204,13 +214,26 @@ class LoopedDecoder:
     # ------------------------------------------------------------ the step
 
     def _update_slots(self) -> None:
+        """Slot of each request's next position; -1 (quantize skips it) past
+        the block table, so a step beyond ``max_tokens`` writes no page."""
         pt = self.config.page_tokens
-        page = torch.div(self.positions, pt, rounding_mode="floor")
+        pages = self.block_table.size(1)
+        page = torch.div(self.positions, pt, rounding_mode="floor").clamp(0, pages - 1)
         block = self.block_table.long().gather(1, page[:, None])[:, 0]
-        self.slots.copy_(block * pt + self.positions % pt)
+        slots = torch.where(self.positions < pages * pt, block * pt + self.positions % pt,
+                            torch.full_like(self.positions, -1))
+        self.slots.copy_(slots)
+
+    def _check_room(self) -> None:
+        if self.next_position >= self.max_tokens:
+            raise RuntimeError(f"decode step at position {self.next_position} is past the cache's "
+                               f"{self.max_tokens} tokens (max_new_tokens reached)")
 
     def step(self) -> torch.Tensor:
         """One decode step for every request; returns the logits and advances the state in place."""
+        capturing = torch.cuda.is_current_stream_capturing()
+        if not capturing:
+            self._check_room()
         c = self.config
         q_size = c.heads * c.head_dim
         eps = c.rms_eps
@@ -221,6 +244,9 @@ class LoopedDecoder:
             x = step_ops.rms_norm(h, self.norms[0][0], eps)
             for layer in range(c.layers):
                 norms = self.norms[layer]
+                tap = (loop, layer) in self.taps and not capturing
+                if tap:
+                    layer_input = (x.clone(), self.residual.clone())
                 qkv = _project(x, self.qkv[layer])
                 key_stage, value_stage = self.staged[layer, loop, 0], self.staged[layer, loop, 1]
                 q, k = step_ops.rope_qkv(qkv, self.positions, self.cos, self.sin, c.heads, c.head_dim,
@@ -228,6 +254,9 @@ class LoopedDecoder:
                 ops.attention(q, k, value_stage, self.caches[layer], self.attn_out, self.query_start_loc,
                               self.seq_lens, self.block_table, self.key_rotation[layer], self.value_rotation[layer],
                               self.key_mean[layer], c.schedule, "anchor", c.anchor, loop, workspace=self.workspace)
+                if tap:
+                    self.tapped[(loop, layer)] = dict(x=layer_input[0], residual=layer_input[1], q=q.clone(),
+                                                      k=k.clone(), v=value_stage.clone(), out=self.attn_out.clone())
                 # Loop group quantize at the anchor loop (install_model.py:40-52).
                 if loop == c.anchor:
                     pairs = [(self.staged[layer, r, 0], self.staged[layer, r, 1]) for r in range(c.loops)]
@@ -243,12 +272,16 @@ class LoopedDecoder:
                 following = self.norms[layer + 1][0] if layer + 1 < c.layers else self.final_norm
                 x, _ = step_ops.rms_norm(m, following, eps, residual=self.residual, pre_weight=norms[3])
             h = x
+            if self.taps and not capturing:
+                self.tapped[("h", loop)] = h.clone()
         logits = _project(h, self.lm_head)
         # Greedy next token and the next position, slot and sequence length.
         self.tokens.copy_(logits.argmax(dim=-1))
         self.positions.add_(1)
         self.seq_lens.add_(1)
         self._update_slots()
+        if not capturing:
+            self.next_position += 1
         return logits
 
     def capture(self) -> torch.cuda.CUDAGraph:
@@ -260,12 +293,22 @@ class LoopedDecoder:
             self.step()  # warm-up outside capture (allocator pools, library handles)
         torch.cuda.current_stream(self.device).wait_stream(stream)
         self._restore(snapshot)
+        self.next_position -= 1  # the warm-up step is undone
         graph = torch.cuda.CUDAGraph()
         with torch.cuda.graph(graph):
             self.logits = self.step()
         self._restore(snapshot)
         self.graph = graph
         return graph
+
+    def replay(self) -> torch.Tensor:
+        """Run the captured step once; refuses a step past ``max_tokens``."""
+        if self.graph is None:
+            raise RuntimeError("capture() the step first")
+        self._check_room()
+        self.graph.replay()
+        self.next_position += 1
+        return self.logits
 
     def _restore(self, snapshot) -> None:
         for tensor, saved in zip((self.tokens, self.positions, self.seq_lens, self.slots), snapshot):
