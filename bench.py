@@ -23,6 +23,7 @@ import argparse
 import json
 import os
 import platform
+import statistics
 import sys
 import time
 
@@ -105,62 +106,137 @@ def capture(torch, fn):
 
 
 def measured_traffic(summary="decode_c2_counters.json"):
-    """HBM bytes per residual-loop decode launch from a committed rocprofv3 counter summary."""
+    """HBM bytes per residual-loop decode launch from a committed rocprofv3
+    FETCH_SIZE/WRITE_SIZE summary, with the commit it was measured on."""
     path = os.path.join(ROOT, "profiles", summary)
     if not os.path.exists(path):
-        return None
+        return {"bytes": None, "commit": None}
     with open(path) as handle:
         data = json.load(handle)
-    return data.get("residual_loop_traffic_bytes")
+    return {"bytes": data.get("residual_loop_traffic_bytes"), "commit": data.get("commit")}
 
 
-def kernel_average_ms(torch, ops, fn, reps):
-    """Average split-K kernel duration from HIP events recorded on the launch stream."""
-    fn()
+def kernel_durations_ms(ops, calls, reps, warmup=10):
+    """Per-launch split-K kernel durations (HIP events on the launch stream) of
+    each call in ``calls``, launched in turn as a step launches them; the first
+    ``warmup`` rounds are dropped.  Returns one list of ``reps`` durations per call."""
+    out = [[] for _ in calls]
+    for round_ in range(warmup + reps):
+        for i, call in enumerate(calls):
+            ops.timing_read()
+            ops.timing_enable(True)
+            call()
+            ms, launches = ops.timing_read()
+            ops.timing_enable(False)
+            if round_ >= warmup and launches == 1:
+                out[i].append(ms)
+    return out
+
+
+def settle(torch, fn, seconds):
+    """Run ``fn`` untimed for ``seconds``: the GPU's clocks leave their idle state.
+
+    Measured on MI355X: the first ~50 replays of the C2 step after an idle
+    second run up to 20% slower (744 -> 610 us per step over the first 60 ms)."""
     torch.cuda.synchronize()
-    ops.timing_read()
-    ops.timing_enable(True)
-    for _ in range(reps):
-        fn()
-    torch.cuda.synchronize()
-    ops.timing_enable(False)
-    ms, launches = ops.timing_read()
-    return ms / max(1, launches), launches
+    end = time.perf_counter() + seconds
+    while time.perf_counter() < end:
+        for _ in range(8):
+            fn()
+        torch.cuda.synchronize()
 
 
-def cpu_baseline(torch, rq, workloads, cache, table, key_rotation, value_rotation, query, key, value,
-                 heads, dim, history, page_tokens, budget_s):
-    """The CPU oracle (single thread) on a bounded sample of one residual-loop call."""
+def host_description(torch):
+    model = platform.processor() or "cpu"
+    try:
+        with open("/proc/cpuinfo") as handle:
+            for line in handle:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    return {"cpu_model": model, "host_cores": len(os.sched_getaffinity(0)), "torch": torch.__version__}
+
+
+def cpu_baseline(torch, workloads, cache, table, key_rotation, value_rotation, query, key, value, history,
+                 budget_s):
+    """The vectorised torch-CPU restatement (oracle/cpu_reference.py) on the host.
+
+    One C2 residual-loop call (loop 0) on a bounded sample of its requests,
+    with every host thread torch is given and with one thread, plus the whole
+    C0 call (B1 x 512 history tokens, 4 loops) at both thread counts; each
+    timing the median of 5 runs after a warm-up.  Reported in GB/s of the
+    same algorithmic bytes as the GPU figures."""
+    import statistics
+
     import numpy as np
-    from oracle import oracle
+    from oracle import cpu_reference
 
-    oracle.lib()
+    heads, dim, page_tokens = query.size(1), query.size(2), cache.size(3)
+    cpu = dict(query=query.cpu(), key=key.cpu(), value=value.cpu(), kr=key_rotation.cpu(), vr=value_rotation.cpu())
+    table_np = table.cpu().numpy()
     pages = (history + page_tokens - 1) // page_tokens
-    bits = workloads.bf16_bits
-    rows_done, elapsed, total_bytes = 0, 0.0, 0
-    kr, vr = bits(key_rotation), bits(value_rotation)
-    for row in range(query.size(0)):
-        blocks = table[row].long()
-        sub = cache[:, blocks].cpu().numpy()
-        sub_table = np.arange(pages, dtype=np.int32).reshape(1, pages)
+    threads_all = max(1, min(torch.get_num_threads(), len(os.sched_getaffinity(0))))
+    saved_threads = torch.get_num_threads()
+
+    def c2_request(b):
+        blocks = torch.as_tensor(table_np[b][:pages], dtype=torch.long)
+        sub = cache[:, blocks.to(cache.device)].cpu()
+        local = np.arange(pages, dtype=np.int32).reshape(1, pages)
         start = time.perf_counter()
-        oracle.attention(bits(query[row:row + 1]), bits(key[row:row + 1]), bits(value[row:row + 1]), sub,
-                         np.array([0, 1], dtype=np.int32), np.array([history + 1], dtype=np.int32),
-                         sub_table, kr, vr, None, SCHEDULE, "anchor", ANCHOR, 0)
-        elapsed += time.perf_counter() - start
-        rows_done += 1
-        total_bytes += staged_call_bytes(1, history, heads, dim, page_tokens, 0)
-        if elapsed >= budget_s:
-            break
+        cpu_reference.attention(cpu["query"][b:b + 1], cpu["key"][b:b + 1], cpu["value"][b:b + 1], sub, [0, 1],
+                                [history + 1], local, cpu["kr"], cpu["vr"], None, SCHEDULE, ANCHOR, 0)
+        return time.perf_counter() - start
+
+    def c0_call(c0):
+        start = time.perf_counter()
+        for loop in range(4):
+            cpu_reference.attention(c0["query"], c0["key"], c0["value"], c0["cache"], [0, 1], [513], c0["table"],
+                                    c0["kr"], c0["vr"], None, SCHEDULE, ANCHOR, loop)
+        return time.perf_counter() - start
+
+    # C0 (BASELINE config 0): 16 heads x D128, B1, 512 history tokens, built on the GPU.
+    import residualquant_amd as rq
+    c0_cache, c0_table, c0_kr, c0_vr = build_packed_cache(torch, rq, workloads, 1, 512, heads, dim, page_tokens,
+                                                          query.device, 7)
+    g = torch.Generator().manual_seed(8)
+    c0 = dict(cache=c0_cache.cpu(), table=c0_table.cpu().numpy(), kr=c0_kr.cpu(), vr=c0_vr.cpu(),
+              query=torch.randn((1, heads, dim), generator=g).to(torch.bfloat16),
+              key=torch.randn((1, heads, dim), generator=g).to(torch.bfloat16),
+              value=torch.randn((1, heads, dim), generator=g).to(torch.bfloat16))
+    c0_bytes = sum(staged_call_bytes(1, 512, heads, dim, page_tokens, loop) for loop in range(4))
+    request_bytes = staged_call_bytes(1, history, heads, dim, page_tokens, 0)
+    rows = {}
+    for threads in (threads_all, 1):
+        torch.set_num_threads(threads)
+        c0_call(c0)
+        c0_s = statistics.median(c0_call(c0) for _ in range(5))
+        c2_request(0)
+        times, spent, b = [], 0.0, 0
+        while b < query.size(0) and (len(times) < 1 or spent < budget_s / 2):
+            times.append(c2_request(b))
+            spent += times[-1]
+            b += 1
+        rows[threads] = {"c2_GBps": request_bytes / statistics.median(times) / 1e9, "c2_requests": len(times),
+                         "c2_s_per_request": statistics.median(times), "c0_GBps": c0_bytes / c0_s / 1e9,
+                         "c0_us_per_4_loop_call": c0_s * 1e6}
+        log(f"[bench] cpu {threads} threads: C2 residual call {rows[threads]['c2_GBps']:.4f} GB/s "
+            f"({len(times)} requests), C0 {rows[threads]['c0_GBps']:.4f} GB/s")
+    torch.set_num_threads(saved_threads)
+    host = host_description(torch)
     return {
-        "value": total_bytes / elapsed / 1e9,
+        "value": rows[threads_all]["c2_GBps"],
         "unit": "GB/s",
-        "cores": 1,
+        "cores": threads_all,
         "kind": "port",
-        "sample": f"{rows_done} of {query.size(0)} rows of one residual-loop call (loop 0), "
-                  f"{history} history tokens x {heads} heads, oracle/rq_oracle.c single-threaded "
-                  f"FP64 attention over restored K/V; {elapsed:.2f} s; host {platform.processor() or 'cpu'}",
-        "us_per_row": elapsed / rows_done * 1e6,
+        "sample": f"vectorised torch-CPU restatement (oracle/cpu_reference.py, float64, checked against the C "
+                  f"oracle) of one C2 residual-loop call, {rows[threads_all]['c2_requests']} of "
+                  f"{query.size(0)} requests x {history} history tokens x {heads} heads, median time per "
+                  f"request at {threads_all} threads; {host['cpu_model']}, torch {host['torch']}",
+        "single_core": rows[1],
+        "all_cores": rows[threads_all],
+        **host,
     }
 
 
@@ -399,11 +475,15 @@ def run_huginn(args):
         for loop in range(len(schedule)):
             call(loop)
 
+    settle(torch, step, 0.3)
+    durations = kernel_durations_ms(ops, [lambda loop=loop: call(loop) for loop in range(4)], max(50, args.steps))
+    residual_runs = durations[0] + durations[1] + durations[2]
+    residual_ms, launches = statistics.median(residual_runs), len(residual_runs)
+    anchor_ms = statistics.median(durations[ANCHOR])
     graph = capture(torch, step)
+    settle(torch, graph.replay, 0.2)
     step_s = timed(torch, graph.replay, args.steps, args.warmup)
     step_bytes = sum(staged_call_bytes(batch, history, heads, dim, page_tokens, loop, schedule) for loop in range(4))
-    residual_ms, launches = kernel_average_ms(torch, ops, lambda: call(0), max(10, args.steps))
-    anchor_ms, _ = kernel_average_ms(torch, ops, lambda: call(ANCHOR), max(10, args.steps))
     residual_bytes = staged_call_bytes(batch, history, heads, dim, page_tokens, 0, schedule)
     anchor_bytes = staged_call_bytes(batch, history, heads, dim, page_tokens, ANCHOR, schedule)
     residual_gbps = residual_bytes / (residual_ms * 1e-3) / 1e9
@@ -419,7 +499,8 @@ def run_huginn(args):
     def bf16_call():
         rq.paged_attention_bf16(query, key, value, bf16_cache, output, qsl, seq_lens, table, workspace=bf16_ws)
 
-    bf16_ms, _ = kernel_average_ms(torch, ops, bf16_call, max(10, args.steps))
+    settle(torch, bf16_call, 0.2)
+    bf16_ms = statistics.median(kernel_durations_ms(ops, [bf16_call], max(50, args.steps))[0])
     bytes_bf16 = bf16_call_bytes(batch, history, heads, dim)
     log(f"[bench] C4 bf16 call {bf16_ms * 1e3:.1f} us ({bytes_bf16 / (bf16_ms * 1e-3) / 1e9:.0f} GB/s)")
     result = {
@@ -459,8 +540,10 @@ def run_huginn(args):
             "peak": PEAK_HBM_GBPS,
             "unit": "GB/s",
             "frac": residual_gbps / PEAK_HBM_GBPS,
-            "traffic": measured_traffic("decode_c4_counters.json"),
-            "kernel": f"decode96_kernel<16,4,32,2,16,true> (residual loop), {launches} HIP-event-timed launches",
+            "traffic": measured_traffic("decode_c4_counters.json")["bytes"],
+            "traffic_measured_at": measured_traffic("decode_c4_counters.json")["commit"],
+            "kernel": f"decode96_kernel<16,4,32,2,16,true> (residual loops 0-2), median of {launches} launches "
+                      "(HIP events on the launch stream, step order, after 10 warm-up rounds)",
         },
         "bf16_baseline": {
             "us_per_call_kernel": bf16_ms * 1e3,
@@ -629,18 +712,29 @@ def run_decode(args):
         for loop in range(len(SCHEDULE)):
             call(loop)
 
+    # Per-launch kernel durations in step order (median of >= 50 per loop after
+    # 10 warm-up rounds), after the GPU's clocks have settled.
+    settle(torch, step, 0.3)
+    reps = max(50, args.steps)
+    durations = kernel_durations_ms(ops, [lambda loop=loop: call(loop) for loop in range(4)], reps)
+    residual_runs = durations[0] + durations[1] + durations[2]
+    residual_ms = statistics.median(residual_runs)
+    anchor_ms = statistics.median(durations[ANCHOR])
+    residual_launches = len(residual_runs)
+
     eager_s = timed(torch, step, args.steps, args.warmup)
-    graph_s = None
+    graph_s = idle_s = None
     if not args.eager:
         graph = capture(torch, step)
+        settle(torch, graph.replay, 0.2)
         graph_s = timed(torch, graph.replay, args.steps, args.warmup)
+        # The same replays right after an idle second (clocks ramping up), for reference.
+        time.sleep(1.0)
+        idle_s = timed(torch, graph.replay, args.steps, 0)
     step_s = eager_s if graph_s is None else graph_s
     step_bytes = sum(staged_call_bytes(batch, history, heads, dim, page_tokens, loop) for loop in range(4))
     log(f"[bench] packed step {step_s * 1e6:.1f} us ({'eager' if graph_s is None else 'graph'}), "
-        f"eager {eager_s * 1e6:.1f} us")
-
-    residual_ms, residual_launches = kernel_average_ms(torch, ops, lambda: call(0), max(10, args.steps))
-    anchor_ms, _ = kernel_average_ms(torch, ops, lambda: call(ANCHOR), max(10, args.steps))
+        f"eager {eager_s * 1e6:.1f} us" + (f", from idle {idle_s * 1e6:.1f} us" if idle_s else ""))
     residual_bytes = staged_call_bytes(batch, history, heads, dim, page_tokens, 0)
     anchor_bytes = staged_call_bytes(batch, history, heads, dim, page_tokens, ANCHOR)
     residual_gbps = residual_bytes / (residual_ms * 1e-3) / 1e9
@@ -663,12 +757,14 @@ def run_decode(args):
             for _ in range(4):
                 bf16_call()
 
+        settle(torch, bf16_step, 0.2)
+        bf16_ms = statistics.median(kernel_durations_ms(ops, [bf16_call], reps)[0])
         bf16_step_s = timed(torch, bf16_step, args.steps, args.warmup)
         if not args.eager:
             bf16_graph = capture(torch, bf16_step)
+            settle(torch, bf16_graph.replay, 0.2)
             bf16_step_s = timed(torch, bf16_graph.replay, args.steps, args.warmup)
             del bf16_graph
-        bf16_ms, _ = kernel_average_ms(torch, ops, bf16_call, max(10, args.steps))
         bytes_bf16 = bf16_call_bytes(batch, history, heads, dim)
         bf16 = {
             "us_per_step": bf16_step_s * 1e6,
@@ -693,11 +789,12 @@ def run_decode(args):
 
     cpu = None
     if args.cpu_budget > 0:
-        log("[bench] cpu baseline (oracle) ...")
-        cpu = cpu_baseline(torch, rq, workloads, cache, table, key_rotation, value_rotation, query, key,
-                           value, heads, dim, history, page_tokens, args.cpu_budget)
-        log(f"[bench] cpu {cpu['value']:.3f} GB/s")
+        log("[bench] cpu baseline (torch-CPU restatement) ...")
+        cpu = cpu_baseline(torch, workloads, cache, table, key_rotation, value_rotation, query, key, value,
+                           history, args.cpu_budget)
+        log(f"[bench] cpu {cpu['value']:.4f} GB/s at {cpu['cores']} threads")
 
+    traffic = measured_traffic()
     result = {
         "metric": "paged decode-attn µs/step + achieved HBM GB/s (% peak), INT2/INT4 vs bf16, 1 GPU",
         "value": step_bytes / step_s / 1e9,
@@ -719,13 +816,18 @@ def run_decode(args):
         },
         "us_per_step": step_s * 1e6,
         "us_per_step_eager": eager_s * 1e6,
-        "timing": "one HIP-graph replay of the 4 calls per step" if graph_s is not None else "eager launches",
+        "us_per_step_from_idle": None if idle_s is None else idle_s * 1e6,
+        "timing": ("one HIP-graph replay of the 4 calls per step, timed after >= 0.2 s of untimed replays "
+                   "(the GPU's clocks ramp up over the first ~50 replays after idle; us_per_step_from_idle "
+                   "times the same replays right after an idle second)") if graph_s is not None
+                  else "eager launches",
         "pct_peak_step": 100.0 * step_bytes / step_s / 1e9 / PEAK_HBM_GBPS,
         "bytes_per_step": step_bytes,
         "tokens_per_s": batch / step_s,
         "decode_kernel": {
             "residual_loop_us": residual_ms * 1e3,
             "anchor_loop_us": anchor_ms * 1e3,
+            "per_loop_median_us": [statistics.median(d) * 1e3 for d in durations],
             "residual_loop_bytes": residual_bytes,
             "anchor_loop_bytes": anchor_bytes,
             "anchor_loop_GBps": anchor_bytes / (anchor_ms * 1e-3) / 1e9,
@@ -736,9 +838,11 @@ def run_decode(args):
             "peak": PEAK_HBM_GBPS,
             "unit": "GB/s",
             "frac": residual_gbps / PEAK_HBM_GBPS,
-            "traffic": measured_traffic(),
-            "kernel": "decode_kernel<128,16,4,32,2,32,true> (residual loop), "
-                      f"{residual_launches} HIP-event-timed launches",
+            "traffic": traffic["bytes"],
+            "traffic_measured_at": traffic["commit"],
+            "kernel": "decode_kernel<128,16,4,32,2,32,true> (residual loops 0-2), median of "
+                      f"{residual_launches} launches (HIP events on the launch stream, step order, "
+                      "after 10 warm-up rounds)",
         },
         "bf16_baseline": bf16,
         "cpu_baseline": cpu,
