@@ -78,6 +78,8 @@ def _declare(l):
         c_vp, c_i64, c_vp, c_i64, c_vp, c_i64, c_vp, c_i64, c_int, c_int, c_vp, c_i64, c_int,
         c_int, c_vp, c_vp, c_i64, c_vp, c_i64, c_vp, c_vp, c_vp, c_int, c_vp, c_vp, c_int,
         c_int, c_int]
+    l.rq_oracle_attention_prefill.restype = c_int
+    l.rq_oracle_attention_prefill.argtypes = l.rq_oracle_attention.argtypes
     l.rq_oracle_paged_attention_bf16.restype = c_int
     l.rq_oracle_paged_attention_bf16.argtypes = [
         c_vp, c_i64, c_vp, c_i64, c_vp, c_i64, c_vp, c_i64, c_int, c_int, c_vp, c_i64, c_int,
@@ -194,6 +196,13 @@ def dequantize(kv_cache, slots, head_dim, key_mean, records, reference_mode, anc
 def attention(query, key, value, kv_cache, query_start_loc, seq_lens, block_table, key_rotation,
               value_rotation, key_mean, records, reference_mode, anchor_index, loop_index):
     """FP64 decode attention [rows, heads, D] over the restored packed history."""
+    return _attention(lib().rq_oracle_attention, query, key, value, kv_cache, query_start_loc, seq_lens,
+                      block_table, key_rotation, value_rotation, key_mean, records, reference_mode, anchor_index,
+                      loop_index)
+
+
+def _attention(function, query, key, value, kv_cache, query_start_loc, seq_lens, block_table, key_rotation,
+               value_rotation, key_mean, records, reference_mode, anchor_index, loop_index):
     q = np.ascontiguousarray(query, dtype=np.uint16)
     k = np.ascontiguousarray(key, dtype=np.uint16)
     v = np.ascontiguousarray(value, dtype=np.uint16)
@@ -208,7 +217,7 @@ def attention(query, key, value, kv_cache, query_start_loc, seq_lens, block_tabl
     vr = None if value_rotation is None else np.ascontiguousarray(value_rotation, dtype=np.uint16)
     km = None if key_mean is None else np.ascontiguousarray(key_mean, dtype=np.float32)
     out = np.zeros((rows, heads, head_dim), dtype=np.float64)
-    rc = lib().rq_oracle_attention(
+    rc = function(
         _ptr(q), heads * head_dim, _ptr(k), heads * head_dim, _ptr(v), heads * head_dim,
         _ptr(out), rows, heads, head_dim, _ptr(kv_cache), blocks, page_tokens, width,
         _ptr(qsl), _ptr(sl), sl.size, _ptr(bt), bt.shape[1], _ptr(kr), _ptr(vr), _ptr(km),
@@ -216,6 +225,15 @@ def attention(query, key, value, kv_cache, query_start_loc, seq_lens, block_tabl
     if rc != 0:
         raise RuntimeError("oracle attention rejected its arguments")
     return out
+
+
+def attention_prefill(query, key, value, kv_cache, query_start_loc, seq_lens, block_table, key_rotation,
+                      value_rotation, key_mean, records, reference_mode, anchor_index, loop_index):
+    """FP64 attention of each request's last n tokens (its query rows) over the packed history
+    (seq_len - n tokens) and, causally, over the request's new keys/values."""
+    return _attention(lib().rq_oracle_attention_prefill, query, key, value, kv_cache, query_start_loc, seq_lens,
+                      block_table, key_rotation, value_rotation, key_mean, records, reference_mode, anchor_index,
+                      loop_index)
 
 
 def paged_attention_bf16(query, key, value, cache, query_start_loc, seq_lens, block_table):

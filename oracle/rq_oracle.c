@@ -549,22 +549,26 @@ static void attention_key(const uint8_t* page, int head_dim, const int* bits, co
 
 /*
  * For each query row i of request b (query_start_loc), head h, loop L:
- *   q' = (q.R_k)/sqrt(D); history t < seq_len-1 scores q'.K_L[t] with K_L the
+ *   q' = (q.R_k)/sqrt(D); history t < H_b scores q'.K_L[t] with K_L the
  *   key the reference decode kernel scores (attention_key above) and V_L[t]
  *   the BF16 restore (restore_token, compute.cuh:28-107);
- *   live score (q.k_live)/sqrt(D); p = softmax over history + live;
- *   out = (sum_t p_t V_L[t]).R_v^T + p_live v_live   (merge.cuh:66-83,
- *   output.cuh:9-31, compute.cuh:688-726, prepare.cuh:13-54).
- * Output is FP64 [rows, heads, D].
+ *   live scores (q.k_j)/sqrt(D) over the live set; p = softmax over history
+ *   and live set; out = (sum_t p_t V_L[t]).R_v^T + sum_j p_j v_j
+ *   (merge.cuh:66-83, output.cuh:9-31, compute.cuh:688-726, prepare.cuh:13-54).
+ * Decode (causal = 0, the reference's attention()): H_b = seq_len - 1 and the
+ * live set is the row's own key/value.  Prefill over packed history
+ * (causal = 1): the n rows of request b are its last n tokens, H_b =
+ * seq_len - n, and row r (0-based within the request) sees the request's
+ * new keys/values j <= r.  Output is FP64 [rows, heads, D].
  */
-int rq_oracle_attention(
+static int attention_rows(
     const uint16_t* query, int64_t query_stride, const uint16_t* key, int64_t key_stride,
     const uint16_t* value, int64_t value_stride, double* output, int64_t rows, int heads,
     int head_dim, const uint8_t* cache, int64_t num_blocks, int page_tokens, int page_width,
     const int32_t* query_start_loc, const int32_t* seq_lens, int64_t requests,
     const int32_t* block_table, int64_t block_table_stride, const uint16_t* key_rotation,
     const uint16_t* value_rotation, const float* key_mean, int records, const int* bits,
-    const int* groups, int reference_mode, int anchor_index, int loop) {
+    const int* groups, int reference_mode, int anchor_index, int loop, int causal) {
     if (records < 1 || records > RQ_ORACLE_MAX_RECORDS || head_dim > RQ_ORACLE_MAX_DIM) return -1;
     if (loop < 0 || loop >= records || anchor_index < 0 || anchor_index >= records) return -1;
     if (rq_oracle_page_width(head_dim, records, bits, groups) != page_width) return -1;
@@ -575,15 +579,19 @@ int rq_oracle_attention(
     double kexact[RQ_ORACLE_MAX_DIM];
 
     for (int64_t b = 0; b < requests; ++b) {
-        const int64_t history = seq_lens[b] > 1 ? seq_lens[b] - 1 : 0;
-        double* scores = (double*)malloc(sizeof(double) * (size_t)(history + 1));
+        const int64_t first = query_start_loc[b];
+        const int64_t n = query_start_loc[b + 1] - first;
+        const int64_t new_tokens = causal ? n : 1;
+        const int64_t history = seq_lens[b] > new_tokens ? seq_lens[b] - new_tokens : 0;
+        double* scores = (double*)malloc(sizeof(double) * (size_t)(history + n + 1));
         if (!scores) return -1;
-        for (int64_t i = query_start_loc[b]; i < query_start_loc[b + 1]; ++i) {
+        double* live_scores = scores + history;
+        for (int64_t i = first; i < first + n; ++i) {
             if (i >= rows) break;
+            const int64_t live_first = causal ? first : i;
+            const int64_t live_count = causal ? i - first + 1 : 1;
             for (int h = 0; h < heads; ++h) {
                 const uint16_t* q = query + i * query_stride + (int64_t)h * head_dim;
-                const uint16_t* kl = key + i * key_stride + (int64_t)h * head_dim;
-                const uint16_t* vl = value + i * value_stride + (int64_t)h * head_dim;
                 double qr[RQ_ORACLE_MAX_DIM];
                 for (int c = 0; c < head_dim; ++c) {
                     double acc = 0.0;
@@ -597,11 +605,15 @@ int rq_oracle_attention(
                     }
                     qr[c] = acc * scale;
                 }
-                double live = 0.0;
-                for (int c = 0; c < head_dim; ++c)
-                    live += (double)rq_oracle_bf16_to_f32(q[c]) * (double)rq_oracle_bf16_to_f32(kl[c]);
-                live *= scale;
-                double maximum = live;
+                double maximum = -INFINITY;
+                for (int64_t j = 0; j < live_count; ++j) {
+                    const uint16_t* kl = key + (live_first + j) * key_stride + (int64_t)h * head_dim;
+                    double live = 0.0;
+                    for (int c = 0; c < head_dim; ++c)
+                        live += (double)rq_oracle_bf16_to_f32(q[c]) * (double)rq_oracle_bf16_to_f32(kl[c]);
+                    live_scores[j] = live * scale;
+                    if (live_scores[j] > maximum) maximum = live_scores[j];
+                }
                 for (int64_t t = 0; t < history; ++t) {
                     const int64_t block = block_table[b * block_table_stride + t / page_tokens];
                     if (block < 0 || block >= num_blocks) {
@@ -616,7 +628,11 @@ int rq_oracle_attention(
                     scores[t] = s;
                     if (s > maximum) maximum = s;
                 }
-                double denominator = exp(live - maximum);
+                double denominator = 0.0;
+                for (int64_t j = 0; j < live_count; ++j) {
+                    live_scores[j] = exp(live_scores[j] - maximum);
+                    denominator += live_scores[j];
+                }
                 for (int64_t t = 0; t < history; ++t) {
                     scores[t] = exp(scores[t] - maximum);
                     denominator += scores[t];
@@ -632,7 +648,6 @@ int rq_oracle_attention(
                     for (int c = 0; c < head_dim; ++c) hist[c] += scores[t] * (double)rq_oracle_bf16_to_f32(vbuf[c]);
                 }
                 double* out = output + (i * heads + h) * (int64_t)head_dim;
-                const double live_weight = exp(live - maximum) / denominator;
                 for (int c = 0; c < head_dim; ++c) {
                     double v = 0.0;
                     if (value_rotation) {
@@ -642,13 +657,46 @@ int rq_oracle_attention(
                     } else {
                         v = hist[c];
                     }
-                    out[c] = v / denominator + live_weight * (double)rq_oracle_bf16_to_f32(vl[c]);
+                    double live = 0.0;
+                    for (int64_t j = 0; j < live_count; ++j) {
+                        const uint16_t* vl = value + (live_first + j) * value_stride + (int64_t)h * head_dim;
+                        live += live_scores[j] * (double)rq_oracle_bf16_to_f32(vl[c]);
+                    }
+                    out[c] = (v + live) / denominator;
                 }
             }
         }
         free(scores);
     }
     return 0;
+}
+
+int rq_oracle_attention(
+    const uint16_t* query, int64_t query_stride, const uint16_t* key, int64_t key_stride,
+    const uint16_t* value, int64_t value_stride, double* output, int64_t rows, int heads,
+    int head_dim, const uint8_t* cache, int64_t num_blocks, int page_tokens, int page_width,
+    const int32_t* query_start_loc, const int32_t* seq_lens, int64_t requests,
+    const int32_t* block_table, int64_t block_table_stride, const uint16_t* key_rotation,
+    const uint16_t* value_rotation, const float* key_mean, int records, const int* bits,
+    const int* groups, int reference_mode, int anchor_index, int loop) {
+    return attention_rows(query, query_stride, key, key_stride, value, value_stride, output, rows, heads,
+                          head_dim, cache, num_blocks, page_tokens, page_width, query_start_loc, seq_lens,
+                          requests, block_table, block_table_stride, key_rotation, value_rotation, key_mean,
+                          records, bits, groups, reference_mode, anchor_index, loop, 0);
+}
+
+int rq_oracle_attention_prefill(
+    const uint16_t* query, int64_t query_stride, const uint16_t* key, int64_t key_stride,
+    const uint16_t* value, int64_t value_stride, double* output, int64_t rows, int heads,
+    int head_dim, const uint8_t* cache, int64_t num_blocks, int page_tokens, int page_width,
+    const int32_t* query_start_loc, const int32_t* seq_lens, int64_t requests,
+    const int32_t* block_table, int64_t block_table_stride, const uint16_t* key_rotation,
+    const uint16_t* value_rotation, const float* key_mean, int records, const int* bits,
+    const int* groups, int reference_mode, int anchor_index, int loop) {
+    return attention_rows(query, query_stride, key, key_stride, value, value_stride, output, rows, heads,
+                          head_dim, cache, num_blocks, page_tokens, page_width, query_start_loc, seq_lens,
+                          requests, block_table, block_table_stride, key_rotation, value_rotation, key_mean,
+                          records, bits, groups, reference_mode, anchor_index, loop, 1);
 }
 
 /*
