@@ -106,6 +106,31 @@ int rq_attention(const void* query, int64_t query_stride, const void* key, int64
                  int loop_index, void* workspace, size_t workspace_bytes, hipStream_t stream);
 
 /*
+ * Attention of each request's last n tokens over its packed history: request
+ * b's rows query_start_loc[b]..query_start_loc[b+1] (n of them) are its last
+ * n of seq_lens[b] tokens; row r attends to the first seq_lens[b] - n tokens
+ * through block_table and, causally, to the request's new key/value rows
+ * 0..r.  The prefill of a prompt chunk over a packed prefix: no counterpart
+ * in the reference, whose scheduler forbids partial prefill and cached
+ * prefixes (src/residual_quantization/scheduler.py:11-18).  Arguments,
+ * validation and workspace (rq_attention_workspace_bytes) are those of
+ * rq_attention; anchor mode at head_dim 128 only (RQ_ENOKERNEL otherwise), at
+ * most 2048 new rows per request.  rq_attention itself routes calls with
+ * several rows per request in anchor mode at head_dim 128 to the same
+ * multi-row kernels (each row then sees seq_lens[b] - 1 history tokens and
+ * its own key/value, the reference's semantics).
+ */
+int rq_packed_prefill_attention(const void* query, int64_t query_stride, const void* key, int64_t key_stride,
+                                const void* value, int64_t value_stride, void* output, int64_t output_stride,
+                                int64_t rows, int heads, int head_dim, const void* kv_cache, int64_t num_blocks,
+                                int page_tokens, int page_width, const int32_t* query_start_loc,
+                                const int32_t* seq_lens, int64_t requests, const int32_t* block_table,
+                                int64_t block_table_stride, int64_t max_pages, const void* key_rotation,
+                                const void* value_rotation, const float* key_mean, int records, const int* bits,
+                                const int* groups, int reference_mode, int anchor_index, int loop_index,
+                                void* workspace, size_t workspace_bytes, hipStream_t stream);
+
+/*
  * rq_attention without a workspace argument, for callers that cannot
  * allocate device memory (code under HIP graph capture, tight serving loops,
  * harnesses that forbid hipMalloc).  No counterpart in the reference, whose

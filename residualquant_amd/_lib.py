@@ -26,6 +26,7 @@ EXPORTED_SYMBOLS = (
     "rq_attention_workspace_bytes",
     "rq_attention",
     "rq_attention_noalloc",
+    "rq_packed_prefill_attention",
     "rq_dequantize",
     "rq_paged_attention_bf16",
     "rq_prefill_attention",
@@ -78,6 +79,8 @@ def _declare(l: ctypes.CDLL) -> None:
     l.rq_attention.argtypes = [vp, i64, vp, i64, vp, i64, vp, i64, i64, i32, i32, vp, i64, i32, i32,
                                vp, vp, i64, vp, i64, i64, vp, vp, vp, i32, vp, vp, i32, i32, i32, vp,
                                sz, vp]
+    l.rq_packed_prefill_attention.restype = i32
+    l.rq_packed_prefill_attention.argtypes = l.rq_attention.argtypes
     l.rq_attention_noalloc.restype = i32
     l.rq_attention_noalloc.argtypes = [vp, i64, vp, i64, vp, i64, vp, i64, i64, i32, i32, vp, i64, i32, i32,
                                        vp, vp, i64, vp, i64, i64, vp, vp, vp, i32, vp, vp, i32, i32, i32, vp]

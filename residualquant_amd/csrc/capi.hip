@@ -128,6 +128,33 @@ struct WorkspaceLayout {
     size_t row_request, arrivals, prep, partials, total;
 };
 
+// Several rows per request (anchor mode, D = 128) run the multi-row MFMA
+// kernels: history splits per (request, head, 32-row tile), sized from the
+// row count so that the workspace depends on host shapes only (two
+// workgroups per compute unit when every row is its own request), at most
+// kMultiRowMaxSplits and no more than the history's 32-token tiles allow
+// (four per split, one per wave).
+int multirow_splits(int64_t rows, int heads, int64_t max_pages, int page_tokens) {
+    const int64_t target = 2LL * compute_units();
+    const int64_t pairs = std::max<int64_t>(1, rows * heads);
+    int64_t splits = (target + pairs - 1) / pairs;
+    const int64_t tiles = std::max<int64_t>(1, (max_pages * page_tokens + 31) / 32);
+    splits = std::min<int64_t>(splits, std::max<int64_t>(1, tiles / 4));
+    return (int)std::max<int64_t>(1, std::min<int64_t>(splits, rq::kMultiRowMaxSplits));
+}
+
+struct MultiRowLayout {
+    size_t partials, row_shift, total;
+};
+
+MultiRowLayout multirow_layout(int64_t rows, int heads, int splits) {
+    MultiRowLayout w;
+    w.partials = 0;
+    w.row_shift = align256(sizeof(float) * (size_t)rows * heads * splits * rq::kMultiRowEntry);
+    w.total = w.row_shift + align256(sizeof(float) * (size_t)rows * heads);
+    return w;
+}
+
 WorkspaceLayout workspace_layout(int64_t rows, int heads, int head_dim, int splits) {
     WorkspaceLayout w;
     w.row_request = 0;
@@ -256,11 +283,20 @@ int rq_quantize(int records, const void* const* key_ptrs, const int64_t* key_str
     return check_launch(rq::launch_quantize(p, head_dim, stream), "quantize launch");
 }
 
+// One workspace serves both paths of a packed attention call (the per-row
+// decode kernels and the multi-row kernels), so its size is the larger one.
+static size_t attention_workspace_total(int64_t rows, int heads, int head_dim, int64_t max_pages,
+                                        int page_tokens) {
+    size_t total = workspace_layout(rows, heads, head_dim, split_count(rows, heads, max_pages)).total;
+    if (head_dim == 128 && (page_tokens == 16 || page_tokens == 32))
+        total = std::max(total, multirow_layout(rows, heads, multirow_splits(rows, heads, max_pages, page_tokens)).total);
+    return total;
+}
+
 size_t rq_attention_workspace_bytes(int64_t rows, int heads, int head_dim, int64_t max_pages,
                                     int page_tokens) {
-    (void)page_tokens;
     if (rows <= 0 || heads <= 0 || head_dim <= 0) return 256;
-    return workspace_layout(rows, heads, head_dim, split_count(rows, heads, max_pages)).total;
+    return attention_workspace_total(rows, heads, head_dim, max_pages, page_tokens);
 }
 
 static int attention_common(const void* query, int64_t query_stride, const void* key, int64_t key_stride,
@@ -283,6 +319,7 @@ static int attention_common(const void* query, int64_t query_stride, const void*
         return fail(RQ_EINVAL, "Contiguous INT32 query starts with one final boundary required");
     if ((rows > 0 && block_table == nullptr) || max_pages < 0 || block_table_stride < max_pages)
         return fail(RQ_EINVAL, "INT32 page table with packed rows required");
+    if (splits <= 0) return RQ_OK;  // validation only
     const WorkspaceLayout layout = workspace_layout(rows, heads, head_dim, splits);
     if (rows > 0 && (workspace == nullptr || workspace_bytes < layout.total))
         return fail(RQ_ENOSPACE, "Attention workspace of %zu bytes required (got %zu)", layout.total,
@@ -333,7 +370,8 @@ static int attention_packed(const void* query, int64_t query_stride, const void*
                             int64_t block_table_stride, int64_t max_pages, const void* key_rotation,
                             const void* value_rotation, const float* key_mean, int records, const int* bits,
                             const int* groups, int reference_mode, int anchor_index, int loop_index,
-                            void* workspace, size_t workspace_bytes, hipStream_t stream, bool timed) {
+                            void* workspace, size_t workspace_bytes, hipStream_t stream, bool timed,
+                            bool causal = false) {
     int status = validate_schedule(head_dim, records, bits, groups, page_tokens, reference_mode,
                                    anchor_index, heads);
     if (status != RQ_OK) return status;
@@ -350,6 +388,74 @@ static int attention_packed(const void* query, int64_t query_stride, const void*
     const int width = rq_page_width(head_dim, records, bits, groups);
     if (width != page_width) return fail(RQ_EINVAL, "Packed cache width differs from records");
     const bool adjacent = records > 1 && reference_mode == RQ_MODE_ADJACENT;
+    // Several rows per request in anchor mode at D = 128 (and every prefill
+    // over packed history) take the multi-row MFMA kernels, which stream each
+    // request's pages once for all its rows.
+    if (causal || (!adjacent && head_dim == 128 && rows > requests)) {
+        if (adjacent || head_dim != 128)
+            return fail(RQ_ENOKERNEL,
+                        "No compiled packed HIP multi-row kernel for head_dim=%d, reference_mode=%s (anchor mode "
+                        "at head_dim 128 only)",
+                        head_dim, adjacent ? "adjacent" : "anchor");
+        status = attention_common(query, query_stride, key, key_stride, value, value_stride, output, output_stride,
+                                  rows, heads, head_dim, query_start_loc, seq_lens, requests, block_table,
+                                  block_table_stride, max_pages, nullptr, 0, 0, nullptr);
+        if (status != RQ_OK) return status;
+        if (rows == 0 || requests == 0) return ok();
+        if (causal && rows - requests + 1 > rq::kMultiRowMaxLive)
+            return fail(RQ_EINVAL, "At most %d new rows per request over packed history", rq::kMultiRowMaxLive);
+        const int splits = multirow_splits(rows, heads, max_pages, page_tokens);
+        const MultiRowLayout layout = multirow_layout(rows, heads, splits);
+        if (workspace == nullptr || workspace_bytes < layout.total)
+            return fail(RQ_ENOSPACE, "Attention workspace of %zu bytes required (got %zu)", layout.total,
+                        workspace_bytes);
+        rq::RecordRegion regions[rq::kMaxRecords];
+        fill_regions(head_dim, records, bits, groups, page_tokens, regions);
+        rq::MultiRowParams m{};
+        m.query = static_cast<const uint16_t*>(query);
+        m.query_stride = query_stride;
+        m.key = static_cast<const uint16_t*>(key);
+        m.key_stride = key_stride;
+        m.value = static_cast<const uint16_t*>(value);
+        m.value_stride = value_stride;
+        m.output = static_cast<uint16_t*>(output);
+        m.output_stride = output_stride;
+        m.rows = rows;
+        m.heads = heads;
+        m.cache = static_cast<const uint8_t*>(kv_cache);
+        m.plane_stride = num_blocks * heads * (int64_t)page_tokens * page_width;
+        m.num_blocks = num_blocks;
+        m.page_tokens = page_tokens;
+        m.page_width = page_width;
+        m.query_start_loc = query_start_loc;
+        m.seq_lens = seq_lens;
+        m.requests = requests;
+        m.block_table = block_table;
+        m.block_table_stride = block_table_stride;
+        m.max_pages = max_pages;
+        m.key_rotation = static_cast<const uint16_t*>(key_rotation);
+        m.value_rotation = static_cast<const uint16_t*>(value_rotation);
+        m.anchor = regions[anchor_index];
+        m.has_residual = loop_index != anchor_index;
+        m.residual = regions[loop_index];
+        m.key_mean_loop = key_mean ? key_mean + (int64_t)loop_index * heads * head_dim : nullptr;
+        m.key_mean_anchor = (key_mean && m.has_residual) ? key_mean + (int64_t)anchor_index * heads * head_dim
+                                                          : nullptr;
+        m.causal = causal ? 1 : 0;
+        m.splits = splits;
+        m.row_tiles = (int)((rows - requests + 1 + 31) / 32);
+        uint8_t* ws = static_cast<uint8_t*>(workspace);
+        m.partials = reinterpret_cast<float*>(ws + layout.partials);
+        m.row_shift = reinterpret_cast<float*>(ws + layout.row_shift);
+        if ((int64_t)m.splits * m.row_tiles > 65535 || requests > (int64_t)INT32_MAX || rows > (int64_t)INT32_MAX)
+            return fail(RQ_EINVAL, "Too many rows for one multi-row attention launch");
+        hipEvent_t begin = nullptr, end = nullptr;
+        if (timed) timing_events(stream, &begin, &end);
+        if (begin) (void)hipEventRecord(begin, stream);
+        const hipError_t launched = rq::launch_multirow(m, stream);
+        if (end) (void)hipEventRecord(end, stream);
+        return check_launch(launched, "multi-row attention launch");
+    }
     rq::AttentionParams p;
     // Never more splits than rq_attention_workspace_bytes() provides for.
     const int splits = packed_splits(rows, heads, head_dim, max_pages);
@@ -435,6 +541,22 @@ int rq_attention(const void* query, int64_t query_stride, const void* key, int64
                             anchor_index, loop_index, workspace, workspace_bytes, stream, true);
 }
 
+int rq_packed_prefill_attention(const void* query, int64_t query_stride, const void* key, int64_t key_stride,
+                                const void* value, int64_t value_stride, void* output, int64_t output_stride,
+                                int64_t rows, int heads, int head_dim, const void* kv_cache, int64_t num_blocks,
+                                int page_tokens, int page_width, const int32_t* query_start_loc,
+                                const int32_t* seq_lens, int64_t requests, const int32_t* block_table,
+                                int64_t block_table_stride, int64_t max_pages, const void* key_rotation,
+                                const void* value_rotation, const float* key_mean, int records, const int* bits,
+                                const int* groups, int reference_mode, int anchor_index, int loop_index,
+                                void* workspace, size_t workspace_bytes, hipStream_t stream) {
+    return attention_packed(query, query_stride, key, key_stride, value, value_stride, output, output_stride,
+                            rows, heads, head_dim, kv_cache, num_blocks, page_tokens, page_width,
+                            query_start_loc, seq_lens, requests, block_table, block_table_stride, max_pages,
+                            key_rotation, value_rotation, key_mean, records, bits, groups, reference_mode,
+                            anchor_index, loop_index, workspace, workspace_bytes, stream, true, true);
+}
+
 int rq_attention_noalloc(const void* query, int64_t query_stride, const void* key, int64_t key_stride,
                          const void* value, int64_t value_stride, void* output, int64_t output_stride,
                          int64_t rows, int heads, int head_dim, const void* kv_cache, int64_t num_blocks,
@@ -445,8 +567,7 @@ int rq_attention_noalloc(const void* query, int64_t query_stride, const void* ke
                          const int* groups, int reference_mode, int anchor_index, int loop_index,
                          hipStream_t stream) {
     if (rows > 0 && heads > 0 && head_dim > 0) {
-        const size_t needed =
-            workspace_layout(rows, heads, head_dim, packed_splits(rows, heads, head_dim, max_pages)).total;
+        const size_t needed = attention_workspace_total(rows, heads, head_dim, max_pages, page_tokens);
         if (needed > kAttentionScratchBytes)
             return fail(RQ_ENOSPACE,
                         "rq_attention_noalloc: this call needs %zu bytes of scratch, the static scratch holds "

@@ -1,0 +1,658 @@
+// Attention of several query rows per request over packed pages, on MFMA
+// tiles (gfx950, wave64).
+//
+// The decode kernel scores one query row per workgroup with integer dot
+// products on the packed codes, so n rows of one request stream the
+// request's pages n times.  Here one workgroup takes a tile of up to 32 rows
+// of one (request, head) and a split of its history, streams each page once,
+// and dequantizes every 32-token tile into LDS as FP16 K (row-major) and BF16
+// V (transposed), so that the tile's rows share it through MFMA:
+//   S^T = K Q'^T     (32 tokens x 32 rows, 8 v_mfma_f32_32x32x16_f16 over D = 128)
+//   O^T += V^T P^T   (128 channels x 32 rows, 8 v_mfma_f32_32x32x16_bf16)
+// The scores take FP16 operands (11-bit significands; each row of q' is
+// scaled by a power of two into [-1, 1], which the scores take back), since
+// BF16 operands there put the outlier channels' score error near the
+// 1e-3 mean bar on short histories.  V is a BF16 restore, exact in BF16.
+// with P kept in the accumulator registers (the token order of each P.V
+// step is permuted to match the accumulator layout, and V^T is read with the
+// same permutation).  Each of the four waves takes every fourth tile with
+// its own online softmax; the waves meet once in LDS at the end and the
+// workgroup writes one partial (m, l, O) per row.  A finish launch per
+// (row, head) merges the splits, applies R_v^T and adds the live tokens.
+//
+// Semantics (reference: attention/compute.cuh:397-505 keys, :28-107 values,
+// prepare.cuh:13-54 and :203-229 live score and mean shift, merge.cuh:8-84,
+// output.cuh:9-31): keys alpha_L (c.s+o + bf16(mu_A))_A + (c.s+o)_L with the
+// current loop's mean as a per-row shift, values the BF16 restore
+// bf16(alpha_L bf16(c.s+o)_A + bf16(c.s+o)_L), P in BF16.
+//
+// Lane layouts of v_mfma_f32_32x32x16_bf16 (checked on gfx950): A row l % 32,
+// k 8 (l / 32) + e; B column l % 32, k 8 (l / 32) + e; C register r holds row
+// 8 (r / 4) + 4 (l / 32) + r % 4, column l % 32.
+#include "rq_device.h"
+#include "rq_kernels.h"
+
+namespace rq {
+
+namespace {
+
+typedef __bf16 Bf16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 F16x8 __attribute__((ext_vector_type(8)));
+typedef float F32x16 __attribute__((ext_vector_type(16)));
+
+constexpr int D = 128;
+constexpr int kThreads = 256;
+constexpr int kWaves = 4;
+constexpr int kTile = 32;            // tokens per MFMA tile (two 16-token units)
+constexpr int KS = D + 8;            // K tile row stride (BF16)
+constexpr int VS = kTile + 8;        // V^T tile row stride (BF16)
+constexpr int kWaveBytes = kTile * KS * 2 + D * VS * 2 + kTile * 4;  // K (FP16), V^T (BF16), alpha_K
+constexpr int kLdsBytes = kWaves * kWaveBytes;
+// Prologue scratch (aliases the tiles): q^T FP32 [D][QTS], R_k FP16 [D][KS], q' FP16 [32][KS], mean dots
+// and row scales.
+constexpr int QTS = 36;
+constexpr int kQtOffset = 0;
+constexpr int kRkOffset = kQtOffset + D * QTS * 4;
+constexpr int kQpOffset = kRkOffset + D * KS * 2;
+constexpr int kQmuOffset = kQpOffset + 32 * KS * 2;
+static_assert(kQmuOffset + 96 * 4 <= kLdsBytes, "prologue scratch fits in the tile LDS");
+// Wave merge (aliases the tiles): O [wave][row][MS] FP32 and (m, l) per wave and row.
+constexpr int MS = D + 4;
+constexpr int kMlOffset = kWaves * 32 * MS * 4;
+static_assert(kMlOffset + kWaves * 32 * 2 * 4 <= kLdsBytes, "merge buffer fits in the tile LDS");
+constexpr float kLog2e = 1.4426950408889634f;
+
+__device__ __forceinline__ F32x16 mfma(Bf16x8 a, Bf16x8 b, F32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+}
+
+__device__ __forceinline__ F32x16 mfma(F16x8 a, F16x8 b, F32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+}
+
+__device__ __forceinline__ uint32_t f16_bits(float x) { return __builtin_bit_cast(uint16_t, (_Float16)x); }
+
+__device__ __forceinline__ float f16_to_f32(uint32_t h) { return (float)__builtin_bit_cast(_Float16, (uint16_t)h); }
+
+// Round to BF16 (nearest even) and back to FP32.
+__device__ __forceinline__ float round_bf16(float x) { return bf16_f32(bf16_rn(x)); }
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t page_rsrc(const uint8_t* page, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(page), (short)0, (int)bytes, 0x00020000);
+}
+
+// One record's bytes for the lane's token and 32-channel quarter.
+struct RecordBytes {
+    uint32_t w[4];   // codes: 16 bytes (INT4) or 8 bytes (INT2)
+    uint32_t scale;  // FP8 scale byte(s): one (group 32) or two (group 16)
+    uint32_t offset;
+    uint32_t alpha;  // BF16 alpha (residual records)
+};
+
+__device__ __forceinline__ void load_record(__amdgpu_buffer_rsrc_t page, const RecordRegion& r, int page_tokens,
+                                            int row, int quarter, bool alpha, RecordBytes& out) {
+    const uint32_t codes = (uint32_t)(r.offset + row * r.code_bytes + quarter * (r.code_bytes / 4));
+    if (r.bits == 4) {
+        const auto v = __builtin_amdgcn_raw_buffer_load_b128(page, codes, 0, kStreamPolicy);
+        out.w[0] = v[0]; out.w[1] = v[1]; out.w[2] = v[2]; out.w[3] = v[3];
+    } else {
+        const auto v = __builtin_amdgcn_raw_buffer_load_b64(page, codes, 0, kStreamPolicy);
+        out.w[0] = v[0]; out.w[1] = v[1]; out.w[2] = 0u; out.w[3] = 0u;
+    }
+    const uint32_t scales = (uint32_t)(r.offset + page_tokens * r.code_bytes + row * r.groups + quarter * (r.groups / 4));
+    const uint32_t offsets = scales + (uint32_t)(page_tokens * r.groups);
+    if (r.group == 32) {
+        out.scale = __builtin_amdgcn_raw_buffer_load_b8(page, scales, 0, 0);
+        out.offset = __builtin_amdgcn_raw_buffer_load_b8(page, offsets, 0, 0);
+    } else {
+        out.scale = __builtin_amdgcn_raw_buffer_load_b16(page, scales, 0, 0);
+        out.offset = __builtin_amdgcn_raw_buffer_load_b16(page, offsets, 0, 0);
+    }
+    out.alpha = alpha ? __builtin_amdgcn_raw_buffer_load_b16(
+                            page, (uint32_t)(r.offset + page_tokens * (r.code_bytes + 2 * r.groups) + 2 * row), 0, 0)
+                      : 0u;
+}
+
+// code * scale + offset for the lane's 32 channels (exact in FP32).  A code
+// held in a byte is the FP8 E4M3 value code * 2^-9, so v_cvt_pk_f32_fp8
+// converts two codes per instruction and the scale carries the 2^9 back.
+__device__ __forceinline__ void dequant(const RecordBytes& r, int bits, int group, float (&x)[32]) {
+    const float s0 = __builtin_amdgcn_cvt_f32_fp8((int)r.scale, 0) * 512.0f;
+    const float o0 = __builtin_amdgcn_cvt_f32_fp8((int)r.offset, 0);
+    const float s1 = group == 32 ? s0 : __builtin_amdgcn_cvt_f32_fp8((int)r.scale, 1) * 512.0f;
+    const float o1 = group == 32 ? o0 : __builtin_amdgcn_cvt_f32_fp8((int)r.offset, 1);
+    if (bits == 4) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const float s = i < 2 ? s0 : s1, o = i < 2 ? o0 : o1;
+            const int lo = (int)(r.w[i] & 0x0f0f0f0fu);         // channels 8i + 0, 2, 4, 6
+            const int hi = (int)((r.w[i] >> 4) & 0x0f0f0f0fu);  // channels 8i + 1, 3, 5, 7
+            const auto l01 = __builtin_amdgcn_cvt_pk_f32_fp8(lo, false);
+            const auto l23 = __builtin_amdgcn_cvt_pk_f32_fp8(lo, true);
+            const auto h01 = __builtin_amdgcn_cvt_pk_f32_fp8(hi, false);
+            const auto h23 = __builtin_amdgcn_cvt_pk_f32_fp8(hi, true);
+            float* a = x + 8 * i;
+            a[0] = fmaf(l01[0], s, o);
+            a[2] = fmaf(l01[1], s, o);
+            a[4] = fmaf(l23[0], s, o);
+            a[6] = fmaf(l23[1], s, o);
+            a[1] = fmaf(h01[0], s, o);
+            a[3] = fmaf(h01[1], s, o);
+            a[5] = fmaf(h23[0], s, o);
+            a[7] = fmaf(h23[1], s, o);
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            const float s = i == 0 ? s0 : s1, o = i == 0 ? o0 : o1;
+            float* a = x + 16 * i;
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                // byte j of part holds channel 4j + k
+                const int part = (int)((r.w[i] >> (2 * k)) & 0x03030303u);
+                const auto c01 = __builtin_amdgcn_cvt_pk_f32_fp8(part, false);
+                const auto c23 = __builtin_amdgcn_cvt_pk_f32_fp8(part, true);
+                a[k] = fmaf(c01[0], s, o);
+                a[4 + k] = fmaf(c01[1], s, o);
+                a[8 + k] = fmaf(c23[0], s, o);
+                a[12 + k] = fmaf(c23[1], s, o);
+            }
+        }
+    }
+}
+
+// The LDS writes of a wave before reads of other lanes of the same wave.
+__device__ __forceinline__ void wave_sync() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+template <int PT, bool HasL>
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2)))
+void multirow_stream_kernel(MultiRowParams p) {
+    __shared__ __attribute__((aligned(16))) uint8_t lds[kLdsBytes];
+    const int request = blockIdx.x;
+    const int head = blockIdx.y;
+    const int split = (int)blockIdx.z % p.splits;
+    const int row0 = 32 * ((int)blockIdx.z / p.splits);
+    const int first = p.query_start_loc[request];
+    int n = p.query_start_loc[request + 1] - first;
+    if (first < 0 || first >= p.rows) return;  // uniform over the workgroup, before any barrier
+    const int new_tokens = p.causal ? n : 1;
+    if (n > p.rows - first) n = (int)(p.rows - first);  // rows past the query tensor are not read or written
+    if (row0 >= n) return;
+    const int seq = p.seq_lens[request];
+    int history = seq > new_tokens ? seq - new_tokens : 0;
+    // Tokens past the page table are never read.
+    if ((int64_t)history > p.max_pages * PT) history = (int)(p.max_pages * PT);
+    const int tiles = (history + kTile - 1) / kTile;
+    const int per_split = (tiles + p.splits - 1) / p.splits;
+    const int tile_begin = split * per_split;
+    const int tile_end = tile_begin + per_split < tiles ? tile_begin + per_split : tiles;
+
+    const int tid = threadIdx.x;
+    const int wave = tid >> 6;
+    const int lane = tid & 63;
+    const int column = lane & 31;
+    const int half = lane >> 5;
+
+    // ---------------------------------------------------------------- q'
+    // q' = (q . R_k) * log2(e) / sqrt(D) for the tile's rows, held as FP16
+    // q' 2^-e with 2^e the row's power-of-two scale, and the row dots
+    // q'.bf16(mu_A) (added per token times alpha_L) and q'.mu_L (the shift of
+    // the history scores against the live ones).
+    float* q_t = reinterpret_cast<float*>(lds + kQtOffset);
+    uint16_t* r_k = reinterpret_cast<uint16_t*>(lds + kRkOffset);
+    uint16_t* q_p = reinterpret_cast<uint16_t*>(lds + kQpOffset);
+    float* q_mu = reinterpret_cast<float*>(lds + kQmuOffset);  // [0..31] q'.bf16(mu_A), [32..63] q'.mu_L
+    float* q_scale = q_mu + 64;                                 // [32] 2^e per row
+    {
+        const int r = tid >> 3, part = tid & 7;  // row, 16-channel part
+        const int row = row0 + r;
+        uint32_t words[8] = {0u, 0u, 0u, 0u, 0u, 0u, 0u, 0u};
+        if (row < n) {
+            const uint2* src = reinterpret_cast<const uint2*>(
+                p.query + (int64_t)(first + row) * p.query_stride + head * D + 16 * part);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const uint2 v = src[i];
+                words[2 * i] = v.x;
+                words[2 * i + 1] = v.y;
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            q_t[(16 * part + 2 * i) * QTS + r] = bf16_f32(words[i] & 0xffffu);
+            q_t[(16 * part + 2 * i + 1) * QTS + r] = bf16_f32(words[i] >> 16);
+        }
+        if (p.key_rotation) {
+            const int k = tid >> 1, h = tid & 1;
+            const uint4* src = reinterpret_cast<const uint4*>(p.key_rotation + ((int64_t)head * D + k) * D + 64 * h);
+            uint4* dst = reinterpret_cast<uint4*>(r_k + k * KS + 64 * h);
+#pragma unroll
+            for (int i = 0; i < 8; ++i) dst[i] = src[i];
+        }
+    }
+    __syncthreads();
+    {
+        const int cb = tid & 31, rb = tid >> 5;  // columns 4 cb .. 4 cb + 3, rows 4 rb .. 4 rb + 3
+        float acc[4][4];
+        if (p.key_rotation) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+#pragma unroll
+                for (int j = 0; j < 4; ++j) acc[i][j] = 0.f;
+#pragma unroll 8
+            for (int k = 0; k < D; ++k) {
+                const float4 q4 = *reinterpret_cast<const float4*>(&q_t[k * QTS + 4 * rb]);
+                const uint2 r4 = *reinterpret_cast<const uint2*>(&r_k[k * KS + 4 * cb]);
+                const float rv[4] = {f16_to_f32(r4.x & 0xffffu), f16_to_f32(r4.x >> 16), f16_to_f32(r4.y & 0xffffu),
+                                     f16_to_f32(r4.y >> 16)};
+                const float qv[4] = {q4.x, q4.y, q4.z, q4.w};
+#pragma unroll
+                for (int i = 0; i < 4; ++i)
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) acc[i][j] = fmaf(qv[i], rv[j], acc[i][j]);
+            }
+        } else {
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+#pragma unroll
+                for (int j = 0; j < 4; ++j) acc[i][j] = q_t[(4 * cb + j) * QTS + 4 * rb + i];
+        }
+        const float scale = kLog2e * 0.08838834764831845f;  // log2(e) / sqrt(128)
+        float mu_a[4] = {0.f, 0.f, 0.f, 0.f}, mu_l[4] = {0.f, 0.f, 0.f, 0.f};
+        if (p.key_mean_anchor) {
+#pragma unroll
+            for (int j = 0; j < 4; ++j) mu_a[j] = round_bf16(p.key_mean_anchor[head * D + 4 * cb + j]);
+        }
+        if (p.key_mean_loop) {
+#pragma unroll
+            for (int j = 0; j < 4; ++j) mu_l[j] = p.key_mean_loop[head * D + 4 * cb + j];
+        }
+        // Row maxima over the 32 lanes of this half-wave (the same four rows)
+        // give each row's power-of-two scale.
+        float row_max[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            row_max[i] = 0.f;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                acc[i][j] *= scale;
+                row_max[i] = fmaxf(row_max[i], fabsf(acc[i][j]));
+            }
+        }
+#pragma unroll
+        for (int d = 16; d; d >>= 1)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) row_max[i] = fmaxf(row_max[i], __shfl_xor(row_max[i], d));
+        float dot_a[4], dot_l[4], row_scale[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            // 2^e >= row_max (e from the exponent field; 1 for an all-zero row)
+            const int e = row_max[i] > 0.f ? __builtin_amdgcn_frexp_expf(row_max[i]) : 0;
+            row_scale[i] = ldexpf(1.0f, e);
+            const float inverse = ldexpf(1.0f, -e);
+            uint32_t bits[4];
+            dot_a[i] = 0.f;
+            dot_l[i] = 0.f;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const _Float16 h = (_Float16)(acc[i][j] * inverse);
+                bits[j] = __builtin_bit_cast(uint16_t, h);
+                const float q = (float)h * row_scale[i];
+                dot_a[i] = fmaf(q, mu_a[j], dot_a[i]);
+                dot_l[i] = fmaf(q, mu_l[j], dot_l[i]);
+            }
+            *reinterpret_cast<uint2*>(&q_p[(4 * rb + i) * KS + 4 * cb]) =
+                make_uint2(bits[0] | (bits[1] << 16), bits[2] | (bits[3] << 16));
+        }
+        // Sum over the 32 lanes of this half-wave (the same four rows).
+#pragma unroll
+        for (int d = 16; d; d >>= 1)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                dot_a[i] += __shfl_xor(dot_a[i], d);
+                dot_l[i] += __shfl_xor(dot_l[i], d);
+            }
+        if (cb == 0) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                q_mu[4 * rb + i] = dot_a[i];
+                q_mu[32 + 4 * rb + i] = dot_l[i];
+                q_scale[4 * rb + i] = row_scale[i];
+            }
+        }
+    }
+    __syncthreads();
+    // Q'^T operand (B of S^T = K Q'^T): chunk m holds channels 16 m + 8 half + e.
+    F16x8 q_operand[D / 16];
+#pragma unroll
+    for (int m = 0; m < D / 16; ++m)
+        q_operand[m] = *reinterpret_cast<const F16x8*>(&q_p[column * KS + 16 * m + 8 * half]);
+    const float q_mu_anchor = q_mu[column];
+    const float row_scale = q_scale[column];
+    if (split == 0 && tid < 32 && row0 + tid < n)
+        p.row_shift[(int64_t)(first + row0 + tid) * p.heads + head] = q_mu[32 + tid];
+    __syncthreads();  // the scratch becomes the tiles
+
+    // ---------------------------------------------------------------- history
+    uint16_t* k_tile = reinterpret_cast<uint16_t*>(lds + wave * kWaveBytes);
+    uint16_t* v_tile = k_tile + kTile * KS;
+    float* alpha_tile = reinterpret_cast<float*>(v_tile + D * VS);
+    const int unit_token = lane >> 2;  // token within a 16-token unit
+    const int quarter = lane & 3;      // 32-channel quarter
+    const uint32_t page_bytes = (uint32_t)(PT * p.page_width);
+    const int pages = (history + PT - 1) / PT;
+    const bool mean_anchor = HasL && p.key_mean_anchor != nullptr;
+
+    F32x16 out[D / 32];
+#pragma unroll
+    for (int t = 0; t < D / 32; ++t)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) out[t][r] = 0.f;
+    float running_max = -__builtin_inff();
+    float running_sum = 0.f;
+
+    for (int tile = tile_begin + wave; tile < tile_end; tile += kWaves) {
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+            const int unit_first = kTile * tile + 16 * u;  // history index of the unit's first token
+            const int page = unit_first / PT;
+            const int row = unit_first % PT + unit_token;
+            const bool valid = unit_first + unit_token < history;
+            int block = -1;
+            if (unit_first < history && page < pages)
+                block = __builtin_amdgcn_readfirstlane(p.block_table[(int64_t)request * p.block_table_stride + page]);
+            const bool page_ok = block >= 0 && block < p.num_blocks;
+            const uint8_t* k_page = p.cache + ((int64_t)(page_ok ? block : 0) * p.heads + head) * page_bytes;
+            const auto k_rsrc = page_rsrc(k_page, page_ok ? page_bytes : 0u);
+            const auto v_rsrc = page_rsrc(k_page + p.plane_stride, page_ok ? page_bytes : 0u);
+            RecordBytes ka, va, kl, vl;
+            load_record(k_rsrc, p.anchor, PT, row, quarter, false, ka);
+            load_record(v_rsrc, p.anchor, PT, row, quarter, false, va);
+            if constexpr (HasL) {
+                load_record(k_rsrc, p.residual, PT, row, quarter, true, kl);
+                load_record(v_rsrc, p.residual, PT, row, quarter, true, vl);
+            }
+            // Tokens past the history (or in pages without a valid block)
+            // hold zeros; their scores are masked below.  K, then V, so that
+            // only one plane's values are live at a time.
+            const int local = 16 * u + unit_token;
+            float alpha_k = 1.f;
+            {
+                float k[32];
+                dequant(ka, p.anchor.bits, p.anchor.group, k);
+                if constexpr (HasL) {
+                    float kx[32];
+                    dequant(kl, p.residual.bits, p.residual.group, kx);
+                    alpha_k = bf16_f32(kl.alpha);
+#pragma unroll
+                    for (int c = 0; c < 32; ++c) k[c] = fmaf(alpha_k, k[c], kx[c]);
+                }
+                uint32_t kw[16];
+#pragma unroll
+                for (int c = 0; c < 16; ++c) {
+                    const float a = valid ? k[2 * c] : 0.f, b = valid ? k[2 * c + 1] : 0.f;
+                    kw[c] = f16_bits(a) | (f16_bits(b) << 16);
+                }
+                uint4* k_dst = reinterpret_cast<uint4*>(&k_tile[local * KS + 32 * quarter]);
+#pragma unroll
+                for (int c = 0; c < 4; ++c)
+                    k_dst[c] = make_uint4(kw[4 * c], kw[4 * c + 1], kw[4 * c + 2], kw[4 * c + 3]);
+            }
+            {
+                float v[32];
+                dequant(va, p.anchor.bits, p.anchor.group, v);
+                if constexpr (HasL) {
+                    float vx[32];
+                    dequant(vl, p.residual.bits, p.residual.group, vx);
+                    const float alpha_v = bf16_f32(vl.alpha);
+#pragma unroll
+                    for (int c = 0; c < 32; ++c) v[c] = fmaf(alpha_v, round_bf16(v[c]), round_bf16(vx[c]));
+                }
+#pragma unroll
+                for (int c = 0; c < 32; ++c)
+                    v_tile[(32 * quarter + c) * VS + local] = (uint16_t)bf16_rn(valid ? v[c] : 0.f);
+            }
+            if (quarter == 0) alpha_tile[local] = alpha_k;
+        }
+        wave_sync();
+
+        // S^T: register r of lane l holds token 8 (r / 4) + 4 half + r % 4 against row `column`.
+        F32x16 s;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) s[r] = 0.f;
+        const uint16_t* k_row = &k_tile[column * KS + 8 * half];
+#pragma unroll
+        for (int m = 0; m < D / 16; ++m) s = mfma(*reinterpret_cast<const F16x8*>(k_row + 16 * m), q_operand[m], s);
+
+        float tile_max = -__builtin_inff();
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            const int local = 8 * (r >> 2) + 4 * half + (r & 3);
+            float x = s[r] * row_scale;
+            if (mean_anchor) x = fmaf(alpha_tile[local], q_mu_anchor, x);
+            x = kTile * tile + local < history ? x : -__builtin_inff();
+            s[r] = x;
+            tile_max = fmaxf(tile_max, x);
+        }
+        tile_max = fmaxf(tile_max, __shfl_xor(tile_max, 32));
+        const float new_max = fmaxf(running_max, tile_max);
+        const float base = new_max == -__builtin_inff() ? 0.f : new_max;
+        const float rescale = __builtin_amdgcn_exp2f(running_max - base);
+        running_max = new_max;
+        // P^T in BF16 as the B operand of O^T += V^T P^T: step j takes
+        // registers 8j..8j+7, i.e. k-slot (half, e) is token
+        // 16 j + 4 half + e + (e >= 4 ? 4 : 0).
+        float tile_sum = 0.f;
+        Bf16x8 p_operand[2];
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                const float w = __builtin_amdgcn_exp2f(s[8 * j + e] - base);
+                p_operand[j][e] = (__bf16)w;
+                tile_sum += w;
+            }
+        tile_sum += __shfl_xor(tile_sum, 32);
+        running_sum = running_sum * rescale + tile_sum;
+        if (!__all(rescale == 1.0f)) {
+#pragma unroll
+            for (int t = 0; t < D / 32; ++t)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) out[t][r] *= rescale;
+        }
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            const int token_offset = 16 * j + 4 * half;
+#pragma unroll
+            for (int t = 0; t < D / 32; ++t) {
+                const uint16_t* v_row = &v_tile[(32 * t + column) * VS + token_offset];
+                const uint2 lo = *reinterpret_cast<const uint2*>(v_row);
+                const uint2 hi = *reinterpret_cast<const uint2*>(v_row + 8);
+                out[t] = mfma(__builtin_bit_cast(Bf16x8, make_uint4(lo.x, lo.y, hi.x, hi.y)), p_operand[j], out[t]);
+            }
+        }
+        wave_sync();  // the next tile overwrites this one
+    }
+
+    // ---------------------------------------------------------------- wave merge
+    __syncthreads();  // the merge buffer aliases every wave's tiles
+    float* merge_o = reinterpret_cast<float*>(lds);
+    float* merge_ml = reinterpret_cast<float*>(lds + kMlOffset);
+#pragma unroll
+    for (int t = 0; t < D / 32; ++t)
+#pragma unroll
+        for (int g = 0; g < 4; ++g)
+            *reinterpret_cast<float4*>(&merge_o[(wave * 32 + column) * MS + 32 * t + 8 * g + 4 * half]) =
+                make_float4(out[t][4 * g], out[t][4 * g + 1], out[t][4 * g + 2], out[t][4 * g + 3]);
+    if (half == 0) {
+        merge_ml[(wave * 32 + column) * 2] = running_max;
+        merge_ml[(wave * 32 + column) * 2 + 1] = running_sum;
+    }
+    __syncthreads();
+    {
+        const int r = tid >> 3, chunk = tid & 7;  // row, 16-channel chunk
+        float m_w[kWaves], total_max = -__builtin_inff();
+#pragma unroll
+        for (int w = 0; w < kWaves; ++w) {
+            m_w[w] = merge_ml[(w * 32 + r) * 2];
+            total_max = fmaxf(total_max, m_w[w]);
+        }
+        float l = 0.f;
+        float o[16];
+#pragma unroll
+        for (int c = 0; c < 16; ++c) o[c] = 0.f;
+#pragma unroll
+        for (int w = 0; w < kWaves; ++w) {
+            if (m_w[w] == -__builtin_inff()) continue;
+            const float weight = __builtin_amdgcn_exp2f(m_w[w] - total_max);
+            l = fmaf(merge_ml[(w * 32 + r) * 2 + 1], weight, l);
+            const float* src = &merge_o[(w * 32 + r) * MS + 16 * chunk];
+#pragma unroll
+            for (int c = 0; c < 16; ++c) o[c] = fmaf(src[c], weight, o[c]);
+        }
+        if (row0 + r < n) {
+            float* entry = p.partials +
+                           (((int64_t)(first + row0 + r) * p.heads + head) * p.splits + split) * kMultiRowEntry;
+            if (chunk == 0) *reinterpret_cast<float4*>(entry) = make_float4(total_max, l, 0.f, 0.f);
+            float4* dst = reinterpret_cast<float4*>(entry + 4 + 16 * chunk);
+#pragma unroll
+            for (int c = 0; c < 4; ++c) dst[c] = make_float4(o[4 * c], o[4 * c + 1], o[4 * c + 2], o[4 * c + 3]);
+        }
+    }
+}
+
+// ---------------------------------------------------------------- finish
+
+__device__ __forceinline__ float block_max(float x, float* scratch) {
+#pragma unroll
+    for (int d = 32; d; d >>= 1) x = fmaxf(x, __shfl_xor(x, d));
+    __syncthreads();
+    if ((threadIdx.x & 63) == 0) scratch[threadIdx.x >> 6] = x;
+    __syncthreads();
+    return fmaxf(scratch[0], scratch[1]);
+}
+
+__device__ __forceinline__ float block_sum(float x, float* scratch) {
+#pragma unroll
+    for (int d = 32; d; d >>= 1) x += __shfl_xor(x, d);
+    __syncthreads();
+    if ((threadIdx.x & 63) == 0) scratch[threadIdx.x >> 6] = x;
+    __syncthreads();
+    return scratch[0] + scratch[1];
+}
+
+// One (row, head) per 128-thread workgroup, thread c = channel c.
+__global__ __launch_bounds__(D) void multirow_finish_kernel(MultiRowParams p) {
+    __shared__ float hist_rot[D];
+    __shared__ float query[D];
+    __shared__ float live[kMultiRowMaxLive];
+    __shared__ float scratch[2];
+    __shared__ int found;
+    const int64_t row = blockIdx.x;
+    const int head = blockIdx.y;
+    const int c = threadIdx.x;
+    if (c == 0) {
+        // Request of the row: the last b with query_start_loc[b] <= row.
+        int64_t lo = 0, hi = p.requests;  // answer in [lo, hi)
+        while (hi - lo > 1) {
+            const int64_t mid = (lo + hi) / 2;
+            if (p.query_start_loc[mid] <= row) lo = mid; else hi = mid;
+        }
+        found = (p.requests > 0 && p.query_start_loc[lo] <= row && row < p.query_start_loc[lo + 1]) ? (int)lo : -1;
+    }
+    __syncthreads();
+    const int request = found;
+    const int first = request < 0 ? -1 : p.query_start_loc[request];
+    if (first < 0) return;  // uniform
+    const int r = (int)(row - first);
+
+    // History: merge the splits' partials (log2 units).
+    const float* entries = p.partials + ((int64_t)row * p.heads + head) * p.splits * kMultiRowEntry;
+    float hist_max = -__builtin_inff();
+    for (int s = 0; s < p.splits; ++s) hist_max = fmaxf(hist_max, entries[s * kMultiRowEntry]);
+    float hist_sum = 0.f, acc = 0.f;
+    if (hist_max != -__builtin_inff()) {
+        for (int s = 0; s < p.splits; ++s) {
+            const float m = entries[s * kMultiRowEntry];
+            if (m == -__builtin_inff()) continue;
+            const float w = __builtin_amdgcn_exp2f(m - hist_max);
+            hist_sum = fmaf(entries[s * kMultiRowEntry + 1], w, hist_sum);
+            acc = fmaf(entries[s * kMultiRowEntry + 4 + c], w, acc);
+        }
+    }
+    hist_rot[c] = acc;
+    query[c] = bf16_f32(p.query[row * p.query_stride + (int64_t)head * D + c]);
+    __syncthreads();
+    float hist = acc;
+    if (p.value_rotation) {
+        // hist . R_v^T: channel c takes row c of R_v.
+        const uint16_t* rv = p.value_rotation + ((int64_t)head * D + c) * D;
+        hist = 0.f;
+#pragma unroll 8
+        for (int k = 0; k < D; ++k) hist = fmaf(hist_rot[k], f16_to_f32(rv[k]), hist);
+    }
+
+    // Live tokens: the row's own (decode) or the request's new rows j <= r (causal).
+    const int64_t live_first = p.causal ? first : row;
+    const int live_count = p.causal ? (r < kMultiRowMaxLive ? r + 1 : kMultiRowMaxLive) : 1;
+    const float shift = p.row_shift[row * p.heads + head];
+    const float scale = kLog2e * 0.08838834764831845f;
+    float local_max = -__builtin_inff();
+    for (int j = c; j < live_count; j += D) {
+        const uint16_t* k = p.key + (live_first + j) * p.key_stride + (int64_t)head * D;
+        float dot = 0.f;
+        for (int d = 0; d < D; d += 4) {
+            const uint2 w = *reinterpret_cast<const uint2*>(k + d);
+            dot = fmaf(query[d], bf16_f32(w.x & 0xffffu), dot);
+            dot = fmaf(query[d + 1], bf16_f32(w.x >> 16), dot);
+            dot = fmaf(query[d + 2], bf16_f32(w.y & 0xffffu), dot);
+            dot = fmaf(query[d + 3], bf16_f32(w.y >> 16), dot);
+        }
+        const float score = dot * scale - shift;
+        live[j] = score;
+        local_max = fmaxf(local_max, score);
+    }
+    const float total_max = fmaxf(block_max(local_max, scratch), hist_max);
+    float local_sum = 0.f;
+    for (int j = c; j < live_count; j += D) {
+        const float w = __builtin_amdgcn_exp2f(live[j] - total_max);
+        live[j] = w;
+        local_sum += w;
+    }
+    const float live_sum = block_sum(local_sum, scratch);  // its barriers publish live[]
+    const float hist_weight = hist_max == -__builtin_inff() ? 0.f : __builtin_amdgcn_exp2f(hist_max - total_max);
+    float o = hist * hist_weight;
+    const uint16_t* v = p.value + live_first * p.value_stride + (int64_t)head * D + c;
+    for (int j = 0; j < live_count; ++j) o = fmaf(live[j], bf16_f32(v[j * p.value_stride]), o);
+    const float total = hist_sum * hist_weight + live_sum;
+    p.output[row * p.output_stride + (int64_t)head * D + c] = (uint16_t)bf16_rn(o / total);
+}
+
+template <int PT>
+void launch_pt(const MultiRowParams& p, hipStream_t stream) {
+    const dim3 grid((unsigned)p.requests, (unsigned)p.heads, (unsigned)(p.splits * p.row_tiles));
+    if (p.has_residual)
+        hipLaunchKernelGGL((multirow_stream_kernel<PT, true>), grid, dim3(kThreads), 0, stream, p);
+    else
+        hipLaunchKernelGGL((multirow_stream_kernel<PT, false>), grid, dim3(kThreads), 0, stream, p);
+}
+
+}  // namespace
+
+hipError_t launch_multirow(const MultiRowParams& p, hipStream_t stream) {
+    if (p.rows == 0 || p.requests == 0) return hipSuccess;
+    if (p.page_tokens == 16)
+        launch_pt<16>(p, stream);
+    else if (p.page_tokens == 32)
+        launch_pt<32>(p, stream);
+    else
+        return hipErrorInvalidValue;
+    hipLaunchKernelGGL(multirow_finish_kernel, dim3((unsigned)p.rows, (unsigned)p.heads), dim3(D), 0, stream, p);
+    return hipGetLastError();
+}
+
+}  // namespace rq

@@ -184,6 +184,53 @@ struct AttentionParams {
 
 hipError_t launch_attention(const AttentionParams& p, hipStream_t stream, hipEvent_t begin,
                             hipEvent_t end);
+
+// Several query rows per request over packed pages (anchor mode, D = 128):
+// one workgroup per (request, head, row tile of 32 rows, history split)
+// streams the split's pages once for all the tile's rows on MFMA tiles, then
+// a finish launch per (row, head) merges the splits, applies R_v^T and adds
+// the live tokens.  causal = 0: the reference decode semantics (history
+// seq_len - 1, the row's own live token); causal = 1: the rows are the
+// request's last n tokens (history seq_len - n, live tokens j <= r).
+constexpr int kMultiRowEntry = 132;        // per (row, head, split): m, l, 2 unused, O[128] (log2 units)
+constexpr int kMultiRowMaxSplits = 8;
+constexpr int kMultiRowMaxLive = 2048;     // new rows per request at most (causal)
+struct MultiRowParams {
+    const uint16_t* query;
+    int64_t query_stride;
+    const uint16_t* key;
+    int64_t key_stride;
+    const uint16_t* value;
+    int64_t value_stride;
+    uint16_t* output;
+    int64_t output_stride;
+    int64_t rows;
+    int heads;
+    const uint8_t* cache;
+    int64_t plane_stride;
+    int64_t num_blocks;
+    int page_tokens;
+    int page_width;
+    const int32_t* query_start_loc;
+    const int32_t* seq_lens;
+    int64_t requests;
+    const int32_t* block_table;
+    int64_t block_table_stride;
+    int64_t max_pages;
+    const uint16_t* key_rotation;
+    const uint16_t* value_rotation;
+    const float* key_mean_loop;    // [heads, D] or null
+    const float* key_mean_anchor;  // [heads, D] or null (residual loops only)
+    RecordRegion anchor;
+    RecordRegion residual;
+    int has_residual;
+    int causal;
+    int splits;     // history splits per (request, head, row tile)
+    int row_tiles;  // 32-row tiles per request in the grid
+    float* partials;   // workspace [rows, heads, splits, kMultiRowEntry]
+    float* row_shift;  // workspace [rows, heads]: q'.mu_L in log2 units
+};
+hipError_t launch_multirow(const MultiRowParams& p, hipStream_t stream);
 hipError_t launch_attention_bf16(const AttentionParams& p, hipStream_t stream, hipEvent_t begin,
                                  hipEvent_t end);
 

@@ -167,6 +167,16 @@ def attention(query: torch.Tensor, key: torch.Tensor, value: torch.Tensor, kv_ca
     in the reference) lets a caller reuse one device buffer of
     ``attention_workspace_bytes(...)`` bytes, e.g. across graph replays.
     """
+    key_rotation_ptr, value_rotation_ptr = _validate_packed_inputs(
+        query, key, value, kv_cache, output, query_start_loc, seq_lens, block_table, key_rotation, value_rotation,
+        key_mean, records, reference_mode, loop_index)
+    _call_packed_attention(_lib.lib().rq_attention, query, key, value, kv_cache, output, query_start_loc,
+                           seq_lens, block_table, key_rotation_ptr, value_rotation_ptr, key_mean, records,
+                           reference_mode, anchor_index, loop_index, workspace)
+
+
+def _validate_packed_inputs(query, key, value, kv_cache, output, query_start_loc, seq_lens, block_table,
+                            key_rotation, value_rotation, key_mean, records, reference_mode, loop_index):
     _validate_attention_inputs(query, key, value, output, query_start_loc, seq_lens, block_table)
     heads, head_dim = query.size(1), query.size(2)
     _require(kv_cache.device == query.device and kv_cache.dtype == torch.uint8
@@ -184,14 +194,46 @@ def attention(query: torch.Tensor, key: torch.Tensor, value: torch.Tensor, kv_ca
              "16-byte aligned key rotation required for asynchronous copies")
     _require(0 <= loop_index < len(records), "Invalid loop index")
     _require(reference_mode in _MODES, f"Unknown packed reference mode: {reference_mode}")
+    return key_rotation_ptr, value_rotation_ptr
 
+
+def packed_prefill_attention(query: torch.Tensor, key: torch.Tensor, value: torch.Tensor,
+                             kv_cache: torch.Tensor, output: torch.Tensor, query_start_loc: torch.Tensor,
+                             seq_lens: torch.Tensor, block_table: torch.Tensor,
+                             key_rotation: Optional[torch.Tensor], value_rotation: Optional[torch.Tensor],
+                             key_mean: Optional[torch.Tensor], records: Sequence[Sequence[int]],
+                             reference_mode: str, anchor_index: int, loop_index: int,
+                             workspace: Optional[torch.Tensor] = None) -> None:
+    """Attention of each request's last n tokens (its query rows) over its packed history.
+
+    Request b's rows ``query_start_loc[b]..query_start_loc[b+1]`` are the
+    last n of its ``seq_lens[b]`` tokens: they attend to the first
+    ``seq_lens[b] - n`` tokens from the cache and, causally, to the request's
+    own new ``key``/``value`` rows (row r sees new rows 0..r).  This is the
+    prefill of a prompt chunk over a packed prefix, which the reference
+    cannot run (its scheduler forbids partial prefill, rq/scheduler.py:11-18);
+    arguments and validation are those of ``attention``.  Anchor mode at
+    head_dim 128, at most 2048 new rows per request.
+    """
+    key_rotation_ptr, value_rotation_ptr = _validate_packed_inputs(
+        query, key, value, kv_cache, output, query_start_loc, seq_lens, block_table, key_rotation, value_rotation,
+        key_mean, records, reference_mode, loop_index)
+    _call_packed_attention(_lib.lib().rq_packed_prefill_attention, query, key, value, kv_cache, output,
+                           query_start_loc, seq_lens, block_table, key_rotation_ptr, value_rotation_ptr, key_mean,
+                           records, reference_mode, anchor_index, loop_index, workspace)
+
+
+def _call_packed_attention(function, query, key, value, kv_cache, output, query_start_loc, seq_lens, block_table,
+                           key_rotation_ptr, value_rotation_ptr, key_mean, records, reference_mode, anchor_index,
+                           loop_index, workspace):
+    heads, head_dim = query.size(1), query.size(2)
     rows = query.size(0)
     max_pages = block_table.size(1)
     needed = attention_workspace_bytes(rows, heads, head_dim, max_pages, kv_cache.size(3))
     ws = _workspace(workspace, needed, query.device)
     bits, groups = _schedule(records)
     with torch.cuda.device(query.device):
-        status = _lib.lib().rq_attention(
+        status = function(
             query.data_ptr(), query.stride(0), key.data_ptr(), key.stride(0), value.data_ptr(),
             value.stride(0), output.data_ptr(), output.stride(0), rows, heads, head_dim,
             kv_cache.data_ptr(), kv_cache.size(1), kv_cache.size(3), kv_cache.size(4),

@@ -1,0 +1,122 @@
+"""Several query rows per request over the packed history on the multi-row
+MFMA kernels (residualquant_amd/csrc/multirow.hip) against the CPU oracle.
+
+- ``packed_prefill_attention``: each request's rows are its last n tokens,
+  seeing seq_len - n history tokens and, causally, the new ones
+  (oracle.attention_prefill);
+- ``attention`` with several rows per request (anchor mode, D128) routes to
+  the same kernels with the reference's decode semantics (oracle.attention).
+
+Bar: within 2e-2 max-abs / 1e-3 mean-abs of the oracle, both in BF16 (the
+oracle's FP64 output rounded to BF16: the BF16 quantum of outputs of
+magnitude ~1 at short histories is half the mean bar by itself).
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+import residualquant_amd as rq
+from residualquant_amd import workloads
+
+from .cases import OURO_G16, OURO_G32, make_decode
+
+pytestmark = pytest.mark.gpu
+
+MAX_ABS = 2e-2
+MEAN_ABS = 1e-3
+
+
+def _bits(t):
+    return None if t is None else workloads.bf16_bits(t)
+
+
+def _bf16(x: np.ndarray) -> np.ndarray:
+    return torch.from_numpy(x).float().to(torch.bfloat16).double().numpy()
+
+
+def _oracle(oracle, d, cache, loop, causal):
+    g = d.group
+    function = oracle.attention_prefill if causal else oracle.attention
+    return function(_bits(d.query), _bits(d.key), _bits(d.value), cache, d.query_start_loc.numpy(),
+                    d.seq_lens.numpy(), d.table.numpy(), _bits(g.key_rotation), _bits(g.value_rotation),
+                    None if g.key_mean is None else g.key_mean.numpy(), g.records, g.mode, g.anchor, loop)
+
+
+def _run(d, device, cache, loop, causal):
+    g = d.group
+    kr, vr, km = g.device_args(device)
+    out = torch.full_like(d.query, float("nan"), device=device)
+    function = rq.packed_prefill_attention if causal else rq.attention
+    function(d.query.to(device), d.key.to(device), d.value.to(device), cache, out, d.query_start_loc.to(device),
+             d.seq_lens.to(device), d.table.to(device), kr, vr, km, g.records, g.mode, g.anchor, loop)
+    torch.cuda.synchronize()
+    return out.float().cpu().numpy()
+
+
+CASES = [
+    # lengths (seq_len incl. the new rows), rows per request, heads, records, page tokens, mean, rotation
+    ([100, 37, 9], [4, 1, 8], 3, OURO_G32, 16, True, True),
+    ([300], [33], 2, OURO_G32, 16, True, True),           # two row tiles
+    ([70, 200], [70, 5], 2, OURO_G16, 32, False, True),   # the first request has no history (prefill)
+    ([16, 40], [16, 3], 2, OURO_G32, 32, True, False),    # no rotation; the first request has no history (prefill)
+    ([2100], [3], 2, OURO_G32, 16, True, True),           # eight history splits
+    ([90, 51], [2, 6], 2, ((2, 16), (2, 16), (4, 32), (2, 32)), 16, True, True),
+    ([77], [5], 1, ((4, 16),), 32, True, True),           # single-record group
+]
+
+
+def _ids(case):
+    return f"n{sum(case[1])}-h{case[2]}-r{len(case[3])}-pt{case[4]}"
+
+
+@pytest.mark.parametrize("case", CASES, ids=_ids)
+@pytest.mark.parametrize("causal", [True, False], ids=["prefill", "decode"])
+def test_multirow_matches_oracle(oracle, device, case, causal):
+    lengths, rows, heads, records, pt, mean, rotation = case
+    print(f"[case] multirow causal={causal} {case}", flush=True)
+    d = make_decode(lengths, heads, 128, records, seed=sum(lengths) + len(rows), page_tokens=pt, mean=mean,
+                    rotation=rotation, rows_per_request=rows)
+    expected_cache = d.group.oracle_cache(oracle)
+    cache = torch.from_numpy(expected_cache).to(device)
+    for loop in range(len(records)):
+        got = _run(d, device, cache, loop, causal)
+        want = _oracle(oracle, d, expected_cache, loop, causal)
+        err = np.abs(got - _bf16(want))
+        print(f"[case]   loop {loop}: max {err.max():.3g} mean {err.mean():.3g}", flush=True)
+        assert np.isfinite(got).all()
+        assert err.max() <= MAX_ABS and err.mean() <= MEAN_ABS, (loop, err.max(), err.mean())
+
+
+def test_decode_rows_agree_with_single_row_calls(oracle, device):
+    """The multi-row route and the per-row decode kernel give the same rows within the bar."""
+    d = make_decode([500, 300], 4, 128, OURO_G32, seed=5, rows_per_request=[3, 2])
+    g = d.group
+    cache = torch.from_numpy(g.oracle_cache(oracle)).to(device)
+    kr, vr, km = g.device_args(device)
+    for loop in (0, 3):
+        multi = _run(d, device, cache, loop, causal=False)
+        starts = d.query_start_loc.tolist()
+        for b in range(2):
+            for i in range(starts[b], starts[b + 1]):
+                out = torch.empty((1, 4, 128), dtype=torch.bfloat16, device=device)
+                rq.attention(d.query[i:i + 1].to(device), d.key[i:i + 1].to(device), d.value[i:i + 1].to(device),
+                             cache, out, torch.tensor([0, 1], dtype=torch.int32, device=device),
+                             d.seq_lens[b:b + 1].to(device), d.table[b:b + 1].to(device), kr, vr, km, g.records,
+                             g.mode, g.anchor, loop)
+                single = out.float().cpu().numpy()[0]
+                assert np.abs(multi[i] - single).max() <= MAX_ABS
+
+
+def test_multirow_rejections(device):
+    d = make_decode([40], 2, 96, OURO_G16, seed=2, rows_per_request=[3])
+    g = d.group
+    cache = torch.zeros(g.cache_shape, dtype=torch.uint8, device=device)
+    kr, vr, km = g.device_args(device)
+    out = torch.empty_like(d.query, device=device)
+    with pytest.raises(RuntimeError, match="multi-row"):
+        rq.packed_prefill_attention(d.query.to(device), d.key.to(device), d.value.to(device), cache, out,
+                                    d.query_start_loc.to(device), d.seq_lens.to(device), d.table.to(device), kr, vr,
+                                    km, g.records, g.mode, g.anchor, 0)
