@@ -435,6 +435,122 @@ def run_prefill(args):
 HUGINN_SCHEDULE = ((2, 16), (2, 16), (2, 16), (4, 32))
 
 
+def run_multiquery(args):
+    """Several query rows per request over the C2 packed history (multi-row MFMA kernels).
+
+    B requests x R rows (--rows-per-request) x 8192 history tokens x 16 heads
+    x D128, the C2 cache and schedule.  One step = the 4 loop calls.  Timed
+    three ways on the same rows: rq.attention with R rows per request (the
+    multi-row kernels, the reference's decode semantics: every row sees the
+    8192 history tokens and its own key), the same rows as B*R one-row
+    requests (the per-row decode kernel, which streams each request's pages R
+    times), and rq.packed_prefill_attention (the rows as the requests' last R
+    tokens, causal among themselves, over the same 8192-token history)."""
+    import torch
+
+    import residualquant_amd as rq
+    from residualquant_amd import ops, workloads
+
+    device = torch.device("cuda:0")
+    torch.cuda.set_device(device)
+    batch, rows_per, history, heads, dim, page_tokens = args.batch, args.rows_per_request, args.history, 16, 128, 16
+    seed = 2026
+    log(f"[bench] building packed cache B={batch} T={history} H={heads} D={dim}, {rows_per} rows per request")
+    cache, table, key_rotation, value_rotation = build_packed_cache(
+        torch, rq, workloads, batch, history, heads, dim, page_tokens, device, seed)
+    rows = batch * rows_per
+    generator = torch.Generator(device=device).manual_seed(seed + 7)
+    query, key, value = (torch.randn((rows, heads, dim), generator=generator, device=device).to(torch.bfloat16)
+                         for _ in range(3))
+    output = torch.empty_like(query)
+    qsl = torch.arange(0, rows + 1, rows_per, dtype=torch.int32, device=device)
+    seq_decode = torch.full((batch,), history + 1, dtype=torch.int32, device=device)
+    seq_prefill = torch.full((batch,), history + rows_per, dtype=torch.int32, device=device)
+    # Per-row baseline: every row its own request over its request's pages.
+    qsl_rows = torch.arange(rows + 1, dtype=torch.int32, device=device)
+    seq_rows = torch.full((rows,), history + 1, dtype=torch.int32, device=device)
+    table_rows = table.repeat_interleave(rows_per, dim=0).contiguous()
+    workspace = torch.empty(ops.attention_workspace_bytes(rows, heads, dim, table.size(1), page_tokens),
+                            dtype=torch.uint8, device=device)
+
+    def multi(loop):
+        rq.attention(query, key, value, cache, output, qsl, seq_decode, table, key_rotation, value_rotation, None,
+                     SCHEDULE, "anchor", ANCHOR, loop, workspace=workspace)
+
+    def per_row(loop):
+        rq.attention(query, key, value, cache, output, qsl_rows, seq_rows, table_rows, key_rotation, value_rotation,
+                     None, SCHEDULE, "anchor", ANCHOR, loop, workspace=workspace)
+
+    def prefill(loop):
+        rq.packed_prefill_attention(query, key, value, cache, output, qsl, seq_prefill, table, key_rotation,
+                                    value_rotation, None, SCHEDULE, "anchor", ANCHOR, loop, workspace=workspace)
+
+    results = {}
+    for name, call in (("multirow", multi), ("per_row_decode", per_row), ("packed_prefill", prefill)):
+        def step(call=call):
+            for loop in range(len(SCHEDULE)):
+                call(loop)
+        settle(torch, step, 0.2)
+        durations = kernel_durations_ms(ops, [lambda loop=loop, call=call: call(loop) for loop in range(4)],
+                                        max(50, args.steps))
+        graph = capture(torch, step)
+        settle(torch, graph.replay, 0.1)
+        step_s = timed(torch, graph.replay, args.steps, args.warmup)
+        residual_ms = statistics.median(durations[0] + durations[1] + durations[2])
+        results[name] = {"us_per_step": step_s * 1e6, "residual_loop_us": residual_ms * 1e3,
+                         "anchor_loop_us": statistics.median(durations[ANCHOR]) * 1e3,
+                         "launches_timed": len(durations[0]) * 4}
+        log(f"[bench] {name}: step {step_s * 1e6:.1f} us, residual call {residual_ms * 1e3:.1f} us, "
+            f"anchor {results[name]['anchor_loop_us']:.1f} us")
+        del graph
+    # Algorithmic bytes: the pages once per (request, head) plus the rows' Q/K/V/out.
+    step_bytes = sum(staged_call_bytes(batch, history, heads, dim, page_tokens, loop) for loop in range(4)) + \
+        4 * 4 * (rows - batch) * heads * dim * 2
+    residual_bytes = staged_call_bytes(batch, history, heads, dim, page_tokens, 0) + 4 * (rows - batch) * heads * dim * 2
+    m = results["multirow"]
+    residual_gbps = residual_bytes / (m["residual_loop_us"] * 1e-6) / 1e9
+    # MFMA work of a residual call: per (request, head) and 32-token tile, 8 + 8
+    # 32x32x16 MFMAs (2 * 32 * 32 * 16 FLOP each) for one 32-row tile.
+    tiles = batch * heads * ((history + 31) // 32) * ((rows_per + 31) // 32)
+    mfma_flop = tiles * 16 * 2 * 32 * 32 * 16
+    result = {
+        "metric": "paged decode-attn µs/step + achieved HBM GB/s (% peak), INT2/INT4 vs bf16, 1 GPU",
+        "value": step_bytes / (m["us_per_step"] * 1e-6) / 1e9,
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": m["us_per_step"] * 1e-3,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "int2/int4 packed codes, fp16/bf16 MFMA operands, fp32 accumulate",
+        "data": "synthetic (seeded anchor N(0,1) + loop residuals N(0,0.15^2), random-sign Hadamard rotations)",
+        "config": {"workload": "several query rows per request over the C2 packed history", "batch": batch,
+                   "rows_per_request": rows_per, "history_tokens": history, "heads": heads, "head_dim": dim,
+                   "page_tokens": page_tokens, "schedule": "[2,32]x3+[4,32] anchor 3 ls"},
+        "us_per_step": m["us_per_step"],
+        "timing": "one HIP-graph replay of the 4 loop calls per step after settle replays; per-call medians of "
+                  ">= 50 launches (HIP events around the call's launches)",
+        "bytes_per_step": step_bytes,
+        "modes": results,
+        "speedup_vs_per_row_decode": results["per_row_decode"]["us_per_step"] / m["us_per_step"],
+        "roofline": {
+            "bound": "hbm",
+            "achieved": residual_gbps,
+            "peak": PEAK_HBM_GBPS,
+            "unit": "GB/s",
+            "frac": residual_gbps / PEAK_HBM_GBPS,
+            "traffic": None,
+            "kernel": "multirow_stream_kernel<16,true> + multirow_finish_kernel (residual loops 0-2), median of "
+                      f"{m['launches_timed'] * 3 // 4} calls",
+            "mfma_TFLOPs": mfma_flop / (m["residual_loop_us"] * 1e-6) / 1e12,
+        },
+        "cpu_baseline": None,
+    }
+    print(json.dumps(result), flush=True)
+
+
 def run_huginn(args):
     """C4: Huginn-shaped deep-loop decode attention, 55 heads x D96, g16 residuals, B8 x T4096.
 
@@ -632,10 +748,13 @@ def run_step(args):
 
 def main():
     parser = argparse.ArgumentParser(description=__doc__)
-    parser.add_argument("--workload", choices=("decode", "quantize", "prefill", "step", "huginn"), default="decode",
+    parser.add_argument("--workload", choices=("decode", "quantize", "prefill", "step", "huginn", "multiquery"),
+                        default="decode",
                         help="decode: C2 paged decode attention (the headline); quantize: C1 quantize-on-write; "
                              "prefill: causal prompt attention; step: C3 looped-model decode step; "
-                             "huginn: C4 deep-loop decode attention (55 heads x D96, g16)")
+                             "huginn: C4 deep-loop decode attention (55 heads x D96, g16); "
+                             "multiquery: several rows per request over the C2 history (multi-row MFMA kernels)")
+    parser.add_argument("--rows-per-request", type=int, default=4, help="multiquery: query rows per request")
     parser.add_argument("--no-sweep", action="store_true", help="step workload: batch 32 x 8k only")
     parser.add_argument("--tokens", type=int, default=4096, help="tokens per quantize call or prompt")
     parser.add_argument("--gpus", type=int, default=1)
@@ -670,6 +789,9 @@ def main():
         return
     if args.workload == "huginn":
         run_huginn(args)
+        return
+    if args.workload == "multiquery":
+        run_multiquery(args)
         return
     run_decode(args)
 

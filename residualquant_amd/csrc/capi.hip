@@ -128,19 +128,29 @@ struct WorkspaceLayout {
     size_t row_request, arrivals, prep, partials, total;
 };
 
+constexpr int64_t kMultiRowMinRows = 6;
+
 // Several rows per request (anchor mode, D = 128) run the multi-row MFMA
-// kernels: history splits per (request, head, 32-row tile), sized from the
-// row count so that the workspace depends on host shapes only (two
-// workgroups per compute unit when every row is its own request), at most
-// kMultiRowMaxSplits and no more than the history's 32-token tiles allow
-// (four per split, one per wave).
-int multirow_splits(int64_t rows, int heads, int64_t max_pages, int page_tokens) {
+// kernels: one workgroup per (request, head, 32-row tile, history split).
+// Splits aim at two workgroups per compute unit over `groups` =
+// requests x heads x row tiles, at most kMultiRowMaxSplits, no more than the
+// history's 32-token tiles allow (four per split, one per wave), and at least
+// enough that no split holds more than kMultiRowMaxSplitPages pages.  The
+// workspace is sized for the most splits any call of these row and head
+// counts can take (one request).
+int multirow_splits(int64_t groups, int64_t max_pages, int page_tokens) {
     const int64_t target = 2LL * compute_units();
-    const int64_t pairs = std::max<int64_t>(1, rows * heads);
-    int64_t splits = (target + pairs - 1) / pairs;
+    int64_t splits = (target + std::max<int64_t>(1, groups) - 1) / std::max<int64_t>(1, groups);
     const int64_t tiles = std::max<int64_t>(1, (max_pages * page_tokens + 31) / 32);
     splits = std::min<int64_t>(splits, std::max<int64_t>(1, tiles / 4));
-    return (int)std::max<int64_t>(1, std::min<int64_t>(splits, rq::kMultiRowMaxSplits));
+    splits = std::min<int64_t>(splits, rq::kMultiRowMaxSplits);
+    const int64_t tiles_per_split_max = (int64_t)(rq::kMultiRowMaxSplitPages - 1) * page_tokens / 32;
+    splits = std::max<int64_t>(splits, (tiles + tiles_per_split_max - 1) / tiles_per_split_max);
+    return (int)std::max<int64_t>(1, splits);
+}
+
+int multirow_workspace_splits(int heads, int64_t max_pages, int page_tokens) {
+    return multirow_splits(heads, max_pages, page_tokens);
 }
 
 struct MultiRowLayout {
@@ -289,7 +299,7 @@ static size_t attention_workspace_total(int64_t rows, int heads, int head_dim, i
                                         int page_tokens) {
     size_t total = workspace_layout(rows, heads, head_dim, split_count(rows, heads, max_pages)).total;
     if (head_dim == 128 && (page_tokens == 16 || page_tokens == 32))
-        total = std::max(total, multirow_layout(rows, heads, multirow_splits(rows, heads, max_pages, page_tokens)).total);
+        total = std::max(total, multirow_layout(rows, heads, multirow_workspace_splits(heads, max_pages, page_tokens)).total);
     return total;
 }
 
@@ -390,8 +400,13 @@ static int attention_packed(const void* query, int64_t query_stride, const void*
     const bool adjacent = records > 1 && reference_mode == RQ_MODE_ADJACENT;
     // Several rows per request in anchor mode at D = 128 (and every prefill
     // over packed history) take the multi-row MFMA kernels, which stream each
-    // request's pages once for all its rows.
-    if (causal || (!adjacent && head_dim == 128 && rows > requests)) {
+    // request's pages once for all its rows but dequantize every page tile
+    // into LDS.  Measured at 8192 history tokens x 16 heads (residual-loop
+    // call): 16 rows per request 439 us against 914 us for the per-row decode
+    // kernel (B16), 4 rows 559 against 500 us (B32: the rows of one request
+    // share its pages in L2), so decode calls take them from an average of
+    // kMultiRowMinRows rows per request.
+    if (causal || (!adjacent && head_dim == 128 && requests > 0 && rows >= kMultiRowMinRows * requests)) {
         if (adjacent || head_dim != 128)
             return fail(RQ_ENOKERNEL,
                         "No compiled packed HIP multi-row kernel for head_dim=%d, reference_mode=%s (anchor mode "
@@ -404,7 +419,8 @@ static int attention_packed(const void* query, int64_t query_stride, const void*
         if (rows == 0 || requests == 0) return ok();
         if (causal && rows - requests + 1 > rq::kMultiRowMaxLive)
             return fail(RQ_EINVAL, "At most %d new rows per request over packed history", rq::kMultiRowMaxLive);
-        const int splits = multirow_splits(rows, heads, max_pages, page_tokens);
+        const int64_t row_tiles = (rows - requests + 1 + 31) / 32;
+        const int splits = multirow_splits(requests * heads * row_tiles, max_pages, page_tokens);
         const MultiRowLayout layout = multirow_layout(rows, heads, splits);
         if (workspace == nullptr || workspace_bytes < layout.total)
             return fail(RQ_ENOSPACE, "Attention workspace of %zu bytes required (got %zu)", layout.total,
@@ -443,7 +459,7 @@ static int attention_packed(const void* query, int64_t query_stride, const void*
                                                           : nullptr;
         m.causal = causal ? 1 : 0;
         m.splits = splits;
-        m.row_tiles = (int)((rows - requests + 1 + 31) / 32);
+        m.row_tiles = (int)row_tiles;
         uint8_t* ws = static_cast<uint8_t*>(workspace);
         m.partials = reinterpret_cast<float*>(ws + layout.partials);
         m.row_shift = reinterpret_cast<float*>(ws + layout.row_shift);

@@ -61,6 +61,9 @@ constexpr int MS = D + 4;
 constexpr int kMlOffset = kWaves * 32 * MS * 4;
 static_assert(kMlOffset + kWaves * 32 * 2 * 4 <= kLdsBytes, "merge buffer fits in the tile LDS");
 constexpr float kLog2e = 1.4426950408889634f;
+// Pages of one history split at most (its block ids are staged in LDS); the
+// host sizes splits so that a split never holds more.
+constexpr int kMaxSplitPages = kMultiRowMaxSplitPages;
 
 __device__ __forceinline__ F32x16 mfma(Bf16x8 a, Bf16x8 b, F32x16 c) {
     return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
@@ -81,23 +84,25 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t page_rsrc(const uint8_t* page,
     return __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(page), (short)0, (int)bytes, 0x00020000);
 }
 
-// One record's bytes for the lane's token and 32-channel quarter.
+// One record's bytes for the lane's token and 32-channel quarter: 16 code
+// bytes (INT4) or 8 (INT2), the FP8 scale and offset byte(s) (one for group
+// 32, two for group 16) and, for residual records, the BF16 alpha.
+template <int Bits>
 struct RecordBytes {
-    uint32_t w[4];   // codes: 16 bytes (INT4) or 8 bytes (INT2)
-    uint32_t scale;  // FP8 scale byte(s): one (group 32) or two (group 16)
-    uint32_t offset;
-    uint32_t alpha;  // BF16 alpha (residual records)
+    uint32_t w[Bits];
+    uint32_t scale, offset, alpha;
 };
 
+template <int Bits>
 __device__ __forceinline__ void load_record(__amdgpu_buffer_rsrc_t page, const RecordRegion& r, int page_tokens,
-                                            int row, int quarter, bool alpha, RecordBytes& out) {
+                                            int row, int quarter, bool alpha, RecordBytes<Bits>& out) {
     const uint32_t codes = (uint32_t)(r.offset + row * r.code_bytes + quarter * (r.code_bytes / 4));
-    if (r.bits == 4) {
+    if constexpr (Bits == 4) {
         const auto v = __builtin_amdgcn_raw_buffer_load_b128(page, codes, 0, kStreamPolicy);
         out.w[0] = v[0]; out.w[1] = v[1]; out.w[2] = v[2]; out.w[3] = v[3];
     } else {
         const auto v = __builtin_amdgcn_raw_buffer_load_b64(page, codes, 0, kStreamPolicy);
-        out.w[0] = v[0]; out.w[1] = v[1]; out.w[2] = 0u; out.w[3] = 0u;
+        out.w[0] = v[0]; out.w[1] = v[1];
     }
     const uint32_t scales = (uint32_t)(r.offset + page_tokens * r.code_bytes + row * r.groups + quarter * (r.groups / 4));
     const uint32_t offsets = scales + (uint32_t)(page_tokens * r.groups);
@@ -116,12 +121,13 @@ __device__ __forceinline__ void load_record(__amdgpu_buffer_rsrc_t page, const R
 // code * scale + offset for the lane's 32 channels (exact in FP32).  A code
 // held in a byte is the FP8 E4M3 value code * 2^-9, so v_cvt_pk_f32_fp8
 // converts two codes per instruction and the scale carries the 2^9 back.
-__device__ __forceinline__ void dequant(const RecordBytes& r, int bits, int group, float (&x)[32]) {
+template <int Bits>
+__device__ __forceinline__ void dequant(const RecordBytes<Bits>& r, int group, float (&x)[32]) {
     const float s0 = __builtin_amdgcn_cvt_f32_fp8((int)r.scale, 0) * 512.0f;
     const float o0 = __builtin_amdgcn_cvt_f32_fp8((int)r.offset, 0);
     const float s1 = group == 32 ? s0 : __builtin_amdgcn_cvt_f32_fp8((int)r.scale, 1) * 512.0f;
     const float o1 = group == 32 ? o0 : __builtin_amdgcn_cvt_f32_fp8((int)r.offset, 1);
-    if (bits == 4) {
+    if constexpr (Bits == 4) {
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             const float s = i < 2 ? s0 : s1, o = i < 2 ? o0 : o1;
@@ -161,6 +167,14 @@ __device__ __forceinline__ void dequant(const RecordBytes& r, int bits, int grou
     }
 }
 
+// Every record byte of one 16-token unit for the lane: K and V planes, the
+// anchor record and the loop's record.
+template <int BA, int BL>
+struct UnitBytes {
+    RecordBytes<BA> ka, va;
+    RecordBytes<BL> kl, vl;
+};
+
 // The LDS writes of a wave before reads of other lanes of the same wave.
 __device__ __forceinline__ void wave_sync() {
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
@@ -168,10 +182,11 @@ __device__ __forceinline__ void wave_sync() {
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
-template <int PT, bool HasL>
+template <int PT, bool HasL, int BA, int BL>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2)))
 void multirow_stream_kernel(MultiRowParams p) {
     __shared__ __attribute__((aligned(16))) uint8_t lds[kLdsBytes];
+    __shared__ int split_blocks[kMaxSplitPages];  // block ids of the split's pages
     const int request = blockIdx.x;
     const int head = blockIdx.y;
     const int split = (int)blockIdx.z % p.splits;
@@ -347,6 +362,34 @@ void multirow_stream_kernel(MultiRowParams p) {
     const int pages = (history + PT - 1) / PT;
     const bool mean_anchor = HasL && p.key_mean_anchor != nullptr;
 
+    // The split's block ids, once, into LDS (-1 past the history or when invalid).
+    const int first_page = tile_begin * kTile / PT;
+    int split_pages = tile_end > tile_begin ? ((tile_end * kTile + PT - 1) / PT - first_page) : 0;
+    if (split_pages > kMaxSplitPages) split_pages = kMaxSplitPages;  // pages past it read as zeros
+    for (int i = tid; i < split_pages; i += kThreads) {
+        const int page = first_page + i;
+        int block = page < pages ? p.block_table[(int64_t)request * p.block_table_stride + page] : -1;
+        split_blocks[i] = (block >= 0 && block < p.num_blocks) ? block : -1;
+    }
+    __syncthreads();
+
+    // Loads of one 16-token unit's bytes into registers (zeros past the history).
+    auto fetch = [&](int unit_first, UnitBytes<BA, BL>& b) {
+        const int row = unit_first % PT + unit_token;
+        const int index = unit_first / PT - first_page;
+        const int block = (unit_first < history && index < split_pages) ? split_blocks[index] : -1;
+        const uint8_t* k_page = p.cache + ((int64_t)(block >= 0 ? block : 0) * p.heads + head) * page_bytes;
+        const uint32_t bytes = block >= 0 ? page_bytes : 0u;
+        const auto k_rsrc = page_rsrc(k_page, bytes);
+        const auto v_rsrc = page_rsrc(k_page + p.plane_stride, bytes);
+        load_record<BA>(k_rsrc, p.anchor, PT, row, quarter, false, b.ka);
+        load_record<BA>(v_rsrc, p.anchor, PT, row, quarter, false, b.va);
+        if constexpr (HasL) {
+            load_record<BL>(k_rsrc, p.residual, PT, row, quarter, true, b.kl);
+            load_record<BL>(v_rsrc, p.residual, PT, row, quarter, true, b.vl);
+        }
+    };
+
     F32x16 out[D / 32];
 #pragma unroll
     for (int t = 0; t < D / 32; ++t)
@@ -355,39 +398,29 @@ void multirow_stream_kernel(MultiRowParams p) {
     float running_max = -__builtin_inff();
     float running_sum = 0.f;
 
+    // Units stream one ahead: the loads of the next unit (the second half of
+    // this tile, or the first of the wave's next tile) are in flight while a
+    // unit is dequantized and while the tile's MFMAs run.
+    UnitBytes<BA, BL> next;
+    if (tile_begin + wave < tile_end) fetch(kTile * (tile_begin + wave), next);
     for (int tile = tile_begin + wave; tile < tile_end; tile += kWaves) {
 #pragma unroll
         for (int u = 0; u < 2; ++u) {
-            const int unit_first = kTile * tile + 16 * u;  // history index of the unit's first token
-            const int page = unit_first / PT;
-            const int row = unit_first % PT + unit_token;
-            const bool valid = unit_first + unit_token < history;
-            int block = -1;
-            if (unit_first < history && page < pages)
-                block = __builtin_amdgcn_readfirstlane(p.block_table[(int64_t)request * p.block_table_stride + page]);
-            const bool page_ok = block >= 0 && block < p.num_blocks;
-            const uint8_t* k_page = p.cache + ((int64_t)(page_ok ? block : 0) * p.heads + head) * page_bytes;
-            const auto k_rsrc = page_rsrc(k_page, page_ok ? page_bytes : 0u);
-            const auto v_rsrc = page_rsrc(k_page + p.plane_stride, page_ok ? page_bytes : 0u);
-            RecordBytes ka, va, kl, vl;
-            load_record(k_rsrc, p.anchor, PT, row, quarter, false, ka);
-            load_record(v_rsrc, p.anchor, PT, row, quarter, false, va);
-            if constexpr (HasL) {
-                load_record(k_rsrc, p.residual, PT, row, quarter, true, kl);
-                load_record(v_rsrc, p.residual, PT, row, quarter, true, vl);
-            }
-            // Tokens past the history (or in pages without a valid block)
-            // hold zeros; their scores are masked below.  K, then V, so that
-            // only one plane's values are live at a time.
+            const UnitBytes<BA, BL> cur = next;
+            const int following = u == 0 ? kTile * tile + 16 : kTile * (tile + kWaves);
+            if (u == 0 || tile + kWaves < tile_end) fetch(following, next);
             const int local = 16 * u + unit_token;
+            // Tokens past the history hold zeros; their scores are masked below.
+            // K, then V, so that only one plane's values are live at a time.
+            const bool valid = kTile * tile + local < history;
             float alpha_k = 1.f;
             {
                 float k[32];
-                dequant(ka, p.anchor.bits, p.anchor.group, k);
+                dequant<BA>(cur.ka, p.anchor.group, k);
                 if constexpr (HasL) {
                     float kx[32];
-                    dequant(kl, p.residual.bits, p.residual.group, kx);
-                    alpha_k = bf16_f32(kl.alpha);
+                    dequant<BL>(cur.kl, p.residual.group, kx);
+                    alpha_k = bf16_f32(cur.kl.alpha);
 #pragma unroll
                     for (int c = 0; c < 32; ++c) k[c] = fmaf(alpha_k, k[c], kx[c]);
                 }
@@ -404,17 +437,20 @@ void multirow_stream_kernel(MultiRowParams p) {
             }
             {
                 float v[32];
-                dequant(va, p.anchor.bits, p.anchor.group, v);
+                dequant<BA>(cur.va, p.anchor.group, v);
                 if constexpr (HasL) {
                     float vx[32];
-                    dequant(vl, p.residual.bits, p.residual.group, vx);
-                    const float alpha_v = bf16_f32(vl.alpha);
+                    dequant<BL>(cur.vl, p.residual.group, vx);
+                    const float alpha_v = bf16_f32(cur.vl.alpha);
 #pragma unroll
-                    for (int c = 0; c < 32; ++c) v[c] = fmaf(alpha_v, round_bf16(v[c]), round_bf16(vx[c]));
+                    for (int c = 0; c < 32; ++c) v[c] = fmaf(alpha_v, (float)(__bf16)v[c], (float)(__bf16)vx[c]);
                 }
+                __bf16 vb[32];
+#pragma unroll
+                for (int c = 0; c < 32; ++c) vb[c] = (__bf16)(valid ? v[c] : 0.f);
 #pragma unroll
                 for (int c = 0; c < 32; ++c)
-                    v_tile[(32 * quarter + c) * VS + local] = (uint16_t)bf16_rn(valid ? v[c] : 0.f);
+                    v_tile[(32 * quarter + c) * VS + local] = __builtin_bit_cast(uint16_t, vb[c]);
             }
             if (quarter == 0) alpha_tile[local] = alpha_k;
         }
@@ -632,13 +668,28 @@ __global__ __launch_bounds__(D) void multirow_finish_kernel(MultiRowParams p) {
     p.output[row * p.output_stride + (int64_t)head * D + c] = (uint16_t)bf16_rn(o / total);
 }
 
+template <int PT, bool HasL, int BA, int BL>
+void launch_one(const MultiRowParams& p, hipStream_t stream) {
+    const dim3 grid((unsigned)p.requests, (unsigned)p.heads, (unsigned)(p.splits * p.row_tiles));
+    hipLaunchKernelGGL((multirow_stream_kernel<PT, HasL, BA, BL>), grid, dim3(kThreads), 0, stream, p);
+}
+
+template <int PT, int BA>
+void launch_anchor(const MultiRowParams& p, hipStream_t stream) {
+    if (!p.has_residual)
+        launch_one<PT, false, BA, 2>(p, stream);
+    else if (p.residual.bits == 2)
+        launch_one<PT, true, BA, 2>(p, stream);
+    else
+        launch_one<PT, true, BA, 4>(p, stream);
+}
+
 template <int PT>
 void launch_pt(const MultiRowParams& p, hipStream_t stream) {
-    const dim3 grid((unsigned)p.requests, (unsigned)p.heads, (unsigned)(p.splits * p.row_tiles));
-    if (p.has_residual)
-        hipLaunchKernelGGL((multirow_stream_kernel<PT, true>), grid, dim3(kThreads), 0, stream, p);
+    if (p.anchor.bits == 4)
+        launch_anchor<PT, 4>(p, stream);
     else
-        hipLaunchKernelGGL((multirow_stream_kernel<PT, false>), grid, dim3(kThreads), 0, stream, p);
+        launch_anchor<PT, 2>(p, stream);
 }
 
 }  // namespace

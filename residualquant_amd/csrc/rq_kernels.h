@@ -193,7 +193,8 @@ hipError_t launch_attention(const AttentionParams& p, hipStream_t stream, hipEve
 // seq_len - 1, the row's own live token); causal = 1: the rows are the
 // request's last n tokens (history seq_len - n, live tokens j <= r).
 constexpr int kMultiRowEntry = 132;        // per (row, head, split): m, l, 2 unused, O[128] (log2 units)
-constexpr int kMultiRowMaxSplits = 8;
+constexpr int kMultiRowMaxSplits = 8;      // for parallelism (more only for very long histories)
+constexpr int kMultiRowMaxSplitPages = 1024;  // pages of one split at most
 constexpr int kMultiRowMaxLive = 2048;     // new rows per request at most (causal)
 struct MultiRowParams {
     const uint16_t* query;
