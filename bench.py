@@ -9,10 +9,11 @@ the three residual-loop calls and the anchor-loop call.  The BF16 paged
 baseline runs the same four calls over a BF16 cache of the same shape.
 
 ``--workload quantize`` instead times quantize-on-write at BASELINE config 1
-(C1): 4096 new tokens x 16 KV heads x D128 x 4 loops, schedule
-[2,16]x2+[2,32]+[4,32] (INT2 residuals at g16 and g32, INT4 anchor at g32),
-least-squares coefficients, seeded random-sign Hadamard rotations, scattered
-to random slots of a paged cache of 16-token blocks.
+(C1): 4096 new tokens x 16 KV heads x D128 x 4 loops with the INT4 g32
+anchor and INT2 residuals at g32 ([2,32]x3+[4,32], the headline) and at g16
+([2,16]x3+[4,32]), plus the mixed [2,16]x2+[2,32]+[4,32]; least-squares
+coefficients, seeded random-sign Hadamard rotations, scattered to random
+slots of a paged cache of 16-token blocks.
 
 Prints ONE JSON line on stdout; everything else goes to stderr.
 """
@@ -36,6 +37,7 @@ PEAK_FP32_TFLOPS = 157.3
 PEAK_BF16_TFLOPS = 2500.0
 SCHEDULE = ((2, 32), (2, 32), (2, 32), (4, 32))
 QUANTIZE_SCHEDULE = ((2, 16), (2, 16), (2, 32), (4, 32))
+HUGINN_SCHEDULE = ((2, 16), (2, 16), (2, 16), (4, 32))
 ANCHOR = 3
 
 
@@ -240,7 +242,8 @@ def cpu_baseline(torch, workloads, cache, table, key_rotation, value_rotation, q
     }
 
 
-def quantize_cpu_baseline(torch, workloads, pairs, slots, key_rotation, value_rotation, cache_shape, budget_s):
+def quantize_cpu_baseline(torch, workloads, pairs, slots, key_rotation, value_rotation, cache_shape, schedule,
+                          budget_s):
     """The CPU oracle (single thread) quantizing a bounded prefix of the same tokens."""
     import numpy as np
     from oracle import oracle
@@ -257,21 +260,42 @@ def quantize_cpu_baseline(torch, workloads, pairs, slots, key_rotation, value_ro
         part = slice(done, min(done + chunk, slot_array.size))
         start = time.perf_counter()
         oracle.quantize([(k[part], v[part]) for k, v in zip(keys, values)], cache, slot_array[part], kr, vr,
-                        None, QUANTIZE_SCHEDULE, "anchor", ANCHOR, "ls")
+                        None, schedule, "anchor", ANCHOR, "ls")
         elapsed += time.perf_counter() - start
         done = part.stop
+    host = host_description(torch)
     return {
         "value": done / elapsed,
         "unit": "tokens/s",
         "cores": 1,
         "kind": "port",
-        "sample": f"first {done} of {slot_array.size} tokens (all heads, both planes), oracle/rq_oracle.c "
-                  f"single-threaded; {elapsed:.2f} s; host {platform.processor() or 'cpu'}",
+        "sample": f"first {done} of {slot_array.size} tokens (all heads, both planes) of the g32 schedule, "
+                  f"oracle/rq_oracle.c single-threaded; {elapsed:.2f} s; {host['cpu_model']}",
+        **host,
     }
 
 
+def schedule_name(schedule):
+    """'[2,32]x3+[4,32]'-style name of a record schedule."""
+    parts, i = [], 0
+    while i < len(schedule):
+        n = 1
+        while i + n < len(schedule) and schedule[i + n] == schedule[i]:
+            n += 1
+        parts.append(f"[{schedule[i][0]},{schedule[i][1]}]" + (f"x{n}" if n > 1 else ""))
+        i += n
+    return "+".join(parts)
+
+
 def run_quantize(args):
-    """C1: one quantize-on-write call per step; kernel time from HIP events on torch's stream."""
+    """C1: one quantize-on-write call per step for each record schedule.
+
+    The two schedules of the configuration (INT2 residuals at g32 and at g16,
+    INT4 g32 anchor) and a mixed one; each is timed with HIP events around
+    every call on torch's current stream (the launch stream) after a settle
+    phase, and reported as the median call.  ``value`` is the g32 schedule."""
+    import statistics
+
     import torch
 
     import residualquant_amd as rq
@@ -280,54 +304,68 @@ def run_quantize(args):
     device = torch.device("cuda:0")
     torch.cuda.set_device(device)
     tokens, heads, dim, page_tokens, seed = args.tokens, 16, 128, 16, 2026
-    width = rq.page_width(dim, QUANTIZE_SCHEDULE)
     blocks = 2 * ((tokens + page_tokens - 1) // page_tokens)
-    cache = torch.zeros((2, blocks, heads, page_tokens, width), dtype=torch.uint8, device=device)
     generator = torch.Generator().manual_seed(seed)
     slots = torch.randperm(blocks * page_tokens, generator=generator)[:tokens].to(device)
-    pairs = workloads.loop_kv(tokens, heads, dim, len(QUANTIZE_SCHEDULE), seed + 1, device=device)
+    pairs = workloads.loop_kv(tokens, heads, dim, 4, seed + 1, device=device)
     key_rotation = workloads.random_sign_rotation(heads, dim, seed + 3, device=device)
     value_rotation = workloads.random_sign_rotation(heads, dim, seed + 4, device=device)
+    flop = 2.0 * tokens * heads * 2 * 4 * dim * dim
+    input_bytes = tokens * heads * dim * 2 * 4 * 2
 
-    def step():
-        rq.quantize(pairs, cache, slots, key_rotation, value_rotation, None, QUANTIZE_SCHEDULE, "anchor",
-                    ANCHOR, "ls")
+    results = {}
+    for name, schedule in (("g32", SCHEDULE), ("g16", HUGINN_SCHEDULE), ("mixed", QUANTIZE_SCHEDULE)):
+        width = rq.page_width(dim, schedule)
+        cache = torch.zeros((2, blocks, heads, page_tokens, width), dtype=torch.uint8, device=device)
 
-    for _ in range(args.warmup):
-        step()
-    torch.cuda.synchronize()
-    begin, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    start = time.perf_counter()
-    begin.record()
-    for _ in range(args.steps):
-        step()
-    end.record()
-    torch.cuda.synchronize()
-    wall_s = (time.perf_counter() - start) / args.steps
-    kernel_ms = begin.elapsed_time(end) / args.steps  # one launch per call
-    records = len(QUANTIZE_SCHEDULE)
-    flop = 2.0 * tokens * heads * 2 * records * dim * dim
-    input_bytes = tokens * heads * dim * 2 * records * 2
-    output_bytes = tokens * heads * 2 * width
-    achieved = flop / (kernel_ms * 1e-3) / 1e12
-    log(f"[bench] quantize {kernel_ms * 1e3:.1f} us/call ({achieved:.1f} TFLOP/s rotation), "
-        f"{(input_bytes + output_bytes) / (kernel_ms * 1e-3) / 1e9:.0f} GB/s")
+        def step(cache=cache, schedule=schedule):
+            rq.quantize(pairs, cache, slots, key_rotation, value_rotation, None, schedule, "anchor", ANCHOR, "ls")
 
+        settle(torch, step, 0.3)
+        for _ in range(args.warmup):
+            step()
+        events = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+                  for _ in range(args.steps)]
+        torch.cuda.synchronize()
+        start = time.perf_counter()
+        for begin, end in events:
+            begin.record()
+            step()
+            end.record()
+        torch.cuda.synchronize()
+        wall_s = (time.perf_counter() - start) / args.steps
+        kernel_ms = statistics.median(b.elapsed_time(e) for b, e in events)  # one launch per call
+        output_bytes = tokens * heads * 2 * width
+        results[name] = {
+            "schedule": schedule_name(schedule) + " anchor 3 ls",
+            "us_per_call": kernel_ms * 1e3,
+            "us_per_call_wall": wall_s * 1e6,
+            "tokens_per_s": tokens / (kernel_ms * 1e-3),
+            "rotation_TFLOPs": flop / (kernel_ms * 1e-3) / 1e12,
+            "hbm_GBps": (input_bytes + output_bytes) / (kernel_ms * 1e-3) / 1e9,
+            "bytes_per_call": input_bytes + output_bytes,
+        }
+        log(f"[bench] quantize {name}: {kernel_ms * 1e3:.1f} us/call "
+            f"({results[name]['rotation_TFLOPs']:.1f} TFLOP/s rotation)")
+        del cache
+
+    head = results["g32"]
     cpu = None
     if args.cpu_budget > 0:
         log("[bench] cpu baseline (oracle quantize) ...")
+        width = rq.page_width(dim, SCHEDULE)
         cpu = quantize_cpu_baseline(torch, workloads, pairs, slots, key_rotation, value_rotation,
-                                    tuple(cache.shape), args.cpu_budget)
+                                    (2, blocks, heads, page_tokens, width), SCHEDULE, args.cpu_budget)
         log(f"[bench] cpu {cpu['value']:.1f} tokens/s")
 
     result = {
         "metric": "quantize-on-write tokens/s (C1), 1 GPU",
-        "value": tokens / (kernel_ms * 1e-3),
+        "value": head["tokens_per_s"],
         "unit": "tokens/s",
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
-        "ms_per_step": kernel_ms,
+        "ms_per_step": head["us_per_call"] * 1e-3,
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
@@ -336,19 +374,17 @@ def run_quantize(args):
                 "random-sign Hadamard rotations, random slots)",
         "config": {
             "workload": "C1 quantize-on-write micro-benchmark",
-            "tokens": tokens, "heads": heads, "head_dim": dim, "loops": records, "page_tokens": page_tokens,
-            "schedule": "[2,16]x2+[2,32]+[4,32] anchor 3 ls", "cache_blocks": blocks,
+            "tokens": tokens, "heads": heads, "head_dim": dim, "loops": 4, "page_tokens": page_tokens,
+            "schedule": head["schedule"], "cache_blocks": blocks,
         },
-        "us_per_call": kernel_ms * 1e3,
-        "us_per_call_wall": wall_s * 1e6,
-        "hbm_GBps": (input_bytes + output_bytes) / (kernel_ms * 1e-3) / 1e9,
-        "bytes_per_call": input_bytes + output_bytes,
+        "timing": "median of per-call HIP events after >= 0.3 s of untimed calls per schedule",
+        "schedules": results,
         "roofline": {
             "bound": "mfma",
-            "achieved": achieved,
+            "achieved": head["rotation_TFLOPs"],
             "peak": PEAK_FP32_TFLOPS,
             "unit": "TFLOP/s",
-            "frac": achieved / PEAK_FP32_TFLOPS,
+            "frac": head["rotation_TFLOPs"] / PEAK_FP32_TFLOPS,
             "traffic": None,
             "kernel": "quantize_mfma_kernel<128,4,3>: FP32 rotation FMAs (K=1 v_mfma_f32_16x16x1_4b_f32 "
                       "chains) against the published FP32 peak; HBM traffic is 6% of peak at this rate",
@@ -432,7 +468,6 @@ def run_prefill(args):
     print(json.dumps(result), flush=True)
 
 
-HUGINN_SCHEDULE = ((2, 16), (2, 16), (2, 16), (4, 32))
 
 
 def run_multiquery(args):

@@ -16,6 +16,10 @@
 // Two kernels share the commit code: quantize_kernel below (VALU rotation,
 // used for short calls such as decode steps) and quantize_mfma_kernel (the
 // rotation on the matrix cores, for calls of kMfmaMinTokens tokens or more).
+// On gfx950 the FP32 MFMAs and the VALU do not execute concurrently (a wave
+// interleaving 8 MFMAs with 64 independent FMAs takes the sum of the two
+// times, at one and at two waves per SIMD), so a call costs its rotation
+// plus its commit.
 //
 // VALU work mapping: one workgroup = one (head, plane) and a run of tokens; its 16
 // waves share the FP32 rotation in LDS.  A wave takes 4 tokens per pass, 16
@@ -402,57 +406,59 @@ __global__ __launch_bounds__(kQuantizeThreads) void quantize_kernel(QuantizePara
 // rounding per step in k order, i.e. exactly the k-ascending fmaf chain
 // (checked on gfx950 including subnormals, signed zeros and cancellation).
 //
-// One wave rotates 16 tokens per pass.  MFMA (record r, half h) takes
-// A = x_r[token l % 16][k] (the same value in all 4 blocks) and
-// B = R[k][64 h + l] (block l / 16 = channels 64 h + 16 b .. + 15), so a
-// k step is 2 R MFMAs fed by one 8-byte LDS read of the token's records and
-// two 4-byte rotation reads: ~5 FMAs per LDS byte instead of < 1 for the
-// VALU form.  Accumulator register i of lane l then holds token
-// 4 (l / 16) + i % 4 at channel 64 h + 16 (i / 4) + l % 16.  The inputs are
-// staged per wave as BF16 [buffer][k][token][record] in a double-buffered
-// 32-k chunk; after the k loop the wave's stage is reused to transpose four
-// tokens at a time into the canonical commit layout, and commit_record runs
-// unchanged (16 lanes per token).
-constexpr int kMfmaWaves = 8;
+// One wave rotates 4 tokens per pass.  The 16 rows of the MFMA are the
+// (token, record slot) pairs of those tokens, row 4 token + slot, so a pass
+// keeps 32 accumulator registers and 12 waves (3 per SIMD) fit a CU: while
+// some waves run their k loop on the matrix core, others commit on the VALU.
+// MFMA (half h) takes A = x[row l % 16][k] (the same value in all 4 blocks)
+// and B = R[k][64 h + l]; accumulator register i of lane l then holds token
+// l / 16, record slot i % 4, channel 64 h + 16 (i / 4) + l % 16.  The commit
+// lanes of token l / 16 are the same 16 lanes, so each record passes through
+// a 4-token transpose in LDS to the canonical layout right before its commit.
+// Slots at or beyond R rotate a copy of record 0 and are never committed.
+//
+// Inputs go straight from global memory to registers (the A operand), in
+// chunks of kInputChunk k double-buffered, the next pass's first chunk in
+// flight during the commit.  The rotation sits in LDS as FP32
+// [k / 2][lane][R[k][l], R[k][64 + l], R[k + 1][l], R[k + 1][64 + l]], one
+// 16-byte read per two k steps.
+constexpr int kMfmaWaves = 12;
 constexpr int kMfmaThreads = 64 * kMfmaWaves;
-constexpr int kMfmaTokens = 16;  // tokens per wave per pass
+constexpr int kMfmaTokens = 4;        // tokens per wave per pass
+constexpr int kTransposeStride = 144;  // floats per token row of the transpose: 16 q + j spreads the banks
 
 typedef float F32x16 __attribute__((ext_vector_type(16)));
 
+template <int D>
+constexpr int kInputChunk = 16;  // an even number of chunks per row at D = 96 and 128
+
 template <int D, int R, int A>
 __global__ __launch_bounds__(kMfmaThreads) void quantize_mfma_kernel(QuantizeParams p, int block_tokens) {
-    static_assert(R <= kStageRecords, "four record slots per staged (k, token)");
-    // Per-wave stage: two 32-k chunks of BF16 [k][token][record] (8 KB), or
-    // during the commit one FP32 [record][channel][4 tokens] transpose (8 KB).
-    constexpr int kStageWords = 2 * kChunk * kMfmaTokens * kStageRecords / 2;
-    static_assert(kStageWords * 4 >= kStageRecords * 128 * 4 * 4, "transpose fits in the stage");
-    __shared__ __attribute__((aligned(16))) uint32_t stage_lds[kMfmaWaves][kStageWords];
-    __shared__ __attribute__((aligned(16))) float rotation_lds[D * D];
-    __shared__ float mean_lds[R * D];
+    static_assert(R <= 4, "four record slots per token");
+    constexpr int C = kInputChunk<D>;
+    constexpr int kChunks = D / C;
+    constexpr int kLoads = C / 4;  // 8-byte loads per chunk
+    __shared__ __attribute__((aligned(16))) float rotation_lds[D * 128];
+    __shared__ __attribute__((aligned(16))) float transpose_lds[kMfmaWaves][kMfmaTokens * kTransposeStride];
+    __shared__ __attribute__((aligned(16))) float mean_lds[R * D];
     __shared__ float inverse_scale[128];
 
     const int plane = blockIdx.z;
     const int head = blockIdx.y;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int lane64 = threadIdx.x & 63;
+    const int q = lane64 >> 4;  // token of the pass (commit and accumulator role)
     const int j = lane64 & 15;
     const bool active[2] = {4 * j < D, 4 * (j + 16) < D};
     const int column[2] = {4 * j, active[1] ? 64 + 4 * j : 64};
 
     const uint16_t* rotation = plane == 0 ? p.key_rotation : p.value_rotation;
     if (rotation != nullptr) {
-        const uint4* source = reinterpret_cast<const uint4*>(rotation + (int64_t)head * D * D);
-        for (int i = threadIdx.x; i < D * D / 8; i += kMfmaThreads) {
-            const uint4 v = source[i];
-            const uint32_t w[4] = {v.x, v.y, v.z, v.w};
-            float f[8];
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                f[2 * e] = (float)__builtin_bit_cast(_Float16, (uint16_t)(w[e] & 0xffffu));
-                f[2 * e + 1] = (float)__builtin_bit_cast(_Float16, (uint16_t)(w[e] >> 16));
-            }
-            *reinterpret_cast<float4*>(&rotation_lds[8 * i]) = make_float4(f[0], f[1], f[2], f[3]);
-            *reinterpret_cast<float4*>(&rotation_lds[8 * i + 4]) = make_float4(f[4], f[5], f[6], f[7]);
+        const uint16_t* source = rotation + (int64_t)head * D * D;
+        for (int i = threadIdx.x; i < D * 128; i += kMfmaThreads) {
+            const int k = i >> 7, c = i & 127;
+            const float v = c < D ? (float)__builtin_bit_cast(_Float16, source[k * D + c]) : 0.f;
+            rotation_lds[((k >> 1) * 64 + (c & 63)) * 4 + 2 * (k & 1) + (c >> 6)] = v;
         }
     }
     const bool has_mean = plane == 0 && p.key_mean != nullptr;
@@ -467,199 +473,152 @@ __global__ __launch_bounds__(kMfmaThreads) void quantize_mfma_kernel(QuantizePar
 
     const int64_t block_first = (int64_t)blockIdx.x * block_tokens;
     const int64_t block_end = block_first + block_tokens < p.tokens ? block_first + block_tokens : p.tokens;
-    uint32_t* stage = stage_lds[wave];
-    uint16_t* stage16 = reinterpret_cast<uint16_t*>(stage);
-    float* transpose = reinterpret_cast<float*>(stage);
-    // Loader role: token `load_token` (lane % 16), record `load_record` (lane / 16).
-    const int load_token = lane64 & 15;
-    const int load_record = lane64 >> 4;
-    // MFMA A role: token lane % 16.
-    const int mfma_token = lane64 & 15;
+    constexpr int64_t kStride = (int64_t)kMfmaWaves * kMfmaTokens;
+    float* transpose = transpose_lds[wave];
 
-    for (int64_t first = block_first + wave * kMfmaTokens; first < block_end;
-         first += kMfmaWaves * kMfmaTokens) {
-        // Slots of the pass's 16 tokens, loaded before any of its stores so
-        // that waiting for them never waits for this pass's scattered writes
-        // (vmcnt counts loads and stores in issue order).
-        int64_t pass_slot = -1;
-        if (lane64 < kMfmaTokens && first + lane64 < block_end) pass_slot = p.slots[first + lane64];
-        F32x16 acc[R][2];
+    // A-operand role: row lane % 16 = (token, record slot).
+    const int a_token = (lane64 & 15) >> 2;
+    const int a_slot = lane64 & 3;
+    const int a_record = a_slot < R ? a_slot : 0;
+    const uint16_t* a_base = nullptr;
+    int64_t a_stride = 0;
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+        if (a_record == r) {
+            a_base = (plane == 0 ? p.key_ptrs[r] : p.value_ptrs[r]) + head * D;
+            a_stride = plane == 0 ? p.key_strides[r] : p.value_strides[r];
+        }
+    auto a_row = [&](int64_t first) {
+        const int64_t n = first + a_token < block_end ? first + a_token : block_end - 1;
+        return a_base + n * a_stride;
+    };
+    // Rows are only guaranteed 8-byte aligned: 8-byte loads.
+    auto load_chunk = [&](uint2 (&buffer)[kLoads], const uint16_t* row, int chunk) {
+#pragma unroll
+        for (int e = 0; e < kLoads; ++e) buffer[e] = reinterpret_cast<const uint2*>(row + chunk * C)[e];
+    };
+    const float4* rotation4 = reinterpret_cast<const float4*>(rotation_lds) + lane64;
+
+    int64_t first = block_first + wave * kMfmaTokens;
+    uint2 input[2][kLoads];
+    const uint16_t* row = nullptr;
+    if (rotation != nullptr && first < block_end) {
+        row = a_row(first);
+        load_chunk(input[0], row, 0);
+    }
+    for (; first < block_end; first += kStride) {
+        const int64_t n = first + q;
+        const int64_t slot = n < block_end ? p.slots[n] : -1;
+        F32x16 acc[2];
         if (rotation != nullptr) {
+            acc[0] = acc[1] = F32x16{};
+            const bool more_passes = first + kStride < block_end;
 #pragma unroll
-            for (int r = 0; r < R; ++r) acc[r][0] = acc[r][1] = F32x16{};
-            const int64_t n_load = first + load_token < block_end ? first + load_token : block_end - 1;
-            const uint16_t* row = nullptr;
-            if (load_record < R)
-                row = (plane == 0 ? p.key_ptrs[load_record] + n_load * p.key_strides[load_record]
-                                  : p.value_ptrs[load_record] + n_load * p.value_strides[load_record]) +
-                      head * D;
-            // Rows are only guaranteed 8-byte aligned: 8 loads of 8 bytes per 32-k chunk.
-            uint2 incoming[kChunk / 4];
-            auto load_chunk = [&](int chunk) {
-#pragma unroll
-                for (int e = 0; e < kChunk / 4; ++e)
-                    incoming[e] = reinterpret_cast<const uint2*>(row + chunk * kChunk)[e];
-            };
-            auto stage_chunk = [&](int buffer) {
-                uint16_t* dst = stage16 + ((buffer * kChunk) * kMfmaTokens + load_token) * kStageRecords + load_record;
-#pragma unroll
-                for (int e = 0; e < kChunk / 4; ++e) {
-                    const uint32_t w[2] = {incoming[e].x, incoming[e].y};
-#pragma unroll
-                    for (int q = 0; q < 4; ++q)
-                        dst[(4 * e + q) * kMfmaTokens * kStageRecords] =
-                            (uint16_t)((q & 1) ? (w[q >> 1] >> 16) : (w[q >> 1] & 0xffffu));
+            for (int chunk = 0; chunk < kChunks; ++chunk) {
+                uint2 (&current)[kLoads] = input[chunk & 1];
+                uint2 (&next)[kLoads] = input[(chunk + 1) & 1];
+                if (chunk + 1 < kChunks) {
+                    load_chunk(next, row, chunk + 1);
+                } else if (more_passes) {
+                    // kChunks is even: the next pass's chunk 0 lands in input[0].
+                    row = a_row(first + kStride);
+                    load_chunk(next, row, 0);
                 }
-            };
-            if (load_record < R) {
-                load_chunk(0);
-                stage_chunk(0);
-            }
-            const float* rotation_half0 = rotation_lds + lane64;
-            const bool half1_ok = 64 + lane64 < D;
-            const float* rotation_half1 = rotation_lds + (half1_ok ? 64 + lane64 : 0);
-            auto read_x = [&](int buffer, int k) {
-                return *reinterpret_cast<const uint2*>(stage16 +
-                                                       ((buffer * kChunk + k) * kMfmaTokens + mfma_token) *
-                                                           kStageRecords);
-            };
-#pragma unroll 1
-            for (int chunk = 0; chunk < D / kChunk; ++chunk) {
-                const bool more = chunk + 1 < D / kChunk;
-                if (more && load_record < R) load_chunk(chunk + 1);
-                const int buffer = chunk & 1;
-                const int k0 = chunk * kChunk;
-                uint2 xv = read_x(buffer, 0);
-                float b0 = rotation_half0[k0 * D];
-                float b1 = half1_ok ? rotation_half1[k0 * D] : 0.f;
-#pragma unroll 8
-                for (int k = 0; k < kChunk; ++k) {
-                    const int next = k + 1 < kChunk ? k + 1 : k;
-                    const uint2 xn = read_x(buffer, next);
-                    const float bn0 = rotation_half0[(k0 + next) * D];
-                    const float bn1 = half1_ok ? rotation_half1[(k0 + next) * D] : 0.f;
-                    __builtin_amdgcn_sched_barrier(0);
-                    const float xs[4] = {__uint_as_float(xv.x << 16), __uint_as_float(xv.x & 0xffff0000u),
-                                         __uint_as_float(xv.y << 16), __uint_as_float(xv.y & 0xffff0000u)};
 #pragma unroll
-                    for (int r = 0; r < R; ++r) {
-                        acc[r][0] = __builtin_amdgcn_mfma_f32_16x16x1f32(xs[r], b0, acc[r][0], 0, 0, 0);
-                        acc[r][1] = __builtin_amdgcn_mfma_f32_16x16x1f32(xs[r], b1, acc[r][1], 0, 0, 0);
-                    }
-                    xv = xn;
-                    b0 = bn0;
-                    b1 = bn1;
+                for (int pair = 0; pair < C / 2; ++pair) {
+                    const float4 b = rotation4[((chunk * C) / 2 + pair) * 64];
+                    const uint32_t word = (pair & 1) ? current[pair >> 1].y : current[pair >> 1].x;
+                    const float a0 = __uint_as_float(word << 16);
+                    const float a1 = __uint_as_float(word & 0xffff0000u);
+                    acc[0] = __builtin_amdgcn_mfma_f32_16x16x1f32(a0, b.x, acc[0], 0, 0, 0);
+                    acc[1] = __builtin_amdgcn_mfma_f32_16x16x1f32(a0, b.y, acc[1], 0, 0, 0);
+                    acc[0] = __builtin_amdgcn_mfma_f32_16x16x1f32(a1, b.z, acc[0], 0, 0, 0);
+                    acc[1] = __builtin_amdgcn_mfma_f32_16x16x1f32(a1, b.w, acc[1], 0, 0, 0);
                 }
-                // The stage is private to this wave and its LDS operations
-                // complete in order; the compiler barriers keep the writes
-                // after this chunk's reads.
-                __asm__ volatile("" ::: "memory");
-                if (more && load_record < R) stage_chunk((chunk + 1) & 1);
-                __asm__ volatile("" ::: "memory");
             }
         }
 
-        // Commit: four rounds of four tokens, 16 lanes per token.
-#pragma unroll 1
-        for (int round = 0; round < kMfmaTokens / 4; ++round) {
-            float x[R][2][4];
-            const int token_in_round = lane64 >> 4;
-            const int64_t n = first + 4 * round + token_in_round;
+        const bool valid = n < block_end && slot >= 0 && slot / p.page_tokens < p.num_blocks;
+        uint8_t* page = nullptr;
+        int token = 0;
+        if (valid) {
+            const int64_t block = slot / p.page_tokens;
+            token = (int)(slot % p.page_tokens);
+            page = p.cache + plane * p.plane_stride + (block * p.heads + head) * (int64_t)p.page_tokens * p.page_width;
+        }
+        uint32_t reference[2][4] = {{0u, 0u, 0u, 0u}, {0u, 0u, 0u, 0u}};
+        // Anchor first, then every other record ascending (kernel.cuh:321-329).
+#pragma unroll
+        for (int step = 0; step < R; ++step) {
+            const int r = step == 0 ? A : (step - 1 < A ? step - 1 : step);
+            const bool is_anchor = r == A;
+            float x[2][4];
             if (rotation != nullptr) {
-                // Lanes holding this round's tokens write [record][channel][4 tokens].
+                // The transpose is private to this wave and its LDS operations
+                // complete in order; the compiler barriers keep this record's
+                // writes after the previous record's reads.
                 __asm__ volatile("" ::: "memory");
-                if ((lane64 >> 4) == round) {
 #pragma unroll
-                    for (int r = 0; r < R; ++r)
+                for (int h = 0; h < 2; ++h)
 #pragma unroll
-                        for (int h = 0; h < 2; ++h)
+                    for (int b = 0; b < 4; ++b)
+                        if (64 * h + 16 * b < D) transpose[q * kTransposeStride + 64 * h + 16 * b + j] = acc[h][4 * b + r];
+                __asm__ volatile("" ::: "memory");
 #pragma unroll
-                            for (int b = 0; b < 4; ++b) {
-                                const int channel = 64 * h + 16 * b + (lane64 & 15);
-                                *reinterpret_cast<float4*>(transpose + (r * 128 + channel) * 4) =
-                                    make_float4(acc[r][h][4 * b], acc[r][h][4 * b + 1], acc[r][h][4 * b + 2],
-                                                acc[r][h][4 * b + 3]);
-                            }
+                for (int h = 0; h < 2; ++h) {
+                    float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+                    if (active[h]) v = *reinterpret_cast<const float4*>(transpose + q * kTransposeStride + column[h]);
+                    x[h][0] = v.x; x[h][1] = v.y; x[h][2] = v.z; x[h][3] = v.w;
                 }
-                __asm__ volatile("" ::: "memory");
-#pragma unroll
-                for (int r = 0; r < R; ++r)
-#pragma unroll
-                    for (int h = 0; h < 2; ++h)
-#pragma unroll
-                        for (int i = 0; i < 4; ++i)
-                            x[r][h][i] = active[h] ? transpose[(r * 128 + column[h] + i) * 4 + token_in_round] : 0.f;
                 __asm__ volatile("" ::: "memory");
             } else {
                 const int64_t nn = n < block_end ? n : block_end - 1;
-#pragma unroll
-                for (int r = 0; r < R; ++r) {
-                    const uint16_t* src = (plane == 0 ? p.key_ptrs[r] + nn * p.key_strides[r]
-                                                      : p.value_ptrs[r] + nn * p.value_strides[r]) + head * D;
-#pragma unroll
-                    for (int h = 0; h < 2; ++h) {
-                        uint2 v = make_uint2(0, 0);
-                        if (active[h]) v = *reinterpret_cast<const uint2*>(src + column[h]);
-                        x[r][h][0] = bf16_f32(v.x & 0xffffu);
-                        x[r][h][1] = bf16_f32(v.x >> 16);
-                        x[r][h][2] = bf16_f32(v.y & 0xffffu);
-                        x[r][h][3] = bf16_f32(v.y >> 16);
-                    }
-                }
-            }
-
-            const int source_lane = 4 * round + token_in_round;
-            const int64_t slot = (int64_t)(((uint64_t)(uint32_t)__shfl((int)(uint32_t)pass_slot, source_lane)) |
-                                           ((uint64_t)(uint32_t)__shfl((int)((uint64_t)pass_slot >> 32), source_lane)
-                                            << 32));
-            const bool valid = n < block_end && slot >= 0 && slot / p.page_tokens < p.num_blocks;
-            uint8_t* page = nullptr;
-            int token = 0;
-            if (valid) {
-                const int64_t block = slot / p.page_tokens;
-                token = (int)(slot % p.page_tokens);
-                page = p.cache + plane * p.plane_stride +
-                       (block * p.heads + head) * (int64_t)p.page_tokens * p.page_width;
-            }
-            uint32_t reference[2][4] = {{0u, 0u, 0u, 0u}, {0u, 0u, 0u, 0u}};
-            // Anchor first, then every other record ascending (kernel.cuh:321-329).
-#pragma unroll
-            for (int step = 0; step < R; ++step) {
-                const int r = step == 0 ? A : (step - 1 < A ? step - 1 : step);
-                const bool is_anchor = r == A;
-                float mean[2][4];
+                const uint16_t* src = (plane == 0 ? p.key_ptrs[r] + nn * p.key_strides[r]
+                                                  : p.value_ptrs[r] + nn * p.value_strides[r]) + head * D;
 #pragma unroll
                 for (int h = 0; h < 2; ++h) {
-                    float4 m = make_float4(0.f, 0.f, 0.f, 0.f);
-                    if (has_mean && active[h]) m = *reinterpret_cast<const float4*>(&mean_lds[r * D + column[h]]);
-                    mean[h][0] = m.x; mean[h][1] = m.y; mean[h][2] = m.z; mean[h][3] = m.w;
+                    uint2 v = make_uint2(0, 0);
+                    if (active[h]) v = *reinterpret_cast<const uint2*>(src + column[h]);
+                    x[h][0] = bf16_f32(v.x & 0xffffu);
+                    x[h][1] = bf16_f32(v.x >> 16);
+                    x[h][2] = bf16_f32(v.y & 0xffffu);
+                    x[h][3] = bf16_f32(v.y >> 16);
                 }
-                commit_record(x[r], active, is_anchor, is_anchor || p.adjacent, p.coefficient, mean, has_mean,
-                              reference, p.region[r], page, token, p.page_tokens, j, valid, inverse_scale);
             }
+            float mean[2][4];
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                float4 m = make_float4(0.f, 0.f, 0.f, 0.f);
+                if (has_mean && active[h]) m = *reinterpret_cast<const float4*>(&mean_lds[r * D + column[h]]);
+                mean[h][0] = m.x; mean[h][1] = m.y; mean[h][2] = m.z; mean[h][3] = m.w;
+            }
+            commit_record(x, active, is_anchor, is_anchor || p.adjacent, p.coefficient, mean, has_mean, reference,
+                          p.region[r], page, token, p.page_tokens, j, valid, inverse_scale);
         }
     }
 }
 
 template <int D, int R, int A>
 hipError_t launch_quantize_mfma(const QuantizeParams& p, hipStream_t stream) {
-    // A workgroup pass covers 128 tokens of one (head, plane); long calls give
-    // each workgroup several passes (one workgroup per CU fits the LDS).
-    const int64_t per_pass = kMfmaWaves * kMfmaTokens;
-    const int64_t work = (p.tokens + per_pass - 1) / per_pass * p.heads * 2;
-    int64_t passes = work / 256;
-    passes = passes < 1 ? 1 : (passes > 8 ? 8 : passes);
-    const int block_tokens = (int)(per_pass * passes);
+    // One workgroup per CU fits the LDS: split each (head, plane)'s tokens
+    // over as many workgroups as make one round on the CUs, in whole passes
+    // of kMfmaTokens per wave.
+    const int64_t pairs = (int64_t)p.heads * 2;
+    int64_t per_pair = p.compute_units > 0 ? p.compute_units / pairs : 1;
+    per_pair = per_pair < 1 ? 1 : per_pair;
+    int64_t block_tokens = (p.tokens + per_pair - 1) / per_pair;
+    block_tokens = (block_tokens + kMfmaTokens - 1) / kMfmaTokens * kMfmaTokens;
+    block_tokens = block_tokens < (1 << 24) ? block_tokens : (1 << 24);
     const dim3 grid((unsigned)((p.tokens + block_tokens - 1) / block_tokens), (unsigned)p.heads, 2);
-    hipLaunchKernelGGL((quantize_mfma_kernel<D, R, A>), grid, dim3(kMfmaThreads), 0, stream, p, block_tokens);
+    hipLaunchKernelGGL((quantize_mfma_kernel<D, R, A>), grid, dim3(kMfmaThreads), 0, stream, p, (int)block_tokens);
     return hipGetLastError();
 }
 
-// Below this many tokens a call is latency-bound (a 16-token MFMA tile per
-// wave leaves most waves idle and its k loop is longer than the VALU one), so
-// the VALU kernel runs: 28 vs 46 us at 32 tokens, equal at 1024, MFMA ahead
-// by 8% at 4096 and 4% at 16384 (one MI355X, C1 shapes).
-constexpr int64_t kMfmaMinTokens = 2048;
+// From this many tokens the matrix-core kernel runs (one MI355X, C1 shapes,
+// median call after a settle phase): 26.7 vs 36.9 us at 128 tokens, 25.0 vs
+// 37.3 us at 256, within 3% either way from 512 to 2048.  Decode-step calls
+// (a few tokens) keep the VALU kernel.
+constexpr int64_t kMfmaMinTokens = 64;
 
 template <int D, int R, int A>
 hipError_t launch_quantize_kernel(const QuantizeParams& p, hipStream_t stream) {

@@ -22,6 +22,7 @@ MEAN_ABS = 1e-3
 
 QUANTIZE_CASES = [
     # tokens, heads, dim, records, page_tokens, mode, anchor, coefficient, rotation, mean, skipped
+    # (calls of fewer than 64 tokens run the VALU kernel, 64 and more the matrix-core one)
     (37, 4, 128, OURO_G32, 16, "anchor", 3, "ls", True, True, 3),
     (20, 3, 128, OURO_G16, 16, "anchor", 3, "ls", True, False, 0),
     (19, 5, 96, OURO_G16, 16, "anchor", 3, "ls", True, True, 2),
@@ -29,13 +30,16 @@ QUANTIZE_CASES = [
     (9, 2, 128, ((2, 32),), 16, "anchor", 0, "unit", True, True, 0),
     (17, 2, 128, ((4, 32),) * 4, 16, "anchor", 3, "unit", False, False, 0),
     (25, 3, 96, ((2, 32),) * 4, 32, "anchor", 0, "ls", True, False, 4),
-    (64, 2, 128, ((4, 16), (2, 16)), 16, "adjacent", 0, "ls", True, True, 0),
+    (64, 2, 128, ((4, 16), (2, 16)), 16, "adjacent", 0, "ls", True, True, 0),  # the first MFMA-kernel size
+    (63, 2, 128, OURO_G32, 16, "anchor", 3, "ls", True, True, 1),  # the last VALU-kernel size
     (300, 4, 128, OURO_G32, 16, "anchor", 3, "norm", True, True, 7),
-    # 2048 tokens and more run the matrix-core rotation kernel.
     (2100, 2, 128, OURO_G32, 16, "anchor", 3, "ls", True, True, 5),
     (2048, 2, 96, OURO_G16, 16, "anchor", 3, "ls", True, True, 3),
     (2053, 1, 128, ((4, 32), (2, 32), (2, 32), (2, 32)), 32, "adjacent", 0, "norm", True, False, 1),
     (2049, 1, 128, ((4, 32), (2, 16)), 16, "anchor", 0, "unit", False, True, 2),
+    (2050, 1, 96, ((2, 16), (4, 32), (2, 32)), 16, "anchor", 1, "ls", True, True, 3),
+    (2048, 1, 128, ((4, 32),), 32, "anchor", 0, "unit", True, False, 0),
+    (6000, 1, 128, OURO_G16, 16, "adjacent", 0, "ls", True, True, 9),  # many passes per wave
 ]
 
 
