@@ -289,6 +289,7 @@ int rq_quantize(int records, const void* const* key_ptrs, const int64_t* key_str
     // A single-record group is always its own anchor (dispatch/schedules.cuh:99-111).
     p.adjacent = records > 1 && reference_mode == RQ_MODE_ADJACENT;
     p.coefficient = coefficient;
+    p.page_shift = page_tokens == 32 ? 5 : 4;
     p.compute_units = compute_units();
     fill_regions(head_dim, records, bits, groups, page_tokens, p.region);
     return check_launch(rq::launch_quantize(p, head_dim, stream), "quantize launch");

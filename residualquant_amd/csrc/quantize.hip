@@ -32,7 +32,7 @@
 //    wave as FP32 in a double-buffered LDS chunk of 32 k.
 //  - commit: the xor-16 level of the butterfly is the in-lane sum of the two
 //    canonical lanes, the other levels and the group min/max run across the
-//    16 lanes of the token with DPP and ds_swizzle.
+//    16 lanes of the token with DPP.
 #include "rq_device.h"
 #include "rq_kernels.h"
 
@@ -50,28 +50,28 @@ constexpr int kStageRecords = 4;  // record slots per staged (token, k)
 
 // ---------------------------------------------------------------- lanes
 
-template <int Distance>
-__device__ __forceinline__ float swizzle_xor(float v) {
-    // ds_swizzle bit mode inside 32 lanes: and 0x1f, or 0, xor Distance.
-    return __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(v), 0x1f | (Distance << 10)));
-}
-
 template <int Control>
 __device__ __forceinline__ float dpp(float v) {
     return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), Control, 0xf, 0xf, false));
 }
 
-constexpr int kXor1 = 0xB1;   // quad_perm [1,0,3,2]
-constexpr int kXor2 = 0x4E;   // quad_perm [2,3,0,1]
-constexpr int kXor8 = 0x128;  // row_ror:8 inside 16 lanes
+constexpr int kXor1 = 0xB1;        // quad_perm [1,0,3,2]
+constexpr int kXor2 = 0x4E;        // quad_perm [2,3,0,1]
+constexpr int kRor4 = 0x124;       // row_ror:4 inside 16 lanes
+constexpr int kXor8 = 0x128;       // row_ror:8 inside 16 lanes
+constexpr int kHalfMirror = 0x141;  // row_half_mirror: lane 7 - i inside each 8 lanes
 
 // The xor butterfly of kernel.cuh:15-20 over the 32 canonical partials, given
 // this lane's two (canonical lanes j and j + 16): the distance-16 level is
 // their in-lane sum, distances 8, 4, 2, 1 pair lanes j ^ d of the token.
+// After the distance-8 level lane j and j ^ 8 hold the same sum (a + b is
+// b + a), so the 16 lanes repeat with period 8 and row_ror:4 brings lane
+// j ^ 4's value: the same operands in the same order as an xor-4 exchange,
+// without an LDS round trip.
 __device__ __forceinline__ float butterfly_sum(float low, float high) {
     float v = low + high;
     v += dpp<kXor8>(v);
-    v += swizzle_xor<4>(v);
+    v += dpp<kRor4>(v);
     v += dpp<kXor2>(v);
     v += dpp<kXor1>(v);
     return v;
@@ -108,26 +108,38 @@ __device__ __forceinline__ float e4m3_value(uint32_t code) {
 // TwoSum; the residual chain of adjacent mode keeps it.
 __device__ __forceinline__ void commit_record(float (&x)[2][4], const bool (&active)[2], bool is_anchor,
                                               bool restore, int coefficient, const float (&mean)[2][4],
-                                              bool has_mean, uint32_t (&reference)[2][4],
+                                              bool has_mean, float (&reference)[2][4],
                                               const RecordRegion& region, uint8_t* page, int token,
                                               int page_tokens, int j, bool store, const float* inverse_scale) {
     float previous[2][4];
 #pragma unroll
     for (int h = 0; h < 2; ++h)
 #pragma unroll
-        for (int i = 0; i < 4; ++i) previous[h][i] = (!is_anchor && active[h]) ? bf16_f32(reference[h][i]) : 0.f;
+        for (int i = 0; i < 4; ++i) previous[h][i] = (!is_anchor && active[h]) ? reference[h][i] : 0.f;
 
     float alpha = 1.0f;
     if (!is_anchor && coefficient != RQ_COEF_UNIT_) {
         float numerator[2] = {0.f, 0.f}, denominator[2] = {0.f, 0.f};
+        // Norm: sum x^2; LS: sum x * previous.  The empty asm keeps this a
+        // uniform branch: speculated, both chains would run plus a select.
+        if (coefficient == RQ_COEF_NORM_) {
+            __asm__ volatile("");
 #pragma unroll
-        for (int h = 0; h < 2; ++h)
+            for (int h = 0; h < 2; ++h)
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                numerator[h] = coefficient == RQ_COEF_NORM_ ? fmaf(x[h][i], x[h][i], numerator[h])
-                                                            : fmaf(x[h][i], previous[h][i], numerator[h]);
-                denominator[h] = fmaf(previous[h][i], previous[h][i], denominator[h]);
-            }
+                for (int i = 0; i < 4; ++i) {
+                    numerator[h] = fmaf(x[h][i], x[h][i], numerator[h]);
+                    denominator[h] = fmaf(previous[h][i], previous[h][i], denominator[h]);
+                }
+        } else {
+#pragma unroll
+            for (int h = 0; h < 2; ++h)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    numerator[h] = fmaf(x[h][i], previous[h][i], numerator[h]);
+                    denominator[h] = fmaf(previous[h][i], previous[h][i], denominator[h]);
+                }
+        }
         const float num = butterfly_sum(numerator[0], numerator[1]);
         const float den = butterfly_sum(denominator[0], denominator[1]);
         if (coefficient == RQ_COEF_NORM_)
@@ -140,22 +152,34 @@ __device__ __forceinline__ void commit_record(float (&x)[2][4], const bool (&act
 
     const int bits = region.bits;
     const float levels = bits == 2 ? 3.0f : 15.0f;
+    const float inverse_levels = bits == 2 ? 1.0f / 3.0f : 1.0f / 15.0f;  // RN(1/levels)
+    const float clip = bits == 2 ? 0.9f : 1.0f;
     uint32_t packed[2];
     uint32_t parameters[2];
+    if (!is_anchor)
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) x[h][i] = fmaf(-previous[h][i], alpha, x[h][i]);
+    if (has_mean) {
+        __asm__ volatile("");  // a uniform branch, not a speculated select
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) x[h][i] = x[h][i] - mean[h][i];
+    }
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            if (!is_anchor) x[h][i] = fmaf(-previous[h][i], alpha, x[h][i]);
-            if (has_mean) x[h][i] = x[h][i] - mean[h][i];
-        }
         float low = fmin_z(fmin_z(x[h][0], x[h][1]), fmin_z(x[h][2], x[h][3]));
         float high = fmax_z(fmax_z(x[h][0], x[h][1]), fmax_z(x[h][2], x[h][3]));
         // A group spans 4 canonical lanes (G16) or 8 (G32), all with the same h;
         // idle canonical lanes (head_dim 96) form groups of their own.
+        // min_z/max_z are exact, commutative and associative, so any exchange
+        // that covers the group's lanes gives the same result: the mirror
+        // pairs lanes i and 7 - i of the 8, the quad levels finish it.
         if (region.group == 32) {
-            low = fmin_z(low, swizzle_xor<4>(low));
-            high = fmax_z(high, swizzle_xor<4>(high));
+            low = fmin_z(low, dpp<kHalfMirror>(low));
+            high = fmax_z(high, dpp<kHalfMirror>(high));
         }
         low = fmin_z(low, dpp<kXor2>(low));
         high = fmax_z(high, dpp<kXor2>(high));
@@ -163,10 +187,17 @@ __device__ __forceinline__ void commit_record(float (&x)[2][4], const bool (&act
         high = fmax_z(high, dpp<kXor1>(high));
 
         const float center = (low + high) * 0.5f;
-        const float radius = bits == 2 ? ((high - low) * 0.9f) * 0.5f : (high - low) * 0.5f;
-        parameters[h] = e4m3_pair(center - radius, (2.0f * radius) / levels);
-        const float offset = e4m3_value(parameters[h] & 0xffu);
-        const float scale = e4m3_value(parameters[h] >> 8);
+        // (high - low) * 0.9 * 0.5 for INT2, (high - low) * 0.5 for INT4 (x * 1 is exact).
+        const float radius = ((high - low) * clip) * 0.5f;
+        // (2 radius) / levels through y = RN(1/levels): q = RN(q0 + RN(v - q0 levels) y),
+        // q0 = RN(v y), equals the IEEE quotient (checked exhaustively over every
+        // binade with subnormal parts, three scale-invariant binades and the top five).
+        const float width = 2.0f * radius;
+        const float q0 = width * inverse_levels;
+        const float step = fmaf(fmaf(-q0, levels, width), inverse_levels, q0);
+        parameters[h] = e4m3_pair(center - radius, step);
+        const float offset = __builtin_amdgcn_cvt_f32_fp8((int)parameters[h], 0);
+        const float scale = __builtin_amdgcn_cvt_f32_fp8((int)parameters[h], 1);
         // RN(1/scale); 0 for a zero (or NaN) scale, which yields code 0.
         const float reciprocal = inverse_scale[(parameters[h] >> 8) & 0x7fu];
 
@@ -184,8 +215,8 @@ __device__ __forceinline__ void commit_record(float (&x)[2][4], const bool (&act
             if (restore) {
                 uint32_t value = bf16_rn(fmaf((float)code, scale, offset));
                 if (has_mean) value = bf16_rn(bf16_f32(value) + bf16_f32(bf16_rn(mean[h][i])));
-                if (!is_anchor) value = bf16_fma_rn(bf16_f32(reference[h][i]), alpha, bf16_f32(value));
-                reference[h][i] = value;
+                if (!is_anchor) value = bf16_fma_rn(reference[h][i], alpha, bf16_f32(value));
+                reference[h][i] = bf16_f32(value);
             }
         }
     }
@@ -371,16 +402,16 @@ __global__ __launch_bounds__(kQuantizeThreads) void quantize_kernel(QuantizePara
         const int64_t n = first + group;
         int64_t slot = -1;
         if (n < block_end) slot = p.slots[n];
-        const bool valid = slot >= 0 && slot / p.page_tokens < p.num_blocks;
+        const bool valid = slot >= 0 && (slot >> p.page_shift) < p.num_blocks;
         uint8_t* page = nullptr;
         int token = 0;
         if (valid) {
-            const int64_t block = slot / p.page_tokens;
-            token = (int)(slot % p.page_tokens);
+            const int64_t block = slot >> p.page_shift;
+            token = (int)(slot & (p.page_tokens - 1));
             page = p.cache + plane * p.plane_stride + (block * p.heads + head) * (int64_t)p.page_tokens * p.page_width;
         }
 
-        uint32_t reference[2][4] = {{0u, 0u, 0u, 0u}, {0u, 0u, 0u, 0u}};
+        float reference[2][4] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};  // restored BF16 values
         // Anchor first, then every other record ascending (kernel.cuh:321-329).
 #pragma unroll
         for (int step = 0; step < R; ++step) {
@@ -408,7 +439,7 @@ __global__ __launch_bounds__(kQuantizeThreads) void quantize_kernel(QuantizePara
 //
 // One wave rotates 4 tokens per pass.  The 16 rows of the MFMA are the
 // (token, record slot) pairs of those tokens, row 4 token + slot, so a pass
-// keeps 32 accumulator registers and 12 waves (3 per SIMD) fit a CU: while
+// keeps 32 accumulator registers and 16 waves (4 per SIMD) fit a CU: while
 // some waves run their k loop on the matrix core, others commit on the VALU.
 // MFMA (half h) takes A = x[row l % 16][k] (the same value in all 4 blocks)
 // and B = R[k][64 h + l]; accumulator register i of lane l then holds token
@@ -422,7 +453,7 @@ __global__ __launch_bounds__(kQuantizeThreads) void quantize_kernel(QuantizePara
 // flight during the commit.  The rotation sits in LDS as FP32
 // [k / 2][lane][R[k][l], R[k][64 + l], R[k + 1][l], R[k + 1][64 + l]], one
 // 16-byte read per two k steps.
-constexpr int kMfmaWaves = 12;
+constexpr int kMfmaWaves = 16;
 constexpr int kMfmaThreads = 64 * kMfmaWaves;
 constexpr int kMfmaTokens = 4;        // tokens per wave per pass
 constexpr int kTransposeStride = 144;  // floats per token row of the transpose: 16 q + j spreads the banks
@@ -432,18 +463,19 @@ typedef float F32x16 __attribute__((ext_vector_type(16)));
 template <int D>
 constexpr int kInputChunk = 16;  // an even number of chunks per row at D = 96 and 128
 
-template <int D, int R, int A>
-__global__ __launch_bounds__(kMfmaThreads) void quantize_mfma_kernel(QuantizeParams p, int block_tokens) {
+template <int D, int R, int A, bool Rotated>
+__global__ __launch_bounds__(kMfmaThreads) void quantize_mfma_kernel(QuantizeParams p, int block_tokens,
+                                                                     int plane_first) {
     static_assert(R <= 4, "four record slots per token");
     constexpr int C = kInputChunk<D>;
     constexpr int kChunks = D / C;
     constexpr int kLoads = C / 4;  // 8-byte loads per chunk
-    __shared__ __attribute__((aligned(16))) float rotation_lds[D * 128];
-    __shared__ __attribute__((aligned(16))) float transpose_lds[kMfmaWaves][kMfmaTokens * kTransposeStride];
-    __shared__ __attribute__((aligned(16))) float mean_lds[R * D];
     __shared__ float inverse_scale[128];
+    __shared__ __attribute__((aligned(16))) float mean_lds[R * D];
+    __shared__ __attribute__((aligned(16))) float transpose_lds[kMfmaWaves][kMfmaTokens * kTransposeStride];
+    __shared__ __attribute__((aligned(16))) float rotation_lds[D * 128];
 
-    const int plane = blockIdx.z;
+    const int plane = plane_first + (int)blockIdx.z;
     const int head = blockIdx.y;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int lane64 = threadIdx.x & 63;
@@ -452,8 +484,8 @@ __global__ __launch_bounds__(kMfmaThreads) void quantize_mfma_kernel(QuantizePar
     const bool active[2] = {4 * j < D, 4 * (j + 16) < D};
     const int column[2] = {4 * j, active[1] ? 64 + 4 * j : 64};
 
-    const uint16_t* rotation = plane == 0 ? p.key_rotation : p.value_rotation;
-    if (rotation != nullptr) {
+    if constexpr (Rotated) {
+        const uint16_t* rotation = plane == 0 ? p.key_rotation : p.value_rotation;
         const uint16_t* source = rotation + (int64_t)head * D * D;
         for (int i = threadIdx.x; i < D * 128; i += kMfmaThreads) {
             const int k = i >> 7, c = i & 127;
@@ -499,31 +531,46 @@ __global__ __launch_bounds__(kMfmaThreads) void quantize_mfma_kernel(QuantizePar
     };
     const float4* rotation4 = reinterpret_cast<const float4*>(rotation_lds) + lane64;
 
+    // The slot of this lane's token of the pass starting at `f` (-1 past the block).
+    auto load_slot = [&](int64_t f) {
+        const bool inside = f + q < block_end;
+        const int64_t slot = p.slots[inside ? f + q : block_end - 1];
+        return inside ? slot : (int64_t)-1;
+    };
+
     int64_t first = block_first + wave * kMfmaTokens;
     uint2 input[2][kLoads];
     const uint16_t* row = nullptr;
-    if (rotation != nullptr && first < block_end) {
+    int64_t next_slot = -1;
+    if (Rotated && first < block_end) {
         row = a_row(first);
         load_chunk(input[0], row, 0);
+        next_slot = load_slot(first);
     }
     for (; first < block_end; first += kStride) {
         const int64_t n = first + q;
-        const int64_t slot = n < block_end ? p.slots[n] : -1;
+        // Rotated passes take the slot prefetched with their first chunk.
+        const int64_t slot = Rotated ? next_slot : load_slot(first);
         F32x16 acc[2];
-        if (rotation != nullptr) {
+        if constexpr (Rotated) {
             acc[0] = acc[1] = F32x16{};
-            const bool more_passes = first + kStride < block_end;
 #pragma unroll
             for (int chunk = 0; chunk < kChunks; ++chunk) {
                 uint2 (&current)[kLoads] = input[chunk & 1];
                 uint2 (&next)[kLoads] = input[(chunk + 1) & 1];
                 if (chunk + 1 < kChunks) {
                     load_chunk(next, row, chunk + 1);
-                } else if (more_passes) {
-                    // kChunks is even: the next pass's chunk 0 lands in input[0].
+                } else {
+                    // The next pass's chunk 0 (into input[0]: kChunks is even),
+                    // issued on the last pass too (a_row clamps it to a row of
+                    // the block) so that no branch joins the load counters.
                     row = a_row(first + kStride);
                     load_chunk(next, row, 0);
+                    next_slot = load_slot(first + kStride);
                 }
+                // Keeps the loads here: left alone, the compiler sinks each
+                // one to its first use and every chunk waits a full round trip.
+                __asm__ volatile("" ::: "memory");
 #pragma unroll
                 for (int pair = 0; pair < C / 2; ++pair) {
                     const float4 b = rotation4[((chunk * C) / 2 + pair) * 64];
@@ -535,25 +582,28 @@ __global__ __launch_bounds__(kMfmaThreads) void quantize_mfma_kernel(QuantizePar
                     acc[0] = __builtin_amdgcn_mfma_f32_16x16x1f32(a1, b.z, acc[0], 0, 0, 0);
                     acc[1] = __builtin_amdgcn_mfma_f32_16x16x1f32(a1, b.w, acc[1], 0, 0, 0);
                 }
+                // Nothing of the next chunk moves above this chunk's MFMAs,
+                // so the loads issued at its start have the chunk to land.
+                __builtin_amdgcn_sched_barrier(0);
             }
         }
 
-        const bool valid = n < block_end && slot >= 0 && slot / p.page_tokens < p.num_blocks;
+        const bool valid = n < block_end && slot >= 0 && (slot >> p.page_shift) < p.num_blocks;
         uint8_t* page = nullptr;
         int token = 0;
         if (valid) {
-            const int64_t block = slot / p.page_tokens;
-            token = (int)(slot % p.page_tokens);
+            const int64_t block = slot >> p.page_shift;
+            token = (int)(slot & (p.page_tokens - 1));
             page = p.cache + plane * p.plane_stride + (block * p.heads + head) * (int64_t)p.page_tokens * p.page_width;
         }
-        uint32_t reference[2][4] = {{0u, 0u, 0u, 0u}, {0u, 0u, 0u, 0u}};
+        float reference[2][4] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};  // restored BF16 values
         // Anchor first, then every other record ascending (kernel.cuh:321-329).
 #pragma unroll
         for (int step = 0; step < R; ++step) {
             const int r = step == 0 ? A : (step - 1 < A ? step - 1 : step);
             const bool is_anchor = r == A;
             float x[2][4];
-            if (rotation != nullptr) {
+            if constexpr (Rotated) {
                 // The transpose is private to this wave and its LDS operations
                 // complete in order; the compiler barriers keep this record's
                 // writes after the previous record's reads.
@@ -602,16 +652,28 @@ template <int D, int R, int A>
 hipError_t launch_quantize_mfma(const QuantizeParams& p, hipStream_t stream) {
     // One workgroup per CU fits the LDS: split each (head, plane)'s tokens
     // over as many workgroups as make one round on the CUs, in whole passes
-    // of kMfmaTokens per wave.
-    const int64_t pairs = (int64_t)p.heads * 2;
+    // of kMfmaTokens per wave.  A plane without a rotation takes the
+    // unrotated instantiation; planes that differ are two launches.
+    const bool key_rotated = p.key_rotation != nullptr, value_rotated = p.value_rotation != nullptr;
+    const int planes = key_rotated == value_rotated ? 2 : 1;
+    const int64_t pairs = (int64_t)p.heads * planes;
     int64_t per_pair = p.compute_units > 0 ? p.compute_units / pairs : 1;
     per_pair = per_pair < 1 ? 1 : per_pair;
     int64_t block_tokens = (p.tokens + per_pair - 1) / per_pair;
     block_tokens = (block_tokens + kMfmaTokens - 1) / kMfmaTokens * kMfmaTokens;
     block_tokens = block_tokens < (1 << 24) ? block_tokens : (1 << 24);
-    const dim3 grid((unsigned)((p.tokens + block_tokens - 1) / block_tokens), (unsigned)p.heads, 2);
-    hipLaunchKernelGGL((quantize_mfma_kernel<D, R, A>), grid, dim3(kMfmaThreads), 0, stream, p, (int)block_tokens);
-    return hipGetLastError();
+    const dim3 grid((unsigned)((p.tokens + block_tokens - 1) / block_tokens), (unsigned)p.heads, (unsigned)planes);
+    for (int plane = 0; plane < 2; plane += planes) {
+        if (plane == 0 ? key_rotated : value_rotated)
+            hipLaunchKernelGGL((quantize_mfma_kernel<D, R, A, true>), grid, dim3(kMfmaThreads), 0, stream, p,
+                               (int)block_tokens, plane);
+        else
+            hipLaunchKernelGGL((quantize_mfma_kernel<D, R, A, false>), grid, dim3(kMfmaThreads), 0, stream, p,
+                               (int)block_tokens, plane);
+        const hipError_t status = hipGetLastError();
+        if (status != hipSuccess) return status;
+    }
+    return hipSuccess;
 }
 
 // From this many tokens the matrix-core kernel runs (one MI355X, C1 shapes,

@@ -27,6 +27,7 @@ struct QuantizeParams {
     const uint16_t* value_rotation;
     const float* key_mean;  // FP32 [records, heads, D] or null
     int heads, page_tokens, page_width, records, anchor, adjacent, coefficient;
+    int page_shift;     // log2(page_tokens): page tokens are 16 or 32
     int compute_units;  // of the launching device, for grid sizing
     RecordRegion region[kMaxRecords];
 };

@@ -14,6 +14,11 @@
  *      pair of finite E4M3 values, so BF16(fma) == BF16(TwoSum form).
  *  bf16_sum: for every pair of finite BF16 values, RNE of the FP32 sum equals
  *      the single-rounded sum (TwoSum plus midpoint correction).
+ *  level_division: the same reciprocal-and-correction form with the divisor
+ *      3 or 15 (the code levels of INT2 and INT4) equals RN(v/levels) for
+ *      every non-negative FP32 v with biased exponent 0..12 (subnormal
+ *      quotients and remainders), 126..128 (the computation is scale
+ *      invariant in between) and 250..254 (the largest values).
  */
 #include <math.h>
 #include <stdint.h>
@@ -100,5 +105,18 @@ int main(void) {
         }
     }
     printf("bf16_sum %ld\n", bad);
+
+    bad = 0;
+    for (int levels = 3; levels <= 15; levels += 12) {
+        const float l = (float)levels, y = 1.0f / l;
+        const uint32_t ranges[3][2] = {{0u, 13u}, {126u, 129u}, {250u, 255u}};
+        for (int range = 0; range < 3; range++)
+            for (uint32_t uv = ranges[range][0] << 23; uv < ranges[range][1] << 23; uv++) {
+                const float v = f(uv);
+                const float q0 = v * y, r = fmaf(-q0, l, v), q = fmaf(r, y, q0);
+                bad += u(q) != u(v / l);
+            }
+    }
+    printf("level_division %ld\n", bad);
     return 0;
 }

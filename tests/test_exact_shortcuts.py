@@ -1,7 +1,8 @@
 """The exact-arithmetic shortcuts of the quantize kernel (csrc/quantize.hip
 commit_record), checked exhaustively on the CPU by tests/exact_shortcuts.c:
-reciprocal-and-correction division by an E4M3 scale, ceil(q - 0.5) rounding,
-the exact code*scale+offset restore and the single-rounded BF16 sum.  The
+reciprocal-and-correction division by an E4M3 scale and by the code levels,
+ceil(q - 0.5) rounding, the exact code*scale+offset restore and the
+single-rounded BF16 sum.  The
 canonical formulas are those of the oracle (quantize/kernel.cuh:120-203)."""
 
 from __future__ import annotations
@@ -23,6 +24,7 @@ def results(tmp_path_factory):
     return {line.split()[0]: int(line.split()[1]) for line in out.splitlines()}
 
 
-@pytest.mark.parametrize("check", ["reciprocal_division", "half_down_rounding", "code_restore", "bf16_sum"])
+@pytest.mark.parametrize("check", ["reciprocal_division", "half_down_rounding", "code_restore", "bf16_sum",
+                                   "level_division"])
 def test_shortcut_is_exact(results, check):
     assert results[check] == 0
