@@ -386,8 +386,9 @@ def run_quantize(args):
             "unit": "TFLOP/s",
             "frac": head["rotation_TFLOPs"] / PEAK_FP32_TFLOPS,
             "traffic": None,
-            "kernel": "quantize_mfma_kernel<128,4,3>: FP32 rotation FMAs (K=1 v_mfma_f32_16x16x1_4b_f32 "
-                      "chains) against the published FP32 peak; HBM traffic is 6% of peak at this rate",
+            "kernel": "quantize_mfma_kernel<128,4,3,true>: FP32 rotation FMAs (K=1 v_mfma_f32_16x16x1_4b_f32 "
+                      "chains) against the published FP32 peak; HBM traffic is 9% of peak at this rate; on gfx950 "
+                      "the FP32 MFMAs and the commit's VALU do not overlap, so the call is their sum",
         },
         "cpu_baseline": cpu,
     }

@@ -448,9 +448,11 @@ __global__ __launch_bounds__(kQuantizeThreads) void quantize_kernel(QuantizePara
 // a 4-token transpose in LDS to the canonical layout right before its commit.
 // Slots at or beyond R rotate a copy of record 0 and are never committed.
 //
-// Inputs go straight from global memory to registers (the A operand), in
-// chunks of kInputChunk k double-buffered, the next pass's first chunk in
-// flight during the commit.  The rotation sits in LDS as FP32
+// Inputs are staged per wave through LDS as FP32 in chunks of kInputChunk k,
+// double-buffered: each lane converts four BF16 inputs per chunk and the
+// MFMAs read their A operands four k at a time (converting in the k loop
+// instead cost two VALU per two k steps in every lane, 7% more C1 time).  The
+// rotation sits in LDS as FP32
 // [k / 2][lane][R[k][l], R[k][64 + l], R[k + 1][l], R[k + 1][64 + l]], one
 // 16-byte read per two k steps.
 constexpr int kMfmaWaves = 16;
@@ -462,6 +464,7 @@ typedef float F32x16 __attribute__((ext_vector_type(16)));
 
 template <int D>
 constexpr int kInputChunk = 16;  // an even number of chunks per row at D = 96 and 128
+constexpr int kAStride4 = 5;     // float4s per staged A row: 16 k + 4 floats of padding
 
 template <int D, int R, int A, bool Rotated>
 __global__ __launch_bounds__(kMfmaThreads) void quantize_mfma_kernel(QuantizeParams p, int block_tokens,
@@ -469,11 +472,11 @@ __global__ __launch_bounds__(kMfmaThreads) void quantize_mfma_kernel(QuantizePar
     static_assert(R <= 4, "four record slots per token");
     constexpr int C = kInputChunk<D>;
     constexpr int kChunks = D / C;
-    constexpr int kLoads = C / 4;  // 8-byte loads per chunk
     __shared__ float inverse_scale[128];
     __shared__ __attribute__((aligned(16))) float mean_lds[R * D];
     __shared__ __attribute__((aligned(16))) float transpose_lds[kMfmaWaves][kMfmaTokens * kTransposeStride];
     __shared__ __attribute__((aligned(16))) float rotation_lds[D * 128];
+    __shared__ float4 a_lds[Rotated ? kMfmaWaves : 1][2][16][kAStride4];
 
     const int plane = plane_first + (int)blockIdx.z;
     const int head = blockIdx.y;
@@ -508,26 +511,34 @@ __global__ __launch_bounds__(kMfmaThreads) void quantize_mfma_kernel(QuantizePar
     constexpr int64_t kStride = (int64_t)kMfmaWaves * kMfmaTokens;
     float* transpose = transpose_lds[wave];
 
-    // A-operand role: row lane % 16 = (token, record slot).
-    const int a_token = (lane64 & 15) >> 2;
-    const int a_slot = lane64 & 3;
-    const int a_record = a_slot < R ? a_slot : 0;
-    const uint16_t* a_base = nullptr;
-    int64_t a_stride = 0;
+    // Loader role: lane l stages row l / 4 = (token, record slot), k quad l % 4
+    // of each chunk: one 8-byte load, four exact BF16 -> FP32 conversions and
+    // one 16-byte LDS write; the MFMAs then read their FP32 A operands, four
+    // k at a time.  Each element is converted once instead of once per k step
+    // in every lane (the A operand repeats in all 4 blocks).
+    const int ld_row = lane64 >> 2, ld_quad = lane64 & 3;
+    const int ld_token = ld_row >> 2, ld_slot = ld_row & 3;
+    const int ld_record = ld_slot < R ? ld_slot : 0;
+    const uint16_t* ld_base = nullptr;
+    int64_t ld_stride = 0;
 #pragma unroll
     for (int r = 0; r < R; ++r)
-        if (a_record == r) {
-            a_base = (plane == 0 ? p.key_ptrs[r] : p.value_ptrs[r]) + head * D;
-            a_stride = plane == 0 ? p.key_strides[r] : p.value_strides[r];
+        if (ld_record == r) {
+            ld_base = (plane == 0 ? p.key_ptrs[r] : p.value_ptrs[r]) + head * D + 4 * ld_quad;
+            ld_stride = plane == 0 ? p.key_strides[r] : p.value_strides[r];
         }
-    auto a_row = [&](int64_t first) {
-        const int64_t n = first + a_token < block_end ? first + a_token : block_end - 1;
-        return a_base + n * a_stride;
+    auto ld_row_of = [&](int64_t f) {
+        const int64_t n = f + ld_token < block_end ? f + ld_token : block_end - 1;
+        return ld_base + n * ld_stride;
     };
-    // Rows are only guaranteed 8-byte aligned: 8-byte loads.
-    auto load_chunk = [&](uint2 (&buffer)[kLoads], const uint16_t* row, int chunk) {
-#pragma unroll
-        for (int e = 0; e < kLoads; ++e) buffer[e] = reinterpret_cast<const uint2*>(row + chunk * C)[e];
+    // Rows are only guaranteed 8-byte aligned: one 8-byte load per chunk.
+    auto load_chunk = [&](const uint16_t* row, int chunk) {
+        return *reinterpret_cast<const uint2*>(row + chunk * C);
+    };
+    float4 (*stage)[16][kAStride4] = a_lds[wave];
+    auto stage_chunk = [&](uint2 w, int buffer) {
+        stage[buffer][ld_row][ld_quad] = make_float4(__uint_as_float(w.x << 16), __uint_as_float(w.x & 0xffff0000u),
+                                                     __uint_as_float(w.y << 16), __uint_as_float(w.y & 0xffff0000u));
     };
     const float4* rotation4 = reinterpret_cast<const float4*>(rotation_lds) + lane64;
 
@@ -538,13 +549,18 @@ __global__ __launch_bounds__(kMfmaThreads) void quantize_mfma_kernel(QuantizePar
         return inside ? slot : (int64_t)-1;
     };
 
+    // Pipeline: at the start of chunk c the data of chunk c + 1 (loaded one
+    // chunk earlier) goes to LDS and chunk c + 2 is loaded; chunks run on
+    // into the next pass's rows (a_row clamps past the block, so the last
+    // pass loads too and no branch joins the load counters).
     int64_t first = block_first + wave * kMfmaTokens;
-    uint2 input[2][kLoads];
     const uint16_t* row = nullptr;
+    uint2 pending = make_uint2(0, 0);
     int64_t next_slot = -1;
     if (Rotated && first < block_end) {
-        row = a_row(first);
-        load_chunk(input[0], row, 0);
+        row = ld_row_of(first);
+        stage_chunk(load_chunk(row, 0), 0);
+        pending = load_chunk(row, 1);
         next_slot = load_slot(first);
     }
     for (; first < block_end; first += kStride) {
@@ -556,34 +572,37 @@ __global__ __launch_bounds__(kMfmaThreads) void quantize_mfma_kernel(QuantizePar
             acc[0] = acc[1] = F32x16{};
 #pragma unroll
             for (int chunk = 0; chunk < kChunks; ++chunk) {
-                uint2 (&current)[kLoads] = input[chunk & 1];
-                uint2 (&next)[kLoads] = input[(chunk + 1) & 1];
-                if (chunk + 1 < kChunks) {
-                    load_chunk(next, row, chunk + 1);
+                // kChunks is even: chunk c of every pass sits in buffer c & 1.
+                stage_chunk(pending, (chunk + 1) & 1);
+                if (chunk + 2 < kChunks) {
+                    pending = load_chunk(row, chunk + 2);
                 } else {
-                    // The next pass's chunk 0 (into input[0]: kChunks is even),
-                    // issued on the last pass too (a_row clamps it to a row of
-                    // the block) so that no branch joins the load counters.
-                    row = a_row(first + kStride);
-                    load_chunk(next, row, 0);
-                    next_slot = load_slot(first + kStride);
+                    if (chunk + 2 == kChunks) {
+                        row = ld_row_of(first + kStride);
+                        next_slot = load_slot(first + kStride);
+                    }
+                    pending = load_chunk(row, chunk + 2 - kChunks);
                 }
-                // Keeps the loads here: left alone, the compiler sinks each
-                // one to its first use and every chunk waits a full round trip.
+                // Keeps the load here: left alone, the compiler sinks it to
+                // its first use and every chunk waits a full round trip.
                 __asm__ volatile("" ::: "memory");
+                const float4* a_read = &stage[chunk & 1][lane64 & 15][0];
 #pragma unroll
-                for (int pair = 0; pair < C / 2; ++pair) {
-                    const float4 b = rotation4[((chunk * C) / 2 + pair) * 64];
-                    const uint32_t word = (pair & 1) ? current[pair >> 1].y : current[pair >> 1].x;
-                    const float a0 = __uint_as_float(word << 16);
-                    const float a1 = __uint_as_float(word & 0xffff0000u);
-                    acc[0] = __builtin_amdgcn_mfma_f32_16x16x1f32(a0, b.x, acc[0], 0, 0, 0);
-                    acc[1] = __builtin_amdgcn_mfma_f32_16x16x1f32(a0, b.y, acc[1], 0, 0, 0);
-                    acc[0] = __builtin_amdgcn_mfma_f32_16x16x1f32(a1, b.z, acc[0], 0, 0, 0);
-                    acc[1] = __builtin_amdgcn_mfma_f32_16x16x1f32(a1, b.w, acc[1], 0, 0, 0);
+                for (int g = 0; g < C / 4; ++g) {
+                    const float4 a = a_read[g];
+                    const float4 b0 = rotation4[((chunk * C) / 2 + 2 * g) * 64];
+                    const float4 b1 = rotation4[((chunk * C) / 2 + 2 * g + 1) * 64];
+                    acc[0] = __builtin_amdgcn_mfma_f32_16x16x1f32(a.x, b0.x, acc[0], 0, 0, 0);
+                    acc[1] = __builtin_amdgcn_mfma_f32_16x16x1f32(a.x, b0.y, acc[1], 0, 0, 0);
+                    acc[0] = __builtin_amdgcn_mfma_f32_16x16x1f32(a.y, b0.z, acc[0], 0, 0, 0);
+                    acc[1] = __builtin_amdgcn_mfma_f32_16x16x1f32(a.y, b0.w, acc[1], 0, 0, 0);
+                    acc[0] = __builtin_amdgcn_mfma_f32_16x16x1f32(a.z, b1.x, acc[0], 0, 0, 0);
+                    acc[1] = __builtin_amdgcn_mfma_f32_16x16x1f32(a.z, b1.y, acc[1], 0, 0, 0);
+                    acc[0] = __builtin_amdgcn_mfma_f32_16x16x1f32(a.w, b1.z, acc[0], 0, 0, 0);
+                    acc[1] = __builtin_amdgcn_mfma_f32_16x16x1f32(a.w, b1.w, acc[1], 0, 0, 0);
                 }
                 // Nothing of the next chunk moves above this chunk's MFMAs,
-                // so the loads issued at its start have the chunk to land.
+                // so the load issued at its start has the chunk to land.
                 __builtin_amdgcn_sched_barrier(0);
             }
         }
