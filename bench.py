@@ -415,17 +415,20 @@ def run_prefill(args):
         rq.flash_attn_varlen_func(q=q, k=k, v=v, out=out, cu_seqlens_q=cu, cu_seqlens_k=cu, max_seqlen_q=tokens,
                                   max_seqlen_k=tokens, softmax_scale=scale, causal=True)
 
-    def event_ms(fn):
+    def event_ms(fn, settle_s=0.3):
+        """Median of per-call HIP events after a settle phase and the warm-up calls."""
+        settle(torch, fn, settle_s)
         for _ in range(args.warmup):
             fn()
+        events = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+                  for _ in range(args.steps)]
         torch.cuda.synchronize()
-        begin, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        begin.record()
-        for _ in range(args.steps):
+        for begin, end in events:
+            begin.record()
             fn()
-        end.record()
+            end.record()
         torch.cuda.synchronize()
-        return begin.elapsed_time(end) / args.steps
+        return statistics.median(b.elapsed_time(e) for b, e in events)
 
     kernel_ms = event_ms(step)  # one launch per call
     flop = 2.0 * 2.0 * heads * dim * tokens * (tokens + 1) / 2.0  # QK^T and PV over the causal half
@@ -434,7 +437,7 @@ def run_prefill(args):
 
     qt, kt, vt = (t.transpose(0, 1).contiguous() for t in (q, k, v))  # [heads, tokens, D]
     torch_ms = event_ms(lambda: torch.nn.functional.scaled_dot_product_attention(qt, kt, vt, is_causal=True,
-                                                                                   scale=scale))
+                                                                                   scale=scale), settle_s=0.0)
     log(f"[bench] torch scaled_dot_product_attention {torch_ms * 1e3:.1f} us/call")
 
     result = {
@@ -454,6 +457,7 @@ def run_prefill(args):
                    "head_dim": dim, "softmax_scale": scale},
         "us_per_call": kernel_ms * 1e3,
         "tokens_per_s": tokens / (kernel_ms * 1e-3),
+        "timing": "median of per-call HIP events after >= 0.3 s of untimed calls",
         "roofline": {
             "bound": "mfma",
             "achieved": achieved,

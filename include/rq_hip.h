@@ -205,8 +205,9 @@ int rq_prefill_attention(const void* query, int64_t query_stride, const void* ke
                          size_t workspace_bytes, hipStream_t stream);
 
 /*
- * Workspace bytes rq_prefill_attention needs for these host shapes (the FP32
- * partials of query blocks whose keys are split over several workgroups);
+ * Workspace bytes rq_prefill_attention needs for these host shapes.  The
+ * current kernels merge within their workgroups and return 0; callers that
+ * allocate what this returns keep working if a later plan needs scratch.
  * same_lengths = 1 when cu_seqlens_q and cu_seqlens_k are the same array.
  * No counterpart in the reference (flash-attn sizes its own scratch).
  */

@@ -714,11 +714,9 @@ int rq_prefill_attention(const void* query, int64_t query_stride, const void* ke
     p.max_seqlen_q = (int)max_seqlen_q;
     p.causal = causal != 0;
     p.softmax_scale = softmax_scale;
-    p.causal_same = p.causal && cu_seqlens_q == cu_seqlens_k;
     const size_t needed = rq::prefill_plan(p, max_seqlen_k);
     if (needed > 0 && (workspace == nullptr || workspace_bytes < needed))
         return fail(RQ_ENOSPACE, "Prefill workspace of %zu bytes required, %zu given", needed, workspace_bytes);
-    p.partials = static_cast<float*>(workspace);
     return check_launch(rq::launch_prefill(p, stream), "prefill attention launch");
 }
 
@@ -837,7 +835,7 @@ size_t rq_prefill_workspace_bytes(int64_t batch, int heads_q, int head_dim, int6
     p.head_dim = head_dim;
     p.max_seqlen_q = (int)max_seqlen_q;
     p.causal = causal != 0;
-    p.causal_same = p.causal && same_lengths != 0;
+    (void)same_lengths;
     return rq::prefill_plan(p, max_seqlen_k);
 }
 

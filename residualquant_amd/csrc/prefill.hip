@@ -6,16 +6,27 @@
 // cu_seqlens_k, max_seqlen_q, max_seqlen_k, softmax_scale, causal=True):
 // out[i] = softmax(scale * q_i . K_j^T over keys j <= i + (len_k - len_q)) V.
 //
-// Work mapping: one workgroup = 128 queries of one (sequence, head), four
-// waves of 32 queries; key tiles of 64 are staged in LDS (K row-major, V
-// transposed) and shared by the waves.  Each wave computes S^T = K Q^T with
-// v_mfma_f32_32x32x16_bf16, so lane l owns query l % 32: the softmax row max
-// and sum are in-lane plus one exchange between the wave's halves, and the
-// probabilities P^T stay in the accumulator registers as the B operand of
-// O^T += V^T P^T.  The key order inside each P.V step is permuted to match
-// the accumulator layout (the A operand reads V^T at the same keys), so P
-// never moves between lanes.  Query blocks launch latest-first, since later
-// blocks see more keys.
+// Work mapping: a workgroup is 8 waves in two groups of 4 and takes a pair of
+// 128-query blocks of one (sequence, head): the heavy block H = n - 1 - i and
+// the light block L = i of the sequence's n blocks (a lone middle block when
+// n is odd).  Under causal attention over equal lengths the pair needs
+// T(H) + T(L) = n + 1 key tiles of 64 for every i, so every workgroup has the
+// same work and no query block is split across workgroups.  Group A takes H's
+// first a = ceil((T(H) + T(L)) / 2) tiles; group B takes all of L, then H's
+// remaining tiles; at the end B hands its partial (max, sum, output) for H to
+// A through LDS and A merges and writes H.  Both groups run the same number
+// of tile steps between workgroup barriers; each stages its own tiles (K
+// row-major, V transposed) into its own double buffer.
+//
+// Per wave: 32 queries.  S^T = K Q^T with v_mfma_f32_32x32x16_bf16, so lane l
+// owns query l % 32: the row max is in-lane plus one exchange between the
+// wave's halves, and the probabilities P^T stay in the accumulator registers
+// as the B operand of O^T += V^T P^T, with the key order of each P.V step
+// permuted to match the accumulator layout (the A operand reads V^T at the
+// same keys).  The row max moves lazily: the output is rescaled only when a
+// row's max grows by more than 2^8 (P then stays below 256, exact in the
+// final normalisation), and each half-wave keeps its own row sum until the
+// end.
 //
 // Lane layouts of v_mfma_f32_32x32x16_bf16 (checked on gfx950): A row l % 32,
 // k 8 (l / 32) + e; B column l % 32, k 8 (l / 32) + e; C register r holds row
@@ -30,43 +41,14 @@ namespace {
 typedef __bf16 Bf16x8 __attribute__((ext_vector_type(8)));
 typedef float F32x16 __attribute__((ext_vector_type(16)));
 
-constexpr int kPrefillWaves = 4;
-constexpr int kPrefillThreads = 64 * kPrefillWaves;
+constexpr int kGroupWaves = 4;
+constexpr int kGroupThreads = 64 * kGroupWaves;
+constexpr int kPrefillThreads = 2 * kGroupThreads;
 constexpr int kBlockQueries = kPrefillBlockQueries;  // 32 per wave
 constexpr int kBlockKeys = kPrefillBlockKeys;
-constexpr int kSplitTiles = 16;  // key tiles per work item at most (1024 keys)
-static_assert(kBlockQueries == 32 * kPrefillWaves, "one 32-query MFMA column block per wave");
-
-// ---------------------------------------------------------------- plan
-
-// Key tiles query block qb may need: all of them, or 2 (qb + 1) when the
-// attention is causal over equal query and key lengths.
-__host__ __device__ inline int planned_tiles(const PrefillParams& p, int block) {
-    const int need = 2 * (block + 1);
-    return (p.causal_same && need < p.max_tiles) ? need : p.max_tiles;
-}
-
-__host__ __device__ inline int block_splits(const PrefillParams& p, int block) {
-    if (p.split_tiles <= 0) return 1;
-    const int n = (planned_tiles(p, block) + p.split_tiles - 1) / p.split_tiles;
-    return n < 1 ? 1 : (n > kMaxSplits ? kMaxSplits : n);
-}
-
-struct PrefillItem {
-    int block, split, splits, slot;  // slot: first partial slot of the block (split blocks only)
-};
-
-// Work items run heaviest first: query blocks from the last, their splits in order.
-__device__ inline PrefillItem decode_item(const PrefillParams& p, int item) {
-    int slot = 0;
-    for (int block = p.query_blocks - 1; block >= 0; --block) {
-        const int n = block_splits(p, block);
-        if (item < n) return {block, item, n, slot};
-        item -= n;
-        if (n > 1) slot += n;
-    }
-    return {-1, 0, 1, 0};
-}
+constexpr float kLazyRescale = 8.0f;  // log2 units: rescale when a row max grows by more
+constexpr int kXcds = 8;              // MI355X accelerator complex dies
+static_assert(kBlockQueries == 32 * kGroupWaves, "one 32-query MFMA column block per wave");
 
 __device__ __forceinline__ F32x16 mfma(Bf16x8 a, Bf16x8 b, F32x16 c) {
     return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
@@ -76,102 +58,119 @@ __device__ __forceinline__ F32x16 mfma(Bf16x8 a, Bf16x8 b, F32x16 c) {
 __device__ __forceinline__ Bf16x8 load8(const uint16_t* src) {
     const uint2 a = reinterpret_cast<const uint2*>(src)[0];
     const uint2 b = reinterpret_cast<const uint2*>(src)[1];
-    const uint4 v = make_uint4(a.x, a.y, b.x, b.y);
-    return __builtin_bit_cast(Bf16x8, v);
+    return __builtin_bit_cast(Bf16x8, make_uint4(a.x, a.y, b.x, b.y));
 }
 
-__device__ __forceinline__ uint4 load16(const uint16_t* src) {
-    const uint2 a = reinterpret_cast<const uint2*>(src)[0];
-    const uint2 b = reinterpret_cast<const uint2*>(src)[1];
-    return make_uint4(a.x, a.y, b.x, b.y);
-}
+template <int D>
+struct Lds {
+    static constexpr int KS = D + 8;               // K tile row stride (halves)
+    static constexpr int VS = kBlockKeys + 4;      // V^T tile row stride (halves)
+    static constexpr int kKHalves = kBlockKeys * KS;
+    static constexpr int kVHalves = D * VS;
+    static constexpr int kGroupHalves = 2 * (kKHalves + kVHalves);  // double-buffered K and V^T
+    static constexpr int kBytes = 2 * kGroupHalves * 2;
+    // The merge hand-off reuses the tiles: [wave][D + 2][32] floats.
+    static constexpr int kMergeBytes = kGroupWaves * (D + 2) * 32 * 4;
+    static_assert(kMergeBytes <= kBytes, "merge buffer fits in the tile buffers");
+};
+
+// One query block's running state for a wave's 32 queries.
+template <int D>
+struct BlockState {
+    F32x16 out[D / 32];
+    float running_max, running_sum;  // log2 units; the sum of this half-wave's keys
+};
 
 template <int D>
 __global__ __launch_bounds__(kPrefillThreads) __attribute__((amdgpu_waves_per_eu(2)))
 void prefill_kernel(PrefillParams p) {
-    // Double-buffered K tile [key][KS] and V^T tile [d][VS]; the pads put the
-    // 32 rows a wave reads at once on distinct banks.
-    constexpr int KS = D + 8;
-    constexpr int VS = kBlockKeys + 4;
-    __shared__ __attribute__((aligned(16))) uint16_t k_tiles[2][kBlockKeys * KS];
-    __shared__ __attribute__((aligned(16))) uint16_t v_tiles[2][D * VS];
+    using L = Lds<D>;
+    constexpr int KS = L::KS, VS = L::VS;
+    __shared__ __attribute__((aligned(16))) uint16_t lds[L::kBytes / 2];
 
-    const int sequence = blockIdx.z;
-    const int head = blockIdx.y;
-    const PrefillItem work = decode_item(p, blockIdx.x);
-    if (work.block < 0) return;
-    const int q_block = work.block;
+    // XCD-aware order: workgroups are dispatched round-robin over the 8
+    // XCDs, so the linear id is remapped to give each XCD a run of
+    // consecutive (item, head, sequence) work, i.e. whole heads whose K/V
+    // tiles stay in that XCD's L2 (when the grid divides by 8).
+    int linear = blockIdx.x + gridDim.x * (blockIdx.y + gridDim.y * blockIdx.z);
+    const int grid_total = gridDim.x * gridDim.y * gridDim.z;
+    if (grid_total % kXcds == 0) linear = (linear % kXcds) * (grid_total / kXcds) + linear / kXcds;
+    const int item = linear % gridDim.x;
+    const int head = (linear / gridDim.x) % gridDim.y;
+    const int sequence = linear / (gridDim.x * gridDim.y);
     const int q_begin = p.cu_seqlens_q[sequence];
     const int q_len = p.cu_seqlens_q[sequence + 1] - q_begin;
     const int k_begin = p.cu_seqlens_k[sequence];
     const int k_len = p.cu_seqlens_k[sequence + 1] - k_begin;
-    const int q0 = q_block * kBlockQueries;
-    if (q0 >= q_len) return;  // uniform over the workgroup, before any barrier
-    const int shift = k_len - q_len;  // query i sees keys j <= i + shift (causal)
+    const int n_blocks = (q_len + kBlockQueries - 1) / kBlockQueries;
+    if (item >= (n_blocks + 1) / 2) return;  // uniform over the workgroup, before any barrier
+    const int shift = k_len - q_len;         // query i sees keys j <= i + shift (causal)
     const int kv_head = head / p.group;
 
+    // Keys a block's queries may see and the key tiles that covers.
+    auto block_keys = [&](int block) {
+        if (!p.causal) return k_len;
+        const int limit = (block + 1) * kBlockQueries + shift;
+        return limit < k_len ? (limit > 0 ? limit : 0) : k_len;
+    };
+    auto block_tiles = [&](int block) { return (block_keys(block) + kBlockKeys - 1) / kBlockKeys; };
+
+    const int heavy = n_blocks - 1 - item;
+    const int light = item < heavy ? item : -1;
+    const int heavy_tiles = block_tiles(heavy);
+    const int light_tiles = light >= 0 ? block_tiles(light) : 0;
+    const int total = heavy_tiles + light_tiles;
+    const int split = heavy_tiles < (total + 1) / 2 ? heavy_tiles : (total + 1) / 2;  // A: heavy [0, split)
+    const int steps = split > total - split ? split : total - split;
+
     const int wave = threadIdx.x >> 6;
+    const int group = wave >> 2;  // 0: A, 1: B
+    const int group_wave = wave & 3;
+    const int group_thread = threadIdx.x & (kGroupThreads - 1);
     const int lane = threadIdx.x & 63;
     const int column = lane & 31;
     const int half = lane >> 5;
-    const int wave_q0 = q0 + 32 * wave;
-    const int my_q = wave_q0 + column;
 
-    int block_keys = k_len;
-    int wave_keys = k_len;
-    if (p.causal) {
-        const int block_limit = q0 + kBlockQueries + shift;
-        const int wave_limit = wave_q0 + 32 + shift;
-        block_keys = block_limit < k_len ? block_limit : k_len;
-        wave_keys = wave_limit < k_len ? wave_limit : k_len;
-    }
-    const int my_limit = p.causal ? my_q + shift : k_len - 1;  // last key this query sees
+    // (block, tile) of this group at a step, or block -1 when idle.
+    auto step_block = [&](int step) {
+        if (group == 0) return step < split ? heavy : -1;
+        if (step < light_tiles) return light;
+        return step - light_tiles < heavy_tiles - split ? heavy : -1;
+    };
+    auto step_tile = [&](int step) {
+        if (group == 0) return step;
+        return step < light_tiles ? step : split + step - light_tiles;
+    };
 
-    // Q^T operand (B of S^T = K Q^T): chunk m holds d = 16m + 8 half + e.
-    Bf16x8 q_operand[D / 16];
-    {
-        const int row = my_q < q_len ? my_q : q_len - 1;
-        const uint16_t* src = p.query + (int64_t)(q_begin + row) * p.query_stride + head * D + 8 * half;
-#pragma unroll
-        for (int m = 0; m < D / 16; ++m) q_operand[m] = load8(src + 16 * m);
-    }
+    uint16_t* group_lds = lds + group * L::kGroupHalves;
+    auto k_tile_of = [&](int buffer) { return group_lds + buffer * L::kKHalves; };
+    auto v_tile_of = [&](int buffer) { return group_lds + 2 * L::kKHalves + buffer * L::kVHalves; };
 
-    F32x16 out[D / 32];
-#pragma unroll
-    for (int t = 0; t < D / 32; ++t)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) out[t][r] = 0.f;
-    float running_max = -__builtin_inff();
-    float running_sum = 0.f;
-    const float c = p.softmax_scale * 1.4426950408889634f;  // scores in log2 units
-
-    const uint16_t* k_base = p.key + (int64_t)k_begin * p.key_stride + kv_head * D;
-    const uint16_t* v_base = p.value + (int64_t)k_begin * p.value_stride + kv_head * D;
-
-    // Tile loads: each thread fetches K chunks (row, 8 channels) and V units
-    // (key pair, 8 channels) of the next tile into registers while the current
-    // tile computes, then stages them (V transposed) into the other buffer.
-    // The loads are raw buffer loads from a wave-uniform resource rebased at
-    // each tile, so rows past the sequence read as zero without a branch and
-    // every per-thread offset is a loop-invariant 32-bit value.
-    constexpr int kKChunks = (kBlockKeys * (D / 8) + kPrefillThreads - 1) / kPrefillThreads;
-    constexpr int kVUnits = ((kBlockKeys / 2) * (D / 8) + kPrefillThreads - 1) / kPrefillThreads;
+    // Tile loads: each thread of a group fetches K chunks (row, 8 channels) and
+    // V units (key pair, 8 channels) of its group's next tile into registers
+    // while the current tile computes, then stages them (V transposed) into
+    // the other buffer.  Raw buffer loads from a wave-uniform resource rebased
+    // at each tile: rows past the sequence read as zero without a branch.
+    constexpr int kKChunks = (kBlockKeys * (D / 8) + kGroupThreads - 1) / kGroupThreads;
+    constexpr int kVUnits = ((kBlockKeys / 2) * (D / 8) + kGroupThreads - 1) / kGroupThreads;
     constexpr uint32_t kOutOfRange = 0x80000000u;  // beyond any tile's record count: loads zero
     const uint32_t key_row_bytes = (uint32_t)p.key_stride * 2, value_row_bytes = (uint32_t)p.value_stride * 2;
     uint32_t k_offset[kKChunks], v_offset[kVUnits];
 #pragma unroll
     for (int i = 0; i < kKChunks; ++i) {
-        const int chunk = threadIdx.x + i * kPrefillThreads;
+        const int chunk = group_thread + i * kGroupThreads;
         k_offset[i] = chunk < kBlockKeys * (D / 8) ? (uint32_t)(chunk / (D / 8)) * key_row_bytes + 16 * (chunk % (D / 8))
                                                    : kOutOfRange;
     }
 #pragma unroll
     for (int i = 0; i < kVUnits; ++i) {
-        const int unit = threadIdx.x + i * kPrefillThreads;
+        const int unit = group_thread + i * kGroupThreads;
         v_offset[i] = unit < (kBlockKeys / 2) * (D / 8)
                           ? (uint32_t)(2 * (unit % (kBlockKeys / 2))) * value_row_bytes + 16 * (unit / (kBlockKeys / 2))
                           : kOutOfRange;
     }
+    const uint16_t* k_base = p.key + (int64_t)k_begin * p.key_stride + kv_head * D;
+    const uint16_t* v_base = p.value + (int64_t)k_begin * p.value_stride + kv_head * D;
     auto tile_resource = [&](const uint16_t* base, int64_t row_elements, int kt) {
         // Bytes from row kt to the end of the tile's last valid row (its D
         // channels); at most one tile of rows, so the count stays small.
@@ -195,53 +194,78 @@ void prefill_kernel(PrefillParams p) {
         }
     };
     auto stage = [&](int buffer) {
+        uint16_t* k_tile = k_tile_of(buffer);
+        uint16_t* v_tile = v_tile_of(buffer);
 #pragma unroll
         for (int i = 0; i < kKChunks; ++i) {
-            const int chunk = threadIdx.x + i * kPrefillThreads;
+            const int chunk = group_thread + i * kGroupThreads;
             if (chunk < kBlockKeys * (D / 8))
-                *reinterpret_cast<uint4*>(&k_tiles[buffer][(chunk / (D / 8)) * KS + 8 * (chunk % (D / 8))]) = k_next[i];
+                *reinterpret_cast<uint4*>(&k_tile[(chunk / (D / 8)) * KS + 8 * (chunk % (D / 8))]) = k_next[i];
         }
 #pragma unroll
         for (int i = 0; i < kVUnits; ++i) {
-            const int unit = threadIdx.x + i * kPrefillThreads;
-            const int pair = unit % (kBlockKeys / 2), group = unit / (kBlockKeys / 2);
+            const int unit = group_thread + i * kGroupThreads;
+            const int pair = unit % (kBlockKeys / 2), chunk = unit / (kBlockKeys / 2);
             if (unit < (kBlockKeys / 2) * (D / 8)) {
                 const uint4 a = v_next[i][0], b = v_next[i][1];
                 const uint32_t av[4] = {a.x, a.y, a.z, a.w}, bv[4] = {b.x, b.y, b.z, b.w};
-                uint16_t* column = &v_tiles[buffer][(8 * group) * VS + 2 * pair];
+                uint16_t* target = &v_tile[(8 * chunk) * VS + 2 * pair];
 #pragma unroll
                 for (int e = 0; e < 4; ++e) {
                     // (key, key + 1) pairs of channels 2e and 2e + 1.
-                    *reinterpret_cast<uint32_t*>(column + (2 * e) * VS) = __builtin_amdgcn_perm(bv[e], av[e], 0x05040100u);
-                    *reinterpret_cast<uint32_t*>(column + (2 * e + 1) * VS) =
+                    *reinterpret_cast<uint32_t*>(target + (2 * e) * VS) = __builtin_amdgcn_perm(bv[e], av[e], 0x05040100u);
+                    *reinterpret_cast<uint32_t*>(target + (2 * e + 1) * VS) =
                         __builtin_amdgcn_perm(bv[e], av[e], 0x07060302u);
                 }
             }
         }
     };
 
-    // This item's share of the block's key tiles.
-    const int block_tiles = block_keys > 0 ? (block_keys + kBlockKeys - 1) / kBlockKeys : 0;
-    const int per_split = (block_tiles + work.splits - 1) / work.splits;
-    const int first_tile = work.split * per_split;
-    const int end_tile = first_tile + per_split < block_tiles ? first_tile + per_split : block_tiles;
-    const int key_end = end_tile * kBlockKeys < block_keys ? end_tile * kBlockKeys : block_keys;
+    const float c = p.softmax_scale * 1.4426950408889634f;  // scores in log2 units
 
-    if (first_tile * kBlockKeys < key_end) {
-        fetch(first_tile * kBlockKeys);
-        stage(0);
-    }
-    __syncthreads();
-    int buffer = 0;
-    for (int kt = first_tile * kBlockKeys; kt < key_end; kt += kBlockKeys, buffer ^= 1) {
-        // Buffer `buffer` holds this tile; every wave finished reading the
-        // other one before the barrier that ended the previous iteration.
-        const bool more = kt + kBlockKeys < key_end;
-        if (more) fetch(kt + kBlockKeys);
-        const uint16_t* k_tile = k_tiles[buffer];
-        const uint16_t* v_tile = v_tiles[buffer];
-        if (kt < wave_keys) {  // wave-uniform: this wave's queries see some of these keys
+    // The running block of this wave and its queries.
+    BlockState<D> st;
+    Bf16x8 q_operand[D / 16];
+    int cur_block = -1, wave_q0 = 0, wave_keys = 0, my_q = 0, my_limit = 0;
+    auto begin_block = [&](int block) {
+        cur_block = block;
+        wave_q0 = block * kBlockQueries + 32 * group_wave;
+        my_q = wave_q0 + column;
+        wave_keys = k_len;
+        if (p.causal) {
+            const int limit = wave_q0 + 32 + shift;
+            wave_keys = limit < k_len ? limit : k_len;
+        }
+        my_limit = p.causal ? my_q + shift : k_len - 1;  // last key this query sees
+        // Q^T operand (B of S^T = K Q^T): chunk m holds d = 16m + 8 half + e.
+        const int row = my_q < q_len ? my_q : q_len - 1;
+        const uint16_t* src = p.query + (int64_t)(q_begin + row) * p.query_stride + head * D + 8 * half;
+#pragma unroll
+        for (int m = 0; m < D / 16; ++m) q_operand[m] = load8(src + 16 * m);
+#pragma unroll
+        for (int t = 0; t < D / 32; ++t)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) st.out[t][r] = 0.f;
+        st.running_max = -__builtin_inff();
+        st.running_sum = 0.f;
+    };
+    // Normalised BF16 output rows of the running block.
+    auto write_block = [&](const BlockState<D>& s, float total_sum) {
+        if (my_q >= q_len) return;
+        const float inverse = total_sum > 0.f ? 1.0f / total_sum : 0.f;
+        uint16_t* dst = p.output + (int64_t)(q_begin + my_q) * p.output_stride + head * D + 4 * half;
+#pragma unroll
+        for (int t = 0; t < D / 32; ++t)
+#pragma unroll
+            for (int g = 0; g < 4; ++g) {
+                const uint32_t b0 = bf16_rn(s.out[t][4 * g] * inverse), b1 = bf16_rn(s.out[t][4 * g + 1] * inverse);
+                const uint32_t b2 = bf16_rn(s.out[t][4 * g + 2] * inverse), b3 = bf16_rn(s.out[t][4 * g + 3] * inverse);
+                *reinterpret_cast<uint2*>(dst + 32 * t + 8 * g) = make_uint2(b0 | (b1 << 16), b2 | (b3 << 16));
+            }
+    };
 
+    // One key tile of the running block.
+    auto compute_tile = [&](int kt, const uint16_t* k_tile, const uint16_t* v_tile) {
         // S^T for two sub-tiles of 32 keys: register r of lane l holds key
         // kt + 32 sub + 8 (r / 4) + 4 half + r % 4 against query my_q.
         F32x16 s[2];
@@ -276,11 +300,21 @@ void prefill_kernel(PrefillParams p) {
                 for (int r = 0; r < 16; ++r) tile_max = fmaxf(tile_max, s[sub][r]);
         }
         tile_max = fmaxf(tile_max, __shfl_xor(tile_max, 32)) * c;
-        const float new_max = fmaxf(running_max, tile_max);
+        // Lazy max: keep the running max unless the tile exceeds it by more
+        // than 2^8; the weights then stay below 256 and cancel in the final
+        // normalisation.
+        const bool grow = tile_max > st.running_max + kLazyRescale;
+        const float new_max = grow ? tile_max : st.running_max;
         // A query with no visible key yet keeps zero weights (no -inf - -inf).
         const float base = new_max == -__builtin_inff() ? 0.f : new_max;
-        const float rescale = __builtin_amdgcn_exp2f(running_max - base);
-        running_max = new_max;
+        const float rescale = grow ? __builtin_amdgcn_exp2f(st.running_max - base) : 1.0f;
+        st.running_max = new_max;
+        if (!__all(!grow)) {
+#pragma unroll
+            for (int t = 0; t < D / 32; ++t)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) st.out[t][r] *= rescale;
+        }
 
         // P^T in BF16 as the B operand of O^T += V^T P^T: step j of sub-tile
         // `sub` takes registers 8j..8j+7, i.e. k-slot (half, e) is key
@@ -297,15 +331,7 @@ void prefill_kernel(PrefillParams p) {
                     p_operand[sub][j][e] = (__bf16)w;
                     tile_sum += w;
                 }
-        tile_sum += __shfl_xor(tile_sum, 32);
-        running_sum = running_sum * rescale + tile_sum;
-        // Once the row maxima settle, most tiles leave every query's max in place.
-        if (!__all(rescale == 1.0f)) {
-#pragma unroll
-            for (int t = 0; t < D / 32; ++t)
-#pragma unroll
-                for (int r = 0; r < 16; ++r) out[t][r] *= rescale;
-        }
+        st.running_sum = st.running_sum * rescale + tile_sum;
 
 #pragma unroll
         for (int sub = 0; sub < 2; ++sub)
@@ -318,121 +344,97 @@ void prefill_kernel(PrefillParams p) {
                     const uint2 lo = *reinterpret_cast<const uint2*>(v_row);
                     const uint2 hi = *reinterpret_cast<const uint2*>(v_row + 8);
                     const Bf16x8 a = __builtin_bit_cast(Bf16x8, make_uint4(lo.x, lo.y, hi.x, hi.y));
-                    out[t] = mfma(a, p_operand[sub][j], out[t]);
+                    st.out[t] = mfma(a, p_operand[sub][j], st.out[t]);
                 }
             }
+    };
+
+    // A owns H from the start, B owns L (when the pair has one): a block with
+    // no visible key still writes its (zero) rows.
+    if (group == 0)
+        begin_block(heavy);
+    else if (light >= 0)
+        begin_block(light);
+    if (steps > 0 && step_block(0) >= 0) {
+        fetch(step_tile(0) * kBlockKeys);
+        stage(0);
+    }
+    __syncthreads();
+    for (int step = 0; step < steps; ++step) {
+        // Buffer step & 1 holds this step's tile; every wave finished reading
+        // the other one before the barrier that ended the previous step.
+        const int block = step_block(step);
+        const int next_block = step + 1 < steps ? step_block(step + 1) : -1;
+        if (next_block >= 0) fetch(step_tile(step + 1) * kBlockKeys);
+        if (block >= 0) {
+            if (block != cur_block) {
+                // Group B moves to H's tail: its L (if any) is complete.
+                if (cur_block >= 0) write_block(st, st.running_sum + __shfl_xor(st.running_sum, 32));
+                begin_block(block);
+            }
+            const int kt = step_tile(step) * kBlockKeys;
+            if (kt < wave_keys) compute_tile(kt, k_tile_of(step & 1), v_tile_of(step & 1));
         }
-        if (more) stage(buffer ^ 1);
+        if (next_block >= 0) stage((step + 1) & 1);
         __syncthreads();
     }
 
-    if (work.splits > 1) {
-        // Unnormalised partial [slot][row][query]: rows 0..D-1 the output,
-        // D the running max (log2 units), D + 1 the running sum.
-        if (my_q < q_len) {
-            const int query = 32 * wave + column;
-            float* partial = p.partials +
-                             ((((int64_t)sequence * p.heads_q + head) * p.partial_slots + work.slot + work.split) *
-                              (D + 2)) * kBlockQueries + query;
-#pragma unroll
-            for (int t = 0; t < D / 32; ++t)
-#pragma unroll
-                for (int r = 0; r < 16; ++r)
-                    partial[(32 * t + 8 * (r >> 2) + 4 * half + (r & 3)) * kBlockQueries] = out[t][r];
-            if (half == 0) {
-                partial[D * kBlockQueries] = running_max;
-                partial[(D + 1) * kBlockQueries] = running_sum;
-            }
-        }
+    const bool handoff = split < heavy_tiles;  // group B holds part of H
+    if (!handoff) {
+        // A's H and B's L (if any) are complete.
+        if (cur_block >= 0) write_block(st, st.running_sum + __shfl_xor(st.running_sum, 32));
         return;
     }
-    if (my_q < q_len) {
-        const float inverse = running_sum > 0.f ? 1.0f / running_sum : 0.f;
-        uint16_t* dst = p.output + (int64_t)(q_begin + my_q) * p.output_stride + head * D + 4 * half;
+    // B's partial for H to LDS as [wave][row][query]: rows 0..D-1 the output,
+    // D the running max (log2 units), D + 1 the running sum (both halves).
+    float* merge = reinterpret_cast<float*>(lds) + group_wave * (D + 2) * 32;
+    const float sum_both = st.running_sum + __shfl_xor(st.running_sum, 32);
+    if (group == 1) {
 #pragma unroll
         for (int t = 0; t < D / 32; ++t)
 #pragma unroll
-            for (int g = 0; g < 4; ++g) {
-                const uint32_t b0 = bf16_rn(out[t][4 * g] * inverse), b1 = bf16_rn(out[t][4 * g + 1] * inverse);
-                const uint32_t b2 = bf16_rn(out[t][4 * g + 2] * inverse), b3 = bf16_rn(out[t][4 * g + 3] * inverse);
-                *reinterpret_cast<uint2*>(dst + 32 * t + 8 * g) = make_uint2(b0 | (b1 << 16), b2 | (b3 << 16));
-            }
+            for (int r = 0; r < 16; ++r) merge[(32 * t + 8 * (r >> 2) + 4 * half + (r & 3)) * 32 + column] = st.out[t][r];
+        if (half == 0) {
+            merge[D * 32 + column] = st.running_max;
+            merge[(D + 1) * 32 + column] = sum_both;
+        }
     }
-}
-
-// Combines the partials of split query blocks: the LSE merge of (max, sum,
-// output) triples in log2 units, then the BF16 row.  Thread = (query, 8
-// channels): grid.x = query_blocks * D / 8 chunk groups of 128 queries.
-template <int D>
-__global__ __launch_bounds__(kBlockQueries) void prefill_merge_kernel(PrefillParams p) {
-    const int block = blockIdx.x / (D / 8), chunk = blockIdx.x % (D / 8);
-    const int head = blockIdx.y, sequence = blockIdx.z;
-    const int splits = block_splits(p, block);
-    if (splits <= 1) return;
-    int slot = 0;
-    for (int b = p.query_blocks - 1; b > block; --b) {
-        const int n = block_splits(p, b);
-        if (n > 1) slot += n;
-    }
-    const int q_begin = p.cu_seqlens_q[sequence];
-    const int q_len = p.cu_seqlens_q[sequence + 1] - q_begin;
-    const int query = threadIdx.x;
-    const int q = block * kBlockQueries + query;
-    if (q >= q_len) return;
-    const float* base = p.partials + ((((int64_t)sequence * p.heads_q + head) * p.partial_slots + slot) * (D + 2)) *
-                                         kBlockQueries + query;
-    const int64_t stride = (int64_t)(D + 2) * kBlockQueries;
-    float maximum = -__builtin_inff();
-    for (int s = 0; s < splits; ++s) maximum = fmaxf(maximum, base[s * stride + D * kBlockQueries]);
-    float total = 0.f, acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-    for (int s = 0; s < splits; ++s) {
-        const float* part = base + s * stride;
-        const float m = part[D * kBlockQueries];
-        const float w = m == -__builtin_inff() ? 0.f : __builtin_amdgcn_exp2f(m - maximum);
-        total += w * part[(D + 1) * kBlockQueries];
+    __syncthreads();
+    if (group == 0) {
+        const float other_max = merge[D * 32 + column];
+        const float other_sum = merge[(D + 1) * 32 + column];
+        const float m = fmaxf(st.running_max, other_max);
+        const float base = m == -__builtin_inff() ? 0.f : m;
+        const float mine = st.running_max == -__builtin_inff() ? 0.f : __builtin_amdgcn_exp2f(st.running_max - base);
+        const float theirs = other_max == -__builtin_inff() ? 0.f : __builtin_amdgcn_exp2f(other_max - base);
 #pragma unroll
-        for (int e = 0; e < 8; ++e) acc[e] += w * part[(8 * chunk + e) * kBlockQueries];
-    }
-    const float inverse = total > 0.f ? 1.0f / total : 0.f;
-    uint32_t packed[4];
+        for (int t = 0; t < D / 32; ++t)
 #pragma unroll
-    for (int e = 0; e < 4; ++e) packed[e] = bf16_rn(acc[2 * e] * inverse) | (bf16_rn(acc[2 * e + 1] * inverse) << 16);
-    uint16_t* dst = p.output + (int64_t)(q_begin + q) * p.output_stride + head * D + 8 * chunk;
-    reinterpret_cast<uint2*>(dst)[0] = make_uint2(packed[0], packed[1]);
-    reinterpret_cast<uint2*>(dst)[1] = make_uint2(packed[2], packed[3]);
+            for (int r = 0; r < 16; ++r)
+                st.out[t][r] = st.out[t][r] * mine +
+                               merge[(32 * t + 8 * (r >> 2) + 4 * half + (r & 3)) * 32 + column] * theirs;
+        write_block(st, sum_both * mine + other_sum * theirs);
+    }
 }
 
 }  // namespace
 
 size_t prefill_plan(PrefillParams& p, int64_t max_seqlen_k) {
+    (void)max_seqlen_k;
     p.query_blocks = (int)((p.max_seqlen_q + kBlockQueries - 1) / kBlockQueries);
-    p.max_tiles = (int)((max_seqlen_k + kBlockKeys - 1) / kBlockKeys);
-    p.split_tiles = kSplitTiles;
-    p.items = 0;
-    p.partial_slots = 0;
-    for (int block = 0; block < p.query_blocks; ++block) {
-        const int n = block_splits(p, block);
-        p.items += n;
-        if (n > 1) p.partial_slots += n;
-    }
-    return sizeof(float) * (size_t)p.batch * p.heads_q * p.partial_slots * (p.head_dim + 2) * kBlockQueries;
+    p.items = (p.query_blocks + 1) / 2;  // block pairs per (sequence, head)
+    return 0;                            // no workspace: blocks merge within their workgroup
 }
 
 hipError_t launch_prefill(const PrefillParams& p, hipStream_t stream) {
     if (p.batch == 0 || p.max_seqlen_q == 0 || p.items == 0) return hipSuccess;
     const dim3 grid((unsigned)p.items, (unsigned)p.heads_q, (unsigned)p.batch);
-    const dim3 merge_grid((unsigned)(p.query_blocks * (p.head_dim / 8)), (unsigned)p.heads_q, (unsigned)p.batch);
-    if (p.head_dim == 128) {
+    if (p.head_dim == 128)
         hipLaunchKernelGGL(prefill_kernel<128>, grid, dim3(kPrefillThreads), 0, stream, p);
-        if (p.partial_slots > 0)
-            hipLaunchKernelGGL(prefill_merge_kernel<128>, merge_grid, dim3(kBlockQueries), 0, stream, p);
-    } else if (p.head_dim == 96) {
+    else if (p.head_dim == 96)
         hipLaunchKernelGGL(prefill_kernel<96>, grid, dim3(kPrefillThreads), 0, stream, p);
-        if (p.partial_slots > 0)
-            hipLaunchKernelGGL(prefill_merge_kernel<96>, merge_grid, dim3(kBlockQueries), 0, stream, p);
-    } else {
+    else
         return hipErrorInvalidValue;
-    }
     return hipGetLastError();
 }
 

@@ -68,18 +68,11 @@ struct PrefillParams {
     int max_seqlen_q;
     int causal;
     float softmax_scale;
-    // Key-split plan (prefill_plan in prefill.hip): query block qb of a
-    // sequence is cut into splits(qb) work items of at most split_tiles key
-    // tiles; blocks with more than one split write FP32 partials
-    // [slot][D + 2][128] (rows D, D + 1: running max, sum) that the merge
-    // kernel combines.
+    // Plan (prefill_plan in prefill.hip): each workgroup takes a pair of
+    // 128-query blocks of one (sequence, head) and merges within itself, so
+    // no workspace is needed.
     int query_blocks;         // ceil(max_seqlen_q / 128)
-    int max_tiles;            // ceil(max_seqlen_k / 64)
-    int causal_same;          // causal with equal query/key lengths: block qb needs <= 2 (qb + 1) tiles
-    int split_tiles;
-    int items;                // work items per (head, sequence)
-    int partial_slots;        // partial slots per (head, sequence)
-    float* partials;
+    int items;                // block pairs per (head, sequence)
 };
 
 constexpr int kPrefillBlockQueries = 128;

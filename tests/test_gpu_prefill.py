@@ -39,9 +39,11 @@ CASES = [
     ([129, 64], None, 8, 2, 128, True),
     ([40, 90], [100, 90], 2, 2, 128, True),
     ([77, 5], [33, 140], 2, 1, 96, False),
-    # long enough for key splits and the partial merge
+    # long enough for many block pairs, the merge of a heavy block's halves and the lone middle block
     ([1500, 700], None, 2, 2, 128, True),
     ([300, 200], [1300, 1250], 2, 1, 96, False),
+    ([640, 130], [700, 200], 2, 2, 128, True),   # keys beyond the queries (bottom-right alignment)
+    ([3, 260], [1, 70], 2, 2, 96, True),         # first rows that see no key
 ]
 
 
@@ -110,9 +112,9 @@ def test_prefill_long_prompt_edges(oracle, device):
 
 
 def test_prefill_split_merge_repeats_exactly(device):
-    """Blocks whose keys are split over several work items are merged from
-    FP32 partials; repeated calls, and calls of other shapes in between, give
-    bit-identical outputs."""
+    """Heavy blocks whose keys are split over the two wave groups of a
+    workgroup are merged in LDS; repeated calls, and calls of other shapes in
+    between, give bit-identical outputs."""
     n, heads, dim = 3000, 4, 128
     q, k, v = (_random((n, heads, dim), s).to(device) for s in (11, 12, 13))
     cu = torch.tensor([0, n], dtype=torch.int32, device=device)
