@@ -31,6 +31,8 @@
 // Lane layouts of v_mfma_f32_32x32x16_bf16 (checked on gfx950): A row l % 32,
 // k 8 (l / 32) + e; B column l % 32, k 8 (l / 32) + e; C register r holds row
 // 8 (r / 4) + 4 (l / 32) + r % 4, column l % 32.
+#include <type_traits>
+
 #include "rq_device.h"
 #include "rq_kernels.h"
 
@@ -59,6 +61,21 @@ __device__ __forceinline__ Bf16x8 load8(const uint16_t* src) {
     const uint2 a = reinterpret_cast<const uint2*>(src)[0];
     const uint2 b = reinterpret_cast<const uint2*>(src)[1];
     return __builtin_bit_cast(Bf16x8, make_uint4(a.x, a.y, b.x, b.y));
+}
+
+// The value of lane l and of lane l ^ 32, low half first in every lane
+// (v_permlane32_swap, one VALU op instead of an LDS permute round trip).
+__device__ __forceinline__ float2 halves(float v) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return make_float2(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float halves_max(float v) {
+    const float2 h = halves(v);
+    return fmaxf(h.x, h.y);
+}
+__device__ __forceinline__ float halves_sum(float v) {
+    const float2 h = halves(v);
+    return h.x + h.y;
 }
 
 template <int D>
@@ -108,12 +125,12 @@ void prefill_kernel(PrefillParams p) {
     const int kv_head = head / p.group;
 
     // Keys a block's queries may see and the key tiles that covers.
-    auto block_keys = [&](int block) {
+    auto block_keys = [&](int block) __attribute__((always_inline)) {
         if (!p.causal) return k_len;
         const int limit = (block + 1) * kBlockQueries + shift;
         return limit < k_len ? (limit > 0 ? limit : 0) : k_len;
     };
-    auto block_tiles = [&](int block) { return (block_keys(block) + kBlockKeys - 1) / kBlockKeys; };
+    auto block_tiles = [&](int block) __attribute__((always_inline)) { return (block_keys(block) + kBlockKeys - 1) / kBlockKeys; };
 
     const int heavy = n_blocks - 1 - item;
     const int light = item < heavy ? item : -1;
@@ -132,19 +149,19 @@ void prefill_kernel(PrefillParams p) {
     const int half = lane >> 5;
 
     // (block, tile) of this group at a step, or block -1 when idle.
-    auto step_block = [&](int step) {
+    auto step_block = [&](int step) __attribute__((always_inline)) {
         if (group == 0) return step < split ? heavy : -1;
         if (step < light_tiles) return light;
         return step - light_tiles < heavy_tiles - split ? heavy : -1;
     };
-    auto step_tile = [&](int step) {
+    auto step_tile = [&](int step) __attribute__((always_inline)) {
         if (group == 0) return step;
         return step < light_tiles ? step : split + step - light_tiles;
     };
 
     uint16_t* group_lds = lds + group * L::kGroupHalves;
-    auto k_tile_of = [&](int buffer) { return group_lds + buffer * L::kKHalves; };
-    auto v_tile_of = [&](int buffer) { return group_lds + 2 * L::kKHalves + buffer * L::kVHalves; };
+    auto k_tile_of = [&](int buffer) __attribute__((always_inline)) { return group_lds + buffer * L::kKHalves; };
+    auto v_tile_of = [&](int buffer) __attribute__((always_inline)) { return group_lds + 2 * L::kKHalves + buffer * L::kVHalves; };
 
     // Tile loads: each thread of a group fetches K chunks (row, 8 channels) and
     // V units (key pair, 8 channels) of its group's next tile into registers
@@ -171,43 +188,50 @@ void prefill_kernel(PrefillParams p) {
     }
     const uint16_t* k_base = p.key + (int64_t)k_begin * p.key_stride + kv_head * D;
     const uint16_t* v_base = p.value + (int64_t)k_begin * p.value_stride + kv_head * D;
-    auto tile_resource = [&](const uint16_t* base, int64_t row_elements, int kt) {
+    auto tile_resource = [&](const uint16_t* base, int64_t row_elements, int kt) __attribute__((always_inline)) {
         // Bytes from row kt to the end of the tile's last valid row (its D
-        // channels); at most one tile of rows, so the count stays small.
-        const int64_t remaining = k_len - kt < kBlockKeys ? k_len - kt : kBlockKeys;
+        // channels); at most one tile of rows, so the count stays small.  A
+        // negative kt (no tile) gives an empty resource: every load reads zero.
+        const int64_t remaining = kt < 0 ? 0 : (k_len - kt < kBlockKeys ? k_len - kt : kBlockKeys);
         const uint32_t bytes = remaining > 0 ? (uint32_t)((remaining - 1) * row_elements * 2 + D * 2) : 0u;
-        return __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(base + (int64_t)kt * row_elements), (short)0,
-                                                 (int)bytes, 0x00020000);
+        return __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(base + (int64_t)(kt < 0 ? 0 : kt) * row_elements),
+                                                 (short)0, (int)bytes, 0x00020000);
     };
-    uint4 k_next[kKChunks], v_next[kVUnits][2];
-    auto fetch = [&](int kt) {
+    // Two register slots: the tile staged at the end of step s was loaded
+    // during step s - 1, so its loads have a whole step of compute to land.
+    uint4 k_next[2][kKChunks], v_next[2][kVUnits][2];
+    auto fetch = [&](auto slot_tag, int kt) __attribute__((always_inline)) {
+        constexpr int slot = decltype(slot_tag)::value;
         const auto k_rsrc = tile_resource(k_base, p.key_stride, kt);
         const auto v_rsrc = tile_resource(v_base, p.value_stride, kt);
 #pragma unroll
         for (int i = 0; i < kKChunks; ++i)
-            k_next[i] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(k_rsrc, k_offset[i], 0, 0));
+            k_next[slot][i] =
+                __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(k_rsrc, k_offset[i], 0, 0));
 #pragma unroll
         for (int i = 0; i < kVUnits; ++i) {
-            v_next[i][0] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(v_rsrc, v_offset[i], 0, 0));
-            v_next[i][1] = __builtin_bit_cast(
+            v_next[slot][i][0] =
+                __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(v_rsrc, v_offset[i], 0, 0));
+            v_next[slot][i][1] = __builtin_bit_cast(
                 uint4, __builtin_amdgcn_raw_buffer_load_b128(v_rsrc, v_offset[i] + value_row_bytes, 0, 0));
         }
     };
-    auto stage = [&](int buffer) {
+    auto stage = [&](auto slot_tag, int buffer) __attribute__((always_inline)) {
+        constexpr int slot = decltype(slot_tag)::value;
         uint16_t* k_tile = k_tile_of(buffer);
         uint16_t* v_tile = v_tile_of(buffer);
 #pragma unroll
         for (int i = 0; i < kKChunks; ++i) {
             const int chunk = group_thread + i * kGroupThreads;
             if (chunk < kBlockKeys * (D / 8))
-                *reinterpret_cast<uint4*>(&k_tile[(chunk / (D / 8)) * KS + 8 * (chunk % (D / 8))]) = k_next[i];
+                *reinterpret_cast<uint4*>(&k_tile[(chunk / (D / 8)) * KS + 8 * (chunk % (D / 8))]) = k_next[slot][i];
         }
 #pragma unroll
         for (int i = 0; i < kVUnits; ++i) {
             const int unit = group_thread + i * kGroupThreads;
             const int pair = unit % (kBlockKeys / 2), chunk = unit / (kBlockKeys / 2);
             if (unit < (kBlockKeys / 2) * (D / 8)) {
-                const uint4 a = v_next[i][0], b = v_next[i][1];
+                const uint4 a = v_next[slot][i][0], b = v_next[slot][i][1];
                 const uint32_t av[4] = {a.x, a.y, a.z, a.w}, bv[4] = {b.x, b.y, b.z, b.w};
                 uint16_t* target = &v_tile[(8 * chunk) * VS + 2 * pair];
 #pragma unroll
@@ -227,7 +251,7 @@ void prefill_kernel(PrefillParams p) {
     BlockState<D> st;
     Bf16x8 q_operand[D / 16];
     int cur_block = -1, wave_q0 = 0, wave_keys = 0, my_q = 0, my_limit = 0;
-    auto begin_block = [&](int block) {
+    auto begin_block = [&](int block) __attribute__((always_inline)) {
         cur_block = block;
         wave_q0 = block * kBlockQueries + 32 * group_wave;
         my_q = wave_q0 + column;
@@ -250,7 +274,7 @@ void prefill_kernel(PrefillParams p) {
         st.running_sum = 0.f;
     };
     // Normalised BF16 output rows of the running block.
-    auto write_block = [&](const BlockState<D>& s, float total_sum) {
+    auto write_block = [&](const BlockState<D>& s, float total_sum) __attribute__((always_inline)) {
         if (my_q >= q_len) return;
         const float inverse = total_sum > 0.f ? 1.0f / total_sum : 0.f;
         uint16_t* dst = p.output + (int64_t)(q_begin + my_q) * p.output_stride + head * D + 4 * half;
@@ -265,7 +289,7 @@ void prefill_kernel(PrefillParams p) {
     };
 
     // One key tile of the running block.
-    auto compute_tile = [&](int kt, const uint16_t* k_tile, const uint16_t* v_tile) {
+    auto compute_tile = [&](int kt, const uint16_t* k_tile, const uint16_t* v_tile) __attribute__((always_inline)) {
         // S^T for two sub-tiles of 32 keys: register r of lane l holds key
         // kt + 32 sub + 8 (r / 4) + 4 half + r % 4 against query my_q.
         F32x16 s[2];
@@ -299,7 +323,7 @@ void prefill_kernel(PrefillParams p) {
 #pragma unroll
                 for (int r = 0; r < 16; ++r) tile_max = fmaxf(tile_max, s[sub][r]);
         }
-        tile_max = fmaxf(tile_max, __shfl_xor(tile_max, 32)) * c;
+        tile_max = halves_max(tile_max) * c;
         // Lazy max: keep the running max unless the tile exceeds it by more
         // than 2^8; the weights then stay below 256 and cancel in the final
         // normalisation.
@@ -355,40 +379,66 @@ void prefill_kernel(PrefillParams p) {
         begin_block(heavy);
     else if (light >= 0)
         begin_block(light);
-    if (steps > 0 && step_block(0) >= 0) {
-        fetch(step_tile(0) * kBlockKeys);
-        stage(0);
-    }
+    // While group B works on L its tile at each step is A's (both start at
+    // key tile 0): A stages that tile once and both groups read A's buffer.
+    // Under full (non-causal) attention every step is shared this way.
+    const int shared_steps = light >= 0 ? (light_tiles < split ? light_tiles : split) : 0;
+    auto own_tile = [&](int step) __attribute__((always_inline)) { return group == 0 || step >= shared_steps; };
+    // Tile loads two steps ahead: step s computes tile s, stages tile s + 1
+    // (loaded during step s - 1) and loads tile s + 2.  A group's tiles past
+    // its last, and B's shared ones, read zeros (an empty resource) and are
+    // staged where nobody reads them.
+    auto tile_key = [&](int step) __attribute__((always_inline)) {
+        return step < steps && step_block(step) >= 0 && own_tile(step) ? step_tile(step) * kBlockKeys : -1;
+    };
+    using Slot0 = std::integral_constant<int, 0>;
+    using Slot1 = std::integral_constant<int, 1>;
+    fetch(Slot0{}, tile_key(0));
+    stage(Slot0{}, 0);
+    fetch(Slot1{}, tile_key(1));
     __syncthreads();
-    for (int step = 0; step < steps; ++step) {
-        // Buffer step & 1 holds this step's tile; every wave finished reading
-        // the other one before the barrier that ended the previous step.
+    auto run_step = [&](auto slot_tag, int step) __attribute__((always_inline)) {
+        // slot_tag: the register slot of tile step + 1 (step + 1 & 1).
+        constexpr int next_slot = decltype(slot_tag)::value;
         const int block = step_block(step);
-        const int next_block = step + 1 < steps ? step_block(step + 1) : -1;
-        if (next_block >= 0) fetch(step_tile(step + 1) * kBlockKeys);
-        if (block >= 0) {
-            if (block != cur_block) {
-                // Group B moves to H's tail: its L (if any) is complete.
-                if (cur_block >= 0) write_block(st, st.running_sum + __shfl_xor(st.running_sum, 32));
-                begin_block(block);
-            }
-            const int kt = step_tile(step) * kBlockKeys;
-            if (kt < wave_keys) compute_tile(kt, k_tile_of(step & 1), v_tile_of(step & 1));
+        if (block >= 0 && block != cur_block) {
+            // Group B moves to H's tail: its L (if any) is complete.  Before
+            // the tile loads below, so that waiting for the new Q operand
+            // never waits for them (loads retire in issue order).
+            if (cur_block >= 0) write_block(st, halves_sum(st.running_sum));
+            begin_block(block);
         }
-        if (next_block >= 0) stage((step + 1) & 1);
+        // The loads are issued unconditionally and held here: as two blocks
+        // under one condition the compiler merged the loads into the staging
+        // after the compute, and every step waited a full round trip.
+        fetch(std::integral_constant<int, 1 - next_slot>{}, tile_key(step + 2));
+        __asm__ volatile("" ::: "memory");
+        if (block >= 0) {
+            const int kt = step_tile(step) * kBlockKeys;
+            const uint16_t* tiles = own_tile(step) ? group_lds : lds;  // shared steps read A's buffers
+            if (kt < wave_keys)
+                compute_tile(kt, tiles + (step & 1) * L::kKHalves, tiles + 2 * L::kKHalves + (step & 1) * L::kVHalves);
+        }
+        stage(slot_tag, (step + 1) & 1);
         __syncthreads();
+    };
+    // Buffer step & 1 holds step's tile; every wave finished reading the
+    // other one before the barrier that ended the previous step.
+    for (int step = 0; step < steps; step += 2) {
+        run_step(Slot1{}, step);
+        if (step + 1 < steps) run_step(Slot0{}, step + 1);
     }
 
     const bool handoff = split < heavy_tiles;  // group B holds part of H
     if (!handoff) {
         // A's H and B's L (if any) are complete.
-        if (cur_block >= 0) write_block(st, st.running_sum + __shfl_xor(st.running_sum, 32));
+        if (cur_block >= 0) write_block(st, halves_sum(st.running_sum));
         return;
     }
     // B's partial for H to LDS as [wave][row][query]: rows 0..D-1 the output,
     // D the running max (log2 units), D + 1 the running sum (both halves).
     float* merge = reinterpret_cast<float*>(lds) + group_wave * (D + 2) * 32;
-    const float sum_both = st.running_sum + __shfl_xor(st.running_sum, 32);
+    const float sum_both = halves_sum(st.running_sum);
     if (group == 1) {
 #pragma unroll
         for (int t = 0; t < D / 32; ++t)
