@@ -38,6 +38,7 @@ PEAK_BF16_TFLOPS = 2500.0
 SCHEDULE = ((2, 32), (2, 32), (2, 32), (4, 32))
 QUANTIZE_SCHEDULE = ((2, 16), (2, 16), (2, 32), (4, 32))
 HUGINN_SCHEDULE = ((2, 16), (2, 16), (2, 16), (4, 32))
+ADJACENT_SCHEDULE = ((4, 32), (2, 32), (2, 32), (2, 32))
 ANCHOR = 3
 
 
@@ -45,12 +46,13 @@ def log(*args):
     print(*args, file=sys.stderr, flush=True)
 
 
-def staged_call_bytes(batch, history, heads, dim, page_tokens, loop, schedule=SCHEDULE):
+def staged_call_bytes(batch, history, heads, dim, page_tokens, loop, schedule=SCHEDULE, mode="anchor",
+                      anchor=ANCHOR):
     """Algorithmic HBM bytes of one decode call (packed pages + Q/K/V/out + page table)."""
     from residualquant_amd.layout import staged_bytes
 
     pages = (history + page_tokens - 1) // page_tokens
-    per_page = staged_bytes(dim, schedule, page_tokens, "anchor", ANCHOR, loop)
+    per_page = staged_bytes(dim, schedule, page_tokens, mode, anchor, loop)
     cache = batch * pages * heads * 2 * per_page
     live = 4 * batch * heads * dim * 2
     table = batch * pages * 4
@@ -62,7 +64,7 @@ def bf16_call_bytes(batch, history, heads, dim):
 
 
 def build_packed_cache(torch, rq, workloads, batch, history, heads, dim, page_tokens, device, seed,
-                       schedule=SCHEDULE):
+                       schedule=SCHEDULE, mode="anchor", anchor=ANCHOR):
     """Quantize synthetic K/V for every history token into a packed paged cache (on the GPU)."""
     pages = (history + page_tokens - 1) // page_tokens
     table = workloads.block_tables(batch, pages, seed + 5, device=device)
@@ -76,7 +78,7 @@ def build_packed_cache(torch, rq, workloads, batch, history, heads, dim, page_to
     for start in range(0, slots.numel(), chunk):
         part = slots[start:start + chunk]
         pairs = workloads.loop_kv(part.numel(), heads, dim, len(schedule), seed + start, device=device)
-        rq.quantize(pairs, cache, part, key_rotation, value_rotation, None, schedule, "anchor", ANCHOR, "ls")
+        rq.quantize(pairs, cache, part, key_rotation, value_rotation, None, schedule, mode, anchor, "ls")
         del pairs
     torch.cuda.synchronize()
     return cache, table, key_rotation, value_rotation
@@ -591,6 +593,86 @@ def run_multiquery(args):
     print(json.dumps(result), flush=True)
 
 
+def run_adjacent(args):
+    """Adjacent-mode decode at the C2 shape: every loop a residual of the
+    previous one ([4,32]+[2,32]x3, anchor 0), so loop L reads and rebuilds the
+    restore chain of records 0..L.  No BASELINE configuration uses this mode;
+    it measures decode_chain_kernel (loops 1-3)."""
+    import torch
+
+    import residualquant_amd as rq
+    from residualquant_amd import ops, workloads
+
+    device = torch.device("cuda:0")
+    torch.cuda.set_device(device)
+    batch, history, heads, dim, page_tokens = args.batch, args.history, 16, 128, 16
+    schedule = ADJACENT_SCHEDULE
+    seed = 2027
+    log(f"[bench] building adjacent-mode packed cache B={batch} T={history} H={heads} D={dim}")
+    cache, table, key_rotation, value_rotation = build_packed_cache(
+        torch, rq, workloads, batch, history, heads, dim, page_tokens, device, seed, schedule, "adjacent", 0)
+    generator = torch.Generator(device=device).manual_seed(seed + 7)
+    query = torch.randn((batch, heads, dim), generator=generator, device=device).to(torch.bfloat16)
+    key = torch.randn((batch, heads, dim), generator=generator, device=device).to(torch.bfloat16)
+    value = torch.randn((batch, heads, dim), generator=generator, device=device).to(torch.bfloat16)
+    output = torch.empty_like(query)
+    qsl = torch.arange(batch + 1, dtype=torch.int32, device=device)
+    seq_lens = torch.full((batch,), history + 1, dtype=torch.int32, device=device)
+    workspace = torch.empty(ops.attention_workspace_bytes(batch, heads, dim, table.size(1), page_tokens),
+                            dtype=torch.uint8, device=device)
+
+    def call(loop):
+        rq.attention(query, key, value, cache, output, qsl, seq_lens, table, key_rotation, value_rotation,
+                     None, schedule, "adjacent", 0, loop, workspace=workspace)
+
+    def step():
+        for loop in range(len(schedule)):
+            call(loop)
+
+    settle(torch, step, 0.3)
+    reps = max(50, args.steps)
+    durations = kernel_durations_ms(ops, [lambda loop=loop: call(loop) for loop in range(4)], reps)
+    per_loop_ms = [statistics.median(d) for d in durations]
+    loop_bytes = [staged_call_bytes(batch, history, heads, dim, page_tokens, loop, schedule, "adjacent", 0)
+                  for loop in range(4)]
+    for loop in range(4):
+        log(f"[bench] adjacent loop {loop}: {per_loop_ms[loop] * 1e3:.1f} us "
+            f"({loop_bytes[loop] / (per_loop_ms[loop] * 1e-3) / 1e9:.0f} GB/s on {loop_bytes[loop] / 1e6:.1f} MB)")
+    step_ms = sum(per_loop_ms)
+    last = loop_bytes[3] / (per_loop_ms[3] * 1e-3) / 1e9
+    result = {
+        "metric": "adjacent-mode paged decode GB/s (restore chain), 1 GPU",
+        "value": sum(loop_bytes) / (step_ms * 1e-3) / 1e9,
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": reps,
+        "warmup": 10,
+        "ms_per_step": step_ms,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "int2/int4 packed codes, bf16 restore chain, fp32 accumulate",
+        "data": "synthetic (seeded anchor N(0,1) + loop residuals N(0,0.15^2), random-sign Hadamard rotations)",
+        "config": {"workload": "adjacent-mode decode at the C2 shape (no BASELINE configuration)",
+                   "batch": batch, "history_tokens": history, "heads": heads, "head_dim": dim,
+                   "page_tokens": page_tokens, "schedule": "[4,32]+[2,32]x3 adjacent anchor 0"},
+        "timing": "per-loop median of HIP events around each launch (step order) after a settle phase",
+        "per_loop_us": [ms * 1e3 for ms in per_loop_ms],
+        "per_loop_bytes": loop_bytes,
+        "roofline": {
+            "bound": "hbm",
+            "achieved": last,
+            "peak": PEAK_HBM_GBPS,
+            "unit": "GB/s",
+            "frac": last / PEAK_HBM_GBPS,
+            "traffic": None,
+            "kernel": "decode_chain_kernel<128,16> at loop 3 (the chain of all 4 records)",
+        },
+        "cpu_baseline": None,
+    }
+    print(json.dumps(result), flush=True)
+
+
 def run_huginn(args):
     """C4: Huginn-shaped deep-loop decode attention, 55 heads x D96, g16 residuals, B8 x T4096.
 
@@ -788,12 +870,14 @@ def run_step(args):
 
 def main():
     parser = argparse.ArgumentParser(description=__doc__)
-    parser.add_argument("--workload", choices=("decode", "quantize", "prefill", "step", "huginn", "multiquery"),
+    parser.add_argument("--workload", choices=("decode", "quantize", "prefill", "step", "huginn", "multiquery",
+                                               "adjacent"),
                         default="decode",
                         help="decode: C2 paged decode attention (the headline); quantize: C1 quantize-on-write; "
                              "prefill: causal prompt attention; step: C3 looped-model decode step; "
                              "huginn: C4 deep-loop decode attention (55 heads x D96, g16); "
-                             "multiquery: several rows per request over the C2 history (multi-row MFMA kernels)")
+                             "multiquery: several rows per request over the C2 history (multi-row MFMA kernels); "
+                             "adjacent: adjacent-mode decode at the C2 shape (the restore-chain kernel)")
     parser.add_argument("--rows-per-request", type=int, default=4, help="multiquery: query rows per request")
     parser.add_argument("--no-sweep", action="store_true", help="step workload: batch 32 x 8k only")
     parser.add_argument("--tokens", type=int, default=4096, help="tokens per quantize call or prompt")
@@ -826,6 +910,9 @@ def main():
         return
     if args.workload == "step":
         run_step(args)
+        return
+    if args.workload == "adjacent":
+        run_adjacent(args)
         return
     if args.workload == "huginn":
         run_huginn(args)

@@ -1544,35 +1544,64 @@ __device__ __forceinline__ void bf16_round2(float& a, float& b) {
     b = __uint_as_float(u & 0xffff0000u);
 }
 
-// BF16 values (as FP32) of the lane's 32 channels [32 lq, 32 lq + 32) of one
-// record at token row `tok` of the page: bf16(code * scale + offset).
+// The raw bytes of one record of one token that a lane needs for its 32
+// channels [32 lq, 32 lq + 32): code words (16 bytes INT4, 8 bytes INT2), the
+// FP8 scale and offset of its groups (one byte each for G32, two for G16) and
+// the BF16 alpha.  Loading every record of a unit before decoding any lets all
+// of their round trips overlap.
+struct ChainRaw {
+    uint4 codes;
+    uint32_t params;  // FP8 scale byte(s) in the low 16 bits, offset byte(s) in the high 16
+    uint32_t alpha;
+};
+
 template <int D, int PT>
-__device__ __forceinline__ void chain_record(__amdgpu_buffer_rsrc_t page, const RecordRegion& reg, int tok,
-                                             int lq, float (&out)[32]) {
+__device__ __forceinline__ void chain_load(__amdgpu_buffer_rsrc_t page, const RecordRegion& reg, int tok, int lq,
+                                           bool with_alpha, ChainRaw& raw) {
     using Policy = PagePolicy<D>;
     const uint32_t params = reg.offset + PT * reg.code_bytes + tok * reg.groups;
-    float scale[2], offset[2];
+    uint32_t scale, offset;
     if (reg.group == 32) {
-        const uint32_t s = __builtin_amdgcn_raw_buffer_load_b8(page, params + lq, 0, Policy::kParams);
-        const uint32_t o = __builtin_amdgcn_raw_buffer_load_b8(page, params + PT * reg.groups + lq, 0, Policy::kParams);
-        scale[0] = scale[1] = fp8_f32<0>(s) * 512.0f;
-        offset[0] = offset[1] = fp8_f32<0>(o);
+        scale = __builtin_amdgcn_raw_buffer_load_b8(page, params + lq, 0, Policy::kParams);
+        offset = __builtin_amdgcn_raw_buffer_load_b8(page, params + PT * reg.groups + lq, 0, Policy::kParams);
     } else {
-        const uint32_t s = __builtin_amdgcn_raw_buffer_load_b16(page, params + 2 * lq, 0, Policy::kParams);
-        const uint32_t o = __builtin_amdgcn_raw_buffer_load_b16(page, params + PT * reg.groups + 2 * lq, 0, Policy::kParams);
-        scale[0] = fp8_f32<0>(s) * 512.0f;
-        scale[1] = fp8_f32<1>(s) * 512.0f;
-        offset[0] = fp8_f32<0>(o);
-        offset[1] = fp8_f32<1>(o);
+        scale = __builtin_amdgcn_raw_buffer_load_b16(page, params + 2 * lq, 0, Policy::kParams);
+        offset = __builtin_amdgcn_raw_buffer_load_b16(page, params + PT * reg.groups + 2 * lq, 0, Policy::kParams);
     }
-    // A code c held in a byte is the FP8 E4M3 value c * 2^-9 (scale carries 2^9).
+    raw.params = scale | (offset << 16);
     const uint32_t codes = reg.offset + tok * reg.code_bytes;
     if (reg.bits == 4) {
         const auto v = __builtin_amdgcn_raw_buffer_load_b128(page, codes + 16 * lq, 0, Policy::kCodes);
+        raw.codes = make_uint4(v[0], v[1], v[2], v[3]);
+    } else {
+        const auto v = __builtin_amdgcn_raw_buffer_load_b64(page, codes + 8 * lq, 0, Policy::kCodes);
+        raw.codes = make_uint4(v[0], v[1], 0u, 0u);
+    }
+    raw.alpha = with_alpha ? __builtin_amdgcn_raw_buffer_load_b16(
+                                 page, reg.offset + PT * (reg.code_bytes + 2 * reg.groups) + 2 * tok, 0, Policy::kParams)
+                           : 0u;
+}
+
+// BF16 values (as FP32) of the lane's 32 channels of one record:
+// bf16(code * scale + offset).
+__device__ __forceinline__ void chain_decode(const ChainRaw& raw, const RecordRegion& reg, float (&out)[32]) {
+    float scale[2], offset[2];
+    if (reg.group == 32) {
+        scale[0] = scale[1] = fp8_f32<0>(raw.params) * 512.0f;
+        offset[0] = offset[1] = fp8_f32<2>(raw.params);
+    } else {
+        scale[0] = fp8_f32<0>(raw.params) * 512.0f;
+        scale[1] = fp8_f32<1>(raw.params) * 512.0f;
+        offset[0] = fp8_f32<2>(raw.params);
+        offset[1] = fp8_f32<3>(raw.params);
+    }
+    // A code c held in a byte is the FP8 E4M3 value c * 2^-9 (scale carries 2^9).
+    const uint32_t w[4] = {raw.codes.x, raw.codes.y, raw.codes.z, raw.codes.w};
+    if (reg.bits == 4) {
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             const int h = i >> 1;
-            const int lo = (int)(v[i] & 0x0f0f0f0fu), hi = (int)((v[i] >> 4) & 0x0f0f0f0fu);
+            const int lo = (int)(w[i] & 0x0f0f0f0fu), hi = (int)((w[i] >> 4) & 0x0f0f0f0fu);
             const auto l01 = __builtin_amdgcn_cvt_pk_f32_fp8(lo, false);
             const auto l23 = __builtin_amdgcn_cvt_pk_f32_fp8(lo, true);
             const auto h01 = __builtin_amdgcn_cvt_pk_f32_fp8(hi, false);
@@ -1582,12 +1611,11 @@ __device__ __forceinline__ void chain_record(__amdgpu_buffer_rsrc_t page, const 
             for (int k = 0; k < 8; ++k) out[8 * i + k] = fmaf(c[k], scale[h], offset[h]);
         }
     } else {
-        const auto v = __builtin_amdgcn_raw_buffer_load_b64(page, codes + 8 * lq, 0, Policy::kCodes);
 #pragma unroll
         for (int i = 0; i < 2; ++i)
 #pragma unroll
             for (int k = 0; k < 4; ++k) {
-                const int part = (int)((v[i] >> (2 * k)) & 0x03030303u);  // byte j: channel 4j + k
+                const int part = (int)((w[i] >> (2 * k)) & 0x03030303u);  // byte j: channel 4j + k
                 const auto c01 = __builtin_amdgcn_cvt_pk_f32_fp8(part, false);
                 const auto c23 = __builtin_amdgcn_cvt_pk_f32_fp8(part, true);
                 out[16 * i + k] = fmaf(c01[0], scale[i], offset[i]);
@@ -1600,8 +1628,12 @@ __device__ __forceinline__ void chain_record(__amdgpu_buffer_rsrc_t page, const 
     for (int i = 0; i < 32; i += 2) bf16_round2(out[i], out[i + 1]);
 }
 
-template <int D, int PT>
-__global__ __launch_bounds__(kDecodeThreads) void decode_chain_kernel(AttentionParams p) {
+// Links = records in the chain (2..4).  A wave's units are software
+// pipelined: the raw bytes of its next unit are loaded before the current
+// unit is decoded, scored and accumulated.
+template <int D, int PT, int Links>
+__global__ __launch_bounds__(kDecodeThreads) __attribute__((amdgpu_waves_per_eu(2)))
+void decode_chain_kernel(AttentionParams p) {
     constexpr int Quarters = D / 32;
     constexpr int UnitsPerPage = PT / kUnitTokens;
     const int lane = threadIdx.x & 63;
@@ -1614,7 +1646,6 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_chain_kernel(AttentionP
     const int64_t rh = blockIdx.x / p.splits;
     const int head = (int)(rh % p.heads);
     const int64_t row = rh / p.heads;
-    const int links = p.chain_length;  // records 0 .. L
     __shared__ __attribute__((aligned(16))) float prep_lds[kPrepFloats];
     // bf16(mu_r) of records 0 .. L - 1 (the K plane's chain), FP32.
     __shared__ __attribute__((aligned(16))) float mean_lds[kMaxRecords][128];
@@ -1639,7 +1670,7 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_chain_kernel(AttentionP
     range.unit_end = uniform64(range.unit_end);
     float* partial = p.partials + (rh * p.splits + split) * (int64_t)(D + 2);
 
-    for (int i = threadIdx.x; i < (links - 1) * 128; i += kDecodeThreads) {
+    for (int i = threadIdx.x; i < (Links - 1) * 128; i += kDecodeThreads) {
         const int r = i / 128, c = i % 128;
         mean_lds[r][c] = (p.key_mean_all != nullptr && c < D)
                              ? bf16_f32(bf16_rn(p.key_mean_all[((int64_t)r * p.heads + head) * D + c]))
@@ -1652,73 +1683,106 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_chain_kernel(AttentionP
         for (int i = threadIdx.x; i < kPrepFloats; i += kDecodeThreads) prep_lds[i] = src[i];
         __syncthreads();
     }
-    // q' of the lane's channels (FP32, log2 units, scale folded in).
-    float qv[32];
-#pragma unroll
-    for (int i = 0; i < 32; ++i) qv[i] = prep_lds[kPrepScalars + 32 * lq + i];
+    // q' of the lane's channels (FP32, log2 units, scale folded in) stays in
+    // LDS and is read per unit: 32 registers fewer keep two waves per SIMD.
+    const float4* qv4 = reinterpret_cast<const float4*>(prep_lds + kPrepScalars + 32 * lq);
 
     const ConstantInt32* table =
         (const ConstantInt32*)(p.block_table + (int64_t)range.request * p.block_table_stride);
     const int64_t page_bytes = (int64_t)PT * p.page_width;
     const bool has_mean = p.key_mean_all != nullptr;
+    RecordRegion regs[Links];
+#pragma unroll
+    for (int r = 0; r < Links; ++r) regs[r] = p.chain[r];
+
+    // Raw bytes of every record of a unit, K and V planes.  Units past the
+    // split read zeros (an empty page resource).
+    ChainRaw rk[Links], rv[Links];
+    struct UnitPages {
+        __amdgpu_buffer_rsrc_t k, v;
+        int tok;
+        bool ok;
+    };
+    auto unit_pages = [&](int64_t u) {
+        const bool inside = u < range.unit_end;
+        const int block = inside ? table[u / UnitsPerPage] : -1;
+        const bool ok = block >= 0 && block < p.num_blocks;
+        const uint8_t* kbase = p.cache + (ok ? ((int64_t)block * p.heads + head) * page_bytes : 0);
+        const uint32_t bytes = ok ? (uint32_t)page_bytes : 0u;
+        return UnitPages{page_resource(kbase, bytes), page_resource(kbase + (ok ? p.plane_stride : 0), bytes),
+                         (int)(u % UnitsPerPage) * kUnitTokens + t, ok};
+    };
+    auto load_plane = [&](__amdgpu_buffer_rsrc_t page, int tok, ChainRaw (&raw)[Links]) {
+#pragma unroll
+        for (int r = 0; r < Links; ++r) chain_load<D, PT>(page, regs[r], tok, lq, r > 0, raw[r]);
+    };
+    // The chain X_0 = bf16(c s + o), X_r = bf16(alpha_r X_{r-1} + bf16(c s + o))
+    // of one plane, the K plane adding bf16(mu_r) to every record but the last.
+    auto build_chain = [&](const ChainRaw (&raw)[Links], bool key_plane, float (&x)[32]) {
+#pragma unroll
+        for (int r = 0; r < Links; ++r) {
+            // One record at a time: interleaved by the scheduler, the records'
+            // 32-channel temporaries pushed the kernel to one wave per SIMD.
+            __builtin_amdgcn_sched_barrier(0);
+            float xr[32];
+            chain_decode(raw[r], regs[r], xr);
+            if (key_plane && has_mean && r + 1 < Links) {
+#pragma unroll
+                for (int i = 0; i < 32; i += 2) {
+                    xr[i] += mean_lds[r][32 * lq + i];
+                    xr[i + 1] += mean_lds[r][32 * lq + i + 1];
+                    bf16_round2(xr[i], xr[i + 1]);
+                }
+            }
+            if (r == 0) {
+#pragma unroll
+                for (int i = 0; i < 32; ++i) x[i] = xr[i];
+            } else {
+                const float alpha = bf16_f32(raw[r].alpha);
+#pragma unroll
+                for (int i = 0; i < 32; i += 2) {
+                    x[i] = fmaf(x[i], alpha, xr[i]);
+                    x[i + 1] = fmaf(x[i + 1], alpha, xr[i + 1]);
+                    bf16_round2(x[i], x[i + 1]);
+                }
+            }
+        }
+    };
 
     float acc[32];
 #pragma unroll
     for (int i = 0; i < 32; ++i) acc[i] = 0.f;
     float m = -INFINITY, l = 0.f;
 
-    for (int64_t u = range.unit_begin + wave; u < range.unit_end; u += kWaves) {
-        const int block = table[u / UnitsPerPage];
-        const bool ok = block >= 0 && block < p.num_blocks;
-        const uint8_t* kbase = p.cache + (ok ? ((int64_t)block * p.heads + head) * page_bytes : 0);
-        const uint32_t bytes = ok ? (uint32_t)page_bytes : 0u;
-        const __amdgpu_buffer_rsrc_t kpage = page_resource(kbase, bytes);
-        const __amdgpu_buffer_rsrc_t vpage = page_resource(kbase + (ok ? p.plane_stride : 0), bytes);
-        const int tok = (int)(u % UnitsPerPage) * kUnitTokens + t;
+    // Software pipeline over a wave's units: a plane's raw registers take the
+    // next unit's bytes as soon as this unit's chain of that plane is built,
+    // so the loads overlap the rest of the unit (the other plane's chain, the
+    // softmax and the accumulation).
+    int64_t u = range.unit_begin + wave;
+    UnitPages pages = unit_pages(u);
+    load_plane(pages.k, pages.tok, rk);
+    load_plane(pages.v, pages.tok, rv);
+    for (; u < range.unit_end; u += kWaves) {
         const int64_t pos = u * kUnitTokens + t;
-        const bool valid = ok && lane_active && pos < range.history;
-
-        float kx[32], vx[32];
-        for (int r = 0; r < links; ++r) {
-            const RecordRegion reg = p.chain[r];
-            float kr[32], vr[32];
-            chain_record<D, PT>(kpage, reg, tok, lq, kr);
-            chain_record<D, PT>(vpage, reg, tok, lq, vr);
-            if (has_mean && r + 1 < links) {
-#pragma unroll
-                for (int i = 0; i < 32; i += 2) {
-                    kr[i] += mean_lds[r][32 * lq + i];
-                    kr[i + 1] += mean_lds[r][32 * lq + i + 1];
-                    bf16_round2(kr[i], kr[i + 1]);
-                }
-            }
-            if (r == 0) {
-#pragma unroll
-                for (int i = 0; i < 32; ++i) {
-                    kx[i] = kr[i];
-                    vx[i] = vr[i];
-                }
-            } else {
-                const uint32_t alpha_offset = reg.offset + PT * (reg.code_bytes + 2 * reg.groups) + 2 * tok;
-                const float ak = bf16_f32(__builtin_amdgcn_raw_buffer_load_b16(kpage, alpha_offset, 0, PagePolicy<D>::kParams));
-                const float av = bf16_f32(__builtin_amdgcn_raw_buffer_load_b16(vpage, alpha_offset, 0, PagePolicy<D>::kParams));
-#pragma unroll
-                for (int i = 0; i < 32; i += 2) {
-                    kx[i] = fmaf(kx[i], ak, kr[i]);
-                    kx[i + 1] = fmaf(kx[i + 1], ak, kr[i + 1]);
-                    vx[i] = fmaf(vx[i], av, vr[i]);
-                    vx[i + 1] = fmaf(vx[i + 1], av, vr[i + 1]);
-                    bf16_round2(kx[i], kx[i + 1]);
-                    bf16_round2(vx[i], vx[i + 1]);
-                }
-            }
-        }
-
+        const bool valid = pages.ok && lane_active && pos < range.history;
+        const UnitPages next = unit_pages(u + kWaves);
+        float x[32];
+        build_chain(rk, true, x);
+        load_plane(next.k, next.tok, rk);
         float s[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int i = 0; i < 32; ++i) s[i & 3] = fmaf(qv[i], kx[i], s[i & 3]);
+        for (int i = 0; i < 8; ++i) {
+            const float4 q4 = qv4[i];
+            s[0] = fmaf(q4.x, x[4 * i], s[0]);
+            s[1] = fmaf(q4.y, x[4 * i + 1], s[1]);
+            s[2] = fmaf(q4.z, x[4 * i + 2], s[2]);
+            s[3] = fmaf(q4.w, x[4 * i + 3], s[3]);
+        }
         float score = quad_sum_fast(lane_active ? (s[0] + s[1]) + (s[2] + s[3]) : 0.f);
         score = valid ? score : -INFINITY;
+        build_chain(rv, false, x);
+        load_plane(next.v, next.tok, rv);
+        pages = next;
         const float unit_max = wave_max(score);
         if (unit_max > m) {
             const float factor = m == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m - unit_max);
@@ -1730,7 +1794,7 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_chain_kernel(AttentionP
         const float prob = valid ? __builtin_amdgcn_exp2f(score - m) : 0.f;
         l += prob;
 #pragma unroll
-        for (int i = 0; i < 32; ++i) acc[i] = fmaf(prob, vx[i], acc[i]);
+        for (int i = 0; i < 32; ++i) acc[i] = fmaf(prob, x[i], acc[i]);
     }
 
     if (p.splits == 1) {
@@ -1880,6 +1944,24 @@ bool dispatch_anchor(const AttentionParams& p, hipStream_t stream) {
     return false;
 }
 
+template <int D, int PT>
+bool launch_chain_pt(const AttentionParams& p, hipStream_t stream) {
+    const unsigned blocks = (unsigned)(p.rows * p.heads * p.splits);
+    switch (p.chain_length) {
+        case 2: hipLaunchKernelGGL((decode_chain_kernel<D, PT, 2>), dim3(blocks), dim3(kDecodeThreads), 0, stream, p); return true;
+        case 3: hipLaunchKernelGGL((decode_chain_kernel<D, PT, 3>), dim3(blocks), dim3(kDecodeThreads), 0, stream, p); return true;
+        case 4: hipLaunchKernelGGL((decode_chain_kernel<D, PT, 4>), dim3(blocks), dim3(kDecodeThreads), 0, stream, p); return true;
+        default: return false;
+    }
+}
+
+template <int D>
+bool launch_chain(const AttentionParams& p, hipStream_t stream) {
+    if (p.page_tokens == 16) return launch_chain_pt<D, 16>(p, stream);
+    if (p.page_tokens == 32) return launch_chain_pt<D, 32>(p, stream);
+    return false;
+}
+
 template <int D>
 hipError_t launch_all(const AttentionParams& p, hipStream_t stream, hipEvent_t begin, hipEvent_t end,
                       bool bf16) {
@@ -1891,13 +1973,7 @@ hipError_t launch_all(const AttentionParams& p, hipStream_t stream, hipEvent_t b
         const unsigned blocks = (unsigned)(p.rows * p.heads * p.splits);
         hipLaunchKernelGGL((decode_bf16_kernel<D>), dim3(blocks), dim3(kDecodeThreads), 0, stream, p);
     } else if (p.chain_length > 1) {
-        const unsigned blocks = (unsigned)(p.rows * p.heads * p.splits);
-        if (p.page_tokens == 16)
-            hipLaunchKernelGGL((decode_chain_kernel<D, 16>), dim3(blocks), dim3(kDecodeThreads), 0, stream, p);
-        else if (p.page_tokens == 32)
-            hipLaunchKernelGGL((decode_chain_kernel<D, 32>), dim3(blocks), dim3(kDecodeThreads), 0, stream, p);
-        else
-            return hipErrorInvalidValue;
+        if (!launch_chain<D>(p, stream)) return hipErrorInvalidValue;
     } else if (!dispatch_anchor<D>(p, stream)) {
         return hipErrorInvalidValue;
     }
