@@ -762,7 +762,8 @@ def run_huginn(args):
             "step": "one loop group: 3 residual-loop calls + 1 anchor-loop call",
         },
         "us_per_step": step_s * 1e6,
-        "timing": "one HIP-graph replay of the 4 calls per step",
+        "timing": "one HIP-graph replay of the 4 calls per step, timed after >= 0.2 s of untimed replays; "
+                  "per-call medians of HIP events after a settle phase",
         "pct_peak_step": 100.0 * step_bytes / step_s / 1e9 / PEAK_HBM_GBPS,
         "bytes_per_step": step_bytes,
         "decode_kernel": {
