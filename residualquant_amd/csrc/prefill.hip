@@ -15,15 +15,17 @@
 // first a = ceil((T(H) + T(L)) / 2) tiles; group B takes all of L, then H's
 // remaining tiles; at the end B hands its partial (max, sum, output) for H to
 // A through LDS and A merges and writes H.  Both groups run the same number
-// of tile steps between workgroup barriers; each stages its own tiles (K
-// row-major, V transposed) into its own double buffer.
+// of tile steps between workgroup barriers; each loads its own K and V tiles
+// (row-major, chunk-swizzled) into its own double buffer with DMA loads
+// straight into LDS, one tile ahead.
 //
 // Per wave: 32 queries.  S^T = K Q^T with v_mfma_f32_32x32x16_bf16, so lane l
 // owns query l % 32: the row max is in-lane plus one exchange between the
 // wave's halves, and the probabilities P^T stay in the accumulator registers
 // as the B operand of O^T += V^T P^T, with the key order of each P.V step
-// permuted to match the accumulator layout (the A operand reads V^T at the
-// same keys).  The row max moves lazily: the output is rescaled only when a
+// permuted to match the accumulator layout.  The A operand V^T comes from the
+// row-major V tile through transposed LDS reads (ds_read_b64_tr_b16) at the
+// same keys.  The row max moves lazily: the output is rescaled only when a
 // row's max grows by more than 2^8 (P then stays below 256, exact in the
 // final normalisation), and each half-wave keeps its own row sum until the
 // end.
@@ -31,7 +33,6 @@
 // Lane layouts of v_mfma_f32_32x32x16_bf16 (checked on gfx950): A row l % 32,
 // k 8 (l / 32) + e; B column l % 32, k 8 (l / 32) + e; C register r holds row
 // 8 (r / 4) + 4 (l / 32) + r % 4, column l % 32.
-#include <type_traits>
 
 #include "rq_device.h"
 #include "rq_kernels.h"
@@ -78,18 +79,51 @@ __device__ __forceinline__ float halves_sum(float v) {
     return h.x + h.y;
 }
 
+// LDS of a workgroup: per group, two buffers of [K tile | V tile], each tile
+// 64 rows of D BF16 with no padding, filled by DMA loads (buffer_load ... lds:
+// lane l of a load writes its 16 bytes at the load's LDS base + 16 l).  The
+// 16-byte chunk c of row r sits at position c ^ swizzle(r) of its row, which
+// keeps the MFMA operand reads free of bank conflicts:
+// - K (ds_read_b128, lane = row, one chunk): 16 consecutive rows at one
+//   chunk fall on distinct banks (8 at D = 96, whose 192-byte rows already
+//   spread rows 0..3);
+// - V^T (ds_read_b64_tr_b16, 16 lanes read 4 consecutive rows x 2 adjacent
+//   chunks): the 4 rows fall on distinct banks (by the row length at D = 96).
 template <int D>
 struct Lds {
-    static constexpr int KS = D + 8;               // K tile row stride (halves)
-    static constexpr int VS = kBlockKeys + 4;      // V^T tile row stride (halves)
-    static constexpr int kKHalves = kBlockKeys * KS;
-    static constexpr int kVHalves = D * VS;
-    static constexpr int kGroupHalves = 2 * (kKHalves + kVHalves);  // double-buffered K and V^T
-    static constexpr int kBytes = 2 * kGroupHalves * 2;
+    static constexpr int kChunks = D / 8;                  // 16-byte chunks per row
+    static constexpr int kRowBytes = 2 * D;
+    static constexpr int kTileBytes = kBlockKeys * kRowBytes;
+    static constexpr int kBufferBytes = 2 * kTileBytes;    // K tile, then V tile
+    static constexpr int kGroupBytes = 2 * kBufferBytes;   // double-buffered
+    static constexpr int kBytes = 2 * kGroupBytes;
+    static constexpr int kLoadsPerWave = kChunks / kGroupWaves;  // 1 KB DMA loads per wave, tile and plane
+    static_assert(kBlockKeys * kChunks == 64 * kGroupWaves * kLoadsPerWave, "a tile is whole 1 KB loads");
     // The merge hand-off reuses the tiles: [wave][D + 2][32] floats.
     static constexpr int kMergeBytes = kGroupWaves * (D + 2) * 32 * 4;
     static_assert(kMergeBytes <= kBytes, "merge buffer fits in the tile buffers");
+
+    __device__ static int k_swizzle(int row) { return D == 128 ? (row & 15) : ((row >> 2) & 1); }
+    __device__ static int v_swizzle(int row) { return D == 128 ? 4 * (row & 3) : 0; }
 };
+
+typedef short Short4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) void LdsVoid;
+typedef __attribute__((address_space(3))) Short4 LdsShort4;
+
+// ds_read_b64_tr_b16 (gfx950, checked on the device): within each 16 lanes,
+// output lane o gets element o % 4 of the 8 bytes addressed by lanes
+// o / 4 + 4 p, p = 0..3.  With lane 4a + b addressing row a, channels
+// 4b..4b+3 of a 4-row block, lane o receives channel o of rows 0..3.
+__device__ __forceinline__ Short4 read_transposed(const char* p) {
+    return __builtin_amdgcn_ds_read_tr16_b64_v4i16((LdsShort4*)p);
+}
+
+// One DMA load: lane l's 16 bytes at `offset` of the resource go to
+// lds + 16 l (lds wave-uniform).
+__device__ __forceinline__ void load_to_lds(__amdgpu_buffer_rsrc_t rsrc, char* lds, uint32_t offset) {
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, (LdsVoid*)lds, 16, offset, 0, 0, 0);
+}
 
 // One query block's running state for a wave's 32 queries.
 template <int D>
@@ -102,8 +136,7 @@ template <int D>
 __global__ __launch_bounds__(kPrefillThreads) __attribute__((amdgpu_waves_per_eu(2)))
 void prefill_kernel(PrefillParams p) {
     using L = Lds<D>;
-    constexpr int KS = L::KS, VS = L::VS;
-    __shared__ __attribute__((aligned(16))) uint16_t lds[L::kBytes / 2];
+    __shared__ __attribute__((aligned(1024))) char lds[L::kBytes];
 
     // XCD-aware order: workgroups are dispatched round-robin over the 8
     // XCDs, so the linear id is remapped to give each XCD a run of
@@ -140,10 +173,11 @@ void prefill_kernel(PrefillParams p) {
     const int split = heavy_tiles < (total + 1) / 2 ? heavy_tiles : (total + 1) / 2;  // A: heavy [0, split)
     const int steps = split > total - split ? split : total - split;
 
-    const int wave = threadIdx.x >> 6;
+    // Wave-uniform by construction; readfirstlane tells the compiler, so the
+    // tile resources stay in SGPRs (no waterfall loop around each load).
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int group = wave >> 2;  // 0: A, 1: B
     const int group_wave = wave & 3;
-    const int group_thread = threadIdx.x & (kGroupThreads - 1);
     const int lane = threadIdx.x & 63;
     const int column = lane & 31;
     const int half = lane >> 5;
@@ -159,91 +193,62 @@ void prefill_kernel(PrefillParams p) {
         return step < light_tiles ? step : split + step - light_tiles;
     };
 
-    uint16_t* group_lds = lds + group * L::kGroupHalves;
-    auto k_tile_of = [&](int buffer) __attribute__((always_inline)) { return group_lds + buffer * L::kKHalves; };
-    auto v_tile_of = [&](int buffer) __attribute__((always_inline)) { return group_lds + 2 * L::kKHalves + buffer * L::kVHalves; };
+    char* group_lds = lds + group * L::kGroupBytes;
 
-    // Tile loads: each thread of a group fetches K chunks (row, 8 channels) and
-    // V units (key pair, 8 channels) of its group's next tile into registers
-    // while the current tile computes, then stages them (V transposed) into
-    // the other buffer.  Raw buffer loads from a wave-uniform resource rebased
-    // at each tile: rows past the sequence read as zero without a branch.
-    constexpr int kKChunks = (kBlockKeys * (D / 8) + kGroupThreads - 1) / kGroupThreads;
-    constexpr int kVUnits = ((kBlockKeys / 2) * (D / 8) + kGroupThreads - 1) / kGroupThreads;
-    constexpr uint32_t kOutOfRange = 0x80000000u;  // beyond any tile's record count: loads zero
+    // Tile loads: DMA from a wave-uniform buffer resource rebased at each
+    // tile straight into LDS (no registers, no staging pass); rows past the
+    // sequence lie outside the resource and arrive as zeros.  Wave w of a
+    // group fills the 1 KB slices w * kLoadsPerWave + j of both planes:
+    // slice slot s = 64 (w kLoadsPerWave + j) + lane holds chunk
+    // (s % kChunks) ^ swizzle(row) of row s / kChunks.
+    constexpr int kLoads = L::kLoadsPerWave;
     const uint32_t key_row_bytes = (uint32_t)p.key_stride * 2, value_row_bytes = (uint32_t)p.value_stride * 2;
-    uint32_t k_offset[kKChunks], v_offset[kVUnits];
+    uint32_t k_offset[kLoads], v_offset[kLoads];
 #pragma unroll
-    for (int i = 0; i < kKChunks; ++i) {
-        const int chunk = group_thread + i * kGroupThreads;
-        k_offset[i] = chunk < kBlockKeys * (D / 8) ? (uint32_t)(chunk / (D / 8)) * key_row_bytes + 16 * (chunk % (D / 8))
-                                                   : kOutOfRange;
-    }
-#pragma unroll
-    for (int i = 0; i < kVUnits; ++i) {
-        const int unit = group_thread + i * kGroupThreads;
-        v_offset[i] = unit < (kBlockKeys / 2) * (D / 8)
-                          ? (uint32_t)(2 * (unit % (kBlockKeys / 2))) * value_row_bytes + 16 * (unit / (kBlockKeys / 2))
-                          : kOutOfRange;
+    for (int j = 0; j < kLoads; ++j) {
+        const int slot = 64 * (group_wave * kLoads + j) + lane;
+        const int row = slot / L::kChunks, position = slot % L::kChunks;
+        k_offset[j] = (uint32_t)row * key_row_bytes + 16 * (position ^ L::k_swizzle(row));
+        v_offset[j] = (uint32_t)row * value_row_bytes + 16 * (position ^ L::v_swizzle(row));
     }
     const uint16_t* k_base = p.key + (int64_t)k_begin * p.key_stride + kv_head * D;
     const uint16_t* v_base = p.value + (int64_t)k_begin * p.value_stride + kv_head * D;
     auto tile_resource = [&](const uint16_t* base, int64_t row_elements, int kt) __attribute__((always_inline)) {
         // Bytes from row kt to the end of the tile's last valid row (its D
-        // channels); at most one tile of rows, so the count stays small.  A
-        // negative kt (no tile) gives an empty resource: every load reads zero.
-        const int64_t remaining = kt < 0 ? 0 : (k_len - kt < kBlockKeys ? k_len - kt : kBlockKeys);
+        // channels); at most one tile of rows, so the count stays small.
+        const int64_t remaining = k_len - kt < kBlockKeys ? k_len - kt : kBlockKeys;
         const uint32_t bytes = remaining > 0 ? (uint32_t)((remaining - 1) * row_elements * 2 + D * 2) : 0u;
-        return __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(base + (int64_t)(kt < 0 ? 0 : kt) * row_elements),
-                                                 (short)0, (int)bytes, 0x00020000);
+        return __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(base + (int64_t)kt * row_elements), (short)0,
+                                                 (int)bytes, 0x00020000);
     };
-    // Two register slots: the tile staged at the end of step s was loaded
-    // during step s - 1, so its loads have a whole step of compute to land.
-    uint4 k_next[2][kKChunks], v_next[2][kVUnits][2];
-    auto fetch = [&](auto slot_tag, int kt) __attribute__((always_inline)) {
-        constexpr int slot = decltype(slot_tag)::value;
+    // Loads of the tile starting at key kt into buffer `buffer` of this
+    // group; kt < 0 (no tile of this group's own) issues nothing.
+    auto fetch = [&](int kt, int buffer) __attribute__((always_inline)) {
+        if (kt < 0) return;
         const auto k_rsrc = tile_resource(k_base, p.key_stride, kt);
         const auto v_rsrc = tile_resource(v_base, p.value_stride, kt);
+        char* slices = group_lds + buffer * L::kBufferBytes + group_wave * kLoads * 1024;
 #pragma unroll
-        for (int i = 0; i < kKChunks; ++i)
-            k_next[slot][i] =
-                __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(k_rsrc, k_offset[i], 0, 0));
+        for (int j = 0; j < kLoads; ++j)
+            load_to_lds(k_rsrc, slices + j * 1024, k_offset[j]);
 #pragma unroll
-        for (int i = 0; i < kVUnits; ++i) {
-            v_next[slot][i][0] =
-                __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(v_rsrc, v_offset[i], 0, 0));
-            v_next[slot][i][1] = __builtin_bit_cast(
-                uint4, __builtin_amdgcn_raw_buffer_load_b128(v_rsrc, v_offset[i] + value_row_bytes, 0, 0));
-        }
+        for (int j = 0; j < kLoads; ++j) load_to_lds(v_rsrc, slices + L::kTileBytes + j * 1024, v_offset[j]);
     };
-    auto stage = [&](auto slot_tag, int buffer) __attribute__((always_inline)) {
-        constexpr int slot = decltype(slot_tag)::value;
-        uint16_t* k_tile = k_tile_of(buffer);
-        uint16_t* v_tile = v_tile_of(buffer);
-#pragma unroll
-        for (int i = 0; i < kKChunks; ++i) {
-            const int chunk = group_thread + i * kGroupThreads;
-            if (chunk < kBlockKeys * (D / 8))
-                *reinterpret_cast<uint4*>(&k_tile[(chunk / (D / 8)) * KS + 8 * (chunk % (D / 8))]) = k_next[slot][i];
-        }
-#pragma unroll
-        for (int i = 0; i < kVUnits; ++i) {
-            const int unit = group_thread + i * kGroupThreads;
-            const int pair = unit % (kBlockKeys / 2), chunk = unit / (kBlockKeys / 2);
-            if (unit < (kBlockKeys / 2) * (D / 8)) {
-                const uint4 a = v_next[slot][i][0], b = v_next[slot][i][1];
-                const uint32_t av[4] = {a.x, a.y, a.z, a.w}, bv[4] = {b.x, b.y, b.z, b.w};
-                uint16_t* target = &v_tile[(8 * chunk) * VS + 2 * pair];
-#pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    // (key, key + 1) pairs of channels 2e and 2e + 1.
-                    *reinterpret_cast<uint32_t*>(target + (2 * e) * VS) = __builtin_amdgcn_perm(bv[e], av[e], 0x05040100u);
-                    *reinterpret_cast<uint32_t*>(target + (2 * e + 1) * VS) =
-                        __builtin_amdgcn_perm(bv[e], av[e], 0x07060302u);
-                }
-            }
-        }
-    };
+    // This wave's DMA writes have landed (vmcnt counts them); a barrier
+    // after it publishes them to the workgroup.
+    auto wait_loads = [&]() __attribute__((always_inline)) { __builtin_amdgcn_s_waitcnt(0x0F70); };
+
+    // Per-lane byte offsets of the operand reads within a tile.
+    // K (A of S^T = K Q^T): row 32 sub + column, chunk 2 m + half.
+    const int k_lane = L::kRowBytes * column + 16 * (half ^ L::k_swizzle(column));
+    auto k_read = [&](int m) __attribute__((always_inline)) { return D == 128 ? (k_lane ^ (32 * m)) : (k_lane + 32 * m); };
+    // V^T (A of O^T += V^T P^T) by transposed reads: lane 16 g + 4 a + b
+    // (g = 2 h + g') addresses row 4 h + a of an 8-row block, channels
+    // 32 t + 16 g' + 4 b..+3, and receives channel 32 t + 16 g' + lane % 16 of
+    // rows 4 h..4 h + 3.
+    const int tr_a = (lane >> 2) & 3, tr_b = lane & 3, tr_g = (lane >> 4) & 1;
+    const int v_lane = L::kRowBytes * (4 * half + tr_a) + 16 * L::v_swizzle(tr_a) + 32 * tr_g + 8 * tr_b;
+    auto v_read = [&](int t) __attribute__((always_inline)) { return D == 128 ? (v_lane ^ (64 * t)) : (v_lane + 64 * t); };
 
     const float c = p.softmax_scale * 1.4426950408889634f;  // scores in log2 units
 
@@ -289,7 +294,7 @@ void prefill_kernel(PrefillParams p) {
     };
 
     // One key tile of the running block.
-    auto compute_tile = [&](int kt, const uint16_t* k_tile, const uint16_t* v_tile) __attribute__((always_inline)) {
+    auto compute_tile = [&](int kt, const char* k_tile, const char* v_tile) __attribute__((always_inline)) {
         // S^T for two sub-tiles of 32 keys: register r of lane l holds key
         // kt + 32 sub + 8 (r / 4) + 4 half + r % 4 against query my_q.
         F32x16 s[2];
@@ -297,10 +302,10 @@ void prefill_kernel(PrefillParams p) {
         for (int sub = 0; sub < 2; ++sub) {
 #pragma unroll
             for (int r = 0; r < 16; ++r) s[sub][r] = 0.f;
-            const uint16_t* k_row = &k_tile[(32 * sub + column) * KS + 8 * half];
+            const char* k_rows = k_tile + 32 * sub * L::kRowBytes;
 #pragma unroll
             for (int m = 0; m < D / 16; ++m)
-                s[sub] = mfma(*reinterpret_cast<const Bf16x8*>(k_row + 16 * m), q_operand[m], s[sub]);
+                s[sub] = mfma(*reinterpret_cast<const Bf16x8*>(k_rows + k_read(m)), q_operand[m], s[sub]);
         }
         // Raw scores: the scale is positive, so the row max of the scaled
         // scores is the scaled row max and is folded into the exp2 argument.
@@ -361,13 +366,14 @@ void prefill_kernel(PrefillParams p) {
         for (int sub = 0; sub < 2; ++sub)
 #pragma unroll
             for (int j = 0; j < 2; ++j) {
-                const int key_offset = 32 * sub + 16 * j + 4 * half;
+                const char* v_rows = v_tile + (32 * sub + 16 * j) * L::kRowBytes;
 #pragma unroll
                 for (int t = 0; t < D / 32; ++t) {
-                    const uint16_t* v_row = &v_tile[(32 * t + column) * VS + key_offset];
-                    const uint2 lo = *reinterpret_cast<const uint2*>(v_row);
-                    const uint2 hi = *reinterpret_cast<const uint2*>(v_row + 8);
-                    const Bf16x8 a = __builtin_bit_cast(Bf16x8, make_uint4(lo.x, lo.y, hi.x, hi.y));
+                    // Keys 4 half + 0..3 and 4 half + 8..11 of the 16, as P^T's k-slots.
+                    const Short4 lo = read_transposed(v_rows + v_read(t));
+                    const Short4 hi = read_transposed(v_rows + 8 * L::kRowBytes + v_read(t));
+                    const Bf16x8 a = __builtin_bit_cast(
+                        Bf16x8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
                     st.out[t] = mfma(a, p_operand[sub][j], st.out[t]);
                 }
             }
@@ -380,53 +386,35 @@ void prefill_kernel(PrefillParams p) {
     else if (light >= 0)
         begin_block(light);
     // While group B works on L its tile at each step is A's (both start at
-    // key tile 0): A stages that tile once and both groups read A's buffer.
+    // key tile 0): A loads that tile once and both groups read A's buffer.
     // Under full (non-causal) attention every step is shared this way.
     const int shared_steps = light >= 0 ? (light_tiles < split ? light_tiles : split) : 0;
     auto own_tile = [&](int step) __attribute__((always_inline)) { return group == 0 || step >= shared_steps; };
-    // Tile loads two steps ahead: step s computes tile s, stages tile s + 1
-    // (loaded during step s - 1) and loads tile s + 2.  A group's tiles past
-    // its last, and B's shared ones, read zeros (an empty resource) and are
-    // staged where nobody reads them.
+    // The key of a group's own tile at a step, or -1 (idle, or a shared step of B).
     auto tile_key = [&](int step) __attribute__((always_inline)) {
         return step < steps && step_block(step) >= 0 && own_tile(step) ? step_tile(step) * kBlockKeys : -1;
     };
-    using Slot0 = std::integral_constant<int, 0>;
-    using Slot1 = std::integral_constant<int, 1>;
-    fetch(Slot0{}, tile_key(0));
-    stage(Slot0{}, 0);
-    fetch(Slot1{}, tile_key(1));
+    // Step s computes tile s from buffer s & 1 while the DMA loads of tile
+    // s + 1 fill buffer (s + 1) & 1, which every wave finished reading
+    // before the barrier that ended step s - 1.
+    fetch(tile_key(0), 0);
+    wait_loads();
     __syncthreads();
-    auto run_step = [&](auto slot_tag, int step) __attribute__((always_inline)) {
-        // slot_tag: the register slot of tile step + 1 (step + 1 & 1).
-        constexpr int next_slot = decltype(slot_tag)::value;
+    for (int step = 0; step < steps; ++step) {
         const int block = step_block(step);
         if (block >= 0 && block != cur_block) {
-            // Group B moves to H's tail: its L (if any) is complete.  Before
-            // the tile loads below, so that waiting for the new Q operand
-            // never waits for them (loads retire in issue order).
+            // Group B moves to H's tail: its L (if any) is complete.
             if (cur_block >= 0) write_block(st, halves_sum(st.running_sum));
             begin_block(block);
         }
-        // The loads are issued unconditionally and held here: as two blocks
-        // under one condition the compiler merged the loads into the staging
-        // after the compute, and every step waited a full round trip.
-        fetch(std::integral_constant<int, 1 - next_slot>{}, tile_key(step + 2));
-        __asm__ volatile("" ::: "memory");
+        fetch(tile_key(step + 1), (step + 1) & 1);
         if (block >= 0) {
             const int kt = step_tile(step) * kBlockKeys;
-            const uint16_t* tiles = own_tile(step) ? group_lds : lds;  // shared steps read A's buffers
-            if (kt < wave_keys)
-                compute_tile(kt, tiles + (step & 1) * L::kKHalves, tiles + 2 * L::kKHalves + (step & 1) * L::kVHalves);
+            const char* buffer = (own_tile(step) ? group_lds : lds) + (step & 1) * L::kBufferBytes;
+            if (kt < wave_keys) compute_tile(kt, buffer, buffer + L::kTileBytes);
         }
-        stage(slot_tag, (step + 1) & 1);
+        wait_loads();
         __syncthreads();
-    };
-    // Buffer step & 1 holds step's tile; every wave finished reading the
-    // other one before the barrier that ended the previous step.
-    for (int step = 0; step < steps; step += 2) {
-        run_step(Slot1{}, step);
-        if (step + 1 < steps) run_step(Slot0{}, step + 1);
     }
 
     const bool handoff = split < heavy_tiles;  // group B holds part of H
