@@ -207,7 +207,7 @@ void multirow_stream_kernel(MultiRowParams p) {
     const int tile_end = tile_begin + per_split < tiles ? tile_begin + per_split : tiles;
 
     const int tid = threadIdx.x;
-    const int wave = tid >> 6;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // provably wave-uniform
     const int lane = tid & 63;
     const int column = lane & 31;
     const int half = lane >> 5;
@@ -377,7 +377,10 @@ void multirow_stream_kernel(MultiRowParams p) {
     auto fetch = [&](int unit_first, UnitBytes<BA, BL>& b) {
         const int row = unit_first % PT + unit_token;
         const int index = unit_first / PT - first_page;
-        const int block = (unit_first < history && index < split_pages) ? split_blocks[index] : -1;
+        // One unit per wave: the block id is wave-uniform, and readfirstlane
+        // keeps the page resources in SGPRs (no waterfall loop per load).
+        const int block = __builtin_amdgcn_readfirstlane(
+            (unit_first < history && index < split_pages) ? split_blocks[index] : -1);
         const uint8_t* k_page = p.cache + ((int64_t)(block >= 0 ? block : 0) * p.heads + head) * page_bytes;
         const uint32_t bytes = block >= 0 ? page_bytes : 0u;
         const auto k_rsrc = page_rsrc(k_page, bytes);
