@@ -601,13 +601,15 @@ struct SplitRange {
     int64_t history, unit_begin, unit_end;
 };
 
-__device__ __forceinline__ SplitRange split_range(const AttentionParams& p, int request, int split) {
+// The split's units of `request` whose sequence holds `seq_len` tokens (the
+// live one included).
+__device__ __forceinline__ SplitRange split_range_of(const AttentionParams& p, int request, int seq_len, int split) {
     SplitRange r;
     r.request = request;
     r.history = 0;
     r.unit_begin = r.unit_end = 0;
     if (r.request < 0) return r;
-    int64_t history = p.seq_lens[r.request] - 1;
+    int64_t history = (int64_t)seq_len - 1;
     if (history < 0) history = 0;
     int64_t pages = (history + p.page_tokens - 1) / p.page_tokens;
     if (pages > p.max_pages) pages = p.max_pages;
@@ -617,6 +619,36 @@ __device__ __forceinline__ SplitRange split_range(const AttentionParams& p, int 
     r.unit_begin = (split * pages / p.splits) * units_per_page;
     r.unit_end = ((split + 1) * pages / p.splits) * units_per_page;
     return r;
+}
+
+__device__ __forceinline__ SplitRange split_range(const AttentionParams& p, int request, int split) {
+    return split_range_of(p, request, request < 0 ? 0 : p.seq_lens[request], split);
+}
+
+// Request and split range of `row` for a workgroup that looks them up itself
+// (the fused prepare).  Decode batches map rows one-to-one to requests
+// (query_start_loc = 0, 1, 2, ...), so request `row` is tried first: its two
+// query_start_loc bounds and its sequence length are read with scalar loads
+// issued together, one round trip, where the lookup and then the length read
+// would take two or more.  Any other mapping takes the parallel lookup.
+// Workgroup-uniform; the lookup's barrier is taken by every thread or none.
+__device__ __forceinline__ SplitRange fused_range(const AttentionParams& p, int64_t row, int split, int* lds_counts) {
+    SplitRange none;
+    none.request = -1;
+    none.history = none.unit_begin = none.unit_end = 0;
+    if (p.requests <= 0) return none;
+    const ConstantInt32* qsl = (const ConstantInt32*)p.query_start_loc;
+    const ConstantInt32* lens = (const ConstantInt32*)p.seq_lens;
+    const int64_t guess = row < p.requests ? row : p.requests - 1;
+    const int lo = qsl[guess], hi = qsl[guess + 1], len = lens[guess];
+    // Everything below uses all three values before any branch, so the three
+    // loads are issued together (with a short-circuit test the compiler
+    // branches after each one and serialises the round trips).
+    const bool own = (lo <= row) & (row < hi);
+    const SplitRange guessed = split_range_of(p, (int)guess, len, split);
+    if (own) return guessed;
+    const int request = find_request_parallel(p.query_start_loc, p.requests, row, lds_counts);
+    return split_range_of(p, request, request < 0 ? 0 : lens[request], split);
 }
 
 // Wave max of one value per token, broadcast to every lane (quad lanes agree).
@@ -852,21 +884,20 @@ void decode_kernel(AttentionParams p) {
     // otherwise prepare_kernel has written the record.  The request lookup
     // comes first either way, so the first units' page loads are in flight
     // while the query record is computed (the loop's first iteration uses them).
-    int request;
+    SplitRange range;
     PrepareInputs<D, kDecodeThreads> in;
     _Float16* rotation_lds = reinterpret_cast<_Float16*>(scratch_lds);
     if (p.fused_prepare) {
         prepare_load<D, kDecodeThreads>(p, row, head, in);
-        request = find_request_parallel(p.query_start_loc, p.requests, row, request_counts);
-        if (request >= 0) prepare_stage<D, kDecodeThreads>(p, in, rotation_lds);
+        range = fused_range(p, row, split, request_counts);
+        if (range.request >= 0) prepare_stage<D, kDecodeThreads>(p, in, rotation_lds);
     } else {
-        request = p.row_request[row];
+        range = split_range(p, p.row_request[row], split);
     }
-    if (request < 0) return;
+    if (range.request < 0) return;
     // The range is the same in every lane; kept in scalar registers so the
     // block table below is read with scalar loads.
-    request = __builtin_amdgcn_readfirstlane(request);
-    SplitRange range = split_range(p, request, split);
+    range.request = __builtin_amdgcn_readfirstlane(range.request);
     range.history = uniform64(range.history);
     range.unit_begin = uniform64(range.unit_begin);
     range.unit_end = uniform64(range.unit_end);
@@ -1322,19 +1353,18 @@ void decode96_kernel(AttentionParams p) {
 
     // Query record and request lookup as in decode_kernel: the lookup first,
     // so the first iteration's page loads overlap the record's arithmetic.
-    int request;
+    SplitRange range;
     PrepareInputs<D, kDecodeThreads> in;
     _Float16* rotation_lds = reinterpret_cast<_Float16*>(scratch_lds);
     if (p.fused_prepare) {
         prepare_load<D, kDecodeThreads>(p, row, head, in);
-        request = find_request_parallel(p.query_start_loc, p.requests, row, request_counts);
-        if (request >= 0) prepare_stage<D, kDecodeThreads>(p, in, rotation_lds);
+        range = fused_range(p, row, split, request_counts);
+        if (range.request >= 0) prepare_stage<D, kDecodeThreads>(p, in, rotation_lds);
     } else {
-        request = p.row_request[row];
+        range = split_range(p, p.row_request[row], split);
     }
-    if (request < 0) return;
-    request = __builtin_amdgcn_readfirstlane(request);
-    SplitRange range = split_range(p, request, split);
+    if (range.request < 0) return;
+    range.request = __builtin_amdgcn_readfirstlane(range.request);
     range.history = uniform64(range.history);
     range.unit_begin = uniform64(range.unit_begin);
     range.unit_end = uniform64(range.unit_end);
@@ -1652,19 +1682,18 @@ void decode_chain_kernel(AttentionParams p) {
     __shared__ __attribute__((aligned(16))) float scratch_lds[kWaves * 16 * 128];
     __shared__ int request_counts[kWaves];
 
-    int request;
+    SplitRange range;
     PrepareInputs<D, kDecodeThreads> in;
     _Float16* rotation_lds = reinterpret_cast<_Float16*>(scratch_lds);
     if (p.fused_prepare) {
         prepare_load<D, kDecodeThreads>(p, row, head, in);
-        request = find_request_parallel(p.query_start_loc, p.requests, row, request_counts);
-        if (request >= 0) prepare_stage<D, kDecodeThreads>(p, in, rotation_lds);
+        range = fused_range(p, row, split, request_counts);
+        if (range.request >= 0) prepare_stage<D, kDecodeThreads>(p, in, rotation_lds);
     } else {
-        request = p.row_request[row];
+        range = split_range(p, p.row_request[row], split);
     }
-    if (request < 0) return;
-    request = __builtin_amdgcn_readfirstlane(request);
-    SplitRange range = split_range(p, request, split);
+    if (range.request < 0) return;
+    range.request = __builtin_amdgcn_readfirstlane(range.request);
     range.history = uniform64(range.history);
     range.unit_begin = uniform64(range.unit_begin);
     range.unit_end = uniform64(range.unit_end);
