@@ -55,21 +55,61 @@ __device__ __forceinline__ float quad_sum(float x) {
     return x + quad_xor2(x);
 }
 
-// Max / sum over the 16 tokens of a unit (lane bits 2..5).
+// Max over the 16 tokens of a unit (lane bits 2..5).
 __device__ __forceinline__ float token_max(float x) {
     x = fmaxf(x, __shfl_xor(x, 4));
     x = fmaxf(x, __shfl_xor(x, 8));
     x = fmaxf(x, __shfl_xor(x, 16));
     return fmaxf(x, __shfl_xor(x, 32));
 }
-__device__ __forceinline__ float token_sum(float x) {
-    x += __shfl_xor(x, 4);
-    x += __shfl_xor(x, 8);
-    x += __shfl_xor(x, 16);
-    return x + __shfl_xor(x, 32);
-}
 
 __device__ __forceinline__ float f16_f32(uint16_t h) { return (float)__builtin_bit_cast(_Float16, h); }
+
+// Reductions over the 16 lanes of a DPP row (lanes 16r..16r+15), the result
+// in every lane of the row: quad exchanges, then rotations by 4 and 8 (each
+// step a VALU operation, where a lane shuffle is an LDS round trip).
+template <int Ctrl>
+__device__ __forceinline__ int dpp_i(int x) {
+    return __builtin_amdgcn_update_dpp(0, x, Ctrl, 0xF, 0xF, true);
+}
+__device__ __forceinline__ float row_sum16(float x) {
+    x += __int_as_float(dpp_i<0xB1>(__float_as_int(x)));   // quad_perm [1,0,3,2]
+    x += __int_as_float(dpp_i<0x4E>(__float_as_int(x)));   // quad_perm [2,3,0,1]
+    x += __int_as_float(dpp_i<0x124>(__float_as_int(x)));  // row_ror:4
+    return x + __int_as_float(dpp_i<0x128>(__float_as_int(x)));  // row_ror:8
+}
+__device__ __forceinline__ float row_max16(float x) {
+    x = fmaxf(x, __int_as_float(dpp_i<0xB1>(__float_as_int(x))));
+    x = fmaxf(x, __int_as_float(dpp_i<0x4E>(__float_as_int(x))));
+    x = fmaxf(x, __int_as_float(dpp_i<0x124>(__float_as_int(x))));
+    return fmaxf(x, __int_as_float(dpp_i<0x128>(__float_as_int(x))));
+}
+// OR over the aligned 8 lanes of x's lane (quad exchanges, then the
+// half-row mirror pairs quad 0 with quad 1).
+__device__ __forceinline__ uint32_t or8(uint32_t x) {
+    x |= (uint32_t)dpp_i<0xB1>((int)x);
+    x |= (uint32_t)dpp_i<0x4E>((int)x);
+    return x | (uint32_t)dpp_i<0x141>((int)x);  // row_half_mirror
+}
+// OR over the 8 lanes of x's DPP row with the same lane parity.
+__device__ __forceinline__ uint32_t or_parity16(uint32_t x) {
+    x |= (uint32_t)dpp_i<0x4E>((int)x);
+    x |= (uint32_t)dpp_i<0x124>((int)x);
+    return x | (uint32_t)dpp_i<0x128>((int)x);
+}
+// Sum / max over the wave of row results (one readlane per row).
+__device__ __forceinline__ float rows_sum(float x) {
+    return (__int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), 0)) +
+            __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), 16))) +
+           (__int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), 32)) +
+            __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), 48)));
+}
+__device__ __forceinline__ float rows_max(float x) {
+    return fmaxf(fmaxf(__int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), 0)),
+                       __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), 16))),
+                 fmaxf(__int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), 32)),
+                       __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), 48))));
+}
 
 // FP8 E4M3 byte `sel` of v to FP32.  gfx950 converts OCP E4M3 in hardware.
 template <int Sel>
@@ -211,23 +251,20 @@ __device__ __forceinline__ void prepare_record(const AttentionParams& p, int hea
     // The anchor term of residual loops uses the BF16 mean (compute.cuh:327-336).
     parts[2] = (active && p.key_mean_anchor) ? qr * bf16_f32(bf16_rn(in.mean_anchor)) : 0.f;
     parts[3] = fabsf(qr);
-#pragma unroll
-    for (int d = 32; d; d >>= 1) {
-        parts[0] += __shfl_xor(parts[0], d);
-        parts[1] += __shfl_xor(parts[1], d);
-        parts[2] += __shfl_xor(parts[2], d);
-        parts[3] = fmaxf(parts[3], __shfl_xor(parts[3], d));
-    }
+    // Wave totals (row reductions, then one readlane per row).
+    const float wave_parts[4] = {rows_sum(row_sum16(parts[0])), rows_sum(row_sum16(parts[1])),
+                                 rows_sum(row_sum16(parts[2])), rows_max(row_max16(parts[3]))};
     if (lane == 0) {
 #pragma unroll
-        for (int i = 0; i < 4; ++i) totals[i][wave] = parts[i];
+        for (int i = 0; i < 4; ++i) totals[i][wave] = wave_parts[i];
     }
 
-    // Group sums of q' over 16 and 32 channels.
-    float q16 = qr;
-#pragma unroll
-    for (int d = 1; d < 16; d <<= 1) q16 += __shfl_xor(q16, d);
-    const float q32 = q16 + __shfl_xor(q16, 16);
+    // Group sums of q' over 16 channels (a DPP row) and 32 (two rows).
+    const float q16 = row_sum16(qr);
+    const float q32 = lane < 32 ? __int_as_float(__builtin_amdgcn_readlane(__float_as_int(q16), 0)) +
+                                      __int_as_float(__builtin_amdgcn_readlane(__float_as_int(q16), 16))
+                                : __int_as_float(__builtin_amdgcn_readlane(__float_as_int(q16), 32)) +
+                                      __int_as_float(__builtin_amdgcn_readlane(__float_as_int(q16), 48));
     __syncthreads();
 
     float sums[4] = {0.f, 0.f, 0.f, 0.f};
@@ -256,16 +293,10 @@ __device__ __forceinline__ void prepare_record(const AttentionParams& p, int hea
     for (int j = 0; j < 4; ++j) {
         const uint32_t nibble = (qu >> (4 * j)) & 15u;
         // INT4 order: word c/8, nibble c%8.
-        uint32_t w4 = nibble << (4 * (c & 7));
-        w4 |= __shfl_xor(w4, 1);
-        w4 |= __shfl_xor(w4, 2);
-        w4 |= __shfl_xor(w4, 4);
+        const uint32_t w4 = or8(nibble << (4 * (c & 7)));
         // INT2 order: 16-channel word c/16 split into even/odd channels,
         // nibble (c%16)/2 of nibble-word 2*(c/16) + c%2.
-        uint32_t w2 = nibble << (4 * ((c & 15) >> 1));
-        w2 |= __shfl_xor(w2, 2);
-        w2 |= __shfl_xor(w2, 4);
-        w2 |= __shfl_xor(w2, 8);
+        const uint32_t w2 = or_parity16(nibble << (4 * ((c & 15) >> 1)));
         if (active && (c & 7) == 0) planes4[j * 16 + c / 8] = w4;
         if (active && (c & 14) == 0) planes2[j * 16 + 2 * (c / 16) + (c & 1)] = w2;
     }
@@ -491,7 +522,11 @@ __device__ __forceinline__ SplitResult merge_waves(float (&acc)[32], float m, fl
     float (*red_acc)[16][128] = reinterpret_cast<float (*)[16][128]>(lds);
     __shared__ float red_m[kWaves], red_l[kWaves];
     const int t = lane >> 2, qd = lane & 3;
-    const float l_wave = token_sum((lane_active && qd == 0) ? l_lane : 0.f);
+    // Sum over the quarter-0 lanes: rotations within each row, then rows.
+    float l_rows = (lane_active && qd == 0) ? l_lane : 0.f;
+    l_rows += __int_as_float(dpp_i<0x124>(__float_as_int(l_rows)));
+    l_rows += __int_as_float(dpp_i<0x128>(__float_as_int(l_rows)));
+    const float l_wave = rows_sum(l_rows);
     if (lane == 0) {
         red_m[wave] = m;
         red_l[wave] = l_wave;
@@ -1281,9 +1316,7 @@ __device__ __forceinline__ SplitResult merge_waves_half(float (&acc)[48], float 
     constexpr int D = 96;
     float (*red_acc)[16][D] = reinterpret_cast<float (*)[16][D]>(lds);
     __shared__ float red_m[kWaves], red_l[kWaves];
-    float l_wave = l_lane;  // carried by the half-0 lanes only
-#pragma unroll
-    for (int d = 1; d < 64; d <<= 1) l_wave += __shfl_xor(l_wave, d);
+    const float l_wave = rows_sum(row_sum16(l_lane));  // carried by the half-0 lanes only
     if (lane == 0) {
         red_m[wave] = m;
         red_l[wave] = l_wave;
