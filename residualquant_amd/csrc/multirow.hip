@@ -5,17 +5,18 @@
 // products on the packed codes, so n rows of one request stream the
 // request's pages n times.  Here one workgroup takes a tile of up to 32 rows
 // of one (request, head) and a split of its history, streams each page once,
-// and dequantizes every 32-token tile into LDS as FP16 K (row-major) and BF16
-// V (transposed), so that the tile's rows share it through MFMA:
+// and dequantizes every 32-token tile into LDS as FP16 K and BF16 V (both
+// row-major; V is read transposed by ds_read_b64_tr_b16), so that the tile's
+// rows share it through MFMA:
 //   S^T = K Q'^T     (32 tokens x 32 rows, 8 v_mfma_f32_32x32x16_f16 over D = 128)
 //   O^T += V^T P^T   (128 channels x 32 rows, 8 v_mfma_f32_32x32x16_bf16)
 // The scores take FP16 operands (11-bit significands; each row of q' is
 // scaled by a power of two into [-1, 1], which the scores take back), since
 // BF16 operands there put the outlier channels' score error near the
-// 1e-3 mean bar on short histories.  V is a BF16 restore, exact in BF16.
-// with P kept in the accumulator registers (the token order of each P.V
-// step is permuted to match the accumulator layout, and V^T is read with the
-// same permutation).  Each of the four waves takes every fourth tile with
+// 1e-3 mean bar on short histories.  K and V are evaluated in FP32 (two fmas
+// per channel and plane) and rounded once, to FP16 and BF16.  P stays in the
+// accumulator registers (the token order of each P.V step is permuted to
+// match the accumulator layout, and V^T is read with the same permutation).  Each of the four waves takes every fourth tile with
 // its own online softmax; the waves meet once in LDS at the end and the
 // workgroup writes one partial (m, l, O) per row.  A finish launch per
 // (row, head) merges the splits, applies R_v^T and adds the live tokens.
@@ -23,8 +24,9 @@
 // Semantics (reference: attention/compute.cuh:397-505 keys, :28-107 values,
 // prepare.cuh:13-54 and :203-229 live score and mean shift, merge.cuh:8-84,
 // output.cuh:9-31): keys alpha_L (c.s+o + bf16(mu_A))_A + (c.s+o)_L with the
-// current loop's mean as a per-row shift, values the BF16 restore
-// bf16(alpha_L bf16(c.s+o)_A + bf16(c.s+o)_L), P in BF16.
+// current loop's mean as a per-row shift, values alpha_L (c.s+o)_A +
+// (c.s+o)_L (the reference rounds each restore step to BF16; one rounding
+// here, within the attention tolerance), P in BF16.
 //
 // Lane layouts of v_mfma_f32_32x32x16_bf16 (checked on gfx950): A row l % 32,
 // k 8 (l / 32) + e; B column l % 32, k 8 (l / 32) + e; C register r holds row
@@ -46,7 +48,8 @@ constexpr int kWaves = 4;
 constexpr int kTile = 32;            // tokens per MFMA tile (two 16-token units)
 constexpr int KS = D + 8;            // K tile row stride (BF16)
 constexpr int VS = kTile + 8;        // V^T tile row stride (BF16)
-constexpr int kWaveBytes = kTile * KS * 2 + D * VS * 2 + kTile * 4;  // K (FP16), V^T (BF16), alpha_K
+constexpr int kWaveBytes = kTile * KS * 2 + D * VS * 2 + kTile * 4;  // K (FP16), V (BF16), alpha_K
+static_assert(kTile * D <= D * VS, "the row-major V tile fits its region");
 constexpr int kLdsBytes = kWaves * kWaveBytes;
 // Prologue scratch (aliases the tiles): q^T FP32 [D][QTS], R_k FP16 [D][KS], q' FP16 [32][KS], mean dots
 // and row scales.
@@ -118,53 +121,98 @@ __device__ __forceinline__ void load_record(__amdgpu_buffer_rsrc_t page, const R
                       : 0u;
 }
 
-// code * scale + offset for the lane's 32 channels (exact in FP32).  A code
-// held in a byte is the FP8 E4M3 value code * 2^-9, so v_cvt_pk_f32_fp8
-// converts two codes per instruction and the scale carries the 2^9 back.
+// The lane's 32 codes of one record as FP32 code * 2^-9: a code held in a
+// byte is that FP8 E4M3 value, so v_cvt_pk_f32_fp8 converts two per
+// instruction (the scales carry the 2^9 back).
 template <int Bits>
-__device__ __forceinline__ void dequant(const RecordBytes<Bits>& r, int group, float (&x)[32]) {
-    const float s0 = __builtin_amdgcn_cvt_f32_fp8((int)r.scale, 0) * 512.0f;
-    const float o0 = __builtin_amdgcn_cvt_f32_fp8((int)r.offset, 0);
-    const float s1 = group == 32 ? s0 : __builtin_amdgcn_cvt_f32_fp8((int)r.scale, 1) * 512.0f;
-    const float o1 = group == 32 ? o0 : __builtin_amdgcn_cvt_f32_fp8((int)r.offset, 1);
+__device__ __forceinline__ void record_codes(const RecordBytes<Bits>& r, float (&c)[32]) {
     if constexpr (Bits == 4) {
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            const float s = i < 2 ? s0 : s1, o = i < 2 ? o0 : o1;
             const int lo = (int)(r.w[i] & 0x0f0f0f0fu);         // channels 8i + 0, 2, 4, 6
             const int hi = (int)((r.w[i] >> 4) & 0x0f0f0f0fu);  // channels 8i + 1, 3, 5, 7
             const auto l01 = __builtin_amdgcn_cvt_pk_f32_fp8(lo, false);
             const auto l23 = __builtin_amdgcn_cvt_pk_f32_fp8(lo, true);
             const auto h01 = __builtin_amdgcn_cvt_pk_f32_fp8(hi, false);
             const auto h23 = __builtin_amdgcn_cvt_pk_f32_fp8(hi, true);
-            float* a = x + 8 * i;
-            a[0] = fmaf(l01[0], s, o);
-            a[2] = fmaf(l01[1], s, o);
-            a[4] = fmaf(l23[0], s, o);
-            a[6] = fmaf(l23[1], s, o);
-            a[1] = fmaf(h01[0], s, o);
-            a[3] = fmaf(h01[1], s, o);
-            a[5] = fmaf(h23[0], s, o);
-            a[7] = fmaf(h23[1], s, o);
+            float* a = c + 8 * i;
+            a[0] = l01[0]; a[2] = l01[1]; a[4] = l23[0]; a[6] = l23[1];
+            a[1] = h01[0]; a[3] = h01[1]; a[5] = h23[0]; a[7] = h23[1];
         }
     } else {
 #pragma unroll
         for (int i = 0; i < 2; ++i) {
-            const float s = i == 0 ? s0 : s1, o = i == 0 ? o0 : o1;
-            float* a = x + 16 * i;
+            float* a = c + 16 * i;
 #pragma unroll
             for (int k = 0; k < 4; ++k) {
                 // byte j of part holds channel 4j + k
                 const int part = (int)((r.w[i] >> (2 * k)) & 0x03030303u);
                 const auto c01 = __builtin_amdgcn_cvt_pk_f32_fp8(part, false);
                 const auto c23 = __builtin_amdgcn_cvt_pk_f32_fp8(part, true);
-                a[k] = fmaf(c01[0], s, o);
-                a[4 + k] = fmaf(c01[1], s, o);
-                a[8 + k] = fmaf(c23[0], s, o);
-                a[12 + k] = fmaf(c23[1], s, o);
+                a[k] = c01[0]; a[4 + k] = c01[1]; a[8 + k] = c23[0]; a[12 + k] = c23[1];
             }
         }
     }
+}
+
+// Scale (times 2^9) and offset of the lane's two 16-channel blocks.
+__device__ __forceinline__ void record_coefficients(uint32_t scale, uint32_t offset, int group, float (&s)[2],
+                                                    float (&o)[2]) {
+    s[0] = __builtin_amdgcn_cvt_f32_fp8((int)scale, 0) * 512.0f;
+    o[0] = __builtin_amdgcn_cvt_f32_fp8((int)offset, 0);
+    s[1] = group == 32 ? s[0] : __builtin_amdgcn_cvt_f32_fp8((int)scale, 1) * 512.0f;
+    o[1] = group == 32 ? o[0] : __builtin_amdgcn_cvt_f32_fp8((int)offset, 1);
+}
+
+// One plane's values for the lane's 32 channels in FP32: alpha (c.s+o)_A +
+// (c.s+o)_L, evaluated per 16-channel block as c_A (alpha s_A) + (c_L s_L +
+// (alpha o_A + o_L)) (two fmas per channel), or (c.s+o)_A without a loop
+// record.
+template <int BA, int BL, bool HasL>
+__device__ __forceinline__ void plane_values(const RecordBytes<BA>& a_rec, int a_group, const RecordBytes<BL>& l_rec,
+                                             int l_group, float alpha, float (&x)[32]) {
+    float sa[2], oa[2];
+    record_coefficients(a_rec.scale, a_rec.offset, a_group, sa, oa);
+    float ca[32];
+    record_codes<BA>(a_rec, ca);
+    if constexpr (HasL) {
+        float sl[2], ol[2];
+        record_coefficients(l_rec.scale, l_rec.offset, l_group, sl, ol);
+        float cl[32];
+        record_codes<BL>(l_rec, cl);
+#pragma unroll
+        for (int b = 0; b < 2; ++b) {
+            const float a = alpha * sa[b], c = fmaf(alpha, oa[b], ol[b]);
+#pragma unroll
+            for (int i = 16 * b; i < 16 * b + 16; ++i) x[i] = fmaf(ca[i], a, fmaf(cl[i], sl[b], c));
+        }
+    } else {
+#pragma unroll
+        for (int b = 0; b < 2; ++b)
+#pragma unroll
+            for (int i = 16 * b; i < 16 * b + 16; ++i) x[i] = fmaf(ca[i], sa[b], oa[b]);
+    }
+}
+
+typedef float F32x2 __attribute__((ext_vector_type(2)));
+typedef _Float16 F16x2 __attribute__((ext_vector_type(2)));
+typedef __bf16 Bf16x2 __attribute__((ext_vector_type(2)));
+typedef short Short4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) Short4 LdsShort4;
+
+// Two FP32 values rounded (nearest even) to a packed FP16 / BF16 pair, low first.
+__device__ __forceinline__ uint32_t pack_f16(float a, float b) {
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(F32x2{a, b}, F16x2));
+}
+__device__ __forceinline__ uint32_t pack_bf16(float a, float b) {
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(F32x2{a, b}, Bf16x2));
+}
+
+// ds_read_b64_tr_b16 (gfx950, checked on the device): within each 16 lanes,
+// output lane o gets element o % 4 of the 8 bytes addressed by lanes
+// o / 4 + 4 p, p = 0..3.
+__device__ __forceinline__ Short4 read_transposed(const uint16_t* p) {
+    return __builtin_amdgcn_ds_read_tr16_b64_v4i16((LdsShort4*)p);
 }
 
 // Every record byte of one 16-token unit for the lane: K and V planes, the
@@ -354,8 +402,15 @@ void multirow_stream_kernel(MultiRowParams p) {
 
     // ---------------------------------------------------------------- history
     uint16_t* k_tile = reinterpret_cast<uint16_t*>(lds + wave * kWaveBytes);
-    uint16_t* v_tile = k_tile + kTile * KS;
+    uint16_t* v_tile = k_tile + kTile * KS;  // [token][D] BF16, chunk-swizzled rows
     float* alpha_tile = reinterpret_cast<float*>(v_tile + D * VS);
+    // V^T operand reads (ds_read_b64_tr_b16): lane 16 g + 4 a + b (g = 2 half
+    // + g') addresses token 4 half + a of an 8-token block, channels
+    // 32 t + 16 g' + 4 b..+3 (chunk 4 t + 2 g' + b / 2 at position
+    // chunk ^ 4 a), and receives channel 32 t + column of tokens 4 half..+3.
+    const int tr_a = (lane >> 2) & 3, tr_b = lane & 3, tr_g = (lane >> 4) & 1;
+    const int v_lane = D * (4 * half + tr_a) + 32 * tr_a + 16 * tr_g + 4 * tr_b;
+    auto v_read = [&](int t) __attribute__((always_inline)) { return v_lane ^ (32 * t); };
     const int unit_token = lane >> 2;  // token within a 16-token unit
     const int quarter = lane & 3;      // 32-channel quarter
     const uint32_t page_bytes = (uint32_t)(PT * p.page_width);
@@ -416,23 +471,13 @@ void multirow_stream_kernel(MultiRowParams p) {
             // Tokens past the history hold zeros; their scores are masked below.
             // K, then V, so that only one plane's values are live at a time.
             const bool valid = kTile * tile + local < history;
-            float alpha_k = 1.f;
+            const float alpha_k = HasL ? bf16_f32(cur.kl.alpha) : 1.f;
             {
                 float k[32];
-                dequant<BA>(cur.ka, p.anchor.group, k);
-                if constexpr (HasL) {
-                    float kx[32];
-                    dequant<BL>(cur.kl, p.residual.group, kx);
-                    alpha_k = bf16_f32(cur.kl.alpha);
-#pragma unroll
-                    for (int c = 0; c < 32; ++c) k[c] = fmaf(alpha_k, k[c], kx[c]);
-                }
+                plane_values<BA, BL, HasL>(cur.ka, p.anchor.group, cur.kl, p.residual.group, alpha_k, k);
                 uint32_t kw[16];
 #pragma unroll
-                for (int c = 0; c < 16; ++c) {
-                    const float a = valid ? k[2 * c] : 0.f, b = valid ? k[2 * c + 1] : 0.f;
-                    kw[c] = f16_bits(a) | (f16_bits(b) << 16);
-                }
+                for (int c = 0; c < 16; ++c) kw[c] = valid ? pack_f16(k[2 * c], k[2 * c + 1]) : 0u;
                 uint4* k_dst = reinterpret_cast<uint4*>(&k_tile[local * KS + 32 * quarter]);
 #pragma unroll
                 for (int c = 0; c < 4; ++c)
@@ -440,20 +485,17 @@ void multirow_stream_kernel(MultiRowParams p) {
             }
             {
                 float v[32];
-                dequant<BA>(cur.va, p.anchor.group, v);
-                if constexpr (HasL) {
-                    float vx[32];
-                    dequant<BL>(cur.vl, p.residual.group, vx);
-                    const float alpha_v = bf16_f32(cur.vl.alpha);
+                plane_values<BA, BL, HasL>(cur.va, p.anchor.group, cur.vl, p.residual.group,
+                                           HasL ? bf16_f32(cur.vl.alpha) : 1.f, v);
+                uint32_t vw[16];
 #pragma unroll
-                    for (int c = 0; c < 32; ++c) v[c] = fmaf(alpha_v, (float)(__bf16)v[c], (float)(__bf16)vx[c]);
-                }
-                __bf16 vb[32];
+                for (int c = 0; c < 16; ++c) vw[c] = valid ? pack_bf16(v[2 * c], v[2 * c + 1]) : 0u;
+                // Row-major V: the lane's 4 chunks of 8 channels at chunk
+                // positions 4 (quarter ^ (token % 4)) + i of the token's row.
+                uint4* v_dst = reinterpret_cast<uint4*>(&v_tile[local * D + 32 * (quarter ^ (local & 3))]);
 #pragma unroll
-                for (int c = 0; c < 32; ++c) vb[c] = (__bf16)(valid ? v[c] : 0.f);
-#pragma unroll
-                for (int c = 0; c < 32; ++c)
-                    v_tile[(32 * quarter + c) * VS + local] = __builtin_bit_cast(uint16_t, vb[c]);
+                for (int c = 0; c < 4; ++c)
+                    v_dst[c] = make_uint4(vw[4 * c], vw[4 * c + 1], vw[4 * c + 2], vw[4 * c + 3]);
             }
             if (quarter == 0) alpha_tile[local] = alpha_k;
         }
@@ -505,13 +547,14 @@ void multirow_stream_kernel(MultiRowParams p) {
         }
 #pragma unroll
         for (int j = 0; j < 2; ++j) {
-            const int token_offset = 16 * j + 4 * half;
+            const uint16_t* v_rows = v_tile + 16 * j * D;
 #pragma unroll
             for (int t = 0; t < D / 32; ++t) {
-                const uint16_t* v_row = &v_tile[(32 * t + column) * VS + token_offset];
-                const uint2 lo = *reinterpret_cast<const uint2*>(v_row);
-                const uint2 hi = *reinterpret_cast<const uint2*>(v_row + 8);
-                out[t] = mfma(__builtin_bit_cast(Bf16x8, make_uint4(lo.x, lo.y, hi.x, hi.y)), p_operand[j], out[t]);
+                // Tokens 4 half + 0..3 and 4 half + 8..11 of the 16, as P^T's k-slots.
+                const Short4 lo = read_transposed(v_rows + v_read(t));
+                const Short4 hi = read_transposed(v_rows + 8 * D + v_read(t));
+                out[t] = mfma(__builtin_bit_cast(Bf16x8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7)),
+                              p_operand[j], out[t]);
             }
         }
         wave_sync();  // the next tile overwrites this one
