@@ -107,15 +107,17 @@ __device__ __forceinline__ void load_record(__amdgpu_buffer_rsrc_t page, const R
         const auto v = __builtin_amdgcn_raw_buffer_load_b64(page, codes, 0, kStreamPolicy);
         out.w[0] = v[0]; out.w[1] = v[1];
     }
+    // The lane's FP8 scale and offset bytes (one group of 32 channels, or two
+    // of 16) through the aligned dword holding them, shifted down: the same
+    // loads for either group size, so no branch sits between the unit's
+    // loads (a conditional load makes the compiler wait for every load in
+    // flight, the next unit's included).  Pages are multiples of 16 bytes,
+    // so the dword never crosses the page end.
     const uint32_t scales = (uint32_t)(r.offset + page_tokens * r.code_bytes + row * r.groups + quarter * (r.groups / 4));
     const uint32_t offsets = scales + (uint32_t)(page_tokens * r.groups);
-    if (r.group == 32) {
-        out.scale = __builtin_amdgcn_raw_buffer_load_b8(page, scales, 0, 0);
-        out.offset = __builtin_amdgcn_raw_buffer_load_b8(page, offsets, 0, 0);
-    } else {
-        out.scale = __builtin_amdgcn_raw_buffer_load_b16(page, scales, 0, 0);
-        out.offset = __builtin_amdgcn_raw_buffer_load_b16(page, offsets, 0, 0);
-    }
+    const uint32_t shift = 8u * (scales & 3u);  // offsets sit page_tokens x groups (a multiple of 4) bytes later
+    out.scale = __builtin_amdgcn_raw_buffer_load_b32(page, scales & ~3u, 0, 0) >> shift;
+    out.offset = __builtin_amdgcn_raw_buffer_load_b32(page, offsets & ~3u, 0, 0) >> shift;
     out.alpha = alpha ? __builtin_amdgcn_raw_buffer_load_b16(
                             page, (uint32_t)(r.offset + page_tokens * (r.code_bytes + 2 * r.groups) + 2 * row), 0, 0)
                       : 0u;
