@@ -458,17 +458,23 @@ void multirow_stream_kernel(MultiRowParams p) {
     float running_max = -__builtin_inff();
     float running_sum = 0.f;
 
-    // Units stream one ahead: the loads of the next unit (the second half of
-    // this tile, or the first of the wave's next tile) are in flight while a
-    // unit is dequantized and while the tile's MFMAs run.
-    UnitBytes<BA, BL> next;
-    if (tile_begin + wave < tile_end) fetch(kTile * (tile_begin + wave), next);
-    for (int tile = tile_begin + wave; tile < tile_end; tile += kWaves) {
+    // Units stream two ahead: a wave's units are the two halves of its
+    // tiles tile_begin + wave + kWaves k, and the loads of the unit two
+    // places on are issued before a unit is dequantized, so about two units'
+    // bytes per wave are in flight while units dequantize and the tiles'
+    // MFMAs run.  The fetches carry no condition (units past the split read
+    // zeros through an empty resource), which keeps the compiler's count of
+    // loads in flight exact.
+    const int first_tile = tile_begin + wave;
+    UnitBytes<BA, BL> ahead1, ahead2;
+    fetch(kTile * first_tile, ahead1);
+    fetch(kTile * first_tile + 16, ahead2);
+    for (int tile = first_tile; tile < tile_end; tile += kWaves) {
 #pragma unroll
         for (int u = 0; u < 2; ++u) {
-            const UnitBytes<BA, BL> cur = next;
-            const int following = u == 0 ? kTile * tile + 16 : kTile * (tile + kWaves);
-            if (u == 0 || tile + kWaves < tile_end) fetch(following, next);
+            const UnitBytes<BA, BL> cur = ahead1;
+            ahead1 = ahead2;
+            fetch(kTile * (tile + kWaves) + 16 * u, ahead2);
             const int local = 16 * u + unit_token;
             // Tokens past the history hold zeros; their scores are masked below.
             // K, then V, so that only one plane's values are live at a time.
