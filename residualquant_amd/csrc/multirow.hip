@@ -476,16 +476,18 @@ void multirow_stream_kernel(MultiRowParams p) {
             ahead1 = ahead2;
             fetch(kTile * (tile + kWaves) + 16 * u, ahead2);
             const int local = 16 * u + unit_token;
-            // Tokens past the history hold zeros; their scores are masked below.
             // K, then V, so that only one plane's values are live at a time.
             const bool valid = kTile * tile + local < history;
+            // Whole unit inside the history (wave-uniform): nothing to mask.
+            const bool unit_valid = kTile * tile + 16 * u + 16 <= history;
             const float alpha_k = HasL ? bf16_f32(cur.kl.alpha) : 1.f;
             {
                 float k[32];
                 plane_values<BA, BL, HasL>(cur.ka, p.anchor.group, cur.kl, p.residual.group, alpha_k, k);
                 uint32_t kw[16];
 #pragma unroll
-                for (int c = 0; c < 16; ++c) kw[c] = valid ? pack_f16(k[2 * c], k[2 * c + 1]) : 0u;
+                // No mask: the scores of tokens past the history become -inf below.
+                for (int c = 0; c < 16; ++c) kw[c] = pack_f16(k[2 * c], k[2 * c + 1]);
                 uint4* k_dst = reinterpret_cast<uint4*>(&k_tile[local * KS + 32 * quarter]);
 #pragma unroll
                 for (int c = 0; c < 4; ++c)
@@ -497,7 +499,14 @@ void multirow_stream_kernel(MultiRowParams p) {
                                            HasL ? bf16_f32(cur.vl.alpha) : 1.f, v);
                 uint32_t vw[16];
 #pragma unroll
-                for (int c = 0; c < 16; ++c) vw[c] = valid ? pack_bf16(v[2 * c], v[2 * c + 1]) : 0u;
+                for (int c = 0; c < 16; ++c) vw[c] = pack_bf16(v[2 * c], v[2 * c + 1]);
+                // Slots past the history may hold any bytes (P is zero there,
+                // but 0 x NaN is not): zero them in a unit that reaches past it.
+                if (!unit_valid) {
+                    asm volatile("");
+#pragma unroll
+                    for (int c = 0; c < 16; ++c) vw[c] = valid ? vw[c] : 0u;
+                }
                 // Row-major V: the lane's 4 chunks of 8 channels at chunk
                 // positions 4 (quarter ^ (token % 4)) + i of the token's row.
                 uint4* v_dst = reinterpret_cast<uint4*>(&v_tile[local * D + 32 * (quarter ^ (local & 3))]);
