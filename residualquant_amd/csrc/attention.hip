@@ -119,28 +119,6 @@ __device__ __forceinline__ float fp8_f32(uint32_t v) {
 
 // ------------------------------------------------------------------ prepare
 
-// Request of `row` for a 128-thread workgroup: the number of boundaries
-// qsl[1..requests] at or below the row (qsl is nondecreasing), -1 if the row
-// lies outside [qsl[0], qsl[requests]).  One round of parallel loads instead
-// of a dependent binary search.
-__device__ __forceinline__ int find_request_parallel(const int32_t* qsl, int64_t requests, int64_t row,
-                                                     int* lds_counts) {
-    const int c = threadIdx.x;
-    const int threads = blockDim.x;
-    // The range bounds are loaded with the counts, before the barrier.
-    const int32_t lo = requests > 0 ? qsl[0] : 0;
-    const int32_t hi = requests > 0 ? qsl[requests] : 0;
-    int count = 0;
-    for (int64_t j = 1 + c; j <= requests; j += threads) count += qsl[j] <= row ? 1 : 0;
-#pragma unroll
-    for (int d = 32; d; d >>= 1) count += __shfl_xor(count, d);
-    if ((c & 63) == 0) lds_counts[c >> 6] = count;
-    __syncthreads();
-    if (requests <= 0 || row < lo || row >= hi) return -1;
-    int total = 0;
-    for (int w = 0; w < threads / 64; ++w) total += lds_counts[w];
-    return total;
-}
 
 // Loads of the prepare that do not depend on the request: q, the live key and
 // the two key means of (row, head), and R_k, all into registers.  Issued

@@ -650,21 +650,20 @@ __global__ __launch_bounds__(D) void multirow_finish_kernel(MultiRowParams p) {
     __shared__ float query[D];
     __shared__ float live[kMultiRowMaxLive];
     __shared__ float scratch[2];
-    __shared__ int found;
+    __shared__ int request_counts[D / 64];
     const int64_t row = blockIdx.x;
     const int head = blockIdx.y;
     const int c = threadIdx.x;
-    if (c == 0) {
-        // Request of the row: the last b with query_start_loc[b] <= row.
-        int64_t lo = 0, hi = p.requests;  // answer in [lo, hi)
-        while (hi - lo > 1) {
-            const int64_t mid = (lo + hi) / 2;
-            if (p.query_start_loc[mid] <= row) lo = mid; else hi = mid;
-        }
-        found = (p.requests > 0 && p.query_start_loc[lo] <= row && row < p.query_start_loc[lo + 1]) ? (int)lo : -1;
+    // R_v row c (16-byte loads, issued before the lookup so that their round
+    // trip overlaps it) for hist . R_v^T.
+    uint4 rv[D / 8];
+    if (p.value_rotation) {
+        const uint4* src = reinterpret_cast<const uint4*>(p.value_rotation + ((int64_t)head * D + c) * D);
+#pragma unroll
+        for (int i = 0; i < D / 8; ++i) rv[i] = src[i];
     }
-    __syncthreads();
-    const int request = found;
+    // Request of the row: one round of parallel loads.
+    const int request = find_request_parallel(p.query_start_loc, p.requests, row, request_counts);
     const int first = request < 0 ? -1 : p.query_start_loc[request];
     if (first < 0) return;  // uniform
     const int r = (int)(row - first);
@@ -689,10 +688,17 @@ __global__ __launch_bounds__(D) void multirow_finish_kernel(MultiRowParams p) {
     float hist = acc;
     if (p.value_rotation) {
         // hist . R_v^T: channel c takes row c of R_v.
-        const uint16_t* rv = p.value_rotation + ((int64_t)head * D + c) * D;
-        hist = 0.f;
-#pragma unroll 8
-        for (int k = 0; k < D; ++k) hist = fmaf(hist_rot[k], f16_to_f32(rv[k]), hist);
+        float h[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int i = 0; i < D / 8; ++i) {
+            const uint32_t w[4] = {rv[i].x, rv[i].y, rv[i].z, rv[i].w};
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                h[j] = fmaf(hist_rot[8 * i + 2 * j], f16_to_f32(w[j] & 0xffffu), h[j]);
+                h[j] = fmaf(hist_rot[8 * i + 2 * j + 1], f16_to_f32(w[j] >> 16), h[j]);
+            }
+        }
+        hist = (h[0] + h[1]) + (h[2] + h[3]);
     }
 
     // Live tokens: the row's own (decode) or the request's new rows j <= r (causal).

@@ -168,6 +168,29 @@ typedef const int32_t __attribute__((address_space(4))) ConstantInt32;
 // operations (loads and stores) are waited for.
 __device__ __forceinline__ void wait_vector_memory() { __builtin_amdgcn_s_waitcnt(0xF70); }
 
+// Request of `row` for a workgroup of whole waves (at most 16): the number of boundaries
+// qsl[1..requests] at or below the row (qsl is nondecreasing), -1 if the row
+// lies outside [qsl[0], qsl[requests]).  One round of parallel loads instead
+// of a dependent binary search.
+__device__ __forceinline__ int find_request_parallel(const int32_t* qsl, int64_t requests, int64_t row,
+                                                     int* lds_counts) {
+    const int c = threadIdx.x;
+    const int threads = blockDim.x;
+    // The range bounds are loaded with the counts, before the barrier.
+    const int32_t lo = requests > 0 ? qsl[0] : 0;
+    const int32_t hi = requests > 0 ? qsl[requests] : 0;
+    int count = 0;
+    for (int64_t j = 1 + c; j <= requests; j += threads) count += qsl[j] <= row ? 1 : 0;
+#pragma unroll
+    for (int d = 32; d; d >>= 1) count += __shfl_xor(count, d);
+    if ((c & 63) == 0) lds_counts[c >> 6] = count;
+    __syncthreads();
+    if (requests <= 0 || row < lo || row >= hi) return -1;
+    int total = 0;
+    for (int w = 0; w < threads / 64; ++w) total += lds_counts[w];
+    return total;
+}
+
 // Counts this workgroup's arrival at `counter` (after every thread's shared
 // stores) and returns true in every thread of the workgroup that arrives last
 // of `expected`.  Nothing waits for other workgroups.
