@@ -1030,26 +1030,35 @@ void decode_kernel(AttentionParams p) {
     float m = -INFINITY, l = 0.f;
 
     // Values of one unit: acc += p * (alpha_v * deq_A + deq_L); offsets go to cst.
-    auto accumulate = [&](const Unit<BA, GA, BL, GL, HasL>& d, float prob) {
+    // A token past the history has p = 0, but its slot may hold any bytes
+    // (0 x NaN is NaN), so its raw scale, offset and alpha bits are selected
+    // to 0 before they are converted (its codes are integers and harmless).
+    auto accumulate = [&](const Unit<BA, GA, BL, GL, HasL>& d, float prob, bool valid) {
         const float p512 = prob * 512.0f;
+        GroupParams<GA> vpa = d.vpa;
+        vpa.scales = valid ? vpa.scales : 0u;
+        vpa.offsets = valid ? vpa.offsets : 0u;
         float w_a[2];
         if constexpr (HasL) {
-            const float alpha_v = __uint_as_float(d.alpha_v_bits << 16);
+            GroupParams<GL> vpl = d.vpl;
+            vpl.scales = valid ? vpl.scales : 0u;
+            vpl.offsets = valid ? vpl.offsets : 0u;
+            const float alpha_v = __uint_as_float((valid ? d.alpha_v_bits : 0u) << 16);
             const float pa = prob * alpha_v;
             const float pa512 = p512 * alpha_v;
-            w_a[0] = pa512 * d.vpa.template scale<0>();
-            w_a[1] = GA == 32 ? w_a[0] : pa512 * d.vpa.template scale<1>();
+            w_a[0] = pa512 * vpa.template scale<0>();
+            w_a[1] = GA == 32 ? w_a[0] : pa512 * vpa.template scale<1>();
             float w_l[2];
-            w_l[0] = p512 * d.vpl.template scale<0>();
-            w_l[1] = GL == 32 ? w_l[0] : p512 * d.vpl.template scale<1>();
-            cst0 = fmaf(pa, d.vpa.template offset<0>(), fmaf(prob, d.vpl.template offset<0>(), cst0));
-            cst1 = fmaf(pa, d.vpa.template offset<1>(), fmaf(prob, d.vpl.template offset<1>(), cst1));
+            w_l[0] = p512 * vpl.template scale<0>();
+            w_l[1] = GL == 32 ? w_l[0] : p512 * vpl.template scale<1>();
+            cst0 += fmaf(pa, vpa.template offset<0>(), prob * vpl.template offset<0>());
+            cst1 += fmaf(pa, vpa.template offset<1>(), prob * vpl.template offset<1>());
             accumulate_codes<BL>(d.vcl, w_l, acc);
         } else {
-            w_a[0] = p512 * d.vpa.template scale<0>();
-            w_a[1] = GA == 32 ? w_a[0] : p512 * d.vpa.template scale<1>();
-            cst0 = fmaf(prob, d.vpa.template offset<0>(), cst0);
-            cst1 = fmaf(prob, d.vpa.template offset<1>(), cst1);
+            w_a[0] = p512 * vpa.template scale<0>();
+            w_a[1] = GA == 32 ? w_a[0] : p512 * vpa.template scale<1>();
+            cst0 += prob * vpa.template offset<0>();
+            cst1 += prob * vpa.template offset<1>();
         }
         accumulate_codes<BA>(d.vca, w_a, acc);
     };
@@ -1093,8 +1102,8 @@ void decode_kernel(AttentionParams p) {
         const float prob0 = valid0 ? __builtin_amdgcn_exp2f(score0 - m) : 0.f;
         const float prob1 = valid1 ? __builtin_amdgcn_exp2f(score1 - m) : 0.f;
         l += prob0 + prob1;
-        accumulate(d0, prob0);
-        accumulate(d1, prob1);
+        accumulate(d0, prob0, valid0);
+        accumulate(d1, prob1, valid1);
     };
 
     // Each iteration streams two consecutive 16-token units of the split
@@ -1519,29 +1528,38 @@ void decode96_kernel(AttentionParams p) {
         l += h == 0 ? prob : 0.f;
 
         // Values: acc += p * (alpha_v * deq_A + deq_L); offsets go to cst.
+        // A token past the history has p = 0, but its slot may hold any
+        // bytes (0 x NaN is NaN): its raw scale, offset and alpha bits are
+        // selected to 0 before they are converted.
         const float p512 = prob * 512.0f;
+        HalfParams<GA> vpa = d.vpa;
+        vpa.s = valid ? vpa.s : 0u;
+        vpa.o = valid ? vpa.o : 0u;
         float sva[3], ova[3];
-        d.vpa.decode(h != 0, sva, ova);
+        vpa.decode(h != 0, sva, ova);
         float w_a[3];
         if constexpr (HasL) {
-            const float alpha_v = __uint_as_float(d.alpha_v_bits << 16);
+            HalfParams<GL> vpl = d.vpl;
+            vpl.s = valid ? vpl.s : 0u;
+            vpl.o = valid ? vpl.o : 0u;
+            const float alpha_v = __uint_as_float((valid ? d.alpha_v_bits : 0u) << 16);
             const float pa = prob * alpha_v;
             const float pa512 = p512 * alpha_v;
             float svl[3], ovl[3];
-            d.vpl.decode(h != 0, svl, ovl);
+            vpl.decode(h != 0, svl, ovl);
             float w_l[3];
 #pragma unroll
             for (int b = 0; b < 3; ++b) {
                 w_a[b] = pa512 * sva[b];
                 w_l[b] = p512 * svl[b];
-                cst[b] = fmaf(pa, ova[b], fmaf(prob, ovl[b], cst[b]));
+                cst[b] += fmaf(pa, ova[b], prob * ovl[b]);
             }
             accumulate_half<BL>(d.vcl, w_l, acc);
         } else {
 #pragma unroll
             for (int b = 0; b < 3; ++b) {
                 w_a[b] = p512 * sva[b];
-                cst[b] = fmaf(prob, ova[b], cst[b]);
+                cst[b] += prob * ova[b];
             }
         }
         accumulate_half<BA>(d.vca, w_a, acc);
@@ -1758,14 +1776,20 @@ void decode_chain_kernel(AttentionParams p) {
     };
     // The chain X_0 = bf16(c s + o), X_r = bf16(alpha_r X_{r-1} + bf16(c s + o))
     // of one plane, the K plane adding bf16(mu_r) to every record but the last.
-    auto build_chain = [&](const ChainRaw (&raw)[Links], bool key_plane, float (&x)[32]) {
+    // `live` false: a token past the history, whose slot may hold any bytes;
+    // its FP8 parameters and alphas count as zero, so its values are zero
+    // (its scores are replaced by -inf, so the key plane needs no such care).
+    auto build_chain = [&](const ChainRaw (&raw)[Links], bool key_plane, bool live, float (&x)[32]) {
 #pragma unroll
         for (int r = 0; r < Links; ++r) {
             // One record at a time: interleaved by the scheduler, the records'
             // 32-channel temporaries pushed the kernel to one wave per SIMD.
             __builtin_amdgcn_sched_barrier(0);
+            ChainRaw record = raw[r];
+            record.params = live ? record.params : 0u;
+            record.alpha = live ? record.alpha : 0u;
             float xr[32];
-            chain_decode(raw[r], regs[r], xr);
+            chain_decode(record, regs[r], xr);
             if (key_plane && has_mean && r + 1 < Links) {
 #pragma unroll
                 for (int i = 0; i < 32; i += 2) {
@@ -1778,7 +1802,7 @@ void decode_chain_kernel(AttentionParams p) {
 #pragma unroll
                 for (int i = 0; i < 32; ++i) x[i] = xr[i];
             } else {
-                const float alpha = bf16_f32(raw[r].alpha);
+                const float alpha = bf16_f32(record.alpha);
 #pragma unroll
                 for (int i = 0; i < 32; i += 2) {
                     x[i] = fmaf(x[i], alpha, xr[i]);
@@ -1807,7 +1831,7 @@ void decode_chain_kernel(AttentionParams p) {
         const bool valid = pages.ok && lane_active && pos < range.history;
         const UnitPages next = unit_pages(u + kWaves);
         float x[32];
-        build_chain(rk, true, x);
+        build_chain(rk, true, true, x);
         load_plane(next.k, next.tok, rk);
         float s[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -1820,7 +1844,7 @@ void decode_chain_kernel(AttentionParams p) {
         }
         float score = quad_sum_fast(lane_active ? (s[0] + s[1]) + (s[2] + s[3]) : 0.f);
         score = valid ? score : -INFINITY;
-        build_chain(rv, false, x);
+        build_chain(rv, false, valid, x);
         load_plane(next.v, next.tok, rv);
         pages = next;
         const float unit_max = wave_max(score);
@@ -1921,7 +1945,9 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_bf16_kernel(AttentionPa
         l += prob;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            const uint32_t w[4] = {vv[i].x, vv[i].y, vv[i].z, vv[i].w};
+            // A token past the history may hold any bytes: its values count as 0.
+            const uint32_t w[4] = {valid ? vv[i].x : 0u, valid ? vv[i].y : 0u, valid ? vv[i].z : 0u,
+                                   valid ? vv[i].w : 0u};
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
                 acc[8 * i + 2 * j] = fmaf(prob, __uint_as_float(w[j] << 16), acc[8 * i + 2 * j]);
