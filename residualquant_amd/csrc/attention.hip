@@ -1587,20 +1587,37 @@ void decode96_kernel(AttentionParams p) {
 // value except the current loop's (the live score carries -q'.mu_L).  The
 // chain is not linear in the codes, so decode_chain_kernel rebuilds each
 // token's K and V (lane = token x 32-channel quarter, one 16-token unit per
-// wave iteration) and scores and accumulates them in FP32.  Each BF16 step is
-// an FP32 operation rounded once to BF16; the reference rounds the exact
-// value once, and the two differ only when the FP32 result sits on a BF16
-// midpoint it did not reach exactly (within the attention tolerance).
+// wave iteration) and scores and accumulates them.  Each chain step is
+//   X_r = dot2(pack(X_{r-1}, k_r), (alpha_r, 1)),
+// one v_cvt_pk_bf16_f32 that rounds the previous link and the record's value
+// to BF16 (RNE) and one v_dot2_f32_bf16 that forms alpha X + k in FP32; the
+// BF16 rounding of X_r happens where it is next packed.  The reference rounds
+// the exact value once; the FP32 sum of the dot (which may differ from an FMA
+// by one FP32 ulp in the last place) is rounded again to BF16, and the two
+// differ only when that sum sits within an FP32 ulp of a BF16 midpoint
+// (within the attention tolerance).
 
-// RNE to BF16 of two FP32 values, returned as FP32: one v_cvt_pk_bf16_f32
-// and two bit operations.
 typedef __bf16 Bf16x2 __attribute__((ext_vector_type(2)));
 typedef float F32x2 __attribute__((ext_vector_type(2)));
-__device__ __forceinline__ void bf16_round2(float& a, float& b) {
+// RNE to BF16 of two FP32 values, packed (lo = a, hi = b): v_cvt_pk_bf16_f32.
+__device__ __forceinline__ uint32_t bf16_pack(float a, float b) {
     const F32x2 f = {a, b};
-    const uint32_t u = __builtin_bit_cast(uint32_t, __builtin_convertvector(f, Bf16x2));
-    a = __uint_as_float(u << 16);
-    b = __uint_as_float(u & 0xffff0000u);
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(f, Bf16x2));
+}
+// a.lo * b.lo + a.hi * b.hi + c over BF16 pairs, FP32 sum: v_dot2_f32_bf16.
+// Keep constant pairs for `b` in registers: the compiler may encode a packed
+// BF16 constant as an FP32 inline constant, which the instruction reads as
+// the pair (0, hi 16 bits of the FP32 value).
+__device__ __forceinline__ float bf16_dot2(uint32_t a, uint32_t b, float c) {
+    return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(Bf16x2, a), __builtin_bit_cast(Bf16x2, b), c, false);
+}
+// a.lo * b.lo + a.hi * b.hi with no addend, as the three-operand VOP3P form:
+// through the builtin the compiler picks the two-operand v_dot2c_f32_bf16,
+// whose accumulator is its destination, and spends a v_mov of 0 on each.
+__device__ __forceinline__ float bf16_dot2_zero(uint32_t a, uint32_t b) {
+    float r;
+    asm("v_dot2_f32_bf16 %0, %1, %2, 0" : "=v"(r) : "v"(a), "v"(b));
+    return r;
 }
 
 // The raw bytes of one record of one token that a lane needs for its 32
@@ -1641,8 +1658,8 @@ __device__ __forceinline__ void chain_load(__amdgpu_buffer_rsrc_t page, const Re
                            : 0u;
 }
 
-// BF16 values (as FP32) of the lane's 32 channels of one record:
-// bf16(code * scale + offset).
+// FP32 code * scale + offset of the lane's 32 channels of one record, before
+// the BF16 rounding (which happens where the value is packed).
 __device__ __forceinline__ void chain_decode(const ChainRaw& raw, const RecordRegion& reg, float (&out)[32]) {
     float scale[2], offset[2];
     if (reg.group == 32) {
@@ -1683,8 +1700,6 @@ __device__ __forceinline__ void chain_decode(const ChainRaw& raw, const RecordRe
                 out[16 * i + 12 + k] = fmaf(c23[1], scale[i], offset[i]);
             }
     }
-#pragma unroll
-    for (int i = 0; i < 32; i += 2) bf16_round2(out[i], out[i + 1]);
 }
 
 // Links = records in the chain (2..4).  A wave's units are software
@@ -1709,6 +1724,8 @@ void decode_chain_kernel(AttentionParams p) {
     // bf16(mu_r) of records 0 .. L - 1 (the K plane's chain), FP32.
     __shared__ __attribute__((aligned(16))) float mean_lds[kMaxRecords][128];
     __shared__ __attribute__((aligned(16))) float scratch_lds[kWaves * 16 * 128];
+    // q' as BF16 pairs of channels (2j, 2j + 1): [0] bf16(q'), [1] bf16(q' - bf16(q')).
+    __shared__ __attribute__((aligned(16))) uint32_t qpair_lds[2][64];
     __shared__ int request_counts[kWaves];
 
     SplitRange range;
@@ -1741,9 +1758,22 @@ void decode_chain_kernel(AttentionParams p) {
         for (int i = threadIdx.x; i < kPrepFloats; i += kDecodeThreads) prep_lds[i] = src[i];
         __syncthreads();
     }
-    // q' of the lane's channels (FP32, log2 units, scale folded in) stays in
-    // LDS and is read per unit: 32 registers fewer keep two waves per SIMD.
-    const float4* qv4 = reinterpret_cast<const float4*>(prep_lds + kPrepScalars + 32 * lq);
+    // q' (FP32, log2 units, scale folded in) as a high and a low BF16 pair
+    // per two channels (16 bits of mantissa: relative error 2^-17), so the
+    // score is two v_dot2_f32_bf16 per channel pair.  It stays in LDS and is
+    // read per unit: registers are what limits the kernel to two waves per SIMD.
+    if (threadIdx.x < 64) {
+        const float a = prep_lds[kPrepScalars + 2 * threadIdx.x], b = prep_lds[kPrepScalars + 2 * threadIdx.x + 1];
+        const uint32_t hi = bf16_pack(a, b);
+        qpair_lds[0][threadIdx.x] = hi;
+        qpair_lds[1][threadIdx.x] = bf16_pack(a - __uint_as_float(hi << 16), b - __uint_as_float(hi & 0xffff0000u));
+    }
+    __syncthreads();
+    const uint4* qhi4 = reinterpret_cast<const uint4*>(&qpair_lds[0][16 * lq]);
+    const uint4* qlo4 = reinterpret_cast<const uint4*>(&qpair_lds[1][16 * lq]);
+    // The pairs (1, 0) and (0, 1) of the mean add, in registers.
+    uint32_t pick_lo = 0x00003f80u, pick_hi = 0x3f800000u;
+    asm("" : "+v"(pick_lo), "+v"(pick_hi));
 
     const ConstantInt32* table =
         (const ConstantInt32*)(p.block_table + (int64_t)range.request * p.block_table_stride);
@@ -1775,7 +1805,10 @@ void decode_chain_kernel(AttentionParams p) {
         for (int r = 0; r < Links; ++r) chain_load<D, PT>(page, regs[r], tok, lq, r > 0, raw[r]);
     };
     // The chain X_0 = bf16(c s + o), X_r = bf16(alpha_r X_{r-1} + bf16(c s + o))
-    // of one plane, the K plane adding bf16(mu_r) to every record but the last.
+    // of one plane, the K plane adding bf16(mu_r) to every record but the last
+    // (k = bf16(bf16(c s + o) + bf16(mu_r)): one pack per channel pair and a
+    // dot with (1, 0) or (0, 1) whose FP32 addend is bf16(mu_r)).  x holds the
+    // last link before its BF16 rounding.
     // `live` false: a token past the history, whose slot may hold any bytes;
     // its FP8 parameters and alphas count as zero, so its values are zero
     // (its scores are replaced by -inf, so the key plane needs no such care).
@@ -1793,22 +1826,18 @@ void decode_chain_kernel(AttentionParams p) {
             if (key_plane && has_mean && r + 1 < Links) {
 #pragma unroll
                 for (int i = 0; i < 32; i += 2) {
-                    xr[i] += mean_lds[r][32 * lq + i];
-                    xr[i + 1] += mean_lds[r][32 * lq + i + 1];
-                    bf16_round2(xr[i], xr[i + 1]);
+                    const uint32_t pair = bf16_pack(xr[i], xr[i + 1]);
+                    xr[i] = bf16_dot2(pair, pick_lo, mean_lds[r][32 * lq + i]);
+                    xr[i + 1] = bf16_dot2(pair, pick_hi, mean_lds[r][32 * lq + i + 1]);
                 }
             }
             if (r == 0) {
 #pragma unroll
                 for (int i = 0; i < 32; ++i) x[i] = xr[i];
             } else {
-                const float alpha = bf16_f32(record.alpha);
+                const uint32_t weights = (record.alpha & 0xffffu) | 0x3f800000u;  // (alpha_r, 1)
 #pragma unroll
-                for (int i = 0; i < 32; i += 2) {
-                    x[i] = fmaf(x[i], alpha, xr[i]);
-                    x[i + 1] = fmaf(x[i + 1], alpha, xr[i + 1]);
-                    bf16_round2(x[i], x[i + 1]);
-                }
+                for (int i = 0; i < 32; ++i) x[i] = bf16_dot2_zero(bf16_pack(x[i], xr[i]), weights);
             }
         }
     };
@@ -1835,12 +1864,15 @@ void decode_chain_kernel(AttentionParams p) {
         load_plane(next.k, next.tok, rk);
         float s[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            const float4 q4 = qv4[i];
-            s[0] = fmaf(q4.x, x[4 * i], s[0]);
-            s[1] = fmaf(q4.y, x[4 * i + 1], s[1]);
-            s[2] = fmaf(q4.z, x[4 * i + 2], s[2]);
-            s[3] = fmaf(q4.w, x[4 * i + 3], s[3]);
+        for (int i = 0; i < 4; ++i) {
+            const uint4 hi = qhi4[i], lo = qlo4[i];
+            const uint32_t h[4] = {hi.x, hi.y, hi.z, hi.w}, l[4] = {lo.x, lo.y, lo.z, lo.w};
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const uint32_t k = bf16_pack(x[8 * i + 2 * j], x[8 * i + 2 * j + 1]);
+                s[j] = bf16_dot2(k, h[j], s[j]);
+                s[j] = bf16_dot2(k, l[j], s[j]);
+            }
         }
         float score = quad_sum_fast(lane_active ? (s[0] + s[1]) + (s[2] + s[3]) : 0.f);
         score = valid ? score : -INFINITY;
@@ -1858,7 +1890,11 @@ void decode_chain_kernel(AttentionParams p) {
         const float prob = valid ? __builtin_amdgcn_exp2f(score - m) : 0.f;
         l += prob;
 #pragma unroll
-        for (int i = 0; i < 32; ++i) acc[i] = fmaf(prob, x[i], acc[i]);
+        for (int i = 0; i < 32; i += 2) {
+            const uint32_t v = bf16_pack(x[i], x[i + 1]);
+            acc[i] = fmaf(prob, __uint_as_float(v << 16), acc[i]);
+            acc[i + 1] = fmaf(prob, __uint_as_float(v & 0xffff0000u), acc[i + 1]);
+        }
     }
 
     if (p.splits == 1) {

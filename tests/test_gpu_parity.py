@@ -179,6 +179,7 @@ def test_adjacent_attention_matches_oracle(oracle, device, case):
                          d.query_start_loc.to(device), d.seq_lens.to(device), d.table.to(device), kr, vr, km,
                          g.records, g.mode, g.anchor, loop)
             err = np.abs(out.float().cpu().numpy().astype(np.float64) - expected)
+            print(f"[case]   loop {loop}: max {err.max():.3g} mean {err.mean():.3g}", flush=True)
             assert err.max() <= MAX_ABS and err.mean() <= MEAN_ABS, (loop, err.max(), err.mean())
     finally:
         rq.ops.set_split_target(0)
