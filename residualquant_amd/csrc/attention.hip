@@ -1658,47 +1658,54 @@ __device__ __forceinline__ void chain_load(__amdgpu_buffer_rsrc_t page, const Re
                            : 0u;
 }
 
-// FP32 code * scale + offset of the lane's 32 channels of one record, before
-// the BF16 rounding (which happens where the value is packed).
-__device__ __forceinline__ void chain_decode(const ChainRaw& raw, const RecordRegion& reg, float (&out)[32]) {
-    float scale[2], offset[2];
+// FP32 code * scale + offset of channels [16 H, 16 H + 16) of the lane's 32
+// channels of one record, before the BF16 rounding (which happens where the
+// value is packed).
+template <int H>
+__device__ __forceinline__ void chain_decode(const ChainRaw& raw, const RecordRegion& reg, float (&out)[16]) {
+    float scale, offset;
     if (reg.group == 32) {
-        scale[0] = scale[1] = fp8_f32<0>(raw.params) * 512.0f;
-        offset[0] = offset[1] = fp8_f32<2>(raw.params);
+        scale = fp8_f32<0>(raw.params) * 512.0f;
+        offset = fp8_f32<2>(raw.params);
     } else {
-        scale[0] = fp8_f32<0>(raw.params) * 512.0f;
-        scale[1] = fp8_f32<1>(raw.params) * 512.0f;
-        offset[0] = fp8_f32<2>(raw.params);
-        offset[1] = fp8_f32<3>(raw.params);
+        scale = fp8_f32<H>(raw.params) * 512.0f;
+        offset = fp8_f32<2 + H>(raw.params);
     }
     // A code c held in a byte is the FP8 E4M3 value c * 2^-9 (scale carries 2^9).
     const uint32_t w[4] = {raw.codes.x, raw.codes.y, raw.codes.z, raw.codes.w};
     if (reg.bits == 4) {
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const int h = i >> 1;
-            const int lo = (int)(w[i] & 0x0f0f0f0fu), hi = (int)((w[i] >> 4) & 0x0f0f0f0fu);
+        for (int i = 0; i < 2; ++i) {
+            const uint32_t word = w[2 * H + i];
+            const int lo = (int)(word & 0x0f0f0f0fu), hi = (int)((word >> 4) & 0x0f0f0f0fu);
             const auto l01 = __builtin_amdgcn_cvt_pk_f32_fp8(lo, false);
             const auto l23 = __builtin_amdgcn_cvt_pk_f32_fp8(lo, true);
             const auto h01 = __builtin_amdgcn_cvt_pk_f32_fp8(hi, false);
             const auto h23 = __builtin_amdgcn_cvt_pk_f32_fp8(hi, true);
             const float c[8] = {l01[0], h01[0], l01[1], h01[1], l23[0], h23[0], l23[1], h23[1]};
 #pragma unroll
-            for (int k = 0; k < 8; ++k) out[8 * i + k] = fmaf(c[k], scale[h], offset[h]);
+            for (int k = 0; k < 8; ++k) out[8 * i + k] = fmaf(c[k], scale, offset);
         }
     } else {
+        // Byte j of part k holds channel 4j + k.  The channels are written in
+        // index order, as in the INT4 branch: stores to different elements in
+        // the two branches get merged through a pointer, which keeps `out` in
+        // scratch memory.
+        float c[4][4];
 #pragma unroll
-        for (int i = 0; i < 2; ++i)
+        for (int k = 0; k < 4; ++k) {
+            const int part = (int)((w[H] >> (2 * k)) & 0x03030303u);
+            const auto c01 = __builtin_amdgcn_cvt_pk_f32_fp8(part, false);
+            const auto c23 = __builtin_amdgcn_cvt_pk_f32_fp8(part, true);
+            c[0][k] = c01[0];
+            c[1][k] = c01[1];
+            c[2][k] = c23[0];
+            c[3][k] = c23[1];
+        }
 #pragma unroll
-            for (int k = 0; k < 4; ++k) {
-                const int part = (int)((w[i] >> (2 * k)) & 0x03030303u);  // byte j: channel 4j + k
-                const auto c01 = __builtin_amdgcn_cvt_pk_f32_fp8(part, false);
-                const auto c23 = __builtin_amdgcn_cvt_pk_f32_fp8(part, true);
-                out[16 * i + k] = fmaf(c01[0], scale[i], offset[i]);
-                out[16 * i + 4 + k] = fmaf(c01[1], scale[i], offset[i]);
-                out[16 * i + 8 + k] = fmaf(c23[0], scale[i], offset[i]);
-                out[16 * i + 12 + k] = fmaf(c23[1], scale[i], offset[i]);
-            }
+        for (int j = 0; j < 4; ++j)
+#pragma unroll
+            for (int k = 0; k < 4; ++k) out[4 * j + k] = fmaf(c[j][k], scale, offset);
     }
 }
 
@@ -1805,42 +1812,47 @@ void decode_chain_kernel(AttentionParams p) {
         for (int r = 0; r < Links; ++r) chain_load<D, PT>(page, regs[r], tok, lq, r > 0, raw[r]);
     };
     // The chain X_0 = bf16(c s + o), X_r = bf16(alpha_r X_{r-1} + bf16(c s + o))
-    // of one plane, the K plane adding bf16(mu_r) to every record but the last
-    // (k = bf16(bf16(c s + o) + bf16(mu_r)): one pack per channel pair and a
-    // dot with (1, 0) or (0, 1) whose FP32 addend is bf16(mu_r)).  x holds the
-    // last link before its BF16 rounding.
+    // of one plane, over the lane's channels [16 H, 16 H + 16), the K plane
+    // adding bf16(mu_r) to every record but the last (k = bf16(bf16(c s + o) +
+    // bf16(mu_r)): one pack per channel pair and a dot with (1, 0) or (0, 1)
+    // whose FP32 addend is bf16(mu_r)).  x holds the last link before its
+    // BF16 rounding.  A plane is built and consumed 16 channels at a time, so
+    // the chain's temporaries take 32 registers, not 64.
     // `live` false: a token past the history, whose slot may hold any bytes;
     // its FP8 parameters and alphas count as zero, so its values are zero
     // (its scores are replaced by -inf, so the key plane needs no such care).
-    auto build_chain = [&](const ChainRaw (&raw)[Links], bool key_plane, bool live, float (&x)[32]) {
+    auto build_chain = [&](auto half, const ChainRaw (&raw)[Links], bool key_plane, bool live, float (&x)[16]) {
+        constexpr int H = decltype(half)::value;
 #pragma unroll
         for (int r = 0; r < Links; ++r) {
             // One record at a time: interleaved by the scheduler, the records'
-            // 32-channel temporaries pushed the kernel to one wave per SIMD.
+            // temporaries would raise the register count.
             __builtin_amdgcn_sched_barrier(0);
             ChainRaw record = raw[r];
             record.params = live ? record.params : 0u;
             record.alpha = live ? record.alpha : 0u;
-            float xr[32];
-            chain_decode(record, regs[r], xr);
+            float xr[16];
+            chain_decode<H>(record, regs[r], xr);
             if (key_plane && has_mean && r + 1 < Links) {
 #pragma unroll
-                for (int i = 0; i < 32; i += 2) {
+                for (int i = 0; i < 16; i += 2) {
                     const uint32_t pair = bf16_pack(xr[i], xr[i + 1]);
-                    xr[i] = bf16_dot2(pair, pick_lo, mean_lds[r][32 * lq + i]);
-                    xr[i + 1] = bf16_dot2(pair, pick_hi, mean_lds[r][32 * lq + i + 1]);
+                    xr[i] = bf16_dot2(pair, pick_lo, mean_lds[r][32 * lq + 16 * H + i]);
+                    xr[i + 1] = bf16_dot2(pair, pick_hi, mean_lds[r][32 * lq + 16 * H + i + 1]);
                 }
             }
             if (r == 0) {
 #pragma unroll
-                for (int i = 0; i < 32; ++i) x[i] = xr[i];
+                for (int i = 0; i < 16; ++i) x[i] = xr[i];
             } else {
                 const uint32_t weights = (record.alpha & 0xffffu) | 0x3f800000u;  // (alpha_r, 1)
 #pragma unroll
-                for (int i = 0; i < 32; ++i) x[i] = bf16_dot2_zero(bf16_pack(x[i], xr[i]), weights);
+                for (int i = 0; i < 16; ++i) x[i] = bf16_dot2_zero(bf16_pack(x[i], xr[i]), weights);
             }
         }
     };
+    using Half0 = std::integral_constant<int, 0>;
+    using Half1 = std::integral_constant<int, 1>;
 
     float acc[32];
 #pragma unroll
@@ -1859,26 +1871,31 @@ void decode_chain_kernel(AttentionParams p) {
         const int64_t pos = u * kUnitTokens + t;
         const bool valid = pages.ok && lane_active && pos < range.history;
         const UnitPages next = unit_pages(u + kWaves);
-        float x[32];
-        build_chain(rk, true, true, x);
-        load_plane(next.k, next.tok, rk);
         float s[4] = {0.f, 0.f, 0.f, 0.f};
+        auto score_half = [&](auto half, const float (&x)[16]) {
+            constexpr int H = decltype(half)::value;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const uint4 hi = qhi4[i], lo = qlo4[i];
-            const uint32_t h[4] = {hi.x, hi.y, hi.z, hi.w}, l[4] = {lo.x, lo.y, lo.z, lo.w};
+            for (int i = 0; i < 2; ++i) {
+                const uint4 hi = qhi4[2 * H + i], lo = qlo4[2 * H + i];
+                const uint32_t h[4] = {hi.x, hi.y, hi.z, hi.w}, l[4] = {lo.x, lo.y, lo.z, lo.w};
 #pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                const uint32_t k = bf16_pack(x[8 * i + 2 * j], x[8 * i + 2 * j + 1]);
-                s[j] = bf16_dot2(k, h[j], s[j]);
-                s[j] = bf16_dot2(k, l[j], s[j]);
+                for (int j = 0; j < 4; ++j) {
+                    const uint32_t k = bf16_pack(x[8 * i + 2 * j], x[8 * i + 2 * j + 1]);
+                    s[j] = bf16_dot2(k, h[j], s[j]);
+                    s[j] = bf16_dot2(k, l[j], s[j]);
+                }
             }
+        };
+        {
+            float x[16];
+            build_chain(Half0{}, rk, true, true, x);
+            score_half(Half0{}, x);
+            build_chain(Half1{}, rk, true, true, x);
+            score_half(Half1{}, x);
         }
+        load_plane(next.k, next.tok, rk);
         float score = quad_sum_fast(lane_active ? (s[0] + s[1]) + (s[2] + s[3]) : 0.f);
         score = valid ? score : -INFINITY;
-        build_chain(rv, false, valid, x);
-        load_plane(next.v, next.tok, rv);
-        pages = next;
         const float unit_max = wave_max(score);
         if (unit_max > m) {
             const float factor = m == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m - unit_max);
@@ -1889,12 +1906,24 @@ void decode_chain_kernel(AttentionParams p) {
         }
         const float prob = valid ? __builtin_amdgcn_exp2f(score - m) : 0.f;
         l += prob;
+        auto accumulate_half = [&](auto half, const float (&x)[16]) {
+            constexpr int H = decltype(half)::value;
 #pragma unroll
-        for (int i = 0; i < 32; i += 2) {
-            const uint32_t v = bf16_pack(x[i], x[i + 1]);
-            acc[i] = fmaf(prob, __uint_as_float(v << 16), acc[i]);
-            acc[i + 1] = fmaf(prob, __uint_as_float(v & 0xffff0000u), acc[i + 1]);
+            for (int i = 0; i < 16; i += 2) {
+                const uint32_t v = bf16_pack(x[i], x[i + 1]);
+                acc[16 * H + i] = fmaf(prob, __uint_as_float(v << 16), acc[16 * H + i]);
+                acc[16 * H + i + 1] = fmaf(prob, __uint_as_float(v & 0xffff0000u), acc[16 * H + i + 1]);
+            }
+        };
+        {
+            float x[16];
+            build_chain(Half0{}, rv, false, valid, x);
+            accumulate_half(Half0{}, x);
+            build_chain(Half1{}, rv, false, valid, x);
+            accumulate_half(Half1{}, x);
         }
+        load_plane(next.v, next.tok, rv);
+        pages = next;
     }
 
     if (p.splits == 1) {

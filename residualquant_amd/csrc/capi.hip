@@ -104,17 +104,17 @@ int compute_units() {
     return g_compute_units[device];
 }
 
-// Splits per (row, head): enough workgroups for `target` (default two per
-// compute unit, or one per compute unit with `one_per_cu`; long page streams
-// per workgroup measured best at batch 32 x 8k), at least 4 pages per split,
-// at most rq::kMaxSplits.
-int split_count(int64_t rows, int heads, int64_t max_pages, bool one_per_cu = false) {
+// Splits per (row, head): enough workgroups for `target` (by default
+// `per_cu` per compute unit: two for the streaming decode kernels, whose long
+// page streams per workgroup measured best at batch 32 x 8k, one at D = 96),
+// at least 4 pages per split, at most rq::kMaxSplits.
+int split_count(int64_t rows, int heads, int64_t max_pages, int per_cu = 2) {
     int64_t target;
     {
         std::lock_guard<std::mutex> lock(g_device_mutex);
         target = g_split_target;
     }
-    if (target <= 0) target = (one_per_cu ? 1LL : 2LL) * compute_units();
+    if (target <= 0) target = (int64_t)per_cu * compute_units();
     const int64_t pairs = std::max<int64_t>(1, rows * heads);
     int64_t splits = (target + pairs - 1) / pairs;
     const int64_t by_pages = std::max<int64_t>(1, (max_pages + 3) / 4);
@@ -297,9 +297,12 @@ int rq_quantize(int records, const void* const* key_ptrs, const int64_t* key_str
 
 // One workspace serves both paths of a packed attention call (the per-row
 // decode kernels and the multi-row kernels), so its size is the larger one.
+static int chain_splits(int64_t rows, int heads, int64_t max_pages);
+
 static size_t attention_workspace_total(int64_t rows, int heads, int head_dim, int64_t max_pages,
                                         int page_tokens) {
-    size_t total = workspace_layout(rows, heads, head_dim, split_count(rows, heads, max_pages)).total;
+    const int splits = std::max(split_count(rows, heads, max_pages), chain_splits(rows, heads, max_pages));
+    size_t total = workspace_layout(rows, heads, head_dim, splits).total;
     if (head_dim == 128 && (page_tokens == 16 || page_tokens == 32))
         total = std::max(total, multirow_layout(rows, heads, multirow_workspace_splits(heads, max_pages, page_tokens)).total);
     return total;
@@ -371,7 +374,17 @@ static int attention_common(const void* query, int64_t query_stride, const void*
 // call's two splits plus the separate prepare launch measured 1-2% slower per
 // loop-group step).
 static int packed_splits(int64_t rows, int heads, int head_dim, int64_t max_pages) {
-    return split_count(rows, heads, max_pages, head_dim == 96);
+    return split_count(rows, heads, max_pages, head_dim == 96 ? 1 : 2);
+}
+
+// Splits per (row, head) of an adjacent-mode call past loop 0
+// (decode_chain_kernel).  That kernel is bound by its VALU work, not by HBM,
+// and shorter page spans per workgroup let one workgroup's prologue and
+// finish overlap another's chain: at batch 32 x 8k x 16 heads, loops 1 / 2 /
+// 3 measured 364 / 512 / 660 us at two workgroups per compute unit and
+// 320 / 498 / 628 us at eight.
+static int chain_splits(int64_t rows, int heads, int64_t max_pages) {
+    return split_count(rows, heads, max_pages, 8);
 }
 
 static int attention_packed(const void* query, int64_t query_stride, const void* key, int64_t key_stride,
@@ -476,7 +489,8 @@ static int attention_packed(const void* query, int64_t query_stride, const void*
     }
     rq::AttentionParams p;
     // Never more splits than rq_attention_workspace_bytes() provides for.
-    const int splits = packed_splits(rows, heads, head_dim, max_pages);
+    const int splits = adjacent && loop_index > 0 ? chain_splits(rows, heads, max_pages)
+                                                  : packed_splits(rows, heads, head_dim, max_pages);
     const int anchor_record = adjacent ? 0 : anchor_index;
     status = attention_common(query, query_stride, key, key_stride, value, value_stride, output,
                               output_stride, rows, heads, head_dim, query_start_loc, seq_lens, requests,
