@@ -27,8 +27,8 @@ COEFFICIENTS = {"unit": 0, "norm": 1, "ls": 2}
 
 
 def build() -> str:
-    """Compile the oracle with its Makefile (gcc); returns the library path."""
-    subprocess.run(["make", "-s", "-C", _HERE], check=True)
+    """Compile the oracle with its Makefile (gcc), every time; returns the library path."""
+    subprocess.run(["make", "-s", "-B", "-C", _HERE], check=True)
     return _LIB_PATH
 
 

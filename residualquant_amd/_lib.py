@@ -43,9 +43,13 @@ EXPORTED_SYMBOLS = (
 _lib = None
 
 
-def build(jobs: int = 4) -> str:
-    """Compile every HIP source for gfx950 into ``librq_hip.so`` (hipcc via make)."""
-    subprocess.run(["make", "-s", "-C", CSRC_DIR, f"-j{jobs}"], check=True)
+def build(jobs: int = 8, force: bool = False) -> str:
+    """Compile every HIP source for gfx950 into ``librq_hip.so`` (hipcc via make).
+
+    ``force`` recompiles every object even where make finds them up to date.
+    """
+    args = ["make", "-s", "-C", CSRC_DIR, f"-j{jobs}"] + (["-B"] if force else [])
+    subprocess.run(args, check=True)
     return LIB_PATH
 
 
