@@ -626,115 +626,318 @@ void multirow_stream_kernel(MultiRowParams p) {
 
 // ---------------------------------------------------------------- finish
 
-__device__ __forceinline__ float block_max(float x, float* scratch) {
-#pragma unroll
-    for (int d = 32; d; d >>= 1) x = fmaxf(x, __shfl_xor(x, d));
-    __syncthreads();
-    if ((threadIdx.x & 63) == 0) scratch[threadIdx.x >> 6] = x;
-    __syncthreads();
-    return fmaxf(scratch[0], scratch[1]);
+// Row strides of the finish kernel's tiles: BF16/FP16 rows (halves), the
+// merged history transposed [channel][row] and rotated [row][channel] (FP32).
+constexpr int FS = D + 8;
+constexpr int HS = 36;
+constexpr int OS = D + 4;
+
+__device__ __forceinline__ float row8_max(float x) {
+    x = fmaxf(x, __shfl_xor(x, 1));
+    x = fmaxf(x, __shfl_xor(x, 2));
+    return fmaxf(x, __shfl_xor(x, 4));
 }
 
-__device__ __forceinline__ float block_sum(float x, float* scratch) {
-#pragma unroll
-    for (int d = 32; d; d >>= 1) x += __shfl_xor(x, d);
-    __syncthreads();
-    if ((threadIdx.x & 63) == 0) scratch[threadIdx.x >> 6] = x;
-    __syncthreads();
-    return scratch[0] + scratch[1];
+__device__ __forceinline__ float row8_sum(float x) {
+    x += __shfl_xor(x, 1);
+    x += __shfl_xor(x, 2);
+    return x + __shfl_xor(x, 4);
 }
 
-// One (row, head) per 128-thread workgroup, thread c = channel c.
-__global__ __launch_bounds__(D) void multirow_finish_kernel(MultiRowParams p) {
-    __shared__ float hist_rot[D];
-    __shared__ float query[D];
-    __shared__ float live[kMultiRowMaxLive];
-    __shared__ float scratch[2];
-    __shared__ int request_counts[D / 64];
-    const int64_t row = blockIdx.x;
-    const int head = blockIdx.y;
-    const int c = threadIdx.x;
-    // R_v row c (16-byte loads, issued before the lookup so that their round
-    // trip overlaps it) for hist . R_v^T.
-    uint4 rv[D / 8];
-    if (p.value_rotation) {
-        const uint4* src = reinterpret_cast<const uint4*>(p.value_rotation + ((int64_t)head * D + c) * D);
+// Whether rows of a BF16 tensor at `base` with row stride `stride`
+// (elements) start on 16-byte boundaries.  The boundary guarantees 8 bytes
+// for queries and keys and 2 bytes for values and outputs.
+__device__ __forceinline__ bool aligned_rows(const void* base, int64_t stride) {
+    return (reinterpret_cast<uintptr_t>(base) & 15u) == 0 && (stride & 7) == 0;
+}
+
+// 16 consecutive BF16 values at `src` (a 32-byte aligned offset of an
+// aligned_rows tensor when `vec`) as two 16-byte words.
+__device__ __forceinline__ void load_halves16(const uint16_t* src, bool vec, uint4 (&w)[2]) {
+    if (vec) {
+        w[0] = reinterpret_cast<const uint4*>(src)[0];
+        w[1] = reinterpret_cast<const uint4*>(src)[1];
+    } else {
+        uint32_t x[8];
 #pragma unroll
-        for (int i = 0; i < D / 8; ++i) rv[i] = src[i];
+        for (int i = 0; i < 8; ++i) x[i] = (uint32_t)src[2 * i] | ((uint32_t)src[2 * i + 1] << 16);
+        w[0] = make_uint4(x[0], x[1], x[2], x[3]);
+        w[1] = make_uint4(x[4], x[5], x[6], x[7]);
     }
-    // Request of the row: one round of parallel loads.
-    const int request = find_request_parallel(p.query_start_loc, p.requests, row, request_counts);
-    const int first = request < 0 ? -1 : p.query_start_loc[request];
-    if (first < 0) return;  // uniform
-    const int r = (int)(row - first);
+}
 
-    // History: merge the splits' partials (log2 units).
-    const float* entries = p.partials + ((int64_t)row * p.heads + head) * p.splits * kMultiRowEntry;
-    float hist_max = -__builtin_inff();
-    for (int s = 0; s < p.splits; ++s) hist_max = fmaxf(hist_max, entries[s * kMultiRowEntry]);
-    float hist_sum = 0.f, acc = 0.f;
-    if (hist_max != -__builtin_inff()) {
-        for (int s = 0; s < p.splits; ++s) {
-            const float m = entries[s * kMultiRowEntry];
-            if (m == -__builtin_inff()) continue;
-            const float w = __builtin_amdgcn_exp2f(m - hist_max);
-            hist_sum = fmaf(entries[s * kMultiRowEntry + 1], w, hist_sum);
-            acc = fmaf(entries[s * kMultiRowEntry + 4 + c], w, acc);
+// Eight BF16 values of a 16-byte word as FP32.
+__device__ __forceinline__ void widen_bf16(uint4 w, float* x) {
+    const uint32_t v[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        x[2 * i] = bf16_f32(v[i] & 0xffffu);
+        x[2 * i + 1] = bf16_f32(v[i] >> 16);
+    }
+}
+
+// One (request, head, 32-row tile) per 256-thread workgroup.  Thread t takes
+// row t / 8 of the tile and part p = t % 8 of it: the 16 channels
+// 16p..16p+15 of the merge, the query-key dots, the live values and the
+// output, and the 4 tokens 4p..4p+3 of a live chunk's scores.  The eight
+// threads of a row are adjacent lanes of one wave.
+//   1. merge the splits' partials (m, l, O) of each row (log2 units);
+//   2. rotate the tile's 32 merged rows by R_v^T at once (R_v staged
+//      transposed in LDS, read once per tile; 4 rows x 4 channels per thread);
+//   3. add the live tokens: in decode semantics the row's own token; in
+//      causal semantics the request's new tokens j <= row, 32 at a time with
+//      an online softmax over the rows' (m, l, O);
+//   4. write O / l in BF16.
+__global__ __launch_bounds__(kThreads) void multirow_finish_kernel(MultiRowParams p) {
+    // Region A holds R_v^T [j][c] (FP16) for the rotation, then the causal
+    // tiles; region B the merged history [c][r], then the rotated history
+    // [r][c] (FP32).
+    __shared__ __attribute__((aligned(16))) uint8_t region_a[D * FS * 2];
+    __shared__ __attribute__((aligned(16))) float region_b[D * HS];
+    static_assert(32 * OS <= D * HS, "the rotated history fits region B");
+    static_assert(3 * 32 * FS * 2 + 32 * 33 * 4 <= D * FS * 2, "the causal tiles fit region A");
+    uint16_t* rv_t = reinterpret_cast<uint16_t*>(region_a);
+    float* hist_t = region_b;
+    float* hist_rot = region_b;
+    uint16_t* q_tile = reinterpret_cast<uint16_t*>(region_a);  // causal: the rows' queries
+    uint16_t* k_tile = q_tile + 32 * FS;                      // causal: 32 live keys
+    uint16_t* v_tile = k_tile + 32 * FS;                      // causal: their values
+    float* probs = reinterpret_cast<float*>(v_tile + 32 * FS);
+    const int request = blockIdx.x;
+    const int head = blockIdx.y;
+    const int row0 = 32 * (int)blockIdx.z;
+    const int tid = threadIdx.x;
+    const int r = tid >> 3, part = tid & 7;
+    const bool rotate = p.value_rotation != nullptr;
+
+    // R_v row t / 2, half t % 2 (16-byte loads issued before the request
+    // lookup, so that the two round trips overlap; written transposed once
+    // the partials are merged).
+    uint4 rv[8];
+    if (rotate) {
+        const uint4* src = reinterpret_cast<const uint4*>(p.value_rotation + ((int64_t)head * D + (tid >> 1)) * D +
+                                                          64 * (tid & 1));
+#pragma unroll
+        for (int i = 0; i < 8; ++i) rv[i] = src[i];
+    }
+    const int first = p.query_start_loc[request];
+    int n = p.query_start_loc[request + 1] - first;
+    if (first < 0 || first >= p.rows) return;  // uniform over the workgroup, before any barrier
+    if (n > p.rows - first) n = (int)(p.rows - first);
+    if (row0 >= n) return;
+
+    const bool valid = row0 + r < n;
+    const int64_t row = (int64_t)first + row0 + (valid ? r : 0);
+    const float scale = kLog2e * 0.08838834764831845f;  // log2(e) / sqrt(128)
+    const int64_t channels = (int64_t)head * D + 16 * part;  // the part's 16 channels of a token row
+
+    // The row's query (and, in decode semantics, its own key and value).
+    const bool q_vec = aligned_rows(p.query, p.query_stride), k_vec = aligned_rows(p.key, p.key_stride),
+               v_vec = aligned_rows(p.value, p.value_stride);
+    uint4 qw[2], kw[2], vw[2];
+    load_halves16(p.query + row * p.query_stride + channels, q_vec, qw);
+    if (!p.causal) {
+        load_halves16(p.key + row * p.key_stride + channels, k_vec, kw);
+        load_halves16(p.value + row * p.value_stride + channels, v_vec, vw);
+    }
+    const float shift = p.row_shift[row * p.heads + head];
+
+    // 1. Merge the splits online, four at a time: every load of a batch is
+    // issued before any of its arithmetic (split indices past the last are
+    // clamped and weighted zero, so no load sits behind a branch).  Rows past
+    // the request merge nothing.
+    float m = -__builtin_inff(), l = 0.f, acc[16];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) acc[i] = 0.f;
+    const float* entries = p.partials + (row * p.heads + head) * p.splits * kMultiRowEntry;
+    for (int s0 = 0; s0 < p.splits; s0 += 4) {
+        float2 ml[4];
+        float4 ox[4][4];
+#pragma unroll
+        for (int b = 0; b < 4; ++b) {
+            const int s = s0 + b < p.splits ? s0 + b : p.splits - 1;
+            const float* e = entries + s * kMultiRowEntry;
+            ml[b] = *reinterpret_cast<const float2*>(e);
+#pragma unroll
+            for (int c = 0; c < 4; ++c) ox[b][c] = reinterpret_cast<const float4*>(e + 4 + 16 * part)[c];
+        }
+#pragma unroll
+        for (int b = 0; b < 4; ++b) {
+            const float ms = (valid && s0 + b < p.splits) ? ml[b].x : -__builtin_inff();
+            const float new_max = fmaxf(m, ms);
+            const float base = new_max == -__builtin_inff() ? 0.f : new_max;
+            const float keep = __builtin_amdgcn_exp2f(m - base), w = __builtin_amdgcn_exp2f(ms - base);
+            m = new_max;
+            l = fmaf(l, keep, ml[b].y * w);
+            const float x[16] = {ox[b][0].x, ox[b][0].y, ox[b][0].z, ox[b][0].w, ox[b][1].x, ox[b][1].y,
+                                 ox[b][1].z, ox[b][1].w, ox[b][2].x, ox[b][2].y, ox[b][2].z, ox[b][2].w,
+                                 ox[b][3].x, ox[b][3].y, ox[b][3].z, ox[b][3].w};
+#pragma unroll
+            for (int i = 0; i < 16; ++i) acc[i] = fmaf(acc[i], keep, x[i] * w);
         }
     }
-    hist_rot[c] = acc;
-    query[c] = bf16_f32(p.query[row * p.query_stride + (int64_t)head * D + c]);
-    __syncthreads();
-    float hist = acc;
-    if (p.value_rotation) {
-        // hist . R_v^T: channel c takes row c of R_v.
-        float h[4] = {0.f, 0.f, 0.f, 0.f};
+
+    // 2. hist . R_v^T for the tile's 32 rows.
+    if (rotate) {
 #pragma unroll
-        for (int i = 0; i < D / 8; ++i) {
+        for (int i = 0; i < 16; ++i) hist_t[(16 * part + i) * HS + r] = acc[i];
+        const int c = tid >> 1, j0 = 64 * (tid & 1);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
             const uint32_t w[4] = {rv[i].x, rv[i].y, rv[i].z, rv[i].w};
 #pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                h[j] = fmaf(hist_rot[8 * i + 2 * j], f16_to_f32(w[j] & 0xffffu), h[j]);
-                h[j] = fmaf(hist_rot[8 * i + 2 * j + 1], f16_to_f32(w[j] >> 16), h[j]);
+            for (int e = 0; e < 4; ++e) {
+                rv_t[(j0 + 8 * i + 2 * e) * FS + c] = (uint16_t)(w[e] & 0xffffu);
+                rv_t[(j0 + 8 * i + 2 * e + 1) * FS + c] = (uint16_t)(w[e] >> 16);
             }
         }
-        hist = (h[0] + h[1]) + (h[2] + h[3]);
+        __syncthreads();
+        const int cb = tid & 31, rb = tid >> 5;  // channels 4 cb .. 4 cb + 3, rows 4 rb .. 4 rb + 3
+        float o[4][4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int k = 0; k < 4; ++k) o[i][k] = 0.f;
+#pragma unroll 8
+        for (int j = 0; j < D; ++j) {
+            const float4 h4 = *reinterpret_cast<const float4*>(&hist_t[j * HS + 4 * rb]);
+            const uint2 w = *reinterpret_cast<const uint2*>(&rv_t[j * FS + 4 * cb]);
+            const float rk[4] = {f16_to_f32(w.x & 0xffffu), f16_to_f32(w.x >> 16), f16_to_f32(w.y & 0xffffu),
+                                 f16_to_f32(w.y >> 16)};
+            const float h[4] = {h4.x, h4.y, h4.z, h4.w};
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+#pragma unroll
+                for (int k = 0; k < 4; ++k) o[i][k] = fmaf(h[i], rk[k], o[i][k]);
+        }
+        __syncthreads();  // the rotated history replaces the merged one
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+            *reinterpret_cast<float4*>(&hist_rot[(4 * rb + i) * OS + 4 * cb]) =
+                make_float4(o[i][0], o[i][1], o[i][2], o[i][3]);
+        __syncthreads();
+#pragma unroll
+        for (int c4 = 0; c4 < 4; ++c4) {
+            const float4 x = *reinterpret_cast<const float4*>(&hist_rot[r * OS + 16 * part + 4 * c4]);
+            acc[4 * c4] = x.x;
+            acc[4 * c4 + 1] = x.y;
+            acc[4 * c4 + 2] = x.z;
+            acc[4 * c4 + 3] = x.w;
+        }
     }
 
-    // Live tokens: the row's own (decode) or the request's new rows j <= r (causal).
-    const int64_t live_first = p.causal ? first : row;
-    const int live_count = p.causal ? (r < kMultiRowMaxLive ? r + 1 : kMultiRowMaxLive) : 1;
-    const float shift = p.row_shift[row * p.heads + head];
-    const float scale = kLog2e * 0.08838834764831845f;
-    float local_max = -__builtin_inff();
-    for (int j = c; j < live_count; j += D) {
-        const uint16_t* k = p.key + (live_first + j) * p.key_stride + (int64_t)head * D;
+    // 3. Live tokens.
+    float q[16];
+    widen_bf16(qw[0], q);
+    widen_bf16(qw[1], q + 8);
+    if (!p.causal) {
+        // The row's own token.
+        float k[16], v[16];
+        widen_bf16(kw[0], k);
+        widen_bf16(kw[1], k + 8);
+        widen_bf16(vw[0], v);
+        widen_bf16(vw[1], v + 8);
         float dot = 0.f;
-        for (int d = 0; d < D; d += 4) {
-            const uint2 w = *reinterpret_cast<const uint2*>(k + d);
-            dot = fmaf(query[d], bf16_f32(w.x & 0xffffu), dot);
-            dot = fmaf(query[d + 1], bf16_f32(w.x >> 16), dot);
-            dot = fmaf(query[d + 2], bf16_f32(w.y & 0xffffu), dot);
-            dot = fmaf(query[d + 3], bf16_f32(w.y >> 16), dot);
+#pragma unroll
+        for (int i = 0; i < 16; ++i) dot = fmaf(q[i], k[i], dot);
+        const float score = row8_sum(dot) * scale - shift;
+        const float total_max = fmaxf(m, score);
+        const float hist_weight = m == -__builtin_inff() ? 0.f : __builtin_amdgcn_exp2f(m - total_max);
+        const float live = __builtin_amdgcn_exp2f(score - total_max);
+        l = fmaf(l, hist_weight, live);
+#pragma unroll
+        for (int i = 0; i < 16; ++i) acc[i] = fmaf(live, v[i], acc[i] * hist_weight);
+    } else {
+        // The request's new tokens 0 .. row0 + r, in chunks of 32 shared by the tile's rows.
+        {
+            uint4* dst = reinterpret_cast<uint4*>(&q_tile[r * FS + 16 * part]);
+            dst[0] = qw[0];
+            dst[1] = qw[1];
         }
-        const float score = dot * scale - shift;
-        live[j] = score;
-        local_max = fmaxf(local_max, score);
+        const int live_end = n < row0 + 32 ? n : row0 + 32;
+        for (int c0 = 0; c0 < live_end; c0 += 32) {
+            __syncthreads();  // the previous chunk's reads are done
+            {
+                // Thread (r, part) stages the part's channels of live token c0 + r.
+                const int j = c0 + r;
+                uint4 kx[2] = {make_uint4(0u, 0u, 0u, 0u), make_uint4(0u, 0u, 0u, 0u)}, vx[2] = {kx[0], kx[1]};
+                if (j < n) {
+                    load_halves16(p.key + ((int64_t)first + j) * p.key_stride + channels, k_vec, kx);
+                    load_halves16(p.value + ((int64_t)first + j) * p.value_stride + channels, v_vec, vx);
+                }
+                uint4* kd = reinterpret_cast<uint4*>(&k_tile[r * FS + 16 * part]);
+                uint4* vd = reinterpret_cast<uint4*>(&v_tile[r * FS + 16 * part]);
+                kd[0] = kx[0];
+                kd[1] = kx[1];
+                vd[0] = vx[0];
+                vd[1] = vx[1];
+            }
+            __syncthreads();
+            // Scores of row r against tokens c0 + 4 part .. + 3.
+            float s[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll 4
+            for (int d = 0; d < D; d += 8) {
+                float qd[8];
+                widen_bf16(*reinterpret_cast<const uint4*>(&q_tile[r * FS + d]), qd);
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    float kd[8];
+                    widen_bf16(*reinterpret_cast<const uint4*>(&k_tile[(4 * part + i) * FS + d]), kd);
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) s[i] = fmaf(qd[e], kd[e], s[i]);
+                }
+            }
+            float chunk_max = -__builtin_inff();
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int j = c0 + 4 * part + i;
+                s[i] = (valid && j <= row0 + r && j < n) ? s[i] * scale - shift : -__builtin_inff();
+                chunk_max = fmaxf(chunk_max, s[i]);
+            }
+            const float new_max = fmaxf(m, row8_max(chunk_max));
+            const float base = new_max == -__builtin_inff() ? 0.f : new_max;
+            const float rescale = __builtin_amdgcn_exp2f(m - base);
+            m = new_max;
+            float chunk_sum = 0.f;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const float w = __builtin_amdgcn_exp2f(s[i] - base);
+                probs[r * 33 + 4 * part + i] = w;
+                chunk_sum += w;
+            }
+            l = fmaf(l, rescale, row8_sum(chunk_sum));
+#pragma unroll
+            for (int i = 0; i < 16; ++i) acc[i] *= rescale;
+            wave_sync();  // row r's probabilities come from lanes of this wave
+#pragma unroll 4
+            for (int jj = 0; jj < 32; ++jj) {
+                const float w = probs[r * 33 + jj];
+                float vd[16];
+                widen_bf16(*reinterpret_cast<const uint4*>(&v_tile[jj * FS + 16 * part]), vd);
+                widen_bf16(*reinterpret_cast<const uint4*>(&v_tile[jj * FS + 16 * part + 8]), vd + 8);
+#pragma unroll
+                for (int i = 0; i < 16; ++i) acc[i] = fmaf(w, vd[i], acc[i]);
+            }
+        }
     }
-    const float total_max = fmaxf(block_max(local_max, scratch), hist_max);
-    float local_sum = 0.f;
-    for (int j = c; j < live_count; j += D) {
-        const float w = __builtin_amdgcn_exp2f(live[j] - total_max);
-        live[j] = w;
-        local_sum += w;
+
+    // 4. Output.
+    if (valid) {
+        uint32_t w[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) w[i] = bf16_rn(acc[2 * i] / l) | (bf16_rn(acc[2 * i + 1] / l) << 16);
+        uint16_t* out = p.output + row * p.output_stride + channels;
+        if (aligned_rows(p.output, p.output_stride)) {
+            reinterpret_cast<uint4*>(out)[0] = make_uint4(w[0], w[1], w[2], w[3]);
+            reinterpret_cast<uint4*>(out)[1] = make_uint4(w[4], w[5], w[6], w[7]);
+        } else {
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                out[2 * i] = (uint16_t)(w[i] & 0xffffu);
+                out[2 * i + 1] = (uint16_t)(w[i] >> 16);
+            }
+        }
     }
-    const float live_sum = block_sum(local_sum, scratch);  // its barriers publish live[]
-    const float hist_weight = hist_max == -__builtin_inff() ? 0.f : __builtin_amdgcn_exp2f(hist_max - total_max);
-    float o = hist * hist_weight;
-    const uint16_t* v = p.value + live_first * p.value_stride + (int64_t)head * D + c;
-    for (int j = 0; j < live_count; ++j) o = fmaf(live[j], bf16_f32(v[j * p.value_stride]), o);
-    const float total = hist_sum * hist_weight + live_sum;
-    p.output[row * p.output_stride + (int64_t)head * D + c] = (uint16_t)bf16_rn(o / total);
 }
 
 template <int PT, bool HasL, int BA, int BL>
@@ -771,7 +974,8 @@ hipError_t launch_multirow(const MultiRowParams& p, hipStream_t stream) {
         launch_pt<32>(p, stream);
     else
         return hipErrorInvalidValue;
-    hipLaunchKernelGGL(multirow_finish_kernel, dim3((unsigned)p.rows, (unsigned)p.heads), dim3(D), 0, stream, p);
+    hipLaunchKernelGGL(multirow_finish_kernel, dim3((unsigned)p.requests, (unsigned)p.heads, (unsigned)p.row_tiles),
+                       dim3(kThreads), 0, stream, p);
     return hipGetLastError();
 }
 
