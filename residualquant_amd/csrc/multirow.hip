@@ -158,28 +158,28 @@ __device__ __forceinline__ void record_codes(const RecordBytes<Bits>& r, float (
 }
 
 // Scale (times 2^9) and offset of the lane's two 16-channel blocks.
-__device__ __forceinline__ void record_coefficients(uint32_t scale, uint32_t offset, int group, float (&s)[2],
-                                                    float (&o)[2]) {
+template <int G>
+__device__ __forceinline__ void record_coefficients(uint32_t scale, uint32_t offset, float (&s)[2], float (&o)[2]) {
     s[0] = __builtin_amdgcn_cvt_f32_fp8((int)scale, 0) * 512.0f;
     o[0] = __builtin_amdgcn_cvt_f32_fp8((int)offset, 0);
-    s[1] = group == 32 ? s[0] : __builtin_amdgcn_cvt_f32_fp8((int)scale, 1) * 512.0f;
-    o[1] = group == 32 ? o[0] : __builtin_amdgcn_cvt_f32_fp8((int)offset, 1);
+    s[1] = G == 32 ? s[0] : __builtin_amdgcn_cvt_f32_fp8((int)scale, 1) * 512.0f;
+    o[1] = G == 32 ? o[0] : __builtin_amdgcn_cvt_f32_fp8((int)offset, 1);
 }
 
 // One plane's values for the lane's 32 channels in FP32: alpha (c.s+o)_A +
 // (c.s+o)_L, evaluated per 16-channel block as c_A (alpha s_A) + (c_L s_L +
 // (alpha o_A + o_L)) (two fmas per channel), or (c.s+o)_A without a loop
 // record.
-template <int BA, int BL, bool HasL>
-__device__ __forceinline__ void plane_values(const RecordBytes<BA>& a_rec, int a_group, const RecordBytes<BL>& l_rec,
-                                             int l_group, float alpha, float (&x)[32]) {
+template <int BA, int GA, int BL, int GL, bool HasL>
+__device__ __forceinline__ void plane_values(const RecordBytes<BA>& a_rec, const RecordBytes<BL>& l_rec, float alpha,
+                                             float (&x)[32]) {
     float sa[2], oa[2];
-    record_coefficients(a_rec.scale, a_rec.offset, a_group, sa, oa);
+    record_coefficients<GA>(a_rec.scale, a_rec.offset, sa, oa);
     float ca[32];
     record_codes<BA>(a_rec, ca);
     if constexpr (HasL) {
         float sl[2], ol[2];
-        record_coefficients(l_rec.scale, l_rec.offset, l_group, sl, ol);
+        record_coefficients<GL>(l_rec.scale, l_rec.offset, sl, ol);
         float cl[32];
         record_codes<BL>(l_rec, cl);
 #pragma unroll
@@ -232,7 +232,7 @@ __device__ __forceinline__ void wave_sync() {
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
-template <int PT, bool HasL, int BA, int BL>
+template <int PT, bool HasL, int BA, int GA, int BL, int GL>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2)))
 void multirow_stream_kernel(MultiRowParams p) {
     __shared__ __attribute__((aligned(16))) uint8_t lds[kLdsBytes];
@@ -483,7 +483,7 @@ void multirow_stream_kernel(MultiRowParams p) {
             const float alpha_k = HasL ? bf16_f32(cur.kl.alpha) : 1.f;
             {
                 float k[32];
-                plane_values<BA, BL, HasL>(cur.ka, p.anchor.group, cur.kl, p.residual.group, alpha_k, k);
+                plane_values<BA, GA, BL, GL, HasL>(cur.ka, cur.kl, alpha_k, k);
                 uint32_t kw[16];
 #pragma unroll
                 // No mask: the scores of tokens past the history become -inf below.
@@ -495,8 +495,7 @@ void multirow_stream_kernel(MultiRowParams p) {
             }
             {
                 float v[32];
-                plane_values<BA, BL, HasL>(cur.va, p.anchor.group, cur.vl, p.residual.group,
-                                           HasL ? bf16_f32(cur.vl.alpha) : 1.f, v);
+                plane_values<BA, GA, BL, GL, HasL>(cur.va, cur.vl, HasL ? bf16_f32(cur.vl.alpha) : 1.f, v);
                 uint32_t vw[16];
 #pragma unroll
                 for (int c = 0; c < 16; ++c) vw[c] = pack_bf16(v[2 * c], v[2 * c + 1]);
@@ -526,16 +525,23 @@ void multirow_stream_kernel(MultiRowParams p) {
 #pragma unroll
         for (int m = 0; m < D / 16; ++m) s = mfma(*reinterpret_cast<const F16x8*>(k_row + 16 * m), q_operand[m], s);
 
-        float tile_max = -__builtin_inff();
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
             const int local = 8 * (r >> 2) + 4 * half + (r & 3);
             float x = s[r] * row_scale;
             if (mean_anchor) x = fmaf(alpha_tile[local], q_mu_anchor, x);
-            x = kTile * tile + local < history ? x : -__builtin_inff();
             s[r] = x;
-            tile_max = fmaxf(tile_max, x);
         }
+        // Tokens past the history score -inf (only in the tile that reaches past it).
+        if (kTile * tile + kTile > history) {
+            asm volatile("");
+#pragma unroll
+            for (int r = 0; r < 16; ++r)
+                s[r] = kTile * tile + 8 * (r >> 2) + 4 * half + (r & 3) < history ? s[r] : -__builtin_inff();
+        }
+        float tile_max = -__builtin_inff();
+#pragma unroll
+        for (int r = 0; r < 16; ++r) tile_max = fmaxf(tile_max, s[r]);
         tile_max = fmaxf(tile_max, __shfl_xor(tile_max, 32));
         const float new_max = fmaxf(running_max, tile_max);
         const float base = new_max == -__builtin_inff() ? 0.f : new_max;
@@ -940,28 +946,44 @@ __global__ __launch_bounds__(kThreads) void multirow_finish_kernel(MultiRowParam
     }
 }
 
-template <int PT, bool HasL, int BA, int BL>
+template <int PT, bool HasL, int BA, int GA, int BL, int GL>
 void launch_one(const MultiRowParams& p, hipStream_t stream) {
     const dim3 grid((unsigned)p.requests, (unsigned)p.heads, (unsigned)(p.splits * p.row_tiles));
-    hipLaunchKernelGGL((multirow_stream_kernel<PT, HasL, BA, BL>), grid, dim3(kThreads), 0, stream, p);
+    hipLaunchKernelGGL((multirow_stream_kernel<PT, HasL, BA, GA, BL, GL>), grid, dim3(kThreads), 0, stream, p);
+}
+
+template <int PT, int BA, int GA, int BL>
+void launch_residual_group(const MultiRowParams& p, hipStream_t stream) {
+    if (p.residual.group == 32)
+        launch_one<PT, true, BA, GA, BL, 32>(p, stream);
+    else
+        launch_one<PT, true, BA, GA, BL, 16>(p, stream);
+}
+
+template <int PT, int BA, int GA>
+void launch_anchor(const MultiRowParams& p, hipStream_t stream) {
+    if (!p.has_residual)
+        launch_one<PT, false, BA, GA, 2, 32>(p, stream);
+    else if (p.residual.bits == 2)
+        launch_residual_group<PT, BA, GA, 2>(p, stream);
+    else
+        launch_residual_group<PT, BA, GA, 4>(p, stream);
 }
 
 template <int PT, int BA>
-void launch_anchor(const MultiRowParams& p, hipStream_t stream) {
-    if (!p.has_residual)
-        launch_one<PT, false, BA, 2>(p, stream);
-    else if (p.residual.bits == 2)
-        launch_one<PT, true, BA, 2>(p, stream);
+void launch_anchor_group(const MultiRowParams& p, hipStream_t stream) {
+    if (p.anchor.group == 32)
+        launch_anchor<PT, BA, 32>(p, stream);
     else
-        launch_one<PT, true, BA, 4>(p, stream);
+        launch_anchor<PT, BA, 16>(p, stream);
 }
 
 template <int PT>
 void launch_pt(const MultiRowParams& p, hipStream_t stream) {
     if (p.anchor.bits == 4)
-        launch_anchor<PT, 4>(p, stream);
+        launch_anchor_group<PT, 4>(p, stream);
     else
-        launch_anchor<PT, 2>(p, stream);
+        launch_anchor_group<PT, 2>(p, stream);
 }
 
 }  // namespace
