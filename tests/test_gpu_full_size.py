@@ -100,8 +100,8 @@ def _decode_full_size(oracle, device, batch, history, heads, dim, records, rows,
 
 
 def test_decode_full_size_ouro_sampled_rows(oracle, device):
-    print("[case] decode B32 x 8192 x 16 heads x D128, rows 0 and 19", flush=True)
-    _decode_full_size(oracle, device, 32, 8192, 16, 128, OURO_G32, rows=(0, 19), loops=(0, 3), seed=8100)
+    print("[case] decode B32 x 8192 x 16 heads x D128, rows 0, 19 and 31, every loop", flush=True)
+    _decode_full_size(oracle, device, 32, 8192, 16, 128, OURO_G32, rows=(0, 19, 31), loops=(0, 1, 2, 3), seed=8100)
 
 
 def test_decode_full_size_huginn_sampled_rows(oracle, device):
