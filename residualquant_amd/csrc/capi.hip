@@ -434,8 +434,13 @@ static int attention_packed(const void* query, int64_t query_stride, const void*
         if (rows == 0 || requests == 0) return ok();
         if (causal && rows - requests + 1 > rq::kMultiRowMaxLive)
             return fail(RQ_EINVAL, "At most %d new rows per request over packed history", rq::kMultiRowMaxLive);
+        // The grid's row tiles cover the longest request the row count allows;
+        // the split count is sized from the average request (tiles past a
+        // request's rows exit at once, so counting them would take too few
+        // splits and leave compute units idle).
         const int64_t row_tiles = (rows - requests + 1 + 31) / 32;
-        const int splits = multirow_splits(requests * heads * row_tiles, max_pages, page_tokens);
+        const int64_t average_tiles = std::max<int64_t>(1, (rows / requests + 31) / 32);
+        const int splits = multirow_splits(requests * heads * average_tiles, max_pages, page_tokens);
         const MultiRowLayout layout = multirow_layout(rows, heads, splits);
         if (workspace == nullptr || workspace_bytes < layout.total)
             return fail(RQ_ENOSPACE, "Attention workspace of %zu bytes required (got %zu)", layout.total,
