@@ -432,13 +432,12 @@ static int attention_packed(const void* query, int64_t query_stride, const void*
                                   block_table_stride, max_pages, nullptr, 0, 0, nullptr);
         if (status != RQ_OK) return status;
         if (rows == 0 || requests == 0) return ok();
-        if (causal && rows - requests + 1 > rq::kMultiRowMaxLive)
-            return fail(RQ_EINVAL, "At most %d new rows per request over packed history", rq::kMultiRowMaxLive);
-        // The grid's row tiles cover the longest request the row count allows;
+        // The grid's row tiles cover the longest request the row count allows
+        // (a request may have no new rows, so one request may hold them all);
         // the split count is sized from the average request (tiles past a
         // request's rows exit at once, so counting them would take too few
         // splits and leave compute units idle).
-        const int64_t row_tiles = (rows - requests + 1 + 31) / 32;
+        const int64_t row_tiles = (rows + 31) / 32;
         const int64_t average_tiles = std::max<int64_t>(1, (rows / requests + 31) / 32);
         const int splits = multirow_splits(requests * heads * average_tiles, max_pages, page_tokens);
         const MultiRowLayout layout = multirow_layout(rows, heads, splits);

@@ -190,7 +190,6 @@ hipError_t launch_attention(const AttentionParams& p, hipStream_t stream, hipEve
 constexpr int kMultiRowEntry = 132;        // per (row, head, split): m, l, 2 unused, O[128] (log2 units)
 constexpr int kMultiRowMaxSplits = 8;      // for parallelism (more only for very long histories)
 constexpr int kMultiRowMaxSplitPages = 1024;  // pages of one split at most
-constexpr int kMultiRowMaxLive = 2048;     // new rows per request at most (causal)
 struct MultiRowParams {
     const uint16_t* query;
     int64_t query_stride;

@@ -213,7 +213,7 @@ def packed_prefill_attention(query: torch.Tensor, key: torch.Tensor, value: torc
     prefill of a prompt chunk over a packed prefix, which the reference
     cannot run (its scheduler forbids partial prefill, rq/scheduler.py:11-18);
     arguments and validation are those of ``attention``.  Anchor mode at
-    head_dim 128, at most 2048 new rows per request.
+    head_dim 128; a request may have no new rows.
     """
     key_rotation_ptr, value_rotation_ptr = _validate_packed_inputs(
         query, key, value, kv_cache, output, query_start_loc, seq_lens, block_table, key_rotation, value_rotation,

@@ -68,6 +68,7 @@ CASES = [
     ([90, 51], [2, 6], 2, ((2, 16), (2, 16), (4, 32), (2, 32)), 16, True, True),
     ([77], [5], 1, ((4, 16),), 32, True, True),           # single-record group
     ([400, 123], [12, 20], 2, OURO_G32, 16, True, True),  # 16 rows per request on average
+    ([50, 300], [0, 33], 2, OURO_G32, 16, True, True),    # a request with no new rows: 33 rows in one request
 ]
 
 
