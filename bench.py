@@ -841,7 +841,7 @@ def run_step(args):
         log(f"[bench] step B={batch} ctx={context}: {step_ms:.2f} ms/step, {entry['tokens_per_s']:.0f} tokens/s, "
             f"split-K attention kernels {attention_ms:.2f} ms in {attention_calls} calls")
         results.append(entry)
-        del graph, model
+        del model
         torch.cuda.empty_cache()
     head = next(r for r in results if (r["batch"], r["context"]) == (32, 8192)) if any(
         (r["batch"], r["context"]) == (32, 8192) for r in results) else results[-1]
