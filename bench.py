@@ -109,15 +109,16 @@ def capture(torch, fn):
     return graph
 
 
-def measured_traffic(summary="decode_c2_counters.json"):
-    """HBM bytes per residual-loop decode launch from a committed rocprofv3
-    FETCH_SIZE/WRITE_SIZE summary, with the commit it was measured on."""
+def measured_traffic(summary="decode_c2_counters.json", key="residual_loop_traffic_bytes"):
+    """HBM bytes per launch of the dominant kernel (by default the residual-loop
+    decode launch) from a committed rocprofv3 FETCH_SIZE/WRITE_SIZE summary,
+    with the commit it was measured on."""
     path = os.path.join(ROOT, "profiles", summary)
     if not os.path.exists(path):
         return {"bytes": None, "commit": None}
     with open(path) as handle:
         data = json.load(handle)
-    return {"bytes": data.get("residual_loop_traffic_bytes"), "commit": data.get("commit")}
+    return {"bytes": data.get(key), "commit": data.get("commit")}
 
 
 def kernel_durations_ms(ops, calls, reps, warmup=10):
@@ -316,7 +317,10 @@ def run_quantize(args):
     input_bytes = tokens * heads * dim * 2 * 4 * 2
 
     results = {}
+    wanted = args.schedules.split(",")
     for name, schedule in (("g32", SCHEDULE), ("g16", HUGINN_SCHEDULE), ("mixed", QUANTIZE_SCHEDULE)):
+        if name not in wanted:
+            continue
         width = rq.page_width(dim, schedule)
         cache = torch.zeros((2, blocks, heads, page_tokens, width), dtype=torch.uint8, device=device)
 
@@ -351,7 +355,7 @@ def run_quantize(args):
             f"({results[name]['rotation_TFLOPs']:.1f} TFLOP/s rotation)")
         del cache
 
-    head = results["g32"]
+    head = results["g32"] if "g32" in results else next(iter(results.values()))
     cpu = None
     if args.cpu_budget > 0:
         log("[bench] cpu baseline (oracle quantize) ...")
@@ -387,7 +391,8 @@ def run_quantize(args):
             "peak": PEAK_FP32_TFLOPS,
             "unit": "TFLOP/s",
             "frac": head["rotation_TFLOPs"] / PEAK_FP32_TFLOPS,
-            "traffic": None,
+            "traffic": measured_traffic("quantize_c1_counters.json", "traffic_bytes")["bytes"],
+            "traffic_measured_at": measured_traffic("quantize_c1_counters.json", "traffic_bytes")["commit"],
             "kernel": "quantize_mfma_kernel<128,4,3,true>: FP32 rotation FMAs (K=1 v_mfma_f32_16x16x1_4b_f32 "
                       "chains) against the published FP32 peak; HBM traffic is 9% of peak at this rate; on gfx950 "
                       "the FP32 MFMAs and the commit's VALU do not overlap, so the call is their sum",
@@ -466,7 +471,8 @@ def run_prefill(args):
             "peak": PEAK_BF16_TFLOPS,
             "unit": "TFLOP/s",
             "frac": achieved / PEAK_BF16_TFLOPS,
-            "traffic": None,
+            "traffic": measured_traffic("prefill_a12_counters.json", "traffic_bytes")["bytes"],
+            "traffic_measured_at": measured_traffic("prefill_a12_counters.json", "traffic_bytes")["commit"],
             "kernel": "prefill_kernel<128>: causal-half QK^T + PV FLOPs against the dense BF16 MFMA peak",
         },
         "torch_sdpa": {"us_per_call": torch_ms * 1e3, "TFLOPs": flop / (torch_ms * 1e-3) / 1e12},
@@ -890,6 +896,8 @@ def main():
     parser.add_argument("--cpu-budget", type=float, default=10.0,
                         help="seconds of CPU oracle work for the cpu_baseline sample (0 = skip)")
     parser.add_argument("--no-bf16", action="store_true")
+    parser.add_argument("--schedules", default="g32,g16,mixed",
+                        help="quantize: the schedules to time (g32 first: the headline; for counter runs)")
     parser.add_argument("--split-target", type=int, default=0,
                         help="split-K workgroups per decode launch (0 = the library's default)")
     parser.add_argument("--eager", action="store_true",
