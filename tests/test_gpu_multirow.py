@@ -94,6 +94,44 @@ def test_multirow_matches_oracle(oracle, device, case, causal):
         assert err.max() <= MAX_ABS and err.mean() <= MEAN_ABS, (loop, err.max(), err.mean())
 
 
+def _view(t: torch.Tensor, device, extra: int, offset: int) -> torch.Tensor:
+    """t as a [rows, heads, D] view with token stride heads * D + extra, starting `offset` elements in."""
+    rows, heads, dim = t.shape
+    width = heads * dim + extra
+    flat = torch.full((rows * width + offset + 8,), float("nan"), dtype=torch.bfloat16, device=device)
+    view = torch.as_strided(flat, (rows, heads, dim), (width, dim, 1), storage_offset=offset)
+    view.copy_(t.to(device))
+    return view
+
+
+@pytest.mark.parametrize("causal", [True, False], ids=["prefill", "decode"])
+def test_multirow_strided_views(oracle, device, causal):
+    """Token strides and offsets the boundary allows: queries and keys 8-byte
+    aligned rows (stride a multiple of 4), values and outputs 2-byte aligned
+    (odd stride, odd offset), so the finish reads and writes them value by
+    value instead of in 16-byte words."""
+    d = make_decode([300, 123], 2, 128, OURO_G32, seed=31, rows_per_request=[40, 12])
+    g = d.group
+    expected_cache = g.oracle_cache(oracle)
+    cache = torch.from_numpy(expected_cache).to(device)
+    kr, vr, km = g.device_args(device)
+    q, k = _view(d.query, device, 4, 4), _view(d.key, device, 4, 4)
+    v = _view(d.value, device, 1, 1)
+    out = _view(torch.zeros_like(d.query), device, 3, 1)
+    function = rq.packed_prefill_attention if causal else rq.attention
+    for loop in (0, 3):
+        out.fill_(float("nan"))
+        function(q, k, v, cache, out, d.query_start_loc.to(device), d.seq_lens.to(device), d.table.to(device), kr, vr,
+                 km, g.records, g.mode, g.anchor, loop)
+        torch.cuda.synchronize()
+        got = out.float().cpu().numpy()
+        want = _oracle(oracle, d, expected_cache, loop, causal)
+        err = np.abs(got - _bf16(want))
+        print(f"[case] strided causal={causal} loop {loop}: max {err.max():.3g} mean {err.mean():.3g}", flush=True)
+        assert np.isfinite(got).all()
+        assert err.max() <= MAX_ABS and err.mean() <= MEAN_ABS, (loop, err.max(), err.mean())
+
+
 def test_decode_rows_agree_with_single_row_calls(oracle, device):
     """The multi-row route and the per-row decode kernel give the same rows within the bar."""
     d = make_decode([500, 300], 4, 128, OURO_G32, seed=5, rows_per_request=[9, 7])
