@@ -637,8 +637,8 @@ void multirow_stream_kernel(MultiRowParams p) {
 
 // ---------------------------------------------------------------- finish
 
-// Row strides of the finish kernel's tiles: BF16/FP16 rows (halves), the
-// merged history transposed [channel][row] and rotated [row][channel] (FP32).
+// Row strides of the finish kernel's tiles: BF16/FP16 rows (halves) and the
+// rotated history [row][channel] (FP32); region B holds D x HS floats.
 constexpr int FS = D + 8;
 constexpr int HS = 36;
 constexpr int OS = D + 4;
@@ -700,15 +700,12 @@ __device__ __forceinline__ void widen_bf16(uint4 w, float* x) {
 //      an online softmax over the rows' (m, l, O);
 //   4. write O / l in BF16.
 __global__ __launch_bounds__(kThreads) void multirow_finish_kernel(MultiRowParams p) {
-    // Region A holds R_v^T [j][c] (FP16) for the rotation, then the causal
-    // tiles; region B the merged history [c][r], then the rotated history
-    // [r][c] (FP32).
+    // Region A holds the merged rows' FP16 parts [r][j] for the rotation,
+    // then the causal tiles; region B the rotated history [r][c] (FP32).
     __shared__ __attribute__((aligned(16))) uint8_t region_a[D * FS * 2];
     __shared__ __attribute__((aligned(16))) float region_b[D * HS];
     static_assert(32 * OS <= D * HS, "the rotated history fits region B");
     static_assert(3 * 32 * FS * 2 + 32 * 33 * 4 <= D * FS * 2, "the causal tiles fit region A");
-    uint16_t* rv_t = reinterpret_cast<uint16_t*>(region_a);
-    float* hist_t = region_b;
     float* hist_rot = region_b;
     uint16_t* q_tile = reinterpret_cast<uint16_t*>(region_a);  // causal: the rows' queries
     uint16_t* k_tile = q_tile + 32 * FS;                      // causal: 32 live keys
@@ -721,15 +718,17 @@ __global__ __launch_bounds__(kThreads) void multirow_finish_kernel(MultiRowParam
     const int r = tid >> 3, part = tid & 7;
     const bool rotate = p.value_rotation != nullptr;
 
-    // R_v row t / 2, half t % 2 (16-byte loads issued before the request
-    // lookup, so that the two round trips overlap; written transposed once
-    // the partials are merged).
-    uint4 rv[8];
+    // R_v as the B operand of the rotation MFMAs (16-byte loads issued
+    // before the request lookup, so that the two round trips overlap): wave
+    // w computes output channels 32 w .. 32 w + 31, lane l takes row
+    // 32 w + l % 32 of R_v at features 16 m + 8 (l / 32) .. + 7.
+    const int lane = tid & 63;
+    F16x8 rv[D / 16];
     if (rotate) {
-        const uint4* src = reinterpret_cast<const uint4*>(p.value_rotation + ((int64_t)head * D + (tid >> 1)) * D +
-                                                          64 * (tid & 1));
+        const uint16_t* src =
+            p.value_rotation + ((int64_t)head * D + 32 * (tid >> 6) + (lane & 31)) * D + 8 * (lane >> 5);
 #pragma unroll
-        for (int i = 0; i < 8; ++i) rv[i] = src[i];
+        for (int m = 0; m < D / 16; ++m) rv[m] = *reinterpret_cast<const F16x8*>(src + 16 * m);
     }
     const int first = p.query_start_loc[request];
     int n = p.query_start_loc[request + 1] - first;
@@ -788,52 +787,52 @@ __global__ __launch_bounds__(kThreads) void multirow_finish_kernel(MultiRowParam
         }
     }
 
-    // 2. hist . R_v^T for the tile's 32 rows.
+    // 2. hist . R_v^T for the tile's 32 rows on the matrix cores: the merged
+    // rows divided by their sums (convex combinations of values, within the
+    // FP16 range) as FP16 high and low parts (~22 significant bits), times
+    // R_v (FP16), FP32 accumulation; the sums are multiplied back.
     if (rotate) {
-#pragma unroll
-        for (int i = 0; i < 16; ++i) hist_t[(16 * part + i) * HS + r] = acc[i];
-        const int c = tid >> 1, j0 = 64 * (tid & 1);
+        uint16_t* high = reinterpret_cast<uint16_t*>(region_a);  // [row][FS]
+        uint16_t* low = high + 32 * FS;
+        const float inverse = l > 0.f ? 1.0f / l : 0.f;
+        uint32_t hw[8], lw[8];
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
-            const uint32_t w[4] = {rv[i].x, rv[i].y, rv[i].z, rv[i].w};
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                rv_t[(j0 + 8 * i + 2 * e) * FS + c] = (uint16_t)(w[e] & 0xffffu);
-                rv_t[(j0 + 8 * i + 2 * e + 1) * FS + c] = (uint16_t)(w[e] >> 16);
-            }
+            const float x0 = acc[2 * i] * inverse, x1 = acc[2 * i + 1] * inverse;
+            const _Float16 h0 = (_Float16)x0, h1 = (_Float16)x1;
+            const _Float16 r0 = (_Float16)(x0 - (float)h0), r1 = (_Float16)(x1 - (float)h1);
+            hw[i] = (uint32_t)__builtin_bit_cast(uint16_t, h0) | ((uint32_t)__builtin_bit_cast(uint16_t, h1) << 16);
+            lw[i] = (uint32_t)__builtin_bit_cast(uint16_t, r0) | ((uint32_t)__builtin_bit_cast(uint16_t, r1) << 16);
         }
+        uint4* hd = reinterpret_cast<uint4*>(&high[r * FS + 16 * part]);
+        uint4* ld = reinterpret_cast<uint4*>(&low[r * FS + 16 * part]);
+        hd[0] = make_uint4(hw[0], hw[1], hw[2], hw[3]);
+        hd[1] = make_uint4(hw[4], hw[5], hw[6], hw[7]);
+        ld[0] = make_uint4(lw[0], lw[1], lw[2], lw[3]);
+        ld[1] = make_uint4(lw[4], lw[5], lw[6], lw[7]);
         __syncthreads();
-        const int cb = tid & 31, rb = tid >> 5;  // channels 4 cb .. 4 cb + 3, rows 4 rb .. 4 rb + 3
-        float o[4][4];
+        // A operand: lane l takes merged row l % 32 at features 16 m + 8 (l / 32) .. + 7.
+        F32x16 rotated;
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
+        for (int e = 0; e < 16; ++e) rotated[e] = 0.f;
+        const int a_offset = (lane & 31) * FS + 8 * (lane >> 5);
 #pragma unroll
-            for (int k = 0; k < 4; ++k) o[i][k] = 0.f;
-#pragma unroll 8
-        for (int j = 0; j < D; ++j) {
-            const float4 h4 = *reinterpret_cast<const float4*>(&hist_t[j * HS + 4 * rb]);
-            const uint2 w = *reinterpret_cast<const uint2*>(&rv_t[j * FS + 4 * cb]);
-            const float rk[4] = {f16_to_f32(w.x & 0xffffu), f16_to_f32(w.x >> 16), f16_to_f32(w.y & 0xffffu),
-                                 f16_to_f32(w.y >> 16)};
-            const float h[4] = {h4.x, h4.y, h4.z, h4.w};
-#pragma unroll
-            for (int i = 0; i < 4; ++i)
-#pragma unroll
-                for (int k = 0; k < 4; ++k) o[i][k] = fmaf(h[i], rk[k], o[i][k]);
+        for (int m = 0; m < D / 16; ++m) {
+            rotated = mfma(*reinterpret_cast<const F16x8*>(&high[a_offset + 16 * m]), rv[m], rotated);
+            rotated = mfma(*reinterpret_cast<const F16x8*>(&low[a_offset + 16 * m]), rv[m], rotated);
         }
-        __syncthreads();  // the rotated history replaces the merged one
+        // Register e of lane l: row 8 (e / 4) + 4 (l / 32) + e % 4, channel 32 w + l % 32.
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
-            *reinterpret_cast<float4*>(&hist_rot[(4 * rb + i) * OS + 4 * cb]) =
-                make_float4(o[i][0], o[i][1], o[i][2], o[i][3]);
+        for (int e = 0; e < 16; ++e)
+            hist_rot[(8 * (e >> 2) + 4 * (lane >> 5) + (e & 3)) * OS + 32 * (tid >> 6) + (lane & 31)] = rotated[e];
         __syncthreads();
 #pragma unroll
         for (int c4 = 0; c4 < 4; ++c4) {
             const float4 x = *reinterpret_cast<const float4*>(&hist_rot[r * OS + 16 * part + 4 * c4]);
-            acc[4 * c4] = x.x;
-            acc[4 * c4 + 1] = x.y;
-            acc[4 * c4 + 2] = x.z;
-            acc[4 * c4 + 3] = x.w;
+            acc[4 * c4] = x.x * l;
+            acc[4 * c4 + 1] = x.y * l;
+            acc[4 * c4 + 2] = x.z * l;
+            acc[4 * c4 + 3] = x.w * l;
         }
     }
 
