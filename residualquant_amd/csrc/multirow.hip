@@ -51,14 +51,16 @@ constexpr int VS = kTile + 8;        // V^T tile row stride (BF16)
 constexpr int kWaveBytes = kTile * KS * 2 + D * VS * 2 + kTile * 4;  // K (FP16), V (BF16), alpha_K
 static_assert(kTile * D <= D * VS, "the row-major V tile fits its region");
 constexpr int kLdsBytes = kWaves * kWaveBytes;
-// Prologue scratch (aliases the tiles): q^T FP32 [D][QTS], R_k FP16 [D][KS], q' FP16 [32][KS], mean dots
-// and row scales.
-constexpr int QTS = 36;
-constexpr int kQtOffset = 0;
-constexpr int kRkOffset = kQtOffset + D * QTS * 4;
-constexpr int kQpOffset = kRkOffset + D * KS * 2;
+// Prologue scratch (aliases the tiles): q scaled into FP16 [32][KS], R_k FP16
+// [D][KS], q.R_k FP32 [32][QRS], q' FP16 [32][KS], mean dots, row scales and
+// the rows' input exponents.
+constexpr int QRS = D + 4;
+constexpr int kQ16Offset = 0;
+constexpr int kRkOffset = kQ16Offset + 32 * KS * 2;
+constexpr int kQrawOffset = kRkOffset + D * KS * 2;
+constexpr int kQpOffset = kQrawOffset + 32 * QRS * 4;
 constexpr int kQmuOffset = kQpOffset + 32 * KS * 2;
-static_assert(kQmuOffset + 96 * 4 <= kLdsBytes, "prologue scratch fits in the tile LDS");
+static_assert(kQmuOffset + 128 * 4 <= kLdsBytes, "prologue scratch fits in the tile LDS");
 // Wave merge (aliases the tiles): O [wave][row][MS] FP32 and (m, l) per wave and row.
 constexpr int MS = D + 4;
 constexpr int kMlOffset = kWaves * 32 * MS * 4;
@@ -267,11 +269,13 @@ void multirow_stream_kernel(MultiRowParams p) {
     // q' 2^-e with 2^e the row's power-of-two scale, and the row dots
     // q'.bf16(mu_A) (added per token times alpha_L) and q'.mu_L (the shift of
     // the history scores against the live ones).
-    float* q_t = reinterpret_cast<float*>(lds + kQtOffset);
+    uint16_t* q16 = reinterpret_cast<uint16_t*>(lds + kQ16Offset);
     uint16_t* r_k = reinterpret_cast<uint16_t*>(lds + kRkOffset);
+    float* q_raw = reinterpret_cast<float*>(lds + kQrawOffset);
     uint16_t* q_p = reinterpret_cast<uint16_t*>(lds + kQpOffset);
     float* q_mu = reinterpret_cast<float*>(lds + kQmuOffset);  // [0..31] q'.bf16(mu_A), [32..63] q'.mu_L
     float* q_scale = q_mu + 64;                                 // [32] 2^e per row
+    float* q_unscale = q_mu + 96;                               // [32] 2^f per row (the input's scale)
     {
         const int r = tid >> 3, part = tid & 7;  // row, 16-channel part
         const int row = row0 + r;
@@ -286,45 +290,87 @@ void multirow_stream_kernel(MultiRowParams p) {
                 words[2 * i + 1] = v.y;
             }
         }
+        float x[16];
+        float magnitude = 0.f;
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
-            q_t[(16 * part + 2 * i) * QTS + r] = bf16_f32(words[i] & 0xffffu);
-            q_t[(16 * part + 2 * i + 1) * QTS + r] = bf16_f32(words[i] >> 16);
+            x[2 * i] = bf16_f32(words[i] & 0xffffu);
+            x[2 * i + 1] = bf16_f32(words[i] >> 16);
+            magnitude = fmaxf(magnitude, fmaxf(fabsf(x[2 * i]), fabsf(x[2 * i + 1])));
         }
         if (p.key_rotation) {
-            const int k = tid >> 1, h = tid & 1;
-            const uint4* src = reinterpret_cast<const uint4*>(p.key_rotation + ((int64_t)head * D + k) * D + 64 * h);
-            uint4* dst = reinterpret_cast<uint4*>(r_k + k * KS + 64 * h);
+            // The row scaled by a power of two 2^-f into [-1, 1]: exact in FP16
+            // (a BF16 significand fits), so q.R_k runs on FP16 MFMAs and the
+            // product takes 2^f back.
+            magnitude = fmaxf(magnitude, __shfl_xor(magnitude, 1));
+            magnitude = fmaxf(magnitude, __shfl_xor(magnitude, 2));
+            magnitude = fmaxf(magnitude, __shfl_xor(magnitude, 4));
+            // (f at most 127, so 2^f stays finite; the scaled row is then within 2.)
+            const int f = magnitude > 0.f ? min(__builtin_amdgcn_frexp_expf(magnitude), 127) : 0;
+            const float down = ldexpf(1.0f, -f);
+            uint32_t h[8];
 #pragma unroll
-            for (int i = 0; i < 8; ++i) dst[i] = src[i];
+            for (int i = 0; i < 8; ++i)
+                h[i] = f16_bits(x[2 * i] * down) | (f16_bits(x[2 * i + 1] * down) << 16);
+            uint4* dst = reinterpret_cast<uint4*>(&q16[r * KS + 16 * part]);
+            dst[0] = make_uint4(h[0], h[1], h[2], h[3]);
+            dst[1] = make_uint4(h[4], h[5], h[6], h[7]);
+            if (part == 0) q_unscale[r] = ldexpf(1.0f, f);
+            const int k = tid >> 1, half_k = tid & 1;
+            const uint4* src = reinterpret_cast<const uint4*>(p.key_rotation + ((int64_t)head * D + k) * D + 64 * half_k);
+            uint4* rdst = reinterpret_cast<uint4*>(r_k + k * KS + 64 * half_k);
+#pragma unroll
+            for (int i = 0; i < 8; ++i) rdst[i] = src[i];
+        } else {
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+                *reinterpret_cast<float4*>(&q_raw[r * QRS + 16 * part + 4 * i]) =
+                    make_float4(x[4 * i], x[4 * i + 1], x[4 * i + 2], x[4 * i + 3]);
+        }
+    }
+    __syncthreads();
+    if (p.key_rotation) {
+        // q.R_k on the matrix cores: wave w takes columns 32 w .. 32 w + 31.
+        // A: lane l reads scaled row l % 32 at k = 16 m + 8 (l / 32) .. + 7.
+        // B: R_k[k][c] for column 32 w + l % 32 and the same k, read
+        // transposed from the row-major R_k tile (ds_read_b64_tr_b16: output
+        // lane o of 16 gets element o % 4 of the 8 bytes addressed by lanes
+        // o / 4 + 4 p, so lane q of a 16-lane group addresses row
+        // k0 + q / 4 at columns c0 + 4 (q % 4) .. + 3 and receives column
+        // c0 + q of rows k0 .. k0 + 3).
+        const int group = lane >> 4, q16_lane = lane & 15;
+        const int c0 = 32 * wave + 16 * (group & 1);
+        const int k_half = 8 * (group >> 1);
+        F32x16 c;
+#pragma unroll
+        for (int e = 0; e < 16; ++e) c[e] = 0.f;
+#pragma unroll
+        for (int m = 0; m < D / 16; ++m) {
+            const F16x8 a = *reinterpret_cast<const F16x8*>(&q16[column * KS + 16 * m + 8 * half]);
+            const int k0 = 16 * m + k_half;
+            const Short4 lo = read_transposed(&r_k[(k0 + (q16_lane >> 2)) * KS + c0 + 4 * (q16_lane & 3)]);
+            const Short4 hi = read_transposed(&r_k[(k0 + 4 + (q16_lane >> 2)) * KS + c0 + 4 * (q16_lane & 3)]);
+            const F16x8 b = __builtin_bit_cast(F16x8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+            c = mfma(a, b, c);
+        }
+        // Register e of lane l: row 8 (e / 4) + 4 (l / 32) + e % 4, column 32 w + l % 32.
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+            const int rr = 8 * (e >> 2) + 4 * half + (e & 3);
+            q_raw[rr * QRS + 32 * wave + column] = c[e] * q_unscale[rr];
         }
     }
     __syncthreads();
     {
         const int cb = tid & 31, rb = tid >> 5;  // columns 4 cb .. 4 cb + 3, rows 4 rb .. 4 rb + 3
         float acc[4][4];
-        if (p.key_rotation) {
 #pragma unroll
-            for (int i = 0; i < 4; ++i)
-#pragma unroll
-                for (int j = 0; j < 4; ++j) acc[i][j] = 0.f;
-#pragma unroll 8
-            for (int k = 0; k < D; ++k) {
-                const float4 q4 = *reinterpret_cast<const float4*>(&q_t[k * QTS + 4 * rb]);
-                const uint2 r4 = *reinterpret_cast<const uint2*>(&r_k[k * KS + 4 * cb]);
-                const float rv[4] = {f16_to_f32(r4.x & 0xffffu), f16_to_f32(r4.x >> 16), f16_to_f32(r4.y & 0xffffu),
-                                     f16_to_f32(r4.y >> 16)};
-                const float qv[4] = {q4.x, q4.y, q4.z, q4.w};
-#pragma unroll
-                for (int i = 0; i < 4; ++i)
-#pragma unroll
-                    for (int j = 0; j < 4; ++j) acc[i][j] = fmaf(qv[i], rv[j], acc[i][j]);
-            }
-        } else {
-#pragma unroll
-            for (int i = 0; i < 4; ++i)
-#pragma unroll
-                for (int j = 0; j < 4; ++j) acc[i][j] = q_t[(4 * cb + j) * QTS + 4 * rb + i];
+        for (int i = 0; i < 4; ++i) {
+            const float4 v = *reinterpret_cast<const float4*>(&q_raw[(4 * rb + i) * QRS + 4 * cb]);
+            acc[i][0] = v.x;
+            acc[i][1] = v.y;
+            acc[i][2] = v.z;
+            acc[i][3] = v.w;
         }
         const float scale = kLog2e * 0.08838834764831845f;  // log2(e) / sqrt(128)
         float mu_a[4] = {0.f, 0.f, 0.f, 0.f}, mu_l[4] = {0.f, 0.f, 0.f, 0.f};
