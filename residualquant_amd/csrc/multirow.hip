@@ -16,10 +16,12 @@
 // 1e-3 mean bar on short histories.  K and V are evaluated in FP32 (two fmas
 // per channel and plane) and rounded once, to FP16 and BF16.  P stays in the
 // accumulator registers (the token order of each P.V step is permuted to
-// match the accumulator layout, and V^T is read with the same permutation).  Each of the four waves takes every fourth tile with
-// its own online softmax; the waves meet once in LDS at the end and the
-// workgroup writes one partial (m, l, O) per row.  A finish launch per
-// (row, head) merges the splits, applies R_v^T and adds the live tokens.
+// match the accumulator layout, and V^T is read with the same permutation).
+// Each of the four waves takes every fourth tile with its own online
+// softmax; the waves meet once in LDS at the end and the workgroup writes one
+// partial (m, l, O) per row.  The query prologue (q . R_k) runs on MFMA as
+// well.  A finish launch per (request, head, 32-row tile) merges the splits,
+// applies R_v^T (on MFMA) and adds the live tokens.
 //
 // Semantics (reference: attention/compute.cuh:397-505 keys, :28-107 values,
 // prepare.cuh:13-54 and :203-229 live score and mean shift, merge.cuh:8-84,
