@@ -56,11 +56,14 @@ def test_noalloc_matches_workspace_entry_point(oracle, device):
     lib = _lib.lib()
     # The first call splits each (row, head) over several workgroups (arrival
     # counters and partials in the scratch); the second is smaller and
-    # reuses the scratch the first one left behind.
-    cases = [([700, 300, 129, 50], 4, 61), ([90, 33], 4, 62)]
-    for lengths, heads, seed in cases:
-        print(f"[case] noalloc lengths={lengths} heads={heads} seed={seed}", flush=True)
-        d = make_decode(lengths, heads, 128, OURO_G32, seed=seed)
+    # reuses the scratch the first one left behind; the third has 12 and 8
+    # rows per request, so it runs the multi-row kernels (their split
+    # partials and row shifts in the scratch); the fourth is the first again.
+    cases = [([700, 300, 129, 50], 4, 61, None), ([90, 33], 4, 62, None), ([300, 120], 4, 63, [12, 8]),
+             ([700, 300, 129, 50], 4, 61, None)]
+    for lengths, heads, seed, rows in cases:
+        print(f"[case] noalloc lengths={lengths} heads={heads} seed={seed} rows={rows}", flush=True)
+        d = make_decode(lengths, heads, 128, OURO_G32, seed=seed, rows_per_request=rows)
         expected_cache = d.group.oracle_cache(oracle)
         cache = torch.from_numpy(expected_cache).to(device)
         for loop in (0, 3):
