@@ -128,7 +128,7 @@ struct WorkspaceLayout {
     size_t row_request, arrivals, prep, partials, total;
 };
 
-constexpr int64_t kMultiRowMinRows = 6;
+constexpr int64_t kMultiRowMinRows = 3;
 
 // Several rows per request (anchor mode, D = 128) run the multi-row MFMA
 // kernels: one workgroup per (request, head, 32-row tile, history split).
@@ -416,11 +416,12 @@ static int attention_packed(const void* query, int64_t query_stride, const void*
     // Several rows per request in anchor mode at D = 128 (and every prefill
     // over packed history) take the multi-row MFMA kernels, which stream each
     // request's pages once for all its rows but dequantize every page tile
-    // into LDS.  Measured at 8192 history tokens x 16 heads (residual-loop
-    // call): 16 rows per request 439 us against 914 us for the per-row decode
-    // kernel (B16), 4 rows 559 against 500 us (B32: the rows of one request
-    // share its pages in L2), so decode calls take them from an average of
-    // kMultiRowMinRows rows per request.
+    // into LDS.  Measured at 8192 history tokens x 16 heads (4-call step,
+    // multi-row against per-row decode kernel): 3 rows per request 973
+    // against 1468 us (B32), 4 rows 260 against 500 us per residual call,
+    // 16 rows 530 against 3280 us (B16); at 2 rows the step is 5-8% faster
+    // but the anchor-loop call slower, so decode calls take them from an
+    // average of kMultiRowMinRows rows per request.
     if (causal || (!adjacent && head_dim == 128 && requests > 0 && rows >= kMultiRowMinRows * requests)) {
         if (adjacent || head_dim != 128)
             return fail(RQ_ENOKERNEL,

@@ -4,7 +4,7 @@ MFMA kernels (residualquant_amd/csrc/multirow.hip) against the CPU oracle.
 - ``packed_prefill_attention``: each request's rows are its last n tokens,
   seeing seq_len - n history tokens and, causally, the new ones
   (oracle.attention_prefill);
-- ``attention`` with an average of 6 or more rows per request (anchor mode,
+- ``attention`` with an average of 3 or more rows per request (anchor mode,
   D128) routes to the same kernels with the reference's decode semantics
   (oracle.attention); fewer rows take the per-row decode kernel, checked
   against the same oracle.
