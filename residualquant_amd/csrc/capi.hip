@@ -128,7 +128,8 @@ struct WorkspaceLayout {
     size_t row_request, arrivals, prep, partials, total;
 };
 
-constexpr int64_t kMultiRowMinRows = 3;
+constexpr int64_t kMultiRowMinRows = 3;          // anchor-loop calls
+constexpr int64_t kMultiRowMinRowsResidual = 2;  // residual-loop calls
 
 // Several rows per request (anchor mode, D = 128) run the multi-row MFMA
 // kernels: one workgroup per (request, head, 32-row tile, history split).
@@ -419,10 +420,13 @@ static int attention_packed(const void* query, int64_t query_stride, const void*
     // into LDS.  Measured at 8192 history tokens x 16 heads (4-call step,
     // multi-row against per-row decode kernel): 3 rows per request 973
     // against 1468 us (B32), 4 rows 260 against 500 us per residual call,
-    // 16 rows 530 against 3280 us (B16); at 2 rows the step is 5-8% faster
-    // but the anchor-loop call slower, so decode calls take them from an
-    // average of kMultiRowMinRows rows per request.
-    if (causal || (!adjacent && head_dim == 128 && requests > 0 && rows >= kMultiRowMinRows * requests)) {
+    // 16 rows 530 against 3280 us (B16); at 2 rows the residual-loop call is
+    // faster (256 against 283 us at B32, 84 against 88 us at B8) but the
+    // anchor-loop call slower (192 against 183 us), so decode calls take them
+    // from an average of kMultiRowMinRowsResidual rows per request in a
+    // residual loop and kMultiRowMinRows in the anchor loop.
+    const int64_t min_rows = loop_index != anchor_index ? kMultiRowMinRowsResidual : kMultiRowMinRows;
+    if (causal || (!adjacent && head_dim == 128 && requests > 0 && rows >= min_rows * requests)) {
         if (adjacent || head_dim != 128)
             return fail(RQ_ENOKERNEL,
                         "No compiled packed HIP multi-row kernel for head_dim=%d, reference_mode=%s (anchor mode "

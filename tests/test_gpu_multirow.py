@@ -4,8 +4,9 @@ MFMA kernels (residualquant_amd/csrc/multirow.hip) against the CPU oracle.
 - ``packed_prefill_attention``: each request's rows are its last n tokens,
   seeing seq_len - n history tokens and, causally, the new ones
   (oracle.attention_prefill);
-- ``attention`` with an average of 3 or more rows per request (anchor mode,
-  D128) routes to the same kernels with the reference's decode semantics
+- ``attention`` with an average of 2 or more rows per request (3 in the
+  anchor loop; anchor mode, D128) routes to the same kernels with the
+  reference's decode semantics
   (oracle.attention); fewer rows take the per-row decode kernel, checked
   against the same oracle.
 
