@@ -17,6 +17,8 @@ magnitude ~1 at short histories is half the mean bar by itself).
 
 from __future__ import annotations
 
+import random
+
 import numpy as np
 import pytest
 import torch
@@ -91,6 +93,42 @@ def test_multirow_matches_oracle(oracle, device, case, causal):
         want = _oracle(oracle, d, expected_cache, loop, causal)
         err = np.abs(got - _bf16(want))
         print(f"[case]   loop {loop}: max {err.max():.3g} mean {err.mean():.3g}", flush=True)
+        assert np.isfinite(got).all()
+        assert err.max() <= MAX_ABS and err.mean() <= MEAN_ABS, (loop, err.max(), err.mean())
+
+
+def _random_cases(seed: int, count: int):
+    """Seeded mixes of row counts (empty requests, one row, exact and ragged
+    32-row tiles), history lengths (none, one token, page-ragged, several
+    splits), heads, schedules, page sizes and mean / rotation switches."""
+    schedules = [OURO_G32, OURO_G16, ((2, 16), (2, 16), (4, 32), (2, 32)), ((4, 32), (2, 32)), ((2, 32), (4, 16))]
+    rng = random.Random(seed)
+    cases = []
+    for _ in range(count):
+        rows = [rng.choice([0, 1, 2, 3, 5, 16, 31, 33, 40]) for _ in range(rng.randint(1, 4))]
+        if sum(rows) == 0:
+            rows[0] = 2
+        lengths = [max(1, r + rng.choice([0, 1, 15, 17, 100, 333, 700])) for r in rows]
+        cases.append((lengths, rows, rng.choice([1, 2, 3]), rng.choice(schedules), rng.choice([16, 32]),
+                      rng.random() < 0.7, rng.random() < 0.7, rng.random() < 0.5))
+    return cases
+
+
+@pytest.mark.parametrize("index,case", list(enumerate(_random_cases(7, 16))),
+                         ids=[f"c{i}" for i in range(16)])
+def test_multirow_random_mixes(oracle, device, index, case):
+    """Every loop of each random mix, through ``attention`` (rows routed per
+    call between the per-row and multi-row kernels) or
+    ``packed_prefill_attention``."""
+    lengths, rows, heads, records, pt, mean, rotation, causal = case
+    print(f"[case] random c{index} causal={causal} {case}", flush=True)
+    d = make_decode(lengths, heads, 128, records, seed=1000 + index, page_tokens=pt, mean=mean, rotation=rotation,
+                    rows_per_request=rows)
+    expected_cache = d.group.oracle_cache(oracle)
+    cache = torch.from_numpy(expected_cache).to(device)
+    for loop in range(len(records)):
+        got = _run(d, device, cache, loop, causal)
+        err = np.abs(got - _bf16(_oracle(oracle, d, expected_cache, loop, causal)))
         assert np.isfinite(got).all()
         assert err.max() <= MAX_ABS and err.mean() <= MEAN_ABS, (loop, err.max(), err.mean())
 
