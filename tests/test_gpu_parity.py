@@ -6,6 +6,8 @@ Bars: packed bytes and restored BF16 K/V bit-exact; attention output within
 
 from __future__ import annotations
 
+import random
+
 import numpy as np
 import pytest
 import torch
@@ -147,6 +149,43 @@ def test_attention_matches_oracle(oracle, device, case):
                      d.query_start_loc.to(device), d.seq_lens.to(device), d.table.to(device), kr, vr, km,
                      g.records, g.mode, g.anchor, loop)
         err = np.abs(out.float().cpu().numpy().astype(np.float64) - expected)
+        assert err.max() <= MAX_ABS and err.mean() <= MEAN_ABS, (loop, err.max(), err.mean())
+
+
+def _random_decode_cases(seed: int, count: int):
+    """Seeded one-row-per-request calls: 1-8 requests with histories from none
+    to several splits, 1-4 heads, D96 / D128, page sizes 16 / 32, five
+    schedules, anchor and adjacent modes, mean and rotation switches."""
+    schedules = [OURO_G32, OURO_G16, ((2, 16), (2, 16), (4, 32), (2, 32)), ((4, 32), (2, 32)), ((2, 32), (4, 16))]
+    rng = random.Random(seed)
+    cases = []
+    for _ in range(count):
+        lengths = [rng.choice([1, 2, 17, 33, 129, 500, 1500, 3000]) for _ in range(rng.randint(1, 8))]
+        cases.append((lengths, rng.randint(1, 4), rng.choice([96, 128]), rng.choice(schedules), rng.choice([16, 32]),
+                      rng.random() < 0.7, rng.random() < 0.7, rng.choice(["anchor", "adjacent"])))
+    return cases
+
+
+@pytest.mark.parametrize("index,case", list(enumerate(_random_decode_cases(11, 16))),
+                         ids=[f"c{i}" for i in range(16)])
+def test_attention_random_calls(oracle, device, index, case):
+    _print_case(f"random attention c{index}", case)
+    lengths, heads, dim, records, pt, rotation, mean, mode = case
+    d = make_decode(lengths, heads, dim, records, seed=2000 + index, page_tokens=pt, mode=mode,
+                    anchor=0 if mode == "adjacent" else None, rotation=rotation, mean=mean)
+    g = d.group
+    cache_np = g.oracle_cache(oracle)
+    cache = torch.from_numpy(cache_np).to(device)
+    kr, vr, km = g.device_args(device)
+    for loop in range(len(records)):
+        expected = oracle_attention(oracle, d, cache_np, loop)
+        out = torch.full_like(d.query, float("nan"), device=device)
+        rq.attention(d.query.to(device), d.key.to(device), d.value.to(device), cache, out,
+                     d.query_start_loc.to(device), d.seq_lens.to(device), d.table.to(device), kr, vr, km,
+                     g.records, g.mode, g.anchor, loop)
+        got = out.float().cpu().numpy().astype(np.float64)
+        err = np.abs(got - expected)
+        assert np.isfinite(got).all()
         assert err.max() <= MAX_ABS and err.mean() <= MEAN_ABS, (loop, err.max(), err.mean())
 
 
