@@ -65,6 +65,40 @@ def test_quantize_bitexact(oracle, device, case):
     assert mismatch.size == 0, f"{len(mismatch)} bytes differ, first at {mismatch[:4].tolist()}"
 
 
+def _random_quantize_cases(seed: int, count: int):
+    """Seeded calls on both sides of the VALU / MFMA kernel switch at 64
+    tokens: 1-2100 tokens, 1-5 heads, D96 / D128, five schedules, any anchor
+    index, adjacent mode, the three coefficients, page sizes 16 / 32, up to a
+    tenth of the slots skipped (-1)."""
+    schedules = [OURO_G32, OURO_G16, ((2, 16), (2, 16), (4, 32), (2, 32)), ((4, 32), (2, 32)), ((2, 32), (4, 16))]
+    rng = random.Random(seed)
+    cases = []
+    for _ in range(count):
+        tokens = rng.choice([1, 7, 63, 64, 65, 130, 777, 2047, 2100])
+        records = rng.choice(schedules)
+        mode = rng.choice(["anchor", "adjacent"])
+        cases.append((tokens, rng.randint(1, 5), rng.choice([96, 128]), records, rng.choice([16, 32]), mode,
+                      rng.randrange(len(records)) if mode == "anchor" else 0, rng.choice(["ls", "norm", "unit"]),
+                      rng.random() < 0.7, rng.random() < 0.7, rng.randint(0, tokens // 10)))
+    return cases
+
+
+@pytest.mark.parametrize("index,case", list(enumerate(_random_quantize_cases(13, 16))),
+                         ids=[f"c{i}" for i in range(16)])
+def test_quantize_random_calls(oracle, device, index, case):
+    _print_case(f"random quantize c{index}", case)
+    tokens, heads, dim, records, pt, mode, anchor, coef, rotation, mean, skipped = case
+    g = make_group(tokens, heads, dim, records, seed=3000 + index, page_tokens=pt, mode=mode, anchor=anchor,
+                   coefficient=coef, rotation=rotation, mean=mean, skipped=skipped)
+    expected = g.oracle_cache(oracle)
+    cache = torch.zeros(g.cache_shape, dtype=torch.uint8, device=device)
+    kr, vr, km = g.device_args(device)
+    rq.quantize([(k.to(device), v.to(device)) for k, v in g.pairs], cache, g.slots.to(device), kr, vr, km,
+                g.records, g.mode, g.anchor, g.coefficient)
+    mismatch = np.argwhere(cache.cpu().numpy() != expected)
+    assert mismatch.size == 0, f"{len(mismatch)} bytes differ, first at {mismatch[:4].tolist()}"
+
+
 def test_quantize_strided_inputs(oracle, device):
     """Token strides wider than heads*D (a [tokens, 3*heads, D] buffer view) are honoured."""
     g = make_group(21, 2, 128, OURO_G32, seed=5)
