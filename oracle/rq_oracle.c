@@ -187,6 +187,18 @@ int rq_oracle_page_width(int head_dim, int records, const int* bits, const int* 
     return width;
 }
 
+/* The schedules the layout admits (cache.cuh:74-96): D a positive multiple
+ * of 32 up to the oracle's buffers, INT2/INT4 records whose group divides D. */
+static int valid_schedule(int head_dim, int records, const int* bits, const int* groups) {
+    if (records < 1 || records > RQ_ORACLE_MAX_RECORDS) return 0;
+    if (head_dim <= 0 || head_dim % 32 || head_dim > RQ_ORACLE_MAX_DIM) return 0;
+    for (int r = 0; r < records; ++r) {
+        if (bits[r] != 2 && bits[r] != 4) return 0;
+        if (groups[r] <= 0 || head_dim % groups[r]) return 0;
+    }
+    return 1;
+}
+
 static int record_offset(int head_dim, int record, const int* bits, const int* groups) {
     int offset = 0;
     for (int r = 0; r < record; ++r) offset += rq_oracle_record_bytes(head_dim, bits[r], groups[r]);
@@ -337,7 +349,7 @@ int rq_oracle_quantize(
     const uint16_t* key_rotation, const uint16_t* value_rotation, const float* key_mean,
     const int* bits, const int* groups, int reference_mode, int anchor_index,
     int coefficient) {
-    if (records < 1 || records > RQ_ORACLE_MAX_RECORDS || head_dim > RQ_ORACLE_MAX_DIM) return -1;
+    if (!valid_schedule(head_dim, records, bits, groups) || heads <= 0 || page_tokens <= 0) return -1;
     if (anchor_index < 0 || anchor_index >= records) return -1;
     if (reference_mode == 1 && anchor_index != 0) return -1;
     if (rq_oracle_page_width(head_dim, records, bits, groups) != page_width) return -1;
@@ -451,7 +463,7 @@ int rq_oracle_dequantize(const uint8_t* cache, int64_t num_blocks, int heads, in
                          const float* key_mean, int records, const int* bits, const int* groups,
                          int reference_mode, int anchor_index, int loop, uint16_t* key_out,
                          uint16_t* value_out) {
-    if (records < 1 || records > RQ_ORACLE_MAX_RECORDS || head_dim > RQ_ORACLE_MAX_DIM) return -1;
+    if (!valid_schedule(head_dim, records, bits, groups) || heads <= 0 || page_tokens <= 0) return -1;
     if (loop < 0 || loop >= records || anchor_index < 0 || anchor_index >= records) return -1;
     if (rq_oracle_page_width(head_dim, records, bits, groups) != page_width) return -1;
     const int adjacent = records > 1 && reference_mode == 1;
@@ -561,6 +573,98 @@ static void attention_key(const uint8_t* page, int head_dim, const int* bits, co
  * seq_len - n, and row r (0-based within the request) sees the request's
  * new keys/values j <= r.  Output is FP64 [rows, heads, D].
  */
+/* One (row i of request b, head h) of attention_rows; -1 on a bad block id. */
+static int attention_row_head(
+    const uint16_t* query, int64_t query_stride, const uint16_t* key, int64_t key_stride,
+    const uint16_t* value, int64_t value_stride, double* output, int heads, int head_dim,
+    const uint8_t* cache, int64_t num_blocks, int page_tokens, int page_width, int64_t first, int64_t n,
+    int64_t seq_len, const int32_t* table_row, const uint16_t* key_rotation, const uint16_t* value_rotation,
+    const float* key_mean, int records, const int* bits, const int* groups, int adjacent, int anchor_index,
+    int loop, int causal, int64_t i, int h) {
+    const int64_t plane_stride = num_blocks * heads * page_tokens * page_width;
+    const double scale = 1.0 / sqrt((double)head_dim);
+    const int64_t new_tokens = causal ? n : 1;
+    const int64_t history = seq_len > new_tokens ? seq_len - new_tokens : 0;
+    const int64_t live_first = causal ? first : i;
+    const int64_t live_count = causal ? i - first + 1 : 1;
+    uint16_t vbuf[RQ_ORACLE_MAX_DIM];
+    double kexact[RQ_ORACLE_MAX_DIM];
+    double* scores = (double*)malloc(sizeof(double) * (size_t)(history + live_count + 1));
+    if (!scores) return -1;
+    double* live_scores = scores + history;
+    const uint16_t* q = query + i * query_stride + (int64_t)h * head_dim;
+    double qr[RQ_ORACLE_MAX_DIM];
+    for (int c = 0; c < head_dim; ++c) {
+        double acc = 0.0;
+        if (key_rotation) {
+            const uint16_t* m = key_rotation + (size_t)h * head_dim * head_dim;
+            for (int k = 0; k < head_dim; ++k)
+                acc += (double)rq_oracle_bf16_to_f32(q[k]) * (double)rq_oracle_f16_to_f32(m[(size_t)k * head_dim + c]);
+        } else {
+            acc = rq_oracle_bf16_to_f32(q[c]);
+        }
+        qr[c] = acc * scale;
+    }
+    double maximum = -INFINITY;
+    for (int64_t j = 0; j < live_count; ++j) {
+        const uint16_t* kl = key + (live_first + j) * key_stride + (int64_t)h * head_dim;
+        double live = 0.0;
+        for (int c = 0; c < head_dim; ++c)
+            live += (double)rq_oracle_bf16_to_f32(q[c]) * (double)rq_oracle_bf16_to_f32(kl[c]);
+        live_scores[j] = live * scale;
+        if (live_scores[j] > maximum) maximum = live_scores[j];
+    }
+    for (int64_t t = 0; t < history; ++t) {
+        const int64_t block = table_row[t / page_tokens];
+        if (block < 0 || block >= num_blocks) {
+            free(scores);
+            return -1;
+        }
+        const uint8_t* page = cache + (block * heads + h) * (int64_t)page_tokens * page_width;
+        attention_key(page, head_dim, bits, groups, page_tokens, (int)(t % page_tokens), adjacent, anchor_index,
+                      loop, key_mean, heads, h, kexact);
+        double s = 0.0;
+        for (int c = 0; c < head_dim; ++c) s += qr[c] * kexact[c];
+        scores[t] = s;
+        if (s > maximum) maximum = s;
+    }
+    double denominator = 0.0;
+    for (int64_t j = 0; j < live_count; ++j) {
+        live_scores[j] = exp(live_scores[j] - maximum);
+        denominator += live_scores[j];
+    }
+    for (int64_t t = 0; t < history; ++t) {
+        scores[t] = exp(scores[t] - maximum);
+        denominator += scores[t];
+    }
+    double hist[RQ_ORACLE_MAX_DIM] = {0};
+    for (int64_t t = 0; t < history; ++t) {
+        const int64_t block = table_row[t / page_tokens];
+        const uint8_t* page = cache + plane_stride + (block * heads + h) * (int64_t)page_tokens * page_width;
+        restore_token(page, head_dim, records, bits, groups, page_tokens, (int)(t % page_tokens), adjacent,
+                      anchor_index, loop, NULL, heads, h, vbuf);
+        for (int c = 0; c < head_dim; ++c) hist[c] += scores[t] * (double)rq_oracle_bf16_to_f32(vbuf[c]);
+    }
+    double* out = output + (i * heads + h) * (int64_t)head_dim;
+    for (int c = 0; c < head_dim; ++c) {
+        double v = 0.0;
+        if (value_rotation) {
+            const uint16_t* m = value_rotation + (size_t)h * head_dim * head_dim;
+            for (int k = 0; k < head_dim; ++k) v += hist[k] * (double)rq_oracle_f16_to_f32(m[(size_t)c * head_dim + k]);
+        } else {
+            v = hist[c];
+        }
+        double live = 0.0;
+        for (int64_t j = 0; j < live_count; ++j) {
+            const uint16_t* vl = value + (live_first + j) * value_stride + (int64_t)h * head_dim;
+            live += live_scores[j] * (double)rq_oracle_bf16_to_f32(vl[c]);
+        }
+        out[c] = (v + live) / denominator;
+    }
+    free(scores);
+    return 0;
+}
+
 static int attention_rows(
     const uint16_t* query, int64_t query_stride, const uint16_t* key, int64_t key_stride,
     const uint16_t* value, int64_t value_stride, double* output, int64_t rows, int heads,
@@ -569,106 +673,33 @@ static int attention_rows(
     const int32_t* block_table, int64_t block_table_stride, const uint16_t* key_rotation,
     const uint16_t* value_rotation, const float* key_mean, int records, const int* bits,
     const int* groups, int reference_mode, int anchor_index, int loop, int causal) {
-    if (records < 1 || records > RQ_ORACLE_MAX_RECORDS || head_dim > RQ_ORACLE_MAX_DIM) return -1;
+    if (!valid_schedule(head_dim, records, bits, groups) || heads <= 0 || page_tokens <= 0) return -1;
     if (loop < 0 || loop >= records || anchor_index < 0 || anchor_index >= records) return -1;
     if (rq_oracle_page_width(head_dim, records, bits, groups) != page_width) return -1;
     const int adjacent = records > 1 && reference_mode == 1;
-    const int64_t plane_stride = num_blocks * heads * page_tokens * page_width;
-    const double scale = 1.0 / sqrt((double)head_dim);
-    uint16_t vbuf[RQ_ORACLE_MAX_DIM];
-    double kexact[RQ_ORACLE_MAX_DIM];
-
-    for (int64_t b = 0; b < requests; ++b) {
+    /* The request of each row (-1: no request owns it; its output stays 0). */
+    int64_t* row_request = (int64_t*)malloc(sizeof(int64_t) * (size_t)(rows > 0 ? rows : 1));
+    if (!row_request) return -1;
+    for (int64_t i = 0; i < rows; ++i) row_request[i] = -1;
+    for (int64_t b = 0; b < requests; ++b)
+        for (int64_t i = query_start_loc[b]; i < query_start_loc[b + 1] && i < rows; ++i) row_request[i] = b;
+    int failed = 0;
+    /* (row, head) pairs are independent: they run in parallel when built with OpenMP. */
+#pragma omp parallel for schedule(dynamic, 1) reduction(| : failed)
+    for (int64_t w = 0; w < rows * heads; ++w) {
+        const int64_t i = w / heads;
+        const int h = (int)(w % heads);
+        const int64_t b = row_request[i];
+        if (b < 0) continue;
         const int64_t first = query_start_loc[b];
-        const int64_t n = query_start_loc[b + 1] - first;
-        const int64_t new_tokens = causal ? n : 1;
-        const int64_t history = seq_lens[b] > new_tokens ? seq_lens[b] - new_tokens : 0;
-        double* scores = (double*)malloc(sizeof(double) * (size_t)(history + n + 1));
-        if (!scores) return -1;
-        double* live_scores = scores + history;
-        for (int64_t i = first; i < first + n; ++i) {
-            if (i >= rows) break;
-            const int64_t live_first = causal ? first : i;
-            const int64_t live_count = causal ? i - first + 1 : 1;
-            for (int h = 0; h < heads; ++h) {
-                const uint16_t* q = query + i * query_stride + (int64_t)h * head_dim;
-                double qr[RQ_ORACLE_MAX_DIM];
-                for (int c = 0; c < head_dim; ++c) {
-                    double acc = 0.0;
-                    if (key_rotation) {
-                        const uint16_t* m = key_rotation + (size_t)h * head_dim * head_dim;
-                        for (int k = 0; k < head_dim; ++k)
-                            acc += (double)rq_oracle_bf16_to_f32(q[k]) *
-                                   (double)rq_oracle_f16_to_f32(m[(size_t)k * head_dim + c]);
-                    } else {
-                        acc = rq_oracle_bf16_to_f32(q[c]);
-                    }
-                    qr[c] = acc * scale;
-                }
-                double maximum = -INFINITY;
-                for (int64_t j = 0; j < live_count; ++j) {
-                    const uint16_t* kl = key + (live_first + j) * key_stride + (int64_t)h * head_dim;
-                    double live = 0.0;
-                    for (int c = 0; c < head_dim; ++c)
-                        live += (double)rq_oracle_bf16_to_f32(q[c]) * (double)rq_oracle_bf16_to_f32(kl[c]);
-                    live_scores[j] = live * scale;
-                    if (live_scores[j] > maximum) maximum = live_scores[j];
-                }
-                for (int64_t t = 0; t < history; ++t) {
-                    const int64_t block = block_table[b * block_table_stride + t / page_tokens];
-                    if (block < 0 || block >= num_blocks) {
-                        free(scores);
-                        return -1;
-                    }
-                    const uint8_t* page = cache + (block * heads + h) * (int64_t)page_tokens * page_width;
-                    attention_key(page, head_dim, bits, groups, page_tokens, (int)(t % page_tokens),
-                                  adjacent, anchor_index, loop, key_mean, heads, h, kexact);
-                    double s = 0.0;
-                    for (int c = 0; c < head_dim; ++c) s += qr[c] * kexact[c];
-                    scores[t] = s;
-                    if (s > maximum) maximum = s;
-                }
-                double denominator = 0.0;
-                for (int64_t j = 0; j < live_count; ++j) {
-                    live_scores[j] = exp(live_scores[j] - maximum);
-                    denominator += live_scores[j];
-                }
-                for (int64_t t = 0; t < history; ++t) {
-                    scores[t] = exp(scores[t] - maximum);
-                    denominator += scores[t];
-                }
-                double hist[RQ_ORACLE_MAX_DIM] = {0};
-                for (int64_t t = 0; t < history; ++t) {
-                    const int64_t block = block_table[b * block_table_stride + t / page_tokens];
-                    const uint8_t* page = cache + plane_stride +
-                                          (block * heads + h) * (int64_t)page_tokens * page_width;
-                    restore_token(page, head_dim, records, bits, groups, page_tokens,
-                                  (int)(t % page_tokens), adjacent, anchor_index, loop, NULL,
-                                  heads, h, vbuf);
-                    for (int c = 0; c < head_dim; ++c) hist[c] += scores[t] * (double)rq_oracle_bf16_to_f32(vbuf[c]);
-                }
-                double* out = output + (i * heads + h) * (int64_t)head_dim;
-                for (int c = 0; c < head_dim; ++c) {
-                    double v = 0.0;
-                    if (value_rotation) {
-                        const uint16_t* m = value_rotation + (size_t)h * head_dim * head_dim;
-                        for (int k = 0; k < head_dim; ++k)
-                            v += hist[k] * (double)rq_oracle_f16_to_f32(m[(size_t)c * head_dim + k]);
-                    } else {
-                        v = hist[c];
-                    }
-                    double live = 0.0;
-                    for (int64_t j = 0; j < live_count; ++j) {
-                        const uint16_t* vl = value + (live_first + j) * value_stride + (int64_t)h * head_dim;
-                        live += live_scores[j] * (double)rq_oracle_bf16_to_f32(vl[c]);
-                    }
-                    out[c] = (v + live) / denominator;
-                }
-            }
-        }
-        free(scores);
+        failed |= attention_row_head(query, query_stride, key, key_stride, value, value_stride, output, heads,
+                                     head_dim, cache, num_blocks, page_tokens, page_width, first,
+                                     query_start_loc[b + 1] - first, seq_lens[b],
+                                     block_table + b * block_table_stride, key_rotation, value_rotation, key_mean,
+                                     records, bits, groups, adjacent, anchor_index, loop, causal, i, h) != 0;
     }
-    return 0;
+    free(row_request);
+    return failed ? -1 : 0;
 }
 
 int rq_oracle_attention(
@@ -710,6 +741,7 @@ int rq_oracle_paged_attention_bf16(
     int head_dim, const uint16_t* cache, int64_t num_blocks, int page_tokens,
     const int32_t* query_start_loc, const int32_t* seq_lens, int64_t requests,
     const int32_t* block_table, int64_t block_table_stride) {
+    if (heads <= 0 || head_dim <= 0 || head_dim > RQ_ORACLE_MAX_DIM) return -1;
     const int64_t plane_stride = num_blocks * heads * page_tokens * head_dim;
     const double scale = 1.0 / sqrt((double)head_dim);
     for (int64_t b = 0; b < requests; ++b) {
@@ -777,11 +809,17 @@ int rq_oracle_prefill_attention(const uint16_t* query, int64_t query_stride, con
         const int64_t q_begin = cu_q[s], q_len = cu_q[s + 1] - cu_q[s];
         const int64_t k_begin = cu_k[s], k_len = cu_k[s + 1] - cu_k[s];
         if (q_len < 0 || k_len < 0) return -1;
-        double* scores = (double*)malloc(sizeof(double) * (size_t)(k_len > 0 ? k_len : 1));
-        if (!scores) return -1;
+        int failed = 0;
+        /* Query rows are independent: they run in parallel when built with OpenMP. */
+#pragma omp parallel for schedule(dynamic, 4) reduction(| : failed)
         for (int64_t i = 0; i < q_len; ++i) {
             int64_t last = causal ? i + k_len - q_len : k_len - 1;
             if (last > k_len - 1) last = k_len - 1;
+            double* scores = (double*)malloc(sizeof(double) * (size_t)(k_len > 0 ? k_len : 1));
+            if (!scores) {
+                failed = 1;
+                continue;
+            }
             for (int h = 0; h < heads_q; ++h) {
                 const int kh = h / group;
                 const uint16_t* q = query + (q_begin + i) * query_stride + (int64_t)h * head_dim;
@@ -806,8 +844,9 @@ int rq_oracle_prefill_attention(const uint16_t* query, int64_t query_stride, con
                 }
                 for (int c = 0; c < head_dim; ++c) out[c] /= denominator;
             }
+            free(scores);
         }
-        free(scores);
+        if (failed) return -1;
     }
     return 0;
 }
