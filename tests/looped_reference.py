@@ -115,13 +115,22 @@ def _stats(got: torch.Tensor, want: torch.Tensor):
     return float(err.max()), float(err.mean()), float(want.abs().max()), float(want.abs().mean())
 
 
-def check_layers(model, oracle, tapped: dict, caches_before: dict, logits: torch.Tensor) -> dict:
+def row_blocks(model, rows) -> torch.Tensor:
+    """Block ids (device, int64) of the pages of ``rows``, row-major: the
+    layout of the sub-caches ``check_layers`` takes when given ``rows``."""
+    return model.block_table[list(rows)].flatten().long()
+
+
+def check_layers(model, oracle, tapped: dict, caches_before: dict, logits: torch.Tensor, rows=None) -> dict:
     """Recompute every tapped layer of one eager step from the decoder's own
     inputs; returns {name: (max err, mean err, max |ref|, mean |ref|)}.
 
     ``tapped`` is the decoder's ``tapped`` after the step, ``caches_before``
     the layer caches (numpy) as the step's attention saw them, ``logits``
-    the step's logits."""
+    the step's logits.  With ``rows``, the packed attention is checked on
+    those rows only and ``caches_before[layer]`` holds just their pages
+    (``cache[:, row_blocks(model, rows)]``); a row's attention reads its own
+    pages only, so the renumbered sub-cache gives the same result."""
     c = model.config
     batch, eps = model.batch, c.rms_eps
     q_size = c.heads * c.head_dim
@@ -146,6 +155,12 @@ def check_layers(model, oracle, tapped: dict, caches_before: dict, logits: torch
     seq_lens = model.seq_lens.cpu().numpy() - 1
     table = model.block_table.cpu().numpy()
     query_start_loc = model.query_start_loc.cpu().numpy()
+    picked = slice(None)
+    if rows is not None:
+        picked = list(rows)
+        seq_lens = seq_lens[picked]
+        table = np.arange(len(picked) * table.shape[1], dtype=np.int32).reshape(len(picked), table.shape[1])
+        query_start_loc = np.arange(len(picked) + 1, dtype=np.int32)
     bits = lambda t: None if t is None else workloads.bf16_bits(t)
     out = {}
     for key in sorted(k for k in tapped if isinstance(k[0], int)):
@@ -158,13 +173,13 @@ def check_layers(model, oracle, tapped: dict, caches_before: dict, logits: torch
         out[f"v{key}"] = _stats(t["v"], qkv[:, 2 * q_size:].reshape(batch, c.heads, c.head_dim))
         mean = model.key_mean[layer]
         attention = oracle.attention(
-            bits(t["q"]), bits(t["k"]), bits(t["v"]), caches_before[layer], query_start_loc, seq_lens, table,
-            bits(model.key_rotation[layer]), bits(model.value_rotation[layer]),
+            bits(t["q"][picked]), bits(t["k"][picked]), bits(t["v"][picked]), caches_before[layer],
+            query_start_loc, seq_lens, table, bits(model.key_rotation[layer]), bits(model.value_rotation[layer]),
             None if mean is None else mean.cpu().numpy(), c.schedule, "anchor", c.anchor, loop)
         # Both sides in BF16 (the parity bar is on BF16 outputs): rounding the
         # oracle keeps the BF16 quantum of outputs of magnitude ~1 (half of
         # the 1e-3 mean bar at short histories) out of the kernel's error.
-        out[f"attention{key}"] = _stats(t["out"], _bf(torch.from_numpy(attention)))
+        out[f"attention{key}"] = _stats(t["out"][picked], _bf(torch.from_numpy(attention)))
         norms = model.norms[layer]
         a = _bf(f(t["out"]).reshape(batch, q_size) @ _f64(model.o[layer]).t())
         x1, residual1 = add_rms(a, residual, norms[2], norms[1])
@@ -187,3 +202,40 @@ def check_layers(model, oracle, tapped: dict, caches_before: dict, logits: torch
     if ("h", c.loops - 1) in tapped:
         out["logits"] = _stats(logits, f(tapped[("h", c.loops - 1)]) @ _f64(model.lm_head).t())
     return out
+
+
+def new_token_pages(model):
+    """Before a step: (slots, blocks, {layer: numpy pages}) of the pages the
+    step's loop-group quantize writes (the blocks of the requests' next
+    slots; slot -1 writes nothing)."""
+    slots = model.slots.clone()
+    live = slots[slots >= 0]
+    blocks = torch.unique(torch.div(live, model.config.page_tokens, rounding_mode="floor"))
+    pages = {layer: cache[:, blocks].cpu().numpy() for layer, cache in enumerate(model.caches)}
+    return slots, blocks, pages
+
+
+def check_new_tokens(model, oracle, slots, blocks, pages_before: dict) -> int:
+    """After a step (eager or replayed): every layer's pages written by the
+    step's quantize equal the oracle's quantize of the staged K/V of all
+    loops (the decoder's ``staged`` buffer, as the step left it) into the
+    pages as they were before the step, bit for bit.  Returns the layers
+    checked."""
+    c = model.config
+    pt = c.page_tokens
+    bits = lambda t: None if t is None else workloads.bf16_bits(t)
+    index = {int(b): i for i, b in enumerate(blocks.cpu().tolist())}
+    sub_slots = np.array([-1 if s < 0 else index[s // pt] * pt + s % pt for s in slots.cpu().tolist()],
+                         dtype=np.int64)
+    for layer, cache in enumerate(model.caches):
+        got = cache[:, blocks].cpu().numpy()
+        expected = pages_before[layer].copy()
+        pairs = [(bits(model.staged[layer, r, 0]), bits(model.staged[layer, r, 1])) for r in range(c.loops)]
+        value_rotation = model.value_rotation[layer]
+        mean = model.key_mean[layer]
+        oracle.quantize(pairs, expected, sub_slots, bits(model.key_rotation[layer]), bits(value_rotation),
+                        None if mean is None else mean.cpu().numpy(), c.schedule, "anchor", c.anchor,
+                        c.coefficient)
+        assert np.array_equal(got, expected), f"new-token pages of layer {layer}"
+        assert not np.array_equal(got, pages_before[layer]), f"layer {layer}: the step wrote nothing"
+    return len(model.caches)

@@ -105,5 +105,5 @@ def test_decode_full_size_ouro_sampled_rows(oracle, device):
 
 
 def test_decode_full_size_huginn_sampled_rows(oracle, device):
-    print("[case] decode B8 x 4096 x 55 heads x D96, row 5", flush=True)
-    _decode_full_size(oracle, device, 8, 4096, 55, 96, OURO_G16, rows=(5,), loops=(0, 2, 3), seed=8200)
+    print("[case] decode B8 x 4096 x 55 heads x D96, rows 0, 5 and 7, every loop", flush=True)
+    _decode_full_size(oracle, device, 8, 4096, 55, 96, OURO_G16, rows=(0, 5, 7), loops=(0, 1, 2, 3), seed=8200)

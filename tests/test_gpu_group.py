@@ -1,13 +1,14 @@
 """The write path on the GPU: a loop group staged loop by loop
 (residualquant_amd/group.py, install_model.py:17-52, packed_backend.py:101-137)
-writes the same cache bytes as one quantize of every record, with the earlier
-loops kept on the device or, during prefill, spilled to pinned host memory
-(residualquant_amd/prefill_offload.py, whose contract is the reference's
-prefill_offload.py:10-200) and recalled in windows or through the lookahead
-ring of layer slots."""
+writes the CPU oracle's bytes for one quantize of every record (bit-exact),
+with the earlier loops kept on the device or, during prefill, spilled to
+pinned host memory (residualquant_amd/prefill_offload.py, whose contract is
+the reference's prefill_offload.py:10-200) and recalled in windows or through
+the lookahead ring of layer slots."""
 
 from __future__ import annotations
 
+import numpy as np
 import pytest
 import torch
 
@@ -34,26 +35,29 @@ def _layer(tokens, seed, device):
     return pairs, slots, kr, vr, mean, shape
 
 
-def _direct(layer, device):
+def _expected(oracle, layer):
+    """The oracle's bytes for one quantize of every record of ``layer``."""
     pairs, slots, kr, vr, mean, shape = layer
-    cache = torch.zeros(shape, dtype=torch.uint8, device=device)
-    rq.quantize(pairs, cache, slots, kr, vr, mean, RECORDS, "anchor", 3, "ls")
+    bits = workloads.bf16_bits
+    cache = np.zeros(shape, dtype=np.uint8)
+    oracle.quantize([(bits(k), bits(v)) for k, v in pairs], cache, slots.cpu().numpy(), bits(kr), bits(vr),
+                    mean.cpu().numpy(), RECORDS, "anchor", 3, "ls")
     return cache
 
 
-def test_group_store_matches_one_quantize(device):
+def test_group_store_matches_one_quantize(oracle, device):
     layer = _layer(333, 11, device)
     pairs, slots, kr, vr, mean, shape = layer
     cache = torch.zeros(shape, dtype=torch.uint8, device=device)
     group = rq.DeferredKVGroup(CONFIG, RECORDS, PT)
     done = [group.store(k, v, cache, slots, kr, vr, mean) for k, v in pairs]
     assert done == [False, False, False, True]
-    assert torch.equal(cache, _direct(layer, device))
+    assert np.array_equal(cache.cpu().numpy(), _expected(oracle, layer))
 
 
 @pytest.mark.parametrize("lookahead,layers,ring", [(False, 3, 8), (True, 3, 8), (True, 5, 2)],
                          ids=["chunks", "lookahead", "lookahead-2-slots"])
-def test_prefill_offload_matches_device_staging(device, monkeypatch, lookahead, layers, ring):
+def test_prefill_offload_matches_device_staging(oracle, device, monkeypatch, lookahead, layers, ring):
     # With 2 layer slots for 5 layers, later layers are recalled as earlier
     # ones free their slot (chain order), and none waits for a slot.
     monkeypatch.setattr(prefill_offload, "RING_MAX_LAYERS", ring)
@@ -80,7 +84,7 @@ def test_prefill_offload_matches_device_staging(device, monkeypatch, lookahead, 
                 done = groups[i].store(key.clone(), value.clone(), caches[i], slots, kr, vr, mean, prefill=True)
                 assert done == (loop == len(RECORDS) - 1)
         for i, d in enumerate(data):
-            assert torch.equal(caches[i], _direct(d, device)), (call, i)
+            assert np.array_equal(caches[i].cpu().numpy(), _expected(oracle, d)), (call, i)
     if lookahead:
         assert offload.prefetched == {}
         assert offload.layers.slots == ring and sorted(offload.layers.free) == list(range(ring))
