@@ -138,8 +138,13 @@ int rq_packed_prefill_attention(const void* query, int64_t query_stride, const v
  * attention() allocates its temporaries per call (attention/launch.cuh:85-98).
  * Same arguments, semantics, kernels and results as rq_attention; the
  * workspace is a static device array of RQ_ATTENTION_NOALLOC_MAX_BYTES per
- * GPU, held until the process ends, so a call whose
- * rq_attention_workspace_bytes(...) exceeds that size returns RQ_ENOSPACE.
+ * GPU, held until the process ends.  A call whose route needs more returns
+ * RQ_ENOSPACE before any device work: the per-row decode kernels need
+ * (272 + 130 x splits) x 4 bytes per (row, head), about 5 000 (row, head)
+ * pairs at one split; the multi-row kernels (2 or more rows per request)
+ * (132 x splits + 1) x 4 bytes, about 2 000 pairs at eight splits.
+ * (rq_attention_workspace_bytes covers both routes, so it may exceed the
+ * scratch for a call that still fits.)
  * Every noalloc call on one GPU shares that array: calls that overlap on one
  * GPU (concurrent streams or threads) race and must be serialized by the
  * caller.  Calls no hipMalloc/hipFree and records no timing events.

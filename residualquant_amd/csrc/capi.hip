@@ -150,8 +150,16 @@ int multirow_splits(int64_t groups, int64_t max_pages, int page_tokens) {
     return (int)std::max<int64_t>(1, splits);
 }
 
-int multirow_workspace_splits(int heads, int64_t max_pages, int page_tokens) {
-    return multirow_splits(heads, max_pages, page_tokens);
+// The most splits a multi-row call of `rows` rows can take.  A call runs
+// requests x heads x average_tiles groups, with average_tiles =
+// max(1, ceil(floor(rows / requests) / 32)) (attention_packed); over every
+// request count that product is at least ceil(rows / 33) x heads, so
+// heads x max(1, rows / 64) is a lower bound on the groups, and
+// multirow_splits, which never grows with the groups, is bounded by its
+// value there.
+int multirow_workspace_splits(int64_t rows, int heads, int64_t max_pages, int page_tokens) {
+    const int64_t min_groups = (int64_t)heads * std::max<int64_t>(1, rows / 64);
+    return multirow_splits(min_groups, max_pages, page_tokens);
 }
 
 struct MultiRowLayout {
@@ -305,8 +313,20 @@ static size_t attention_workspace_total(int64_t rows, int heads, int head_dim, i
     const int splits = std::max(split_count(rows, heads, max_pages), chain_splits(rows, heads, max_pages));
     size_t total = workspace_layout(rows, heads, head_dim, splits).total;
     if (head_dim == 128 && (page_tokens == 16 || page_tokens == 32))
-        total = std::max(total, multirow_layout(rows, heads, multirow_workspace_splits(heads, max_pages, page_tokens)).total);
+        total = std::max(total,
+                         multirow_layout(rows, heads, multirow_workspace_splits(rows, heads, max_pages, page_tokens)).total);
     return total;
+}
+
+// RQ_ENOSPACE for a workspace smaller than the route of the call needs; a
+// call of rq_attention_noalloc names its static scratch instead.
+static int workspace_too_small(size_t needed, size_t got, bool static_scratch) {
+    if (static_scratch)
+        return fail(RQ_ENOSPACE,
+                    "rq_attention_noalloc: this call needs %zu bytes of scratch, the static scratch holds %zu; "
+                    "call rq_attention with a workspace instead",
+                    needed, got);
+    return fail(RQ_ENOSPACE, "Attention workspace of %zu bytes required (got %zu)", needed, got);
 }
 
 size_t rq_attention_workspace_bytes(int64_t rows, int heads, int head_dim, int64_t max_pages,
@@ -320,7 +340,8 @@ static int attention_common(const void* query, int64_t query_stride, const void*
                             int64_t rows, int heads, int head_dim, const int32_t* query_start_loc,
                             const int32_t* seq_lens, int64_t requests, const int32_t* block_table,
                             int64_t block_table_stride, int64_t max_pages, void* workspace,
-                            size_t workspace_bytes, int splits, rq::AttentionParams* p) {
+                            size_t workspace_bytes, int splits, rq::AttentionParams* p,
+                            bool static_scratch = false) {
     if (rows < 0 || heads <= 0) return fail(RQ_EINVAL, "Q/K/V/output must have matching shapes and devices");
     if (rows > 0 && (query == nullptr || key == nullptr || value == nullptr || output == nullptr))
         return fail(RQ_EINVAL, "Q/K/V/output must have matching shapes and devices");
@@ -338,8 +359,7 @@ static int attention_common(const void* query, int64_t query_stride, const void*
     if (splits <= 0) return RQ_OK;  // validation only
     const WorkspaceLayout layout = workspace_layout(rows, heads, head_dim, splits);
     if (rows > 0 && (workspace == nullptr || workspace_bytes < layout.total))
-        return fail(RQ_ENOSPACE, "Attention workspace of %zu bytes required (got %zu)", layout.total,
-                    workspace_bytes);
+        return workspace_too_small(layout.total, workspace_bytes, static_scratch);
     uint8_t* ws = static_cast<uint8_t*>(workspace);
     *p = rq::AttentionParams{};
     p->query = static_cast<const uint16_t*>(query);
@@ -397,7 +417,7 @@ static int attention_packed(const void* query, int64_t query_stride, const void*
                             const void* value_rotation, const float* key_mean, int records, const int* bits,
                             const int* groups, int reference_mode, int anchor_index, int loop_index,
                             void* workspace, size_t workspace_bytes, hipStream_t stream, bool timed,
-                            bool causal = false) {
+                            bool causal = false, bool static_scratch = false) {
     int status = validate_schedule(head_dim, records, bits, groups, page_tokens, reference_mode,
                                    anchor_index, heads);
     if (status != RQ_OK) return status;
@@ -447,8 +467,7 @@ static int attention_packed(const void* query, int64_t query_stride, const void*
         const int splits = multirow_splits(requests * heads * average_tiles, max_pages, page_tokens);
         const MultiRowLayout layout = multirow_layout(rows, heads, splits);
         if (workspace == nullptr || workspace_bytes < layout.total)
-            return fail(RQ_ENOSPACE, "Attention workspace of %zu bytes required (got %zu)", layout.total,
-                        workspace_bytes);
+            return workspace_too_small(layout.total, workspace_bytes, static_scratch);
         rq::RecordRegion regions[rq::kMaxRecords];
         fill_regions(head_dim, records, bits, groups, page_tokens, regions);
         rq::MultiRowParams m{};
@@ -503,7 +522,8 @@ static int attention_packed(const void* query, int64_t query_stride, const void*
     const int anchor_record = adjacent ? 0 : anchor_index;
     status = attention_common(query, query_stride, key, key_stride, value, value_stride, output,
                               output_stride, rows, heads, head_dim, query_start_loc, seq_lens, requests,
-                              block_table, block_table_stride, max_pages, workspace, workspace_bytes, splits, &p);
+                              block_table, block_table_stride, max_pages, workspace, workspace_bytes, splits, &p,
+                              static_scratch);
     if (status != RQ_OK) return status;
     if (rows == 0) return ok();
     rq::RecordRegion regions[rq::kMaxRecords];
@@ -607,14 +627,8 @@ int rq_attention_noalloc(const void* query, int64_t query_stride, const void* ke
                          const void* value_rotation, const float* key_mean, int records, const int* bits,
                          const int* groups, int reference_mode, int anchor_index, int loop_index,
                          hipStream_t stream) {
-    if (rows > 0 && heads > 0 && head_dim > 0) {
-        const size_t needed = attention_workspace_total(rows, heads, head_dim, max_pages, page_tokens);
-        if (needed > kAttentionScratchBytes)
-            return fail(RQ_ENOSPACE,
-                        "rq_attention_noalloc: this call needs %zu bytes of scratch, the static scratch holds "
-                        "%zu; call rq_attention with a workspace instead",
-                        needed, kAttentionScratchBytes);
-    }
+    // The route the call takes (per-row or multi-row kernels) checks its own
+    // workspace size against the scratch, before any device work.
     void* workspace = nullptr;
     const int status = scratch_address(&workspace);
     if (status != RQ_OK) return status;
@@ -622,7 +636,8 @@ int rq_attention_noalloc(const void* query, int64_t query_stride, const void* ke
                             rows, heads, head_dim, kv_cache, num_blocks, page_tokens, page_width,
                             query_start_loc, seq_lens, requests, block_table, block_table_stride, max_pages,
                             key_rotation, value_rotation, key_mean, records, bits, groups, reference_mode,
-                            anchor_index, loop_index, workspace, kAttentionScratchBytes, stream, false);
+                            anchor_index, loop_index, workspace, kAttentionScratchBytes, stream, false, false,
+                            true);
 }
 
 int rq_dequantize(const void* kv_cache, int64_t num_blocks, int heads, int page_tokens, int page_width,

@@ -128,6 +128,21 @@ def test_workspace_size_depends_on_shapes_only(lib):
     assert lib.rq_attention_workspace_bytes(64, 16, 128, 512, 16) > a
 
 
+def test_workspace_grows_no_faster_than_linearly_in_rows(lib):
+    """The workspace bound of a call with many rows (prefill over packed
+    history) is sized for the splits its row count allows: from 64 rows up
+    the bytes per row never grow with the rows, and a 4096-row x 16-head
+    call over 8192 history tokens needs the per-row route's one-split layout
+    (query records of 272 floats plus partials of 130 floats per (row,
+    head): ~105 MB), not eight multi-row splits' worth (~277 MB)."""
+    rows = (64, 128, 256, 512, 1024, 2048, 4096, 8192, 32768)
+    for history_pages in (64, 512, 2048):
+        sizes = [lib.rq_attention_workspace_bytes(n, 16, 128, history_pages, 16) for n in rows]
+        for (n_small, small), (n_large, large) in zip(zip(rows, sizes), zip(rows[1:], sizes[1:])):
+            assert large * n_small <= small * n_large + 4096 * n_large, (history_pages, sizes)
+    assert lib.rq_attention_workspace_bytes(4096, 16, 128, 512, 16) < 110 * 10 ** 6
+
+
 def test_python_ops_mirror_reference_messages():
     cpu = torch.zeros((2, 16, 128), dtype=torch.bfloat16)
     cache = torch.zeros((2, 4, 16, 16, 200), dtype=torch.uint8)

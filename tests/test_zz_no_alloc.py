@@ -74,6 +74,52 @@ def test_noalloc_matches_workspace_entry_point(oracle, device):
             assert err.max() <= 2e-2 and err.mean() <= 1e-3, (err.max(), err.mean())
 
 
+def test_noalloc_one_row_decode_at_batch_128(device):
+    """A plain decode step of 128 requests x 1 row x 16 heads over 2047
+    history tokens runs the per-row kernels, whose workspace (~3.3 MB) fits
+    the scratch even though a multi-row call of 128 rows would not: the
+    call is checked against the route it takes, and its output equals
+    rq_attention's bit for bit at every loop."""
+    import residualquant_amd as rq
+    from residualquant_amd import workloads
+
+    lib = _lib.lib()
+    batch, heads, dim, history, pt = 128, 16, 128, 2047, 16
+    print(f"[case] noalloc decode batch {batch} x {heads} heads x {history} history", flush=True)
+    pages = (history + pt) // pt
+    table = workloads.block_tables(batch, pages, 71, device=device)
+    cache = torch.zeros((2, batch * pages, heads, pt, rq.page_width(dim, OURO_G32)), dtype=torch.uint8, device=device)
+    kr = workloads.random_sign_rotation(heads, dim, 72, device=device)
+    vr = workloads.random_sign_rotation(heads, dim, 73, device=device)
+    km = workloads.key_means(4, heads, dim, 74, device=device)
+    slots = workloads.history_slots(table, [history] * batch, pt).to(device)
+    for start in range(0, slots.numel(), 32768):
+        part = slots[start:start + 32768]
+        pairs = workloads.loop_kv(part.numel(), heads, dim, 4, 75 + start, device=device, anchor_index=3)
+        rq.quantize(pairs, cache, part, kr, vr, km, OURO_G32, "anchor", 3, "ls")
+    generator = torch.Generator().manual_seed(76)
+    q, k, v = (torch.randn((batch, heads, dim), generator=generator).to(torch.bfloat16) for _ in range(3))
+
+    class Inputs:  # the fields _call reads
+        pass
+
+    d = Inputs()
+    d.query, d.key, d.value = q, k, v
+    d.query_start_loc = torch.arange(batch + 1, dtype=torch.int32)
+    d.seq_lens = torch.full((batch,), history + 1, dtype=torch.int32)
+    d.lengths = [history + 1] * batch
+    d.table = table
+    d.group = Inputs()
+    d.group.records, d.group.mode, d.group.anchor = OURO_G32, "anchor", 3
+    d.group.device_args = lambda dev: (kr, vr, km)
+    assert lib.rq_attention_workspace_bytes(batch, heads, dim, pages, pt) > _lib.RQ_ATTENTION_NOALLOC_MAX_BYTES
+    for loop in range(4):
+        want = _call(lib, d, device, cache, loop, noalloc=False)
+        got = _call(lib, d, device, cache, loop, noalloc=True)
+        assert bool(torch.isfinite(want.float()).all())
+        assert torch.equal(got.view(torch.int16), want.view(torch.int16)), f"loop {loop}"
+
+
 def test_noalloc_rejects_calls_beyond_the_scratch(device):
     lib = _lib.lib()
     heads, dim, rows = 16, 128, 8192
