@@ -114,12 +114,11 @@ int rq_attention(const void* query, int64_t query_stride, const void* key, int64
  * in the reference, whose scheduler forbids partial prefill and cached
  * prefixes (src/residual_quantization/scheduler.py:11-18).  Arguments,
  * validation and workspace (rq_attention_workspace_bytes) are those of
- * rq_attention; anchor mode at head_dim 128 only (RQ_ENOKERNEL otherwise).
- * A request may have no new rows.  rq_attention itself routes calls with an
- * average of 2 or more rows per request (3 in the anchor loop) in anchor
- * mode at head_dim 128 to the same multi-row kernels (each row then sees
- * seq_lens[b] - 1 history tokens and its own key/value, the reference's
- * semantics).
+ * rq_attention (head_dim 96 or 128, anchor or adjacent mode).  A request
+ * may have no new rows.  rq_attention itself routes calls with an average
+ * of 2 or more rows per request (3 in the anchor-only loop) to the same
+ * multi-row kernels (each row then sees seq_lens[b] - 1 history tokens and
+ * its own key/value, the reference's semantics).
  */
 int rq_packed_prefill_attention(const void* query, int64_t query_stride, const void* key, int64_t key_stride,
                                 const void* value, int64_t value_stride, void* output, int64_t output_stride,

@@ -312,7 +312,7 @@ static size_t attention_workspace_total(int64_t rows, int heads, int head_dim, i
                                         int page_tokens) {
     const int splits = std::max(split_count(rows, heads, max_pages), chain_splits(rows, heads, max_pages));
     size_t total = workspace_layout(rows, heads, head_dim, splits).total;
-    if (head_dim == 128 && (page_tokens == 16 || page_tokens == 32))
+    if ((head_dim == 96 || head_dim == 128) && (page_tokens == 16 || page_tokens == 32))
         total = std::max(total,
                          multirow_layout(rows, heads, multirow_workspace_splits(rows, heads, max_pages, page_tokens)).total);
     return total;
@@ -434,24 +434,21 @@ static int attention_packed(const void* query, int64_t query_stride, const void*
     const int width = rq_page_width(head_dim, records, bits, groups);
     if (width != page_width) return fail(RQ_EINVAL, "Packed cache width differs from records");
     const bool adjacent = records > 1 && reference_mode == RQ_MODE_ADJACENT;
-    // Several rows per request in anchor mode at D = 128 (and every prefill
-    // over packed history) take the multi-row MFMA kernels, which stream each
-    // request's pages once for all its rows but dequantize every page tile
-    // into LDS.  Measured at 8192 history tokens x 16 heads (4-call step,
-    // multi-row against per-row decode kernel): 3 rows per request 973
-    // against 1468 us (B32), 4 rows 260 against 500 us per residual call,
-    // 16 rows 530 against 3280 us (B16); at 2 rows the residual-loop call is
-    // faster (256 against 283 us at B32, 84 against 88 us at B8) but the
-    // anchor-loop call slower (192 against 183 us), so decode calls take them
-    // from an average of kMultiRowMinRowsResidual rows per request in a
-    // residual loop and kMultiRowMinRows in the anchor loop.
-    const int64_t min_rows = loop_index != anchor_index ? kMultiRowMinRowsResidual : kMultiRowMinRows;
-    if (causal || (!adjacent && head_dim == 128 && requests > 0 && rows >= min_rows * requests)) {
-        if (adjacent || head_dim != 128)
-            return fail(RQ_ENOKERNEL,
-                        "No compiled packed HIP multi-row kernel for head_dim=%d, reference_mode=%s (anchor mode "
-                        "at head_dim 128 only)",
-                        head_dim, adjacent ? "adjacent" : "anchor");
+    // Several rows per request (and every prefill over packed history) take
+    // the multi-row MFMA kernels, which stream each request's pages once for
+    // all its rows but dequantize every page tile into LDS.  Measured at 8192
+    // history tokens x 16 heads x D128 in anchor mode (4-call step, multi-row
+    // against per-row decode kernel): 3 rows per request 973 against 1468 us
+    // (B32), 4 rows 260 against 500 us per residual call, 16 rows 530 against
+    // 3280 us (B16); at 2 rows the residual-loop call is faster (256 against
+    // 283 us at B32, 84 against 88 us at B8) but the anchor-loop call slower
+    // (192 against 183 us), so decode calls take them from an average of
+    // kMultiRowMinRowsResidual rows per request in a residual loop (and in
+    // adjacent mode past loop 0, where the per-row kernel rebuilds the chain
+    // once per row) and kMultiRowMinRows in the anchor-only loop.
+    const bool anchor_only = adjacent ? loop_index == 0 : loop_index == anchor_index;
+    const int64_t min_rows = anchor_only ? kMultiRowMinRows : kMultiRowMinRowsResidual;
+    if (causal || (requests > 0 && rows >= min_rows * requests)) {
         status = attention_common(query, query_stride, key, key_stride, value, value_stride, output, output_stride,
                                   rows, heads, head_dim, query_start_loc, seq_lens, requests, block_table,
                                   block_table_stride, max_pages, nullptr, 0, 0, nullptr);
@@ -481,6 +478,7 @@ static int attention_packed(const void* query, int64_t query_stride, const void*
         m.output_stride = output_stride;
         m.rows = rows;
         m.heads = heads;
+        m.head_dim = head_dim;
         m.cache = static_cast<const uint8_t*>(kv_cache);
         m.plane_stride = num_blocks * heads * (int64_t)page_tokens * page_width;
         m.num_blocks = num_blocks;
@@ -494,12 +492,17 @@ static int attention_packed(const void* query, int64_t query_stride, const void*
         m.max_pages = max_pages;
         m.key_rotation = static_cast<const uint16_t*>(key_rotation);
         m.value_rotation = static_cast<const uint16_t*>(value_rotation);
-        m.anchor = regions[anchor_index];
-        m.has_residual = loop_index != anchor_index;
+        // Adjacent mode: loop 0 is its own anchor (record 0 alone, as the
+        // per-row route decodes it); later loops decode the restore chain.
+        const int anchor = adjacent ? 0 : anchor_index;
+        m.anchor = regions[anchor];
+        m.has_residual = !adjacent && loop_index != anchor;
         m.residual = regions[loop_index];
+        m.chain_length = adjacent && loop_index > 0 ? loop_index + 1 : 0;
+        for (int r = 0; r < m.chain_length; ++r) m.chain[r] = regions[r];
+        m.key_mean_all = m.chain_length > 0 ? key_mean : nullptr;
         m.key_mean_loop = key_mean ? key_mean + (int64_t)loop_index * heads * head_dim : nullptr;
-        m.key_mean_anchor = (key_mean && m.has_residual) ? key_mean + (int64_t)anchor_index * heads * head_dim
-                                                          : nullptr;
+        m.key_mean_anchor = (key_mean && m.has_residual) ? key_mean + (int64_t)anchor * heads * head_dim : nullptr;
         m.causal = causal ? 1 : 0;
         m.splits = splits;
         m.row_tiles = (int)row_tiles;

@@ -1,5 +1,5 @@
 // Attention of several query rows per request over packed pages, on MFMA
-// tiles (gfx950, wave64).
+// tiles (gfx950, wave64), for head dims 96 and 128, anchor and adjacent mode.
 //
 // The decode kernel scores one query row per workgroup with integer dot
 // products on the packed codes, so n rows of one request stream the
@@ -8,31 +8,40 @@
 // and dequantizes every 32-token tile into LDS as FP16 K and BF16 V (both
 // row-major; V is read transposed by ds_read_b64_tr_b16), so that the tile's
 // rows share it through MFMA:
-//   S^T = K Q'^T     (32 tokens x 32 rows, 8 v_mfma_f32_32x32x16_f16 over D = 128)
-//   O^T += V^T P^T   (128 channels x 32 rows, 8 v_mfma_f32_32x32x16_bf16)
+//   S^T = K Q'^T     (32 tokens x 32 rows, D / 16 v_mfma_f32_32x32x16_f16)
+//   O^T += V^T P^T   (D channels x 32 rows, D / 16 v_mfma_f32_32x32x16_bf16)
 // The scores take FP16 operands (11-bit significands; each row of q' is
 // scaled by a power of two into [-1, 1], which the scores take back), since
 // BF16 operands there put the outlier channels' score error near the
-// 1e-3 mean bar on short histories.  K and V are evaluated in FP32 (two fmas
-// per channel and plane) and rounded once, to FP16 and BF16.  P stays in the
-// accumulator registers (the token order of each P.V step is permuted to
-// match the accumulator layout, and V^T is read with the same permutation).
-// Each of the four waves takes every fourth tile with its own online
-// softmax; the waves meet once in LDS at the end and the workgroup writes one
-// partial (m, l, O) per row.  The query prologue (q . R_k) runs on MFMA as
-// well.  A finish launch per (request, head, 32-row tile) merges the splits,
-// applies R_v^T (on MFMA) and adds the live tokens.
+// 1e-3 mean bar on short histories.  P stays in the accumulator registers
+// (the token order of each P.V step is permuted to match the accumulator
+// layout, and V^T is read with the same permutation).  Each of the four
+// waves takes every fourth tile with its own online softmax; the waves meet
+// once in LDS at the end and the workgroup writes one partial (m, l, O) per
+// row.  The query prologue (q . R_k) runs on MFMA as well.  A finish launch
+// per (request, head, 32-row tile) merges the splits, applies R_v^T (on
+// MFMA) and adds the live tokens.
+//
+// A lane dequantizes one token's 32-channel quarter of a 16-token unit
+// (lane = token x quarter); at D = 96 the fourth quarter's lanes load a copy
+// of the first quarter's bytes and store nothing.
 //
 // Semantics (reference: attention/compute.cuh:397-505 keys, :28-107 values,
-// prepare.cuh:13-54 and :203-229 live score and mean shift, merge.cuh:8-84,
-// output.cuh:9-31): keys alpha_L (c.s+o + bf16(mu_A))_A + (c.s+o)_L with the
-// current loop's mean as a per-row shift, values alpha_L (c.s+o)_A +
-// (c.s+o)_L (the reference rounds each restore step to BF16; one rounding
-// here, within the attention tolerance), P in BF16.
+// :120-197 and :506-623 the adjacent-mode chain, prepare.cuh:13-54 and
+// :203-229 live score and mean shift, merge.cuh:8-84, output.cuh:9-31):
+//   anchor mode: keys alpha_L (c.s+o + bf16(mu_A))_A + (c.s+o)_L with the
+//     current loop's mean as a per-row shift, values alpha_L (c.s+o)_A +
+//     (c.s+o)_L (the reference rounds each restore step to BF16; one
+//     rounding here, within the attention tolerance) (AnchorDecoder);
+//   adjacent mode past loop 0: keys and values the BF16 restore chain over
+//     records 0..L, the key chain adding bf16(mu_r) to every record but the
+//     current loop's (rq_chain.h; ChainDecoder);
+// P in BF16.
 //
 // Lane layouts of v_mfma_f32_32x32x16_bf16 (checked on gfx950): A row l % 32,
 // k 8 (l / 32) + e; B column l % 32, k 8 (l / 32) + e; C register r holds row
 // 8 (r / 4) + 4 (l / 32) + r % 4, column l % 32.
+#include "rq_chain.h"
 #include "rq_device.h"
 #include "rq_kernels.h"
 
@@ -44,29 +53,46 @@ typedef __bf16 Bf16x8 __attribute__((ext_vector_type(8)));
 typedef _Float16 F16x8 __attribute__((ext_vector_type(8)));
 typedef float F32x16 __attribute__((ext_vector_type(16)));
 
-constexpr int D = 128;
 constexpr int kThreads = 256;
 constexpr int kWaves = 4;
-constexpr int kTile = 32;            // tokens per MFMA tile (two 16-token units)
-constexpr int KS = D + 8;            // K tile row stride (BF16)
-constexpr int VS = kTile + 8;        // V^T tile row stride (BF16)
-constexpr int kWaveBytes = kTile * KS * 2 + D * VS * 2 + kTile * 4;  // K (FP16), V (BF16), alpha_K
-static_assert(kTile * D <= D * VS, "the row-major V tile fits its region");
-constexpr int kLdsBytes = kWaves * kWaveBytes;
-// Prologue scratch (aliases the tiles): q scaled into FP16 [32][KS], R_k FP16
-// [D][KS], q.R_k FP32 [32][QRS], q' FP16 [32][KS], mean dots, row scales and
-// the rows' input exponents.
-constexpr int QRS = D + 4;
-constexpr int kQ16Offset = 0;
-constexpr int kRkOffset = kQ16Offset + 32 * KS * 2;
-constexpr int kQrawOffset = kRkOffset + D * KS * 2;
-constexpr int kQpOffset = kQrawOffset + 32 * QRS * 4;
-constexpr int kQmuOffset = kQpOffset + 32 * KS * 2;
-static_assert(kQmuOffset + 128 * 4 <= kLdsBytes, "prologue scratch fits in the tile LDS");
-// Wave merge (aliases the tiles): O [wave][row][MS] FP32 and (m, l) per wave and row.
-constexpr int MS = D + 4;
-constexpr int kMlOffset = kWaves * 32 * MS * 4;
-static_assert(kMlOffset + kWaves * 32 * 2 * 4 <= kLdsBytes, "merge buffer fits in the tile LDS");
+constexpr int kTile = 32;  // tokens per MFMA tile (two 16-token units)
+constexpr int kMaxD = 128;
+
+// LDS geometry of the stream kernel for head dim D.
+template <int D>
+struct Geometry {
+    static constexpr int Quarters = D / 32;  // 32-channel quarters a token's lanes cover
+    static constexpr int Parts = D / 16;     // 16-channel parts (MFMA k steps of the scores)
+    static constexpr int KS = D + 8;         // K tile row stride (halves)
+    // V tile [token][VROW] BF16.  At D = 128 the row is unpadded and its four
+    // 32-channel chunks are swizzled by token (chunk q at position q ^
+    // (token % 4)), which keeps the transposed reads free of bank conflicts;
+    // at D = 96 the rows are padded to 104 halves instead (16-byte aligned
+    // rows for the stores, 8-byte aligned reads).
+    static constexpr bool kSwizzleV = D == 128;
+    static constexpr int VROW = D == 128 ? D : D + 8;
+    static constexpr int kVBytes = D == 128 ? D * (kTile + 8) * 2 : kTile * VROW * 2;
+    static constexpr int kWaveBytes = kTile * KS * 2 + kVBytes + kTile * 4;  // K (FP16), V (BF16), alpha_K
+    static constexpr int kLdsBytes = kWaves * kWaveBytes;
+    // Prologue scratch (aliases the tiles): q scaled into FP16 [32][KS], R_k
+    // FP16 [D][KS], q.R_k FP32 [32][QRS], q' FP16 [32][KS], mean dots, row
+    // scales and the rows' input exponents.
+    static constexpr int QRS = D + 4;
+    static constexpr int kQ16Offset = 0;
+    static constexpr int kRkOffset = kQ16Offset + 32 * KS * 2;
+    static constexpr int kQrawOffset = kRkOffset + D * KS * 2;
+    static constexpr int kQpOffset = kQrawOffset + 32 * QRS * 4;
+    static constexpr int kQmuOffset = kQpOffset + 32 * KS * 2;
+    // Wave merge (aliases the tiles): O [wave][row][MS] FP32 and (m, l) per wave and row.
+    static constexpr int MS = D + 4;
+    static constexpr int kMlOffset = kWaves * 32 * MS * 4;
+    static_assert(kTile * VROW * 2 <= kVBytes, "the row-major V tile fits its region");
+    static_assert(kQmuOffset + 128 * 4 <= kLdsBytes, "prologue scratch fits in the tile LDS");
+    static_assert(kMlOffset + kWaves * 32 * 2 * 4 <= kLdsBytes, "merge buffer fits in the tile LDS");
+    // log2(e) / sqrt(D)
+    static constexpr float kScoreScale = D == 128 ? 1.4426950408889634f * 0.08838834764831845f
+                                                  : 1.4426950408889634f * 0.10206207261596575f;
+};
 constexpr float kLog2e = 1.4426950408889634f;
 // Pages of one history split at most (its block ids are staged in LDS); the
 // host sizes splits so that a split never holds more.
@@ -100,10 +126,11 @@ struct RecordBytes {
     uint32_t scale, offset, alpha;
 };
 
-template <int Bits>
+template <int Bits, int G>
 __device__ __forceinline__ void load_record(__amdgpu_buffer_rsrc_t page, const RecordRegion& r, int page_tokens,
                                             int row, int quarter, bool alpha, RecordBytes<Bits>& out) {
-    const uint32_t codes = (uint32_t)(r.offset + row * r.code_bytes + quarter * (r.code_bytes / 4));
+    // A 32-channel quarter holds 4 x Bits code bytes and 32 / G groups.
+    const uint32_t codes = (uint32_t)(r.offset + row * r.code_bytes + quarter * 4 * Bits);
     if constexpr (Bits == 4) {
         const auto v = __builtin_amdgcn_raw_buffer_load_b128(page, codes, 0, kStreamPolicy);
         out.w[0] = v[0]; out.w[1] = v[1]; out.w[2] = v[2]; out.w[3] = v[3];
@@ -117,7 +144,7 @@ __device__ __forceinline__ void load_record(__amdgpu_buffer_rsrc_t page, const R
     // loads (a conditional load makes the compiler wait for every load in
     // flight, the next unit's included).  Pages are multiples of 16 bytes,
     // so the dword never crosses the page end.
-    const uint32_t scales = (uint32_t)(r.offset + page_tokens * r.code_bytes + row * r.groups + quarter * (r.groups / 4));
+    const uint32_t scales = (uint32_t)(r.offset + page_tokens * r.code_bytes + row * r.groups + quarter * (32 / G));
     const uint32_t offsets = scales + (uint32_t)(page_tokens * r.groups);
     const uint32_t shift = 8u * (scales & 3u);  // offsets sit page_tokens x groups (a multiple of 4) bytes later
     out.scale = __builtin_amdgcn_raw_buffer_load_b32(page, scales & ~3u, 0, 0) >> shift;
@@ -221,14 +248,6 @@ __device__ __forceinline__ Short4 read_transposed(const uint16_t* p) {
     return __builtin_amdgcn_ds_read_tr16_b64_v4i16((LdsShort4*)p);
 }
 
-// Every record byte of one 16-token unit for the lane: K and V planes, the
-// anchor record and the loop's record.
-template <int BA, int BL>
-struct UnitBytes {
-    RecordBytes<BA> ka, va;
-    RecordBytes<BL> kl, vl;
-};
-
 // The LDS writes of a wave before reads of other lanes of the same wave.
 __device__ __forceinline__ void wave_sync() {
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
@@ -236,11 +255,122 @@ __device__ __forceinline__ void wave_sync() {
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
+// The page resources of one 16-token unit (wave-uniform) and the lane's row in the page.
+struct UnitPages {
+    __amdgpu_buffer_rsrc_t k, v;
+    int row;
+};
+
+// Anchor mode: K and V of the anchor record and, for a residual loop, the
+// loop's record (BA/GA and BL/GL their bits and groups).  Units stream two
+// ahead: the loads of the unit two places on are issued before a unit is
+// dequantized, so about two units' bytes per wave are in flight while units
+// dequantize and the tiles' MFMAs run.
 template <int PT, bool HasL, int BA, int GA, int BL, int GL>
-__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2)))
-void multirow_stream_kernel(MultiRowParams p) {
-    __shared__ __attribute__((aligned(16))) uint8_t lds[kLdsBytes];
-    __shared__ int split_blocks[kMaxSplitPages];  // block ids of the split's pages
+struct AnchorDecoder {
+    static constexpr bool kAnchorMeanTerm = HasL;  // scores add alpha_K q'.bf16(mu_A)
+    struct Bytes {
+        RecordBytes<BA> ka, va;
+        RecordBytes<BL> kl, vl;
+    };
+    RecordRegion anchor, residual;
+    int lq;
+    Bytes ahead1, ahead2;
+
+    __device__ __forceinline__ void fetch(const UnitPages& u, Bytes& b) const {
+        load_record<BA, GA>(u.k, anchor, PT, u.row, lq, false, b.ka);
+        load_record<BA, GA>(u.v, anchor, PT, u.row, lq, false, b.va);
+        if constexpr (HasL) {
+            load_record<BL, GL>(u.k, residual, PT, u.row, lq, true, b.kl);
+            load_record<BL, GL>(u.v, residual, PT, u.row, lq, true, b.vl);
+        }
+    }
+    __device__ __forceinline__ void prime(const UnitPages& first, const UnitPages& second) {
+        fetch(first, ahead1);
+        fetch(second, ahead2);
+    }
+    // Dequantizes the current unit (K, then V, so that only one plane's
+    // values are live at a time) after issuing the loads of `two_on`;
+    // store_k / store_v take the lane's 32 channels in two halves of 16.
+    // Returns the token's K alpha (1 without a loop record).
+    template <class StoreK, class StoreV>
+    __device__ __forceinline__ float unit(const UnitPages& /*next*/, const UnitPages& two_on, StoreK store_k,
+                                          StoreV store_v) {
+        const Bytes cur = ahead1;
+        ahead1 = ahead2;
+        fetch(two_on, ahead2);
+        const float alpha_k = HasL ? bf16_f32(cur.kl.alpha) : 1.f;
+        {
+            float k[32];
+            plane_values<BA, GA, BL, GL, HasL>(cur.ka, cur.kl, alpha_k, k);
+            store_k(k, k + 16);
+        }
+        {
+            float v[32];
+            plane_values<BA, GA, BL, GL, HasL>(cur.va, cur.vl, HasL ? bf16_f32(cur.vl.alpha) : 1.f, v);
+            store_v(v, v + 16);
+        }
+        return alpha_k;
+    }
+};
+
+// Adjacent mode past loop 0: K and V are the BF16 restore chain over the
+// Links records 0..L (rq_chain.h), K adding bf16(mu_r) of records r < L
+// (FP32 copies in LDS, `mean`: [Links - 1][kMaxD], or null).  A unit's raw
+// bytes of all its records take ~6 registers per record and plane, so units
+// stream one ahead: a plane's registers take the next unit's bytes as soon as
+// this unit's chain of that plane is built.  Keys are rounded to BF16 (the
+// chain's last link) before the FP16 tile takes them, which is exact.
+template <int D, int PT, int Links>
+struct ChainDecoder {
+    static constexpr bool kAnchorMeanTerm = false;
+    RecordRegion regs[Links];
+    const float* mean;  // [Links - 1][kMaxD] in LDS (zeros without means)
+    bool add_mean;
+    int lq;
+    uint32_t pick_lo, pick_hi;
+    ChainRaw k[Links], v[Links];
+
+    __device__ __forceinline__ void fetch_plane(__amdgpu_buffer_rsrc_t page, int row, ChainRaw (&raw)[Links]) const {
+#pragma unroll
+        for (int r = 0; r < Links; ++r) chain_load<PT, kStreamPolicy, 0>(page, regs[r], row, lq, r > 0, raw[r]);
+    }
+    __device__ __forceinline__ void prime(const UnitPages& first, const UnitPages& /*second*/) {
+        fetch_plane(first.k, first.row, k);
+        fetch_plane(first.v, first.row, v);
+    }
+    template <class StoreK, class StoreV>
+    __device__ __forceinline__ float unit(const UnitPages& next, const UnitPages& /*two_on*/, StoreK store_k,
+                                          StoreV store_v) {
+        const float* m = mean + 32 * lq;
+        float lo[16], hi[16];
+        chain_build<0, Links>(k, regs, add_mean, m, kMaxD, true, pick_lo, pick_hi, lo);
+        chain_build<1, Links>(k, regs, add_mean, m + 16, kMaxD, true, pick_lo, pick_hi, hi);
+        // The last link's BF16 rounding, one pack per channel pair.
+#pragma unroll
+        for (int i = 0; i < 16; i += 2) {
+            const uint32_t a = bf16_pack(lo[i], lo[i + 1]), b = bf16_pack(hi[i], hi[i + 1]);
+            lo[i] = __uint_as_float(a << 16);
+            lo[i + 1] = __uint_as_float(a & 0xffff0000u);
+            hi[i] = __uint_as_float(b << 16);
+            hi[i + 1] = __uint_as_float(b & 0xffff0000u);
+        }
+        fetch_plane(next.k, next.row, k);
+        store_k(lo, hi);
+        chain_build<0, Links>(v, regs, false, m, kMaxD, true, pick_lo, pick_hi, lo);
+        chain_build<1, Links>(v, regs, false, m, kMaxD, true, pick_lo, pick_hi, hi);
+        fetch_plane(next.v, next.row, v);
+        store_v(lo, hi);
+        return 1.f;
+    }
+};
+
+template <int D, int PT, class Decoder>
+__device__ __forceinline__ void multirow_stream(const MultiRowParams& p, Decoder& dec, uint8_t* lds,
+                                                int* split_blocks) {
+    using G = Geometry<D>;
+    constexpr int KS = G::KS;
+    constexpr int QRS = G::QRS;
     const int request = blockIdx.x;
     const int head = blockIdx.y;
     const int split = (int)blockIdx.z % p.splits;
@@ -271,18 +401,19 @@ void multirow_stream_kernel(MultiRowParams p) {
     // q' 2^-e with 2^e the row's power-of-two scale, and the row dots
     // q'.bf16(mu_A) (added per token times alpha_L) and q'.mu_L (the shift of
     // the history scores against the live ones).
-    uint16_t* q16 = reinterpret_cast<uint16_t*>(lds + kQ16Offset);
-    uint16_t* r_k = reinterpret_cast<uint16_t*>(lds + kRkOffset);
-    float* q_raw = reinterpret_cast<float*>(lds + kQrawOffset);
-    uint16_t* q_p = reinterpret_cast<uint16_t*>(lds + kQpOffset);
-    float* q_mu = reinterpret_cast<float*>(lds + kQmuOffset);  // [0..31] q'.bf16(mu_A), [32..63] q'.mu_L
-    float* q_scale = q_mu + 64;                                 // [32] 2^e per row
-    float* q_unscale = q_mu + 96;                               // [32] 2^f per row (the input's scale)
+    uint16_t* q16 = reinterpret_cast<uint16_t*>(lds + G::kQ16Offset);
+    uint16_t* r_k = reinterpret_cast<uint16_t*>(lds + G::kRkOffset);
+    float* q_raw = reinterpret_cast<float*>(lds + G::kQrawOffset);
+    uint16_t* q_p = reinterpret_cast<uint16_t*>(lds + G::kQpOffset);
+    float* q_mu = reinterpret_cast<float*>(lds + G::kQmuOffset);  // [0..31] q'.bf16(mu_A), [32..63] q'.mu_L
+    float* q_scale = q_mu + 64;                                    // [32] 2^e per row
+    float* q_unscale = q_mu + 96;                                  // [32] 2^f per row (the input's scale)
     {
         const int r = tid >> 3, part = tid & 7;  // row, 16-channel part
+        const bool part_active = part < G::Parts;
         const int row = row0 + r;
         uint32_t words[8] = {0u, 0u, 0u, 0u, 0u, 0u, 0u, 0u};
-        if (row < n) {
+        if (row < n && part_active) {
             const uint2* src = reinterpret_cast<const uint2*>(
                 p.query + (int64_t)(first + row) * p.query_stride + head * D + 16 * part);
 #pragma unroll
@@ -314,16 +445,19 @@ void multirow_stream_kernel(MultiRowParams p) {
 #pragma unroll
             for (int i = 0; i < 8; ++i)
                 h[i] = f16_bits(x[2 * i] * down) | (f16_bits(x[2 * i + 1] * down) << 16);
-            uint4* dst = reinterpret_cast<uint4*>(&q16[r * KS + 16 * part]);
-            dst[0] = make_uint4(h[0], h[1], h[2], h[3]);
-            dst[1] = make_uint4(h[4], h[5], h[6], h[7]);
+            if (part_active) {
+                uint4* dst = reinterpret_cast<uint4*>(&q16[r * KS + 16 * part]);
+                dst[0] = make_uint4(h[0], h[1], h[2], h[3]);
+                dst[1] = make_uint4(h[4], h[5], h[6], h[7]);
+            }
             if (part == 0) q_unscale[r] = ldexpf(1.0f, f);
-            const int k = tid >> 1, half_k = tid & 1;
-            const uint4* src = reinterpret_cast<const uint4*>(p.key_rotation + ((int64_t)head * D + k) * D + 64 * half_k);
-            uint4* rdst = reinterpret_cast<uint4*>(r_k + k * KS + 64 * half_k);
+            // R_k [D][D] FP16 into rows of KS halves, 16 bytes per copy.
+            constexpr int kChunks = D / 8;
+            const uint4* src = reinterpret_cast<const uint4*>(p.key_rotation + (int64_t)head * D * D);
 #pragma unroll
-            for (int i = 0; i < 8; ++i) rdst[i] = src[i];
-        } else {
+            for (int i = tid; i < D * kChunks; i += kThreads)
+                *reinterpret_cast<uint4*>(&r_k[(i / kChunks) * KS + 8 * (i % kChunks)]) = src[i];
+        } else if (part_active) {
 #pragma unroll
             for (int i = 0; i < 4; ++i)
                 *reinterpret_cast<float4*>(&q_raw[r * QRS + 16 * part + 4 * i]) =
@@ -331,7 +465,7 @@ void multirow_stream_kernel(MultiRowParams p) {
         }
     }
     __syncthreads();
-    if (p.key_rotation) {
+    if (p.key_rotation && wave < G::Quarters) {
         // q.R_k on the matrix cores: wave w takes columns 32 w .. 32 w + 31.
         // A: lane l reads scaled row l % 32 at k = 16 m + 8 (l / 32) .. + 7.
         // B: R_k[k][c] for column 32 w + l % 32 and the same k, read
@@ -347,7 +481,7 @@ void multirow_stream_kernel(MultiRowParams p) {
 #pragma unroll
         for (int e = 0; e < 16; ++e) c[e] = 0.f;
 #pragma unroll
-        for (int m = 0; m < D / 16; ++m) {
+        for (int m = 0; m < G::Parts; ++m) {
             const F16x8 a = *reinterpret_cast<const F16x8*>(&q16[column * KS + 16 * m + 8 * half]);
             const int k0 = 16 * m + k_half;
             const Short4 lo = read_transposed(&r_k[(k0 + (q16_lane >> 2)) * KS + c0 + 4 * (q16_lane & 3)]);
@@ -365,22 +499,24 @@ void multirow_stream_kernel(MultiRowParams p) {
     __syncthreads();
     {
         const int cb = tid & 31, rb = tid >> 5;  // columns 4 cb .. 4 cb + 3, rows 4 rb .. 4 rb + 3
+        const bool cb_active = 4 * cb < D;
         float acc[4][4];
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            const float4 v = *reinterpret_cast<const float4*>(&q_raw[(4 * rb + i) * QRS + 4 * cb]);
+            const float4 v = cb_active ? *reinterpret_cast<const float4*>(&q_raw[(4 * rb + i) * QRS + 4 * cb])
+                                       : make_float4(0.f, 0.f, 0.f, 0.f);
             acc[i][0] = v.x;
             acc[i][1] = v.y;
             acc[i][2] = v.z;
             acc[i][3] = v.w;
         }
-        const float scale = kLog2e * 0.08838834764831845f;  // log2(e) / sqrt(128)
+        const float scale = G::kScoreScale;
         float mu_a[4] = {0.f, 0.f, 0.f, 0.f}, mu_l[4] = {0.f, 0.f, 0.f, 0.f};
-        if (p.key_mean_anchor) {
+        if (Decoder::kAnchorMeanTerm && p.key_mean_anchor && cb_active) {
 #pragma unroll
             for (int j = 0; j < 4; ++j) mu_a[j] = round_bf16(p.key_mean_anchor[head * D + 4 * cb + j]);
         }
-        if (p.key_mean_loop) {
+        if (p.key_mean_loop && cb_active) {
 #pragma unroll
             for (int j = 0; j < 4; ++j) mu_l[j] = p.key_mean_loop[head * D + 4 * cb + j];
         }
@@ -418,8 +554,9 @@ void multirow_stream_kernel(MultiRowParams p) {
                 dot_a[i] = fmaf(q, mu_a[j], dot_a[i]);
                 dot_l[i] = fmaf(q, mu_l[j], dot_l[i]);
             }
-            *reinterpret_cast<uint2*>(&q_p[(4 * rb + i) * KS + 4 * cb]) =
-                make_uint2(bits[0] | (bits[1] << 16), bits[2] | (bits[3] << 16));
+            if (cb_active)
+                *reinterpret_cast<uint2*>(&q_p[(4 * rb + i) * KS + 4 * cb]) =
+                    make_uint2(bits[0] | (bits[1] << 16), bits[2] | (bits[3] << 16));
         }
         // Sum over the 32 lanes of this half-wave (the same four rows).
 #pragma unroll
@@ -440,9 +577,9 @@ void multirow_stream_kernel(MultiRowParams p) {
     }
     __syncthreads();
     // Q'^T operand (B of S^T = K Q'^T): chunk m holds channels 16 m + 8 half + e.
-    F16x8 q_operand[D / 16];
+    F16x8 q_operand[G::Parts];
 #pragma unroll
-    for (int m = 0; m < D / 16; ++m)
+    for (int m = 0; m < G::Parts; ++m)
         q_operand[m] = *reinterpret_cast<const F16x8*>(&q_p[column * KS + 16 * m + 8 * half]);
     const float q_mu_anchor = q_mu[column];
     const float row_scale = q_scale[column];
@@ -451,21 +588,26 @@ void multirow_stream_kernel(MultiRowParams p) {
     __syncthreads();  // the scratch becomes the tiles
 
     // ---------------------------------------------------------------- history
-    uint16_t* k_tile = reinterpret_cast<uint16_t*>(lds + wave * kWaveBytes);
-    uint16_t* v_tile = k_tile + kTile * KS;  // [token][D] BF16, chunk-swizzled rows
-    float* alpha_tile = reinterpret_cast<float*>(v_tile + D * VS);
+    uint16_t* k_tile = reinterpret_cast<uint16_t*>(lds + wave * G::kWaveBytes);
+    uint16_t* v_tile = k_tile + kTile * KS;  // [token][VROW] BF16
+    float* alpha_tile = reinterpret_cast<float*>(reinterpret_cast<uint8_t*>(v_tile) + G::kVBytes);
     // V^T operand reads (ds_read_b64_tr_b16): lane 16 g + 4 a + b (g = 2 half
     // + g') addresses token 4 half + a of an 8-token block, channels
-    // 32 t + 16 g' + 4 b..+3 (chunk 4 t + 2 g' + b / 2 at position
-    // chunk ^ 4 a), and receives channel 32 t + column of tokens 4 half..+3.
+    // 32 t + 16 g' + 4 b..+3, and receives channel 32 t + column of tokens
+    // 4 half..+3.  With the D = 128 swizzle, chunk 4 t + 2 g' + b / 2 sits at
+    // position chunk ^ 4 a.
     const int tr_a = (lane >> 2) & 3, tr_b = lane & 3, tr_g = (lane >> 4) & 1;
-    const int v_lane = D * (4 * half + tr_a) + 32 * tr_a + 16 * tr_g + 4 * tr_b;
-    auto v_read = [&](int t) __attribute__((always_inline)) { return v_lane ^ (32 * t); };
+    const int v_lane = G::kSwizzleV ? D * (4 * half + tr_a) + 32 * tr_a + 16 * tr_g + 4 * tr_b
+                                    : G::VROW * (4 * half + tr_a) + 16 * tr_g + 4 * tr_b;
+    auto v_read = [&](int t) __attribute__((always_inline)) {
+        return G::kSwizzleV ? v_lane ^ (32 * t) : v_lane + 32 * t;
+    };
     const int unit_token = lane >> 2;  // token within a 16-token unit
     const int quarter = lane & 3;      // 32-channel quarter
+    const bool quarter_active = quarter < G::Quarters;
     const uint32_t page_bytes = (uint32_t)(PT * p.page_width);
     const int pages = (history + PT - 1) / PT;
-    const bool mean_anchor = HasL && p.key_mean_anchor != nullptr;
+    const bool mean_anchor = Decoder::kAnchorMeanTerm && p.key_mean_anchor != nullptr;
 
     // The split's block ids, once, into LDS (-1 past the history or when invalid).
     const int first_page = tile_begin * kTile / PT;
@@ -478,9 +620,8 @@ void multirow_stream_kernel(MultiRowParams p) {
     }
     __syncthreads();
 
-    // Loads of one 16-token unit's bytes into registers (zeros past the history).
-    auto fetch = [&](int unit_first, UnitBytes<BA, BL>& b) {
-        const int row = unit_first % PT + unit_token;
+    // The page resources of one 16-token unit (empty past the history).
+    auto unit_pages = [&](int unit_first) __attribute__((always_inline)) {
         const int index = unit_first / PT - first_page;
         // One unit per wave: the block id is wave-uniform, and readfirstlane
         // keeps the page resources in SGPRs (no waterfall loop per load).
@@ -488,65 +629,56 @@ void multirow_stream_kernel(MultiRowParams p) {
             (unit_first < history && index < split_pages) ? split_blocks[index] : -1);
         const uint8_t* k_page = p.cache + ((int64_t)(block >= 0 ? block : 0) * p.heads + head) * page_bytes;
         const uint32_t bytes = block >= 0 ? page_bytes : 0u;
-        const auto k_rsrc = page_rsrc(k_page, bytes);
-        const auto v_rsrc = page_rsrc(k_page + p.plane_stride, bytes);
-        load_record<BA>(k_rsrc, p.anchor, PT, row, quarter, false, b.ka);
-        load_record<BA>(v_rsrc, p.anchor, PT, row, quarter, false, b.va);
-        if constexpr (HasL) {
-            load_record<BL>(k_rsrc, p.residual, PT, row, quarter, true, b.kl);
-            load_record<BL>(v_rsrc, p.residual, PT, row, quarter, true, b.vl);
-        }
+        return UnitPages{page_rsrc(k_page, bytes), page_rsrc(k_page + p.plane_stride, bytes),
+                         unit_first % PT + unit_token};
     };
 
-    F32x16 out[D / 32];
+    F32x16 out[G::Quarters];
 #pragma unroll
-    for (int t = 0; t < D / 32; ++t)
+    for (int t = 0; t < G::Quarters; ++t)
 #pragma unroll
         for (int r = 0; r < 16; ++r) out[t][r] = 0.f;
     float running_max = -__builtin_inff();
     float running_sum = 0.f;
 
-    // Units stream two ahead: a wave's units are the two halves of its
-    // tiles tile_begin + wave + kWaves k, and the loads of the unit two
-    // places on are issued before a unit is dequantized, so about two units'
-    // bytes per wave are in flight while units dequantize and the tiles'
-    // MFMAs run.  The fetches carry no condition (units past the split read
+    // A wave's units are the two halves of its tiles tile_begin + wave +
+    // kWaves k.  The fetches carry no condition (units past the split read
     // zeros through an empty resource), which keeps the compiler's count of
     // loads in flight exact.
     const int first_tile = tile_begin + wave;
-    UnitBytes<BA, BL> ahead1, ahead2;
-    fetch(kTile * first_tile, ahead1);
-    fetch(kTile * first_tile + 16, ahead2);
+    dec.prime(unit_pages(kTile * first_tile), unit_pages(kTile * first_tile + 16));
     for (int tile = first_tile; tile < tile_end; tile += kWaves) {
 #pragma unroll
         for (int u = 0; u < 2; ++u) {
-            const UnitBytes<BA, BL> cur = ahead1;
-            ahead1 = ahead2;
-            fetch(kTile * (tile + kWaves) + 16 * u, ahead2);
             const int local = 16 * u + unit_token;
-            // K, then V, so that only one plane's values are live at a time.
             const bool valid = kTile * tile + local < history;
             // Whole unit inside the history (wave-uniform): nothing to mask.
             const bool unit_valid = kTile * tile + 16 * u + 16 <= history;
-            const float alpha_k = HasL ? bf16_f32(cur.kl.alpha) : 1.f;
-            {
-                float k[32];
-                plane_values<BA, GA, BL, GL, HasL>(cur.ka, cur.kl, alpha_k, k);
+            // The unit after this one, and the one after that.
+            const int next_first = u == 0 ? kTile * tile + 16 : kTile * (tile + kWaves);
+            const int two_on_first = kTile * (tile + kWaves) + 16 * u;
+            auto store_k = [&](const float* lo, const float* hi) __attribute__((always_inline)) {
                 uint32_t kw[16];
-#pragma unroll
                 // No mask: the scores of tokens past the history become -inf below.
-                for (int c = 0; c < 16; ++c) kw[c] = pack_f16(k[2 * c], k[2 * c + 1]);
-                uint4* k_dst = reinterpret_cast<uint4*>(&k_tile[local * KS + 32 * quarter]);
 #pragma unroll
-                for (int c = 0; c < 4; ++c)
-                    k_dst[c] = make_uint4(kw[4 * c], kw[4 * c + 1], kw[4 * c + 2], kw[4 * c + 3]);
-            }
-            {
-                float v[32];
-                plane_values<BA, GA, BL, GL, HasL>(cur.va, cur.vl, HasL ? bf16_f32(cur.vl.alpha) : 1.f, v);
+                for (int c = 0; c < 8; ++c) {
+                    kw[c] = pack_f16(lo[2 * c], lo[2 * c + 1]);
+                    kw[8 + c] = pack_f16(hi[2 * c], hi[2 * c + 1]);
+                }
+                if (quarter_active) {
+                    uint4* k_dst = reinterpret_cast<uint4*>(&k_tile[local * KS + 32 * quarter]);
+#pragma unroll
+                    for (int c = 0; c < 4; ++c)
+                        k_dst[c] = make_uint4(kw[4 * c], kw[4 * c + 1], kw[4 * c + 2], kw[4 * c + 3]);
+                }
+            };
+            auto store_v = [&](const float* lo, const float* hi) __attribute__((always_inline)) {
                 uint32_t vw[16];
 #pragma unroll
-                for (int c = 0; c < 16; ++c) vw[c] = pack_bf16(v[2 * c], v[2 * c + 1]);
+                for (int c = 0; c < 8; ++c) {
+                    vw[c] = pack_bf16(lo[2 * c], lo[2 * c + 1]);
+                    vw[8 + c] = pack_bf16(hi[2 * c], hi[2 * c + 1]);
+                }
                 // Slots past the history may hold any bytes (P is zero there,
                 // but 0 x NaN is not): zero them in a unit that reaches past it.
                 if (!unit_valid) {
@@ -554,13 +686,17 @@ void multirow_stream_kernel(MultiRowParams p) {
 #pragma unroll
                     for (int c = 0; c < 16; ++c) vw[c] = valid ? vw[c] : 0u;
                 }
-                // Row-major V: the lane's 4 chunks of 8 channels at chunk
-                // positions 4 (quarter ^ (token % 4)) + i of the token's row.
-                uint4* v_dst = reinterpret_cast<uint4*>(&v_tile[local * D + 32 * (quarter ^ (local & 3))]);
+                if (quarter_active) {
+                    // Row-major V: the lane's 4 chunks of 8 channels (at D =
+                    // 128 at chunk positions 4 (quarter ^ (token % 4)) + i).
+                    const int chunk = G::kSwizzleV ? (quarter ^ (local & 3)) : quarter;
+                    uint4* v_dst = reinterpret_cast<uint4*>(&v_tile[local * G::VROW + 32 * chunk]);
 #pragma unroll
-                for (int c = 0; c < 4; ++c)
-                    v_dst[c] = make_uint4(vw[4 * c], vw[4 * c + 1], vw[4 * c + 2], vw[4 * c + 3]);
-            }
+                    for (int c = 0; c < 4; ++c)
+                        v_dst[c] = make_uint4(vw[4 * c], vw[4 * c + 1], vw[4 * c + 2], vw[4 * c + 3]);
+                }
+            };
+            const float alpha_k = dec.unit(unit_pages(next_first), unit_pages(two_on_first), store_k, store_v);
             if (quarter == 0) alpha_tile[local] = alpha_k;
         }
         wave_sync();
@@ -575,7 +711,8 @@ void multirow_stream_kernel(MultiRowParams p) {
         for (int r = 0; r < 16; ++r) s[r] = 0.f;
         const uint16_t* k_row = &k_tile[column * KS + 8 * half];
 #pragma unroll
-        for (int m = 0; m < D / 16; ++m) s = mfma(*reinterpret_cast<const F16x8*>(k_row + 16 * m), q_operand[m], s);
+        for (int m = 0; m < G::Parts; ++m)
+            s = mfma(*reinterpret_cast<const F16x8*>(k_row + 16 * m), q_operand[m], s);
 
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
@@ -616,18 +753,18 @@ void multirow_stream_kernel(MultiRowParams p) {
         running_sum = running_sum * rescale + tile_sum;
         if (!__all(rescale == 1.0f)) {
 #pragma unroll
-            for (int t = 0; t < D / 32; ++t)
+            for (int t = 0; t < G::Quarters; ++t)
 #pragma unroll
                 for (int r = 0; r < 16; ++r) out[t][r] *= rescale;
         }
 #pragma unroll
         for (int j = 0; j < 2; ++j) {
-            const uint16_t* v_rows = v_tile + 16 * j * D;
+            const uint16_t* v_rows = v_tile + 16 * j * G::VROW;
 #pragma unroll
-            for (int t = 0; t < D / 32; ++t) {
+            for (int t = 0; t < G::Quarters; ++t) {
                 // Tokens 4 half + 0..3 and 4 half + 8..11 of the 16, as P^T's k-slots.
                 const Short4 lo = read_transposed(v_rows + v_read(t));
-                const Short4 hi = read_transposed(v_rows + 8 * D + v_read(t));
+                const Short4 hi = read_transposed(v_rows + 8 * G::VROW + v_read(t));
                 out[t] = mfma(__builtin_bit_cast(Bf16x8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7)),
                               p_operand[j], out[t]);
             }
@@ -638,10 +775,11 @@ void multirow_stream_kernel(MultiRowParams p) {
 
     // ---------------------------------------------------------------- wave merge
     __syncthreads();  // the merge buffer aliases every wave's tiles
+    constexpr int MS = G::MS;
     float* merge_o = reinterpret_cast<float*>(lds);
-    float* merge_ml = reinterpret_cast<float*>(lds + kMlOffset);
+    float* merge_ml = reinterpret_cast<float*>(lds + G::kMlOffset);
 #pragma unroll
-    for (int t = 0; t < D / 32; ++t)
+    for (int t = 0; t < G::Quarters; ++t)
 #pragma unroll
         for (int g = 0; g < 4; ++g)
             *reinterpret_cast<float4*>(&merge_o[(wave * 32 + column) * MS + 32 * t + 8 * g + 4 * half]) =
@@ -663,12 +801,13 @@ void multirow_stream_kernel(MultiRowParams p) {
         float o[16];
 #pragma unroll
         for (int c = 0; c < 16; ++c) o[c] = 0.f;
+        const bool chunk_active = chunk < G::Parts;
 #pragma unroll
         for (int w = 0; w < kWaves; ++w) {
             if (m_w[w] == -__builtin_inff()) continue;
             const float weight = __builtin_amdgcn_exp2f(m_w[w] - total_max);
             l = fmaf(merge_ml[(w * 32 + r) * 2 + 1], weight, l);
-            const float* src = &merge_o[(w * 32 + r) * MS + 16 * chunk];
+            const float* src = &merge_o[(w * 32 + r) * MS + 16 * (chunk_active ? chunk : 0)];
 #pragma unroll
             for (int c = 0; c < 16; ++c) o[c] = fmaf(src[c], weight, o[c]);
         }
@@ -676,20 +815,74 @@ void multirow_stream_kernel(MultiRowParams p) {
             float* entry = p.partials +
                            (((int64_t)(first + row0 + r) * p.heads + head) * p.splits + split) * kMultiRowEntry;
             if (chunk == 0) *reinterpret_cast<float4*>(entry) = make_float4(total_max, l, 0.f, 0.f);
-            float4* dst = reinterpret_cast<float4*>(entry + 4 + 16 * chunk);
+            if (chunk_active) {
+                float4* dst = reinterpret_cast<float4*>(entry + 4 + 16 * chunk);
 #pragma unroll
-            for (int c = 0; c < 4; ++c) dst[c] = make_float4(o[4 * c], o[4 * c + 1], o[4 * c + 2], o[4 * c + 3]);
+                for (int c = 0; c < 4; ++c) dst[c] = make_float4(o[4 * c], o[4 * c + 1], o[4 * c + 2], o[4 * c + 3]);
+            }
         }
     }
 }
 
+template <int D, int PT, bool HasL, int BA, int GA, int BL, int GL>
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2)))
+void multirow_stream_kernel(MultiRowParams p) {
+    __shared__ __attribute__((aligned(16))) uint8_t lds[Geometry<D>::kLdsBytes];
+    __shared__ int split_blocks[kMaxSplitPages];  // block ids of the split's pages
+    AnchorDecoder<PT, HasL, BA, GA, BL, GL> dec;
+    dec.anchor = p.anchor;
+    dec.residual = p.residual;
+    const int quarter = threadIdx.x & 3;
+    dec.lq = quarter < Geometry<D>::Quarters ? quarter : 0;
+    multirow_stream<D, PT>(p, dec, lds, split_blocks);
+}
+
+template <int D, int PT, int Links>
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2)))
+void multirow_chain_kernel(MultiRowParams p) {
+    __shared__ __attribute__((aligned(16))) uint8_t lds[Geometry<D>::kLdsBytes];
+    __shared__ int split_blocks[kMaxSplitPages];  // block ids of the split's pages
+    // bf16(mu_r) of records 0 .. L - 1 (the K plane's chain), FP32.
+    __shared__ __attribute__((aligned(16))) float mean_lds[Links - 1][kMaxD];
+    const int head = blockIdx.y;
+    const bool has_mean = p.key_mean_all != nullptr;
+    for (int i = threadIdx.x; i < (Links - 1) * kMaxD; i += kThreads) {
+        const int r = i / kMaxD, c = i % kMaxD;
+        mean_lds[r][c] = (has_mean && c < D) ? bf16_f32(bf16_rn(p.key_mean_all[((int64_t)r * p.heads + head) * D + c]))
+                                             : 0.f;
+    }
+    // (The stream's first barrier orders these stores before any read.)
+    ChainDecoder<D, PT, Links> dec;
+#pragma unroll
+    for (int r = 0; r < Links; ++r) dec.regs[r] = p.chain[r];
+    dec.mean = &mean_lds[0][0];
+    dec.add_mean = has_mean;
+    const int quarter = threadIdx.x & 3;
+    dec.lq = quarter < Geometry<D>::Quarters ? quarter : 0;
+    // The pairs (1, 0) and (0, 1) of the mean add, in registers.
+    uint32_t pick_lo = 0x00003f80u, pick_hi = 0x3f800000u;
+    asm("" : "+v"(pick_lo), "+v"(pick_hi));
+    dec.pick_lo = pick_lo;
+    dec.pick_hi = pick_hi;
+    multirow_stream<D, PT>(p, dec, lds, split_blocks);
+}
+
 // ---------------------------------------------------------------- finish
 
-// Row strides of the finish kernel's tiles: BF16/FP16 rows (halves) and the
-// rotated history [row][channel] (FP32); region B holds D x HS floats.
-constexpr int FS = D + 8;
-constexpr int HS = 36;
-constexpr int OS = D + 4;
+// Row strides of the finish kernel's tiles for head dim D: BF16/FP16 rows
+// (halves) and the rotated history [row][channel] (FP32).  Region A holds
+// the merged rows' FP16 parts for the rotation, then the causal tiles;
+// region B the rotated history.
+template <int D>
+struct FinishGeometry {
+    static constexpr int Parts = D / 16;
+    static constexpr int FS = D + 8;
+    static constexpr int OS = D + 4;
+    static constexpr int kRotationBytes = 2 * 32 * FS * 2;                  // high and low FP16 parts
+    static constexpr int kCausalBytes = 3 * 32 * FS * 2 + 32 * 33 * 4;     // q, k, v tiles and probabilities
+    static constexpr int kRegionABytes = kRotationBytes > kCausalBytes ? kRotationBytes : kCausalBytes;
+    static constexpr int kRegionBFloats = 32 * OS;
+};
 
 __device__ __forceinline__ float row8_max(float x) {
     x = fmaxf(x, __shfl_xor(x, 1));
@@ -738,22 +931,22 @@ __device__ __forceinline__ void widen_bf16(uint4 w, float* x) {
 // One (request, head, 32-row tile) per 256-thread workgroup.  Thread t takes
 // row t / 8 of the tile and part p = t % 8 of it: the 16 channels
 // 16p..16p+15 of the merge, the query-key dots, the live values and the
-// output, and the 4 tokens 4p..4p+3 of a live chunk's scores.  The eight
-// threads of a row are adjacent lanes of one wave.
+// output (parts p < D / 16), and the 4 tokens 4p..4p+3 of a live chunk's
+// scores.  The eight threads of a row are adjacent lanes of one wave.
 //   1. merge the splits' partials (m, l, O) of each row (log2 units);
-//   2. rotate the tile's 32 merged rows by R_v^T at once (R_v staged
-//      transposed in LDS, read once per tile; 4 rows x 4 channels per thread);
+//   2. rotate the tile's 32 merged rows by R_v^T on the matrix cores (wave w
+//      computes output channels 32 w .. 32 w + 31);
 //   3. add the live tokens: in decode semantics the row's own token; in
 //      causal semantics the request's new tokens j <= row, 32 at a time with
 //      an online softmax over the rows' (m, l, O);
 //   4. write O / l in BF16.
+template <int D>
 __global__ __launch_bounds__(kThreads) void multirow_finish_kernel(MultiRowParams p) {
-    // Region A holds the merged rows' FP16 parts [r][j] for the rotation,
-    // then the causal tiles; region B the rotated history [r][c] (FP32).
-    __shared__ __attribute__((aligned(16))) uint8_t region_a[D * FS * 2];
-    __shared__ __attribute__((aligned(16))) float region_b[D * HS];
-    static_assert(32 * OS <= D * HS, "the rotated history fits region B");
-    static_assert(3 * 32 * FS * 2 + 32 * 33 * 4 <= D * FS * 2, "the causal tiles fit region A");
+    using G = FinishGeometry<D>;
+    constexpr int FS = G::FS;
+    constexpr int OS = G::OS;
+    __shared__ __attribute__((aligned(16))) uint8_t region_a[G::kRegionABytes];
+    __shared__ __attribute__((aligned(16))) float region_b[G::kRegionBFloats];
     float* hist_rot = region_b;
     uint16_t* q_tile = reinterpret_cast<uint16_t*>(region_a);  // causal: the rows' queries
     uint16_t* k_tile = q_tile + 32 * FS;                      // causal: 32 live keys
@@ -764,19 +957,21 @@ __global__ __launch_bounds__(kThreads) void multirow_finish_kernel(MultiRowParam
     const int row0 = 32 * (int)blockIdx.z;
     const int tid = threadIdx.x;
     const int r = tid >> 3, part = tid & 7;
+    const bool part_active = part < G::Parts;
     const bool rotate = p.value_rotation != nullptr;
+    const int wave = tid >> 6;
+    const bool rotation_wave = wave < D / 32;
 
     // R_v as the B operand of the rotation MFMAs (16-byte loads issued
     // before the request lookup, so that the two round trips overlap): wave
     // w computes output channels 32 w .. 32 w + 31, lane l takes row
     // 32 w + l % 32 of R_v at features 16 m + 8 (l / 32) .. + 7.
     const int lane = tid & 63;
-    F16x8 rv[D / 16];
-    if (rotate) {
-        const uint16_t* src =
-            p.value_rotation + ((int64_t)head * D + 32 * (tid >> 6) + (lane & 31)) * D + 8 * (lane >> 5);
+    F16x8 rv[G::Parts];
+    if (rotate && rotation_wave) {
+        const uint16_t* src = p.value_rotation + ((int64_t)head * D + 32 * wave + (lane & 31)) * D + 8 * (lane >> 5);
 #pragma unroll
-        for (int m = 0; m < D / 16; ++m) rv[m] = *reinterpret_cast<const F16x8*>(src + 16 * m);
+        for (int m = 0; m < G::Parts; ++m) rv[m] = *reinterpret_cast<const F16x8*>(src + 16 * m);
     }
     const int first = p.query_start_loc[request];
     int n = p.query_start_loc[request + 1] - first;
@@ -786,14 +981,17 @@ __global__ __launch_bounds__(kThreads) void multirow_finish_kernel(MultiRowParam
 
     const bool valid = row0 + r < n;
     const int64_t row = (int64_t)first + row0 + (valid ? r : 0);
-    const float scale = kLog2e * 0.08838834764831845f;  // log2(e) / sqrt(128)
-    const int64_t channels = (int64_t)head * D + 16 * part;  // the part's 16 channels of a token row
+    const float scale = Geometry<D>::kScoreScale;  // log2(e) / sqrt(D)
+    // The part's 16 channels of a token row (part 0's for an inactive part,
+    // whose values are never used).
+    const int64_t channels = (int64_t)head * D + 16 * (part_active ? part : 0);
 
     // The row's query (and, in decode semantics, its own key and value).
     const bool q_vec = aligned_rows(p.query, p.query_stride), k_vec = aligned_rows(p.key, p.key_stride),
                v_vec = aligned_rows(p.value, p.value_stride);
     uint4 qw[2], kw[2], vw[2];
     load_halves16(p.query + row * p.query_stride + channels, q_vec, qw);
+    if (!part_active) qw[0] = qw[1] = make_uint4(0u, 0u, 0u, 0u);  // no share of the row's dots
     if (!p.causal) {
         load_halves16(p.key + row * p.key_stride + channels, k_vec, kw);
         load_halves16(p.value + row * p.value_stride + channels, v_vec, vw);
@@ -808,6 +1006,7 @@ __global__ __launch_bounds__(kThreads) void multirow_finish_kernel(MultiRowParam
 #pragma unroll
     for (int i = 0; i < 16; ++i) acc[i] = 0.f;
     const float* entries = p.partials + (row * p.heads + head) * p.splits * kMultiRowEntry;
+    const int entry_part = part_active ? part : 0;
     for (int s0 = 0; s0 < p.splits; s0 += 4) {
         float2 ml[4];
         float4 ox[4][4];
@@ -817,7 +1016,7 @@ __global__ __launch_bounds__(kThreads) void multirow_finish_kernel(MultiRowParam
             const float* e = entries + s * kMultiRowEntry;
             ml[b] = *reinterpret_cast<const float2*>(e);
 #pragma unroll
-            for (int c = 0; c < 4; ++c) ox[b][c] = reinterpret_cast<const float4*>(e + 4 + 16 * part)[c];
+            for (int c = 0; c < 4; ++c) ox[b][c] = reinterpret_cast<const float4*>(e + 4 + 16 * entry_part)[c];
         }
 #pragma unroll
         for (int b = 0; b < 4; ++b) {
@@ -852,35 +1051,41 @@ __global__ __launch_bounds__(kThreads) void multirow_finish_kernel(MultiRowParam
             hw[i] = (uint32_t)__builtin_bit_cast(uint16_t, h0) | ((uint32_t)__builtin_bit_cast(uint16_t, h1) << 16);
             lw[i] = (uint32_t)__builtin_bit_cast(uint16_t, r0) | ((uint32_t)__builtin_bit_cast(uint16_t, r1) << 16);
         }
-        uint4* hd = reinterpret_cast<uint4*>(&high[r * FS + 16 * part]);
-        uint4* ld = reinterpret_cast<uint4*>(&low[r * FS + 16 * part]);
-        hd[0] = make_uint4(hw[0], hw[1], hw[2], hw[3]);
-        hd[1] = make_uint4(hw[4], hw[5], hw[6], hw[7]);
-        ld[0] = make_uint4(lw[0], lw[1], lw[2], lw[3]);
-        ld[1] = make_uint4(lw[4], lw[5], lw[6], lw[7]);
-        __syncthreads();
-        // A operand: lane l takes merged row l % 32 at features 16 m + 8 (l / 32) .. + 7.
-        F32x16 rotated;
-#pragma unroll
-        for (int e = 0; e < 16; ++e) rotated[e] = 0.f;
-        const int a_offset = (lane & 31) * FS + 8 * (lane >> 5);
-#pragma unroll
-        for (int m = 0; m < D / 16; ++m) {
-            rotated = mfma(*reinterpret_cast<const F16x8*>(&high[a_offset + 16 * m]), rv[m], rotated);
-            rotated = mfma(*reinterpret_cast<const F16x8*>(&low[a_offset + 16 * m]), rv[m], rotated);
+        if (part_active) {
+            uint4* hd = reinterpret_cast<uint4*>(&high[r * FS + 16 * part]);
+            uint4* ld = reinterpret_cast<uint4*>(&low[r * FS + 16 * part]);
+            hd[0] = make_uint4(hw[0], hw[1], hw[2], hw[3]);
+            hd[1] = make_uint4(hw[4], hw[5], hw[6], hw[7]);
+            ld[0] = make_uint4(lw[0], lw[1], lw[2], lw[3]);
+            ld[1] = make_uint4(lw[4], lw[5], lw[6], lw[7]);
         }
-        // Register e of lane l: row 8 (e / 4) + 4 (l / 32) + e % 4, channel 32 w + l % 32.
-#pragma unroll
-        for (int e = 0; e < 16; ++e)
-            hist_rot[(8 * (e >> 2) + 4 * (lane >> 5) + (e & 3)) * OS + 32 * (tid >> 6) + (lane & 31)] = rotated[e];
         __syncthreads();
+        if (rotation_wave) {
+            // A operand: lane l takes merged row l % 32 at features 16 m + 8 (l / 32) .. + 7.
+            F32x16 rotated;
 #pragma unroll
-        for (int c4 = 0; c4 < 4; ++c4) {
-            const float4 x = *reinterpret_cast<const float4*>(&hist_rot[r * OS + 16 * part + 4 * c4]);
-            acc[4 * c4] = x.x * l;
-            acc[4 * c4 + 1] = x.y * l;
-            acc[4 * c4 + 2] = x.z * l;
-            acc[4 * c4 + 3] = x.w * l;
+            for (int e = 0; e < 16; ++e) rotated[e] = 0.f;
+            const int a_offset = (lane & 31) * FS + 8 * (lane >> 5);
+#pragma unroll
+            for (int mm = 0; mm < G::Parts; ++mm) {
+                rotated = mfma(*reinterpret_cast<const F16x8*>(&high[a_offset + 16 * mm]), rv[mm], rotated);
+                rotated = mfma(*reinterpret_cast<const F16x8*>(&low[a_offset + 16 * mm]), rv[mm], rotated);
+            }
+            // Register e of lane l: row 8 (e / 4) + 4 (l / 32) + e % 4, channel 32 w + l % 32.
+#pragma unroll
+            for (int e = 0; e < 16; ++e)
+                hist_rot[(8 * (e >> 2) + 4 * (lane >> 5) + (e & 3)) * OS + 32 * wave + (lane & 31)] = rotated[e];
+        }
+        __syncthreads();
+        if (part_active) {
+#pragma unroll
+            for (int c4 = 0; c4 < 4; ++c4) {
+                const float4 x = *reinterpret_cast<const float4*>(&hist_rot[r * OS + 16 * part + 4 * c4]);
+                acc[4 * c4] = x.x * l;
+                acc[4 * c4 + 1] = x.y * l;
+                acc[4 * c4 + 2] = x.z * l;
+                acc[4 * c4 + 3] = x.w * l;
+            }
         }
     }
 
@@ -907,7 +1112,7 @@ __global__ __launch_bounds__(kThreads) void multirow_finish_kernel(MultiRowParam
         for (int i = 0; i < 16; ++i) acc[i] = fmaf(live, v[i], acc[i] * hist_weight);
     } else {
         // The request's new tokens 0 .. row0 + r, in chunks of 32 shared by the tile's rows.
-        {
+        if (part_active) {
             uint4* dst = reinterpret_cast<uint4*>(&q_tile[r * FS + 16 * part]);
             dst[0] = qw[0];
             dst[1] = qw[1];
@@ -915,7 +1120,7 @@ __global__ __launch_bounds__(kThreads) void multirow_finish_kernel(MultiRowParam
         const int live_end = n < row0 + 32 ? n : row0 + 32;
         for (int c0 = 0; c0 < live_end; c0 += 32) {
             __syncthreads();  // the previous chunk's reads are done
-            {
+            if (part_active) {
                 // Thread (r, part) stages the part's channels of live token c0 + r.
                 const int j = c0 + r;
                 uint4 kx[2] = {make_uint4(0u, 0u, 0u, 0u), make_uint4(0u, 0u, 0u, 0u)}, vx[2] = {kx[0], kx[1]};
@@ -967,20 +1172,22 @@ __global__ __launch_bounds__(kThreads) void multirow_finish_kernel(MultiRowParam
 #pragma unroll
             for (int i = 0; i < 16; ++i) acc[i] *= rescale;
             wave_sync();  // row r's probabilities come from lanes of this wave
+            if (part_active) {
 #pragma unroll 4
-            for (int jj = 0; jj < 32; ++jj) {
-                const float w = probs[r * 33 + jj];
-                float vd[16];
-                widen_bf16(*reinterpret_cast<const uint4*>(&v_tile[jj * FS + 16 * part]), vd);
-                widen_bf16(*reinterpret_cast<const uint4*>(&v_tile[jj * FS + 16 * part + 8]), vd + 8);
+                for (int jj = 0; jj < 32; ++jj) {
+                    const float w = probs[r * 33 + jj];
+                    float vd[16];
+                    widen_bf16(*reinterpret_cast<const uint4*>(&v_tile[jj * FS + 16 * part]), vd);
+                    widen_bf16(*reinterpret_cast<const uint4*>(&v_tile[jj * FS + 16 * part + 8]), vd + 8);
 #pragma unroll
-                for (int i = 0; i < 16; ++i) acc[i] = fmaf(w, vd[i], acc[i]);
+                    for (int i = 0; i < 16; ++i) acc[i] = fmaf(w, vd[i], acc[i]);
+                }
             }
         }
     }
 
     // 4. Output.
-    if (valid) {
+    if (valid && part_active) {
         uint32_t w[8];
 #pragma unroll
         for (int i = 0; i < 8; ++i) w[i] = bf16_rn(acc[2 * i] / l) | (bf16_rn(acc[2 * i + 1] / l) << 16);
@@ -998,58 +1205,79 @@ __global__ __launch_bounds__(kThreads) void multirow_finish_kernel(MultiRowParam
     }
 }
 
-template <int PT, bool HasL, int BA, int GA, int BL, int GL>
+template <int D, int PT, bool HasL, int BA, int GA, int BL, int GL>
 void launch_one(const MultiRowParams& p, hipStream_t stream) {
     const dim3 grid((unsigned)p.requests, (unsigned)p.heads, (unsigned)(p.splits * p.row_tiles));
-    hipLaunchKernelGGL((multirow_stream_kernel<PT, HasL, BA, GA, BL, GL>), grid, dim3(kThreads), 0, stream, p);
+    hipLaunchKernelGGL((multirow_stream_kernel<D, PT, HasL, BA, GA, BL, GL>), grid, dim3(kThreads), 0, stream, p);
 }
 
-template <int PT, int BA, int GA, int BL>
+template <int D, int PT, int BA, int GA, int BL>
 void launch_residual_group(const MultiRowParams& p, hipStream_t stream) {
     if (p.residual.group == 32)
-        launch_one<PT, true, BA, GA, BL, 32>(p, stream);
+        launch_one<D, PT, true, BA, GA, BL, 32>(p, stream);
     else
-        launch_one<PT, true, BA, GA, BL, 16>(p, stream);
+        launch_one<D, PT, true, BA, GA, BL, 16>(p, stream);
 }
 
-template <int PT, int BA, int GA>
+template <int D, int PT, int BA, int GA>
 void launch_anchor(const MultiRowParams& p, hipStream_t stream) {
     if (!p.has_residual)
-        launch_one<PT, false, BA, GA, 2, 32>(p, stream);
+        launch_one<D, PT, false, BA, GA, 2, 32>(p, stream);
     else if (p.residual.bits == 2)
-        launch_residual_group<PT, BA, GA, 2>(p, stream);
+        launch_residual_group<D, PT, BA, GA, 2>(p, stream);
     else
-        launch_residual_group<PT, BA, GA, 4>(p, stream);
+        launch_residual_group<D, PT, BA, GA, 4>(p, stream);
 }
 
-template <int PT, int BA>
+template <int D, int PT, int BA>
 void launch_anchor_group(const MultiRowParams& p, hipStream_t stream) {
     if (p.anchor.group == 32)
-        launch_anchor<PT, BA, 32>(p, stream);
+        launch_anchor<D, PT, BA, 32>(p, stream);
     else
-        launch_anchor<PT, BA, 16>(p, stream);
+        launch_anchor<D, PT, BA, 16>(p, stream);
 }
 
-template <int PT>
-void launch_pt(const MultiRowParams& p, hipStream_t stream) {
+template <int D, int PT>
+bool launch_pt(const MultiRowParams& p, hipStream_t stream) {
+    if (p.chain_length > 1) {
+        const dim3 grid((unsigned)p.requests, (unsigned)p.heads, (unsigned)(p.splits * p.row_tiles));
+        switch (p.chain_length) {
+            case 2: hipLaunchKernelGGL((multirow_chain_kernel<D, PT, 2>), grid, dim3(kThreads), 0, stream, p); return true;
+            case 3: hipLaunchKernelGGL((multirow_chain_kernel<D, PT, 3>), grid, dim3(kThreads), 0, stream, p); return true;
+            case 4: hipLaunchKernelGGL((multirow_chain_kernel<D, PT, 4>), grid, dim3(kThreads), 0, stream, p); return true;
+            default: return false;
+        }
+    }
     if (p.anchor.bits == 4)
-        launch_anchor_group<PT, 4>(p, stream);
+        launch_anchor_group<D, PT, 4>(p, stream);
     else
-        launch_anchor_group<PT, 2>(p, stream);
+        launch_anchor_group<D, PT, 2>(p, stream);
+    return true;
+}
+
+template <int D>
+bool launch_d(const MultiRowParams& p, hipStream_t stream) {
+    bool launched = false;
+    if (p.page_tokens == 16)
+        launched = launch_pt<D, 16>(p, stream);
+    else if (p.page_tokens == 32)
+        launched = launch_pt<D, 32>(p, stream);
+    if (!launched) return false;
+    hipLaunchKernelGGL(multirow_finish_kernel<D>, dim3((unsigned)p.requests, (unsigned)p.heads, (unsigned)p.row_tiles),
+                       dim3(kThreads), 0, stream, p);
+    return true;
 }
 
 }  // namespace
 
 hipError_t launch_multirow(const MultiRowParams& p, hipStream_t stream) {
     if (p.rows == 0 || p.requests == 0) return hipSuccess;
-    if (p.page_tokens == 16)
-        launch_pt<16>(p, stream);
-    else if (p.page_tokens == 32)
-        launch_pt<32>(p, stream);
-    else
-        return hipErrorInvalidValue;
-    hipLaunchKernelGGL(multirow_finish_kernel, dim3((unsigned)p.requests, (unsigned)p.heads, (unsigned)p.row_tiles),
-                       dim3(kThreads), 0, stream, p);
+    bool launched = false;
+    if (p.head_dim == 128)
+        launched = launch_d<128>(p, stream);
+    else if (p.head_dim == 96)
+        launched = launch_d<96>(p, stream);
+    if (!launched) return hipErrorInvalidValue;
     return hipGetLastError();
 }
 

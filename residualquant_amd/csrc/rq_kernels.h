@@ -180,14 +180,15 @@ struct AttentionParams {
 hipError_t launch_attention(const AttentionParams& p, hipStream_t stream, hipEvent_t begin,
                             hipEvent_t end);
 
-// Several query rows per request over packed pages (anchor mode, D = 128):
-// one workgroup per (request, head, row tile of 32 rows, history split)
-// streams the split's pages once for all the tile's rows on MFMA tiles, then
-// a finish launch per (row, head) merges the splits, applies R_v^T and adds
-// the live tokens.  causal = 0: the reference decode semantics (history
-// seq_len - 1, the row's own live token); causal = 1: the rows are the
-// request's last n tokens (history seq_len - n, live tokens j <= r).
-constexpr int kMultiRowEntry = 132;        // per (row, head, split): m, l, 2 unused, O[128] (log2 units)
+// Several query rows per request over packed pages (D = 96 or 128, anchor
+// and adjacent mode): one workgroup per (request, head, row tile of 32 rows,
+// history split) streams the split's pages once for all the tile's rows on
+// MFMA tiles, then a finish launch per (row, head) merges the splits,
+// applies R_v^T and adds the live tokens.  causal = 0: the reference decode
+// semantics (history seq_len - 1, the row's own live token); causal = 1: the
+// rows are the request's last n tokens (history seq_len - n, live tokens
+// j <= r).
+constexpr int kMultiRowEntry = 132;        // per (row, head, split): m, l, 2 unused, O[D <= 128] (log2 units)
 constexpr int kMultiRowMaxSplits = 8;      // for parallelism (more only for very long histories)
 constexpr int kMultiRowMaxSplitPages = 1024;  // pages of one split at most
 struct MultiRowParams {
@@ -201,6 +202,7 @@ struct MultiRowParams {
     int64_t output_stride;
     int64_t rows;
     int heads;
+    int head_dim;  // 96 or 128
     const uint8_t* cache;
     int64_t plane_stride;
     int64_t num_blocks;
@@ -215,10 +217,16 @@ struct MultiRowParams {
     const uint16_t* key_rotation;
     const uint16_t* value_rotation;
     const float* key_mean_loop;    // [heads, D] or null
-    const float* key_mean_anchor;  // [heads, D] or null (residual loops only)
+    const float* key_mean_anchor;  // [heads, D] or null (anchor mode, residual loops only)
     RecordRegion anchor;
     RecordRegion residual;
     int has_residual;
+    // Adjacent mode past loop 0: the restore chain over records 0..L
+    // (chain_length = L + 1 >= 2; 0 in anchor mode) and every record's key
+    // mean [records, heads, D] (or null).
+    int chain_length;
+    RecordRegion chain[kMaxRecords];
+    const float* key_mean_all;
     int causal;
     int splits;     // history splits per (request, head, row tile)
     int row_tiles;  // 32-row tiles per request in the grid

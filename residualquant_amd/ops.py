@@ -212,8 +212,8 @@ def packed_prefill_attention(query: torch.Tensor, key: torch.Tensor, value: torc
     own new ``key``/``value`` rows (row r sees new rows 0..r).  This is the
     prefill of a prompt chunk over a packed prefix, which the reference
     cannot run (its scheduler forbids partial prefill, rq/scheduler.py:11-18);
-    arguments and validation are those of ``attention``.  Anchor mode at
-    head_dim 128; a request may have no new rows.
+    arguments and validation are those of ``attention`` (head_dim 96 or
+    128, anchor or adjacent mode); a request may have no new rows.
     """
     key_rotation_ptr, value_rotation_ptr = _validate_packed_inputs(
         query, key, value, kv_cache, output, query_start_loc, seq_lens, block_table, key_rotation, value_rotation,

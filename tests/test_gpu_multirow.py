@@ -5,10 +5,13 @@ MFMA kernels (residualquant_amd/csrc/multirow.hip) against the CPU oracle.
   seeing seq_len - n history tokens and, causally, the new ones
   (oracle.attention_prefill);
 - ``attention`` with an average of 2 or more rows per request (3 in the
-  anchor loop; anchor mode, D128) routes to the same kernels with the
-  reference's decode semantics
-  (oracle.attention); fewer rows take the per-row decode kernel, checked
-  against the same oracle.
+  anchor-only loop) routes to the same kernels with the reference's decode
+  semantics (oracle.attention); fewer rows take the per-row decode kernel,
+  checked against the same oracle.
+
+Both head dims of the reference's attention registry (96 and 128) and both
+reference modes: anchor mode (compute.cuh:397-505) and adjacent mode, whose
+loops past 0 rebuild the BF16 restore chain (compute.cuh:120-197, :506-623).
 
 Bar: within 2e-2 max-abs / 1e-3 mean-abs of the oracle, both in BF16 (the
 oracle's FP64 output rounded to BF16: the BF16 quantum of outputs of
@@ -61,31 +64,46 @@ def _run(d, device, cache, loop, causal):
     return out.float().cpu().numpy()
 
 
+ADJACENT_G32 = ((4, 32), (2, 32), (2, 32), (2, 32))
+ADJACENT_G16 = ((4, 32), (2, 16), (2, 16), (2, 16))
+
 CASES = [
-    # lengths (seq_len incl. the new rows), rows per request, heads, records, page tokens, mean, rotation
-    ([100, 37, 9], [4, 1, 8], 3, OURO_G32, 16, True, True),
-    ([300], [33], 2, OURO_G32, 16, True, True),           # two row tiles
-    ([70, 200], [70, 5], 2, OURO_G16, 32, False, True),   # the first request has no history (prefill)
-    ([16, 40], [16, 3], 2, OURO_G32, 32, True, False),    # no rotation; the first request has no history (prefill)
-    ([2100], [3], 2, OURO_G32, 16, True, True),           # eight history splits
-    ([90, 51], [2, 6], 2, ((2, 16), (2, 16), (4, 32), (2, 32)), 16, True, True),
-    ([77], [5], 1, ((4, 16),), 32, True, True),           # single-record group
-    ([400, 123], [12, 20], 2, OURO_G32, 16, True, True),  # 16 rows per request on average
-    ([50, 300], [0, 33], 2, OURO_G32, 16, True, True),    # a request with no new rows: 33 rows in one request
+    # lengths (seq_len incl. the new rows), rows per request, heads, records, page tokens, mean, rotation,
+    # head dim, mode
+    ([100, 37, 9], [4, 1, 8], 3, OURO_G32, 16, True, True, 128, "anchor"),
+    ([300], [33], 2, OURO_G32, 16, True, True, 128, "anchor"),           # two row tiles
+    ([70, 200], [70, 5], 2, OURO_G16, 32, False, True, 128, "anchor"),   # the first request has no history (prefill)
+    ([16, 40], [16, 3], 2, OURO_G32, 32, True, False, 128, "anchor"),    # no rotation; no history (prefill)
+    ([2100], [3], 2, OURO_G32, 16, True, True, 128, "anchor"),           # eight history splits
+    ([90, 51], [2, 6], 2, ((2, 16), (2, 16), (4, 32), (2, 32)), 16, True, True, 128, "anchor"),
+    ([77], [5], 1, ((4, 16),), 32, True, True, 128, "anchor"),           # single-record group
+    ([400, 123], [12, 20], 2, OURO_G32, 16, True, True, 128, "anchor"),  # 16 rows per request on average
+    ([50, 300], [0, 33], 2, OURO_G32, 16, True, True, 128, "anchor"),    # a request with no new rows
+    # D96 (the Huginn geometry: three 32-channel quarters per token)
+    ([100, 37, 9], [4, 1, 8], 3, OURO_G16, 16, True, True, 96, "anchor"),
+    ([300, 70], [33, 70], 2, OURO_G32, 32, True, True, 96, "anchor"),    # two row tiles; no history (prefill)
+    ([2100], [3], 2, OURO_G16, 16, False, True, 96, "anchor"),           # eight history splits
+    ([77, 50], [5, 0], 1, ((4, 16),), 16, True, False, 96, "anchor"),    # single-record group, no rotation
+    # adjacent mode (every loop past 0 rebuilds the restore chain of records 0..L)
+    ([100, 37, 9], [4, 1, 8], 3, ADJACENT_G32, 16, True, True, 128, "adjacent"),
+    ([300, 40], [33, 2], 2, ADJACENT_G16, 32, True, True, 128, "adjacent"),
+    ([2100], [3], 2, ADJACENT_G32, 16, False, False, 128, "adjacent"),   # eight history splits
+    ([100, 37, 9], [4, 1, 8], 2, ADJACENT_G16, 16, True, True, 96, "adjacent"),
+    ([400, 123], [12, 20], 2, ((4, 32), (2, 32), (4, 16)), 32, True, True, 96, "adjacent"),
 ]
 
 
 def _ids(case):
-    return f"n{sum(case[1])}-h{case[2]}-r{len(case[3])}-pt{case[4]}"
+    return f"n{sum(case[1])}-h{case[2]}-r{len(case[3])}-pt{case[4]}-d{case[7]}-{case[8]}"
 
 
 @pytest.mark.parametrize("case", CASES, ids=_ids)
 @pytest.mark.parametrize("causal", [True, False], ids=["prefill", "decode"])
 def test_multirow_matches_oracle(oracle, device, case, causal):
-    lengths, rows, heads, records, pt, mean, rotation = case
+    lengths, rows, heads, records, pt, mean, rotation, dim, mode = case
     print(f"[case] multirow causal={causal} {case}", flush=True)
-    d = make_decode(lengths, heads, 128, records, seed=sum(lengths) + len(rows), page_tokens=pt, mean=mean,
-                    rotation=rotation, rows_per_request=rows)
+    d = make_decode(lengths, heads, dim, records, seed=sum(lengths) + len(rows), page_tokens=pt, mean=mean,
+                    rotation=rotation, rows_per_request=rows, mode=mode, anchor=0 if mode == "adjacent" else None)
     expected_cache = d.group.oracle_cache(oracle)
     cache = torch.from_numpy(expected_cache).to(device)
     for loop in range(len(records)):
@@ -110,7 +128,8 @@ def _random_cases(seed: int, count: int):
             rows[0] = 2
         lengths = [max(1, r + rng.choice([0, 1, 15, 17, 100, 333, 700])) for r in rows]
         cases.append((lengths, rows, rng.choice([1, 2, 3]), rng.choice(schedules), rng.choice([16, 32]),
-                      rng.random() < 0.7, rng.random() < 0.7, rng.random() < 0.5))
+                      rng.random() < 0.7, rng.random() < 0.7, rng.random() < 0.5, rng.choice([96, 128]),
+                      rng.choice(["anchor", "anchor", "adjacent"])))
     return cases
 
 
@@ -119,11 +138,11 @@ def _random_cases(seed: int, count: int):
 def test_multirow_random_mixes(oracle, device, index, case):
     """Every loop of each random mix, through ``attention`` (rows routed per
     call between the per-row and multi-row kernels) or
-    ``packed_prefill_attention``."""
-    lengths, rows, heads, records, pt, mean, rotation, causal = case
+    ``packed_prefill_attention``, at D 96 or 128, in anchor or adjacent mode."""
+    lengths, rows, heads, records, pt, mean, rotation, causal, dim, mode = case
     print(f"[case] random c{index} causal={causal} {case}", flush=True)
-    d = make_decode(lengths, heads, 128, records, seed=1000 + index, page_tokens=pt, mean=mean, rotation=rotation,
-                    rows_per_request=rows)
+    d = make_decode(lengths, heads, dim, records, seed=1000 + index, page_tokens=pt, mean=mean, rotation=rotation,
+                    rows_per_request=rows, mode=mode, anchor=0 if mode == "adjacent" else None)
     expected_cache = d.group.oracle_cache(oracle)
     cache = torch.from_numpy(expected_cache).to(device)
     for loop in range(len(records)):
@@ -192,12 +211,38 @@ def test_decode_rows_agree_with_single_row_calls(oracle, device):
 
 
 def test_multirow_rejections(device):
-    d = make_decode([40], 2, 96, OURO_G16, seed=2, rows_per_request=[3])
+    """Head dims outside the attention registry (96, 128) are refused before any launch."""
+    d = make_decode([40], 2, 64, ((4, 32), (2, 32)), seed=2, rows_per_request=[3])
     g = d.group
     cache = torch.zeros(g.cache_shape, dtype=torch.uint8, device=device)
     kr, vr, km = g.device_args(device)
     out = torch.empty_like(d.query, device=device)
-    with pytest.raises(RuntimeError, match="multi-row"):
+    with pytest.raises(RuntimeError, match="No compiled packed HIP"):
         rq.packed_prefill_attention(d.query.to(device), d.key.to(device), d.value.to(device), cache, out,
                                     d.query_start_loc.to(device), d.seq_lens.to(device), d.table.to(device), kr, vr,
                                     km, g.records, g.mode, g.anchor, 0)
+
+
+@pytest.mark.parametrize("dim,mode,records", [(96, "anchor", OURO_G16), (128, "adjacent", ADJACENT_G32),
+                                              (96, "adjacent", ADJACENT_G16)])
+def test_multirow_agrees_with_per_row_kernels(oracle, device, dim, mode, records):
+    """At D96 and in adjacent mode, decode rows on the multi-row route agree
+    with the same rows called one at a time (the per-row decode kernels:
+    decode96_kernel, decode_chain_kernel) within the bar, at every loop."""
+    d = make_decode([500, 300], 3, dim, records, seed=6, rows_per_request=[9, 7], mode=mode,
+                    anchor=0 if mode == "adjacent" else None)
+    g = d.group
+    cache = torch.from_numpy(g.oracle_cache(oracle)).to(device)
+    kr, vr, km = g.device_args(device)
+    for loop in range(len(records)):
+        multi = _run(d, device, cache, loop, causal=False)
+        starts = d.query_start_loc.tolist()
+        for b in range(2):
+            for i in range(starts[b], starts[b + 1]):
+                out = torch.empty((1, 3, dim), dtype=torch.bfloat16, device=device)
+                rq.attention(d.query[i:i + 1].to(device), d.key[i:i + 1].to(device), d.value[i:i + 1].to(device),
+                             cache, out, torch.tensor([0, 1], dtype=torch.int32, device=device),
+                             d.seq_lens[b:b + 1].to(device), d.table[b:b + 1].to(device), kr, vr, km, g.records,
+                             g.mode, g.anchor, loop)
+                single = out.float().cpu().numpy()[0]
+                assert np.abs(multi[i] - single).max() <= MAX_ABS, (loop, i)
