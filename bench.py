@@ -484,16 +484,20 @@ def run_prefill(args):
 
 
 def run_multiquery(args):
-    """Several query rows per request over the C2 packed history (multi-row MFMA kernels).
+    """Several query rows per request over a packed history (multi-row MFMA kernels).
 
-    B requests x R rows (--rows-per-request) x 8192 history tokens x 16 heads
-    x D128, the C2 cache and schedule.  One step = the 4 loop calls.  Timed
-    three ways on the same rows: rq.attention with R rows per request (the
-    multi-row kernels, the reference's decode semantics: every row sees the
-    8192 history tokens and its own key), the same rows as B*R one-row
-    requests (the per-row decode kernel, which streams each request's pages R
-    times), and rq.packed_prefill_attention (the rows as the requests' last R
-    tokens, causal among themselves, over the same 8192-token history)."""
+    --geometry ouro (default): B requests x R rows (--rows-per-request) x 8192
+    history tokens x 16 heads x D128, the C2 cache and schedule; --geometry
+    huginn: 8 requests x 4096 tokens x 55 heads x D96, the C4 cache and
+    schedule (--batch / --history override either).  --mode adjacent uses
+    the adjacent-mode schedule [4,32]+[2,32]x3 (anchor 0), whose loops past 0
+    rebuild the restore chain.  One step = the 4 loop calls.  Timed three ways
+    on the same rows: rq.attention with R rows per request (the multi-row
+    kernels, the reference's decode semantics: every row sees the history and
+    its own key), the same rows as B*R one-row requests (the per-row decode
+    kernel, which streams each request's pages R times), and
+    rq.packed_prefill_attention (the rows as the requests' last R tokens,
+    causal among themselves, over the same history)."""
     import torch
 
     import residualquant_amd as rq
@@ -501,11 +505,20 @@ def run_multiquery(args):
 
     device = torch.device("cuda:0")
     torch.cuda.set_device(device)
-    batch, rows_per, history, heads, dim, page_tokens = args.batch, args.rows_per_request, args.history, 16, 128, 16
+    huginn = args.geometry == "huginn"
+    heads, dim = (55, 96) if huginn else (16, 128)
+    batch = args.batch if args.batch is not None else (8 if huginn else 32)
+    history = args.history if args.history is not None else (4096 if huginn else 8192)
+    rows_per, page_tokens = args.rows_per_request, 16
+    adjacent = args.mode == "adjacent"
+    if adjacent:
+        schedule, mode, anchor = ADJACENT_SCHEDULE, "adjacent", 0
+    else:
+        schedule, mode, anchor = (HUGINN_SCHEDULE if huginn else SCHEDULE), "anchor", ANCHOR
     seed = 2026
-    log(f"[bench] building packed cache B={batch} T={history} H={heads} D={dim}, {rows_per} rows per request")
+    log(f"[bench] building packed cache B={batch} T={history} H={heads} D={dim} {mode}, {rows_per} rows per request")
     cache, table, key_rotation, value_rotation = build_packed_cache(
-        torch, rq, workloads, batch, history, heads, dim, page_tokens, device, seed)
+        torch, rq, workloads, batch, history, heads, dim, page_tokens, device, seed, schedule, mode, anchor)
     rows = batch * rows_per
     generator = torch.Generator(device=device).manual_seed(seed + 7)
     query, key, value = (torch.randn((rows, heads, dim), generator=generator, device=device).to(torch.bfloat16)
@@ -523,44 +536,54 @@ def run_multiquery(args):
 
     def multi(loop):
         rq.attention(query, key, value, cache, output, qsl, seq_decode, table, key_rotation, value_rotation, None,
-                     SCHEDULE, "anchor", ANCHOR, loop, workspace=workspace)
+                     schedule, mode, anchor, loop, workspace=workspace)
 
     def per_row(loop):
         rq.attention(query, key, value, cache, output, qsl_rows, seq_rows, table_rows, key_rotation, value_rotation,
-                     None, SCHEDULE, "anchor", ANCHOR, loop, workspace=workspace)
+                     None, schedule, mode, anchor, loop, workspace=workspace)
 
     def prefill(loop):
         rq.packed_prefill_attention(query, key, value, cache, output, qsl, seq_prefill, table, key_rotation,
-                                    value_rotation, None, SCHEDULE, "anchor", ANCHOR, loop, workspace=workspace)
+                                    value_rotation, None, schedule, mode, anchor, loop, workspace=workspace)
 
+    loops = len(schedule)
+    # The call the roofline is quoted on: the residual loops in anchor mode,
+    # the longest chain (loop 3) in adjacent mode.
+    measured = [loops - 1] if adjacent else [loop for loop in range(loops) if loop != anchor]
     results = {}
     for name, call in (("multirow", multi), ("per_row_decode", per_row), ("packed_prefill", prefill)):
         def step(call=call):
-            for loop in range(len(SCHEDULE)):
+            for loop in range(loops):
                 call(loop)
         settle(torch, step, 0.2)
-        durations = kernel_durations_ms(ops, [lambda loop=loop, call=call: call(loop) for loop in range(4)],
+        durations = kernel_durations_ms(ops, [lambda loop=loop, call=call: call(loop) for loop in range(loops)],
                                         max(50, args.steps))
         graph = capture(torch, step)
         settle(torch, graph.replay, 0.1)
         step_s = timed(torch, graph.replay, args.steps, args.warmup)
-        residual_ms = statistics.median(durations[0] + durations[1] + durations[2])
-        results[name] = {"us_per_step": step_s * 1e6, "residual_loop_us": residual_ms * 1e3,
-                         "anchor_loop_us": statistics.median(durations[ANCHOR]) * 1e3,
-                         "launches_timed": len(durations[0]) * 4}
-        log(f"[bench] {name}: step {step_s * 1e6:.1f} us, residual call {residual_ms * 1e3:.1f} us, "
-            f"anchor {results[name]['anchor_loop_us']:.1f} us")
+        measured_ms = statistics.median([d for loop in measured for d in durations[loop]])
+        results[name] = {"us_per_step": step_s * 1e6, "measured_call_us": measured_ms * 1e3,
+                         "per_loop_median_us": [statistics.median(d) * 1e3 for d in durations],
+                         "launches_timed": len(durations[0]) * loops}
+        log(f"[bench] {name}: step {step_s * 1e6:.1f} us, per loop "
+            f"{' / '.join(f'{x:.1f}' for x in results[name]['per_loop_median_us'])} us")
         del graph
     # Algorithmic bytes: the pages once per (request, head) plus the rows' Q/K/V/out.
-    step_bytes = sum(staged_call_bytes(batch, history, heads, dim, page_tokens, loop) for loop in range(4)) + \
-        4 * 4 * (rows - batch) * heads * dim * 2
-    residual_bytes = staged_call_bytes(batch, history, heads, dim, page_tokens, 0) + 4 * (rows - batch) * heads * dim * 2
+    extra_rows = 4 * (rows - batch) * heads * dim * 2
+
+    def call_bytes(loop):
+        return staged_call_bytes(batch, history, heads, dim, page_tokens, loop, schedule, mode, anchor) + extra_rows
+
+    step_bytes = sum(call_bytes(loop) for loop in range(loops))
+    measured_bytes = statistics.mean(call_bytes(loop) for loop in measured)
     m = results["multirow"]
-    residual_gbps = residual_bytes / (m["residual_loop_us"] * 1e-6) / 1e9
-    # MFMA work of a residual call: per (request, head) and 32-token tile, 8 + 8
-    # 32x32x16 MFMAs (2 * 32 * 32 * 16 FLOP each) for one 32-row tile.
+    measured_gbps = measured_bytes / (m["measured_call_us"] * 1e-6) / 1e9
+    # MFMA work of one call: per (request, head) and 32-token tile, D / 16 +
+    # D / 16 32x32x16 MFMAs (2 * 32 * 32 * 16 FLOP each) per 32-row tile.
     tiles = batch * heads * ((history + 31) // 32) * ((rows_per + 31) // 32)
-    mfma_flop = tiles * 16 * 2 * 32 * 32 * 16
+    mfma_flop = tiles * 2 * (dim // 16) * 2 * 32 * 32 * 16
+    kernel = (f"multirow_chain_kernel<{dim},16,4>" if adjacent else
+              f"multirow_stream_kernel<{dim},16,true,...>") + " + multirow_finish_kernel"
     result = {
         "metric": "paged decode-attn µs/step + achieved HBM GB/s (% peak), INT2/INT4 vs bf16, 1 GPU",
         "value": step_bytes / (m["us_per_step"] * 1e-6) / 1e9,
@@ -574,9 +597,11 @@ def run_multiquery(args):
         "vs_baseline": None,
         "dtype": "int2/int4 packed codes, fp16/bf16 MFMA operands, fp32 accumulate",
         "data": "synthetic (seeded anchor N(0,1) + loop residuals N(0,0.15^2), random-sign Hadamard rotations)",
-        "config": {"workload": "several query rows per request over the C2 packed history", "batch": batch,
-                   "rows_per_request": rows_per, "history_tokens": history, "heads": heads, "head_dim": dim,
-                   "page_tokens": page_tokens, "schedule": "[2,32]x3+[4,32] anchor 3 ls"},
+        "config": {"workload": "several query rows per request over the "
+                               f"{'C4' if huginn else 'C2'} packed history ({mode} mode)",
+                   "batch": batch, "rows_per_request": rows_per, "history_tokens": history, "heads": heads,
+                   "head_dim": dim, "page_tokens": page_tokens, "schedule": str(schedule), "mode": mode,
+                   "anchor": anchor},
         "us_per_step": m["us_per_step"],
         "timing": "one HIP-graph replay of the 4 loop calls per step after settle replays; per-call medians of "
                   ">= 50 launches (HIP events around the call's launches)",
@@ -585,14 +610,13 @@ def run_multiquery(args):
         "speedup_vs_per_row_decode": results["per_row_decode"]["us_per_step"] / m["us_per_step"],
         "roofline": {
             "bound": "hbm",
-            "achieved": residual_gbps,
+            "achieved": measured_gbps,
             "peak": PEAK_HBM_GBPS,
             "unit": "GB/s",
-            "frac": residual_gbps / PEAK_HBM_GBPS,
+            "frac": measured_gbps / PEAK_HBM_GBPS,
             "traffic": None,
-            "kernel": "multirow_stream_kernel<16,true> + multirow_finish_kernel (residual loops 0-2), median of "
-                      f"{m['launches_timed'] * 3 // 4} calls",
-            "mfma_TFLOPs": mfma_flop / (m["residual_loop_us"] * 1e-6) / 1e12,
+            "kernel": f"{kernel} (loops {measured}), median of {m['launches_timed'] * len(measured) // loops} calls",
+            "mfma_TFLOPs": mfma_flop / (m["measured_call_us"] * 1e-6) / 1e12,
         },
         "cpu_baseline": None,
     }
@@ -611,7 +635,7 @@ def run_adjacent(args):
 
     device = torch.device("cuda:0")
     torch.cuda.set_device(device)
-    batch, history, heads, dim, page_tokens = args.batch, args.history, 16, 128, 16
+    batch, history, heads, dim, page_tokens = args.batch or 32, args.history or 8192, 16, 128, 16
     schedule = ADJACENT_SCHEDULE
     seed = 2027
     log(f"[bench] building adjacent-mode packed cache B={batch} T={history} H={heads} D={dim}")
@@ -886,13 +910,18 @@ def main():
                              "multiquery: several rows per request over the C2 history (multi-row MFMA kernels); "
                              "adjacent: adjacent-mode decode at the C2 shape (the restore-chain kernel)")
     parser.add_argument("--rows-per-request", type=int, default=4, help="multiquery: query rows per request")
+    parser.add_argument("--geometry", choices=("ouro", "huginn"), default="ouro",
+                        help="multiquery: the C2 (16 heads x D128) or C4 (55 heads x D96) cache")
+    parser.add_argument("--mode", choices=("anchor", "adjacent"), default="anchor",
+                        help="multiquery: anchor-mode schedule or the adjacent-mode one")
     parser.add_argument("--no-sweep", action="store_true", help="step workload: batch 32 x 8k only")
     parser.add_argument("--tokens", type=int, default=4096, help="tokens per quantize call or prompt")
     parser.add_argument("--gpus", type=int, default=1)
     parser.add_argument("--steps", type=int, default=20)
     parser.add_argument("--warmup", type=int, default=5)
-    parser.add_argument("--batch", type=int, default=32)
-    parser.add_argument("--history", type=int, default=8192)
+    parser.add_argument("--batch", type=int, default=None, help="requests (default: the workload's configuration)")
+    parser.add_argument("--history", type=int, default=None, help="history tokens per request (default: the "
+                                                                  "workload's configuration)")
     parser.add_argument("--cpu-budget", type=float, default=10.0,
                         help="seconds of CPU oracle work for the cpu_baseline sample (0 = skip)")
     parser.add_argument("--no-bf16", action="store_true")
@@ -943,7 +972,7 @@ def run_decode(args):
     torch.cuda.set_device(device)
     if args.split_target:
         ops.set_split_target(args.split_target)
-    batch, history, heads, dim, page_tokens = args.batch, args.history, 16, 128, 16
+    batch, history, heads, dim, page_tokens = args.batch or 32, args.history or 8192, 16, 128, 16
     seed = 2026
 
     log(f"[bench] building packed cache B={batch} T={history} H={heads} D={dim}")

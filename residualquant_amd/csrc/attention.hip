@@ -1573,6 +1573,385 @@ void decode96_kernel(AttentionParams p) {
     }
 }
 
+// ------------------------------------------------------------------ D = 96 decode with DMA-staged pages
+//
+// decode96_kernel's arithmetic, with each wave iteration's page spans staged
+// in LDS by direct-to-LDS buffer loads (buffer_load_dwordx4 ... lds) instead
+// of per-lane register loads.  A 1 KB DMA load moves 64 lane-linear 16-byte
+// chunks of the staged spans (the loop record with its alphas, then the
+// anchor record without them, async_copy.cuh:24-42), so one iteration's two
+// pages of K and V take 6 loads (C4 schedule) where the register form issues
+// 16 narrow loads per lane; and the staged bytes sit in LDS, not in
+// registers, so each wave keeps kDma96Stages iterations of loads in flight.
+// A no-arithmetic gather of a C4 residual call through such rings measured
+// 56.8 us against 71.7 us for the register loads of decode96_kernel.  Lanes
+// then read their token half's code words, FP8 parameters and alpha from LDS
+// in decode96_kernel's layout (lane = 2 * slot + half).
+constexpr int kDma96Stages = 3;
+
+template <int PT, int BA, int GA, int BL, int GL, bool HasL>
+struct Dma96Layout {
+    static constexpr int D = 96;
+    static constexpr int CodeA = D * BA / 8, GroupsA = D / GA;
+    static constexpr int CodeL = D * BL / 8, GroupsL = D / GL;
+    static constexpr int BytesA = CodeA + 2 * GroupsA + 2, BytesL = CodeL + 2 * GroupsL + 2;
+    static constexpr int SpanL = HasL ? PT * BytesL : 0;       // the loop record, alphas included
+    static constexpr int SpanA = PT * (BytesA - 2);            // the anchor record without its alphas
+    static constexpr int PageBytes = SpanL + SpanA;            // staged bytes of one page and plane
+    static constexpr int Pages = 32 / PT;                      // pages of one wave iteration (32 tokens)
+    static constexpr int PlaneChunks = Pages * PageBytes / 16;
+    static constexpr int PlaneLoads = (PlaneChunks + 63) / 64;  // 1 KB DMA loads per plane and iteration
+    static constexpr int PlaneBytes = PlaneLoads * 1024;
+    static constexpr int StageBytes = 2 * PlaneBytes;          // K region, then V region
+    // One stage of the ring, [wave][K region, V region], plus 64 bytes: a
+    // lane's FP8 parameter words are read as two aligned dwords, which can
+    // reach 4 bytes past the last staged span.
+    static constexpr int RingStageBytes = kWaves * StageBytes + 64;
+    static_assert(SpanL % 16 == 0 && SpanA % 16 == 0, "staged spans are whole 16-byte chunks");
+};
+
+typedef __attribute__((address_space(3))) void LdsVoid96;
+
+// One DMA load: lane l's 16 bytes at `offset` of the resource go to lds + 16 l
+// (lds wave-uniform).  A __device__ function, not a call inside a kernel's
+// lambda: there the host pass drops the kernel's launch stub.
+__device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t rsrc, uint8_t* lds, uint32_t offset) {
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, (LdsVoid96*)lds, 16, offset, 0, 0, kStreamPolicy);
+}
+
+// s_waitcnt vmcnt(N) (bits [3:0] and [15:14]), not waiting on expcnt or lgkmcnt.
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+    static_assert(N >= 0 && N < 64, "vmcnt takes 6 bits");
+    __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+
+template <int PT, int BA, int GA, int BL, int GL, bool HasL>
+__global__ __launch_bounds__(kDecodeThreads) __attribute__((amdgpu_waves_per_eu(2)))
+void decode96_dma_kernel(AttentionParams p) {
+    using L = Dma96Layout<PT, BA, GA, BL, GL, HasL>;
+    constexpr int D = 96;
+    constexpr int UnitsPerPage = PT / kUnitTokens;
+    constexpr int CodeA = L::CodeA, GroupsA = L::GroupsA, CodeL = L::CodeL, GroupsL = L::GroupsL;
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int slot = lane >> 1;          // token slot of the iteration, 0..31
+    const int h = lane & 1;              // channel half
+    const bool upper = slot >= 16;       // slot on the iteration's second unit
+    const int tok = PT == 32 ? slot : (slot & 15);  // token row inside the slot's page
+    const int page_of_slot = PT == 32 ? 0 : (upper ? 1 : 0);
+    const int split = blockIdx.x % p.splits;
+    const int64_t rh = blockIdx.x / p.splits;
+    const int head = (int)(rh % p.heads);
+    const int64_t row = rh / p.heads;
+    __shared__ __attribute__((aligned(16))) float prep_lds[kPrepFloats];
+    __shared__ __attribute__((aligned(16))) uint32_t half_planes[2][2][6][4];
+    __shared__ int request_counts[kWaves];
+    // The three stages of the staging ring are separate LDS objects: the
+    // compiler makes an LDS read wait for every DMA load in flight that may
+    // write the object it reads, so with one object for all stages the
+    // reads of one stage would wait for the loads of the others.  Stage 2
+    // also holds the R_k staging of the fused prepare (D x D halves), before
+    // its first load (the prologue's barriers order the two), and the wave
+    // merge (kWaves x 16 x D floats), after the last.
+    constexpr int kScratchBytes = (int)sizeof(float) * kWaves * 16 * D;
+    static_assert(D * D * 2 <= kScratchBytes, "R_k staging fits the merge scratch");
+    __shared__ __attribute__((aligned(16))) uint8_t ring0[L::RingStageBytes];
+    __shared__ __attribute__((aligned(16))) uint8_t ring1[L::RingStageBytes];
+    __shared__ __attribute__((aligned(16))) uint8_t ring2[L::RingStageBytes > kScratchBytes ? L::RingStageBytes
+                                                                                           : kScratchBytes];
+    float* scratch_lds = reinterpret_cast<float*>(ring2);
+
+    SplitRange range;
+    PrepareInputs<D, kDecodeThreads> in;
+    _Float16* rotation_lds = reinterpret_cast<_Float16*>(scratch_lds);
+    if (p.fused_prepare) {
+        prepare_load<D, kDecodeThreads>(p, row, head, in);
+        range = fused_range(p, row, split, request_counts);
+        if (range.request >= 0) prepare_stage<D, kDecodeThreads>(p, in, rotation_lds);
+    } else {
+        range = split_range(p, p.row_request[row], split);
+    }
+    if (range.request < 0) return;
+    range.request = __builtin_amdgcn_readfirstlane(range.request);
+    range.history = uniform64(range.history);
+    range.unit_begin = uniform64(range.unit_begin);
+    range.unit_end = uniform64(range.unit_end);
+    float* partial = p.partials + (rh * p.splits + split) * (int64_t)(D + 2);
+
+    const ConstantInt32* table =
+        (const ConstantInt32*)(p.block_table + (int64_t)range.request * p.block_table_stride);
+    const uint32_t page_bytes = (uint32_t)PT * (uint32_t)p.page_width;
+    const __amdgpu_buffer_rsrc_t kplane = page_resource(p.cache, (uint32_t)p.plane_stride);
+    const __amdgpu_buffer_rsrc_t vplane = page_resource(p.cache + p.plane_stride, (uint32_t)p.plane_stride);
+    // A page that is missing (past the split or an invalid block id) is
+    // addressed past every plane: its loads return zeros and fetch nothing.
+    constexpr uint32_t kMissing = 0xFFFF0000u;
+
+    // Each lane's chunks of the DMA loads: load j of a plane moves chunks
+    // 64 j + lane of the iteration's staged bytes (page-major, then the loop
+    // record's span, then the anchor's), i.e. page q = chunk / (PageBytes /
+    // 16) at byte offset chunk_offset[j] of that page.  Chunks past the end
+    // repeat the first (their LDS bytes are never read).
+    uint32_t chunk_offset[L::PlaneLoads];
+    bool chunk_second[L::PlaneLoads];
+#pragma unroll
+    for (int j = 0; j < L::PlaneLoads; ++j) {
+        int c = 64 * j + lane;
+        c = c < L::PlaneChunks ? c : 0;
+        const int q = c / (L::PageBytes / 16);
+        const int b = 16 * (c % (L::PageBytes / 16));
+        chunk_second[j] = q == 1;
+        chunk_offset[j] = b < L::SpanL ? (uint32_t)p.residual.offset + b : (uint32_t)p.anchor.offset + (b - L::SpanL);
+    }
+
+    // Iteration g of this wave covers units (u, u + 1), u = first + 2 kWaves g.
+    const int64_t first = range.unit_begin + 2 * wave;
+    const int64_t unit_step = 2 * kWaves;
+    const int iterations = first < range.unit_end ? (int)((range.unit_end - first + unit_step - 1) / unit_step) : 0;
+    struct PagePair {
+        uint32_t base0, base1;  // page byte offsets in the plane (kMissing if absent)
+    };
+    auto pages_of = [&](int g) -> PagePair {
+        const int64_t u = first + unit_step * g;
+        PagePair r{kMissing, kMissing};
+        if (g < iterations) {
+            const int b0 = table[u / UnitsPerPage];
+            if (b0 >= 0 && b0 < p.num_blocks) r.base0 = ((uint32_t)b0 * (uint32_t)p.heads + (uint32_t)head) * page_bytes;
+            if (PT == 16 && u + 1 < range.unit_end) {
+                const int b1 = table[(u + 1) / UnitsPerPage];
+                if (b1 >= 0 && b1 < p.num_blocks)
+                    r.base1 = ((uint32_t)b1 * (uint32_t)p.heads + (uint32_t)head) * page_bytes;
+            }
+        }
+        return r;
+    };
+    auto stage_base = [&](auto stage_constant) __attribute__((always_inline)) {
+        constexpr int stage = decltype(stage_constant)::value;
+        return (stage == 0 ? ring0 : stage == 1 ? ring1 : ring2) + wave * L::StageBytes;
+    };
+    using Stage0 = std::integral_constant<int, 0>;
+    using Stage1 = std::integral_constant<int, 1>;
+    using Stage2 = std::integral_constant<int, 2>;
+    uint32_t dma_offset[L::PlaneLoads];
+    auto issue = [&](const PagePair& pages, auto stage_constant) __attribute__((always_inline)) {
+        uint8_t* dst = stage_base(stage_constant);
+#pragma unroll
+        for (int j = 0; j < L::PlaneLoads; ++j) {
+            const uint32_t base = chunk_second[j] ? pages.base1 : pages.base0;
+            dma_offset[j] = base == kMissing ? kMissing : base + chunk_offset[j];
+            dma16(kplane, dst + 1024 * j, dma_offset[j]);
+        }
+#pragma unroll
+        for (int j = 0; j < L::PlaneLoads; ++j) dma16(vplane, dst + L::PlaneBytes + 1024 * j, dma_offset[j]);
+    };
+
+    // The first two stages' loads are in flight while the query record is
+    // prepared.  The stages' page pairs live in three variables (an array
+    // indexed by the loop counter would sit in scratch memory, whose loads
+    // share vmcnt with the DMA loads).
+    static_assert(kDma96Stages == 3, "the loop below rotates three stages");
+    PagePair pages0 = pages_of(0), pages1 = pages_of(1), pages2;
+    issue(pages0, Stage0{});
+    issue(pages1, Stage1{});
+
+    if (p.fused_prepare) {
+        prepare_record<D, kDecodeThreads>(p, head, in, prep_lds, rotation_lds);
+    } else {
+        const float* src = p.prep + rh * (int64_t)kPrepFloats;
+        for (int i = threadIdx.x; i < kPrepFloats; i += kDecodeThreads) prep_lds[i] = src[i];
+        __syncthreads();
+    }
+    const float* prep = prep_lds;
+    const float delta = prep[0];
+    const float q_mean_anchor = h == 0 ? prep[2] : 0.f;  // added once per token
+    float q_sum[3];
+#pragma unroll
+    for (int b = 0; b < 3; ++b) q_sum[b] = prep[3 + 3 * h + b];
+    // Nibble planes per half, [record (anchor, loop)][half][word][plane].
+    if (threadIdx.x < 96) {
+        const int record = threadIdx.x / 48, half = (threadIdx.x / 24) & 1;
+        const int word = (threadIdx.x >> 2) % 6, plane = threadIdx.x & 3;
+        const int bits = record == 0 ? BA : BL;
+        const uint32_t* base = reinterpret_cast<const uint32_t*>(prep + kPrepScalars + kPrepQuery) +
+                               (bits == 2 ? kPrepPlanes : 0);
+        half_planes[record][half][word][plane] = base[plane * 16 + 6 * half + word];
+    }
+    __syncthreads();
+    const uint32_t (*planes_a)[4] = half_planes[0][h];
+    const uint32_t (*planes_l)[4] = half_planes[1][h];
+
+    // Byte offsets of the lane's fields inside a staged page (plane region).
+    const uint32_t first_a = tok * GroupsA + (GA == 16 ? 3 * h : h);
+    const uint32_t first_l = tok * GroupsL + (GL == 16 ? 3 * h : h);
+    const uint32_t shift_a = first_a & 3u, shift_l = first_l & 3u;
+    const uint32_t lds_page = page_of_slot * L::PageBytes;
+    const uint32_t at_codes_a = lds_page + L::SpanL + tok * CodeA + h * (CodeA / 2);
+    const uint32_t at_scale_a = lds_page + L::SpanL + PT * CodeA + (first_a & ~3u);
+    const uint32_t at_offs_a = at_scale_a + PT * GroupsA;
+    const uint32_t at_codes_l = lds_page + tok * CodeL + h * (CodeL / 2);
+    const uint32_t at_scale_l = lds_page + PT * CodeL + (first_l & ~3u);
+    const uint32_t at_offs_l = at_scale_l + PT * GroupsL;
+    const uint32_t at_alpha = lds_page + PT * (CodeL + 2 * GroupsL) + 2 * tok;
+
+    auto word_at = [](const uint8_t* base, uint32_t at) { return *reinterpret_cast<const uint32_t*>(base + at); };
+    auto codes_at = [&](const uint8_t* plane, uint32_t at, auto& c) __attribute__((always_inline)) {
+        // INT4: 24 bytes at an 8-byte boundary; INT2: 12 bytes at a 4-byte boundary.
+        constexpr int Words = std::remove_reference_t<decltype(c)>::kWords;
+        if constexpr (Words == 6) {
+#pragma unroll
+            for (int i = 0; i < 3; ++i) {
+                const uint2 v = *reinterpret_cast<const uint2*>(plane + at + 8 * i);
+                c.w[2 * i] = v.x;
+                c.w[2 * i + 1] = v.y;
+            }
+        } else {
+#pragma unroll
+            for (int i = 0; i < 3; ++i) c.w[i] = word_at(plane, at + 4 * i);
+        }
+    };
+    auto params_at = [&](const uint8_t* plane, uint32_t at_scale, uint32_t at_offs, uint32_t shift, auto& prm)
+        __attribute__((always_inline)) {
+        prm.s = __builtin_amdgcn_alignbyte(word_at(plane, at_scale + 4), word_at(plane, at_scale), shift);
+        prm.o = __builtin_amdgcn_alignbyte(word_at(plane, at_offs + 4), word_at(plane, at_offs), shift);
+    };
+
+    float acc[48];
+#pragma unroll
+    for (int i = 0; i < 48; ++i) acc[i] = 0.f;
+    float cst[3] = {0.f, 0.f, 0.f};
+    float m = -INFINITY, l = 0.f;
+
+    // Iteration g consumes stage g % 3 after issuing stage (g + 2) % 3
+    // (iteration g - 1's stage, whose reads are complete).
+    auto iteration = [&](int g, auto stage_constant) __attribute__((always_inline)) {
+        constexpr int stage = decltype(stage_constant)::value;
+        constexpr int ahead = (stage + 2) % 3;
+        const PagePair next = pages_of(g + 2);
+        issue(next, std::integral_constant<int, ahead>{});
+        const PagePair cur = stage == 0 ? pages0 : stage == 1 ? pages1 : pages2;
+        if constexpr (ahead == 0)
+            pages0 = next;
+        else if constexpr (ahead == 1)
+            pages1 = next;
+        else
+            pages2 = next;
+        wait_vmcnt<2 * 2 * L::PlaneLoads>();
+        const uint8_t* kst = stage_base(stage_constant);
+        const uint8_t* vst = kst + L::PlaneBytes;
+        const int64_t u = first + unit_step * g;
+        const int64_t unit = u + (upper ? 1 : 0);
+        // Branch-free (a divergent branch here makes the compiler wait for
+        // every DMA load in flight before the stage's first LDS read).
+        const bool ok = (page_of_slot ? cur.base1 : cur.base0) != kMissing;
+        const bool valid = ok & (unit < range.unit_end) & (16 * unit + (slot & 15) < range.history);
+        HalfUnit<BA, GA, BL, GL, HasL> d;
+        codes_at(kst, at_codes_a, d.kca);
+        params_at(kst, at_scale_a, at_offs_a, shift_a, d.kpa);
+        if constexpr (HasL) {
+            codes_at(kst, at_codes_l, d.kcl);
+            params_at(kst, at_scale_l, at_offs_l, shift_l, d.kpl);
+            d.alpha_k_bits = *reinterpret_cast<const uint16_t*>(kst + at_alpha);
+        }
+
+        float sa[3], oa[3];
+        d.kpa.decode(h != 0, sa, oa);
+        int da[3];
+        half_dots<BA>(d.kca, planes_a, da);
+        float s = half_score(sa, oa, da, delta, q_sum);
+        if constexpr (HasL) {
+            float sl[3], ol[3];
+            d.kpl.decode(h != 0, sl, ol);
+            int dl[3];
+            half_dots<BL>(d.kcl, planes_l, dl);
+            s = __uint_as_float(d.alpha_k_bits << 16) * (s + q_mean_anchor) + half_score(sl, ol, dl, delta, q_sum);
+        }
+        float score = s + quad_xor1(s);  // the token's two halves
+        score = valid ? score : -INFINITY;
+
+        const float unit_max = slot_wave_max(score);
+        if (unit_max > m) {
+            const float factor = m == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m - unit_max);
+#pragma unroll
+            for (int i = 0; i < 48; ++i) acc[i] *= factor;
+#pragma unroll
+            for (int b = 0; b < 3; ++b) cst[b] *= factor;
+            l *= factor;
+            m = unit_max;
+        }
+        const float prob = valid ? __builtin_amdgcn_exp2f(score - m) : 0.f;
+        l += h == 0 ? prob : 0.f;
+
+        codes_at(vst, at_codes_a, d.vca);
+        params_at(vst, at_scale_a, at_offs_a, shift_a, d.vpa);
+        if constexpr (HasL) {
+            codes_at(vst, at_codes_l, d.vcl);
+            params_at(vst, at_scale_l, at_offs_l, shift_l, d.vpl);
+            d.alpha_v_bits = *reinterpret_cast<const uint16_t*>(vst + at_alpha);
+        }
+        // Values: acc += p * (alpha_v * deq_A + deq_L); offsets go to cst.  A
+        // token past the history (or of a missing page) has p = 0, but its
+        // bytes may be anything (0 x NaN is NaN): its raw scale, offset and
+        // alpha bits are selected to 0 before they are converted.
+        const float p512 = prob * 512.0f;
+        HalfParams<GA> vpa = d.vpa;
+        vpa.s = valid ? vpa.s : 0u;
+        vpa.o = valid ? vpa.o : 0u;
+        float sva[3], ova[3];
+        vpa.decode(h != 0, sva, ova);
+        float w_a[3];
+        if constexpr (HasL) {
+            HalfParams<GL> vpl = d.vpl;
+            vpl.s = valid ? vpl.s : 0u;
+            vpl.o = valid ? vpl.o : 0u;
+            const float alpha_v = __uint_as_float((valid ? d.alpha_v_bits : 0u) << 16);
+            const float pa = prob * alpha_v;
+            const float pa512 = p512 * alpha_v;
+            float svl[3], ovl[3];
+            vpl.decode(h != 0, svl, ovl);
+            float w_l[3];
+#pragma unroll
+            for (int b = 0; b < 3; ++b) {
+                w_a[b] = pa512 * sva[b];
+                w_l[b] = p512 * svl[b];
+                cst[b] += fmaf(pa, ova[b], prob * ovl[b]);
+            }
+            accumulate_half<BL>(d.vcl, w_l, acc);
+        } else {
+#pragma unroll
+            for (int b = 0; b < 3; ++b) {
+                w_a[b] = p512 * sva[b];
+                cst[b] += prob * ova[b];
+            }
+        }
+        accumulate_half<BA>(d.vca, w_a, acc);
+        // This stage's LDS reads are complete before the next iteration's
+        // DMA into it can land.
+        __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
+        __builtin_amdgcn_sched_barrier(0);
+    };
+    for (int g = 0; g < iterations; g += 3) {
+        iteration(g, Stage0{});
+        if (g + 1 < iterations) iteration(g + 1, Stage1{});
+        if (g + 2 < iterations) iteration(g + 2, Stage2{});
+    }
+    // The loads of the stages past the last iteration (zero-byte fetches of
+    // missing pages) have landed before the LDS is reused or the wave exits.
+    wait_vmcnt<0>();
+
+#pragma unroll
+    for (int b = 0; b < 3; ++b)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) acc[16 * b + i] += cst[b];
+    if (p.splits == 1) {
+        finish_single<D>(p, row, head, prep_lds[1],
+                         [&] { return merge_waves_half(acc, m, l, lane, wave, scratch_lds); });
+    } else {
+        write_partial<D>(merge_waves_half(acc, m, l, lane, wave, scratch_lds), partial);
+        finish_split<D>(p, row, head);
+    }
+}
+
 // ------------------------------------------------------------------ adjacent mode, loops > 0
 //
 // Adjacent mode stores each loop as a residual of the previous loop, so the
@@ -1873,13 +2252,11 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_bf16_kernel(AttentionPa
 template <int D, int PT, int BA, int GA, int BL, int GL, bool HasL>
 void launch_decode(const AttentionParams& p, hipStream_t stream) {
     const unsigned blocks = (unsigned)(p.rows * p.heads * p.splits);
-    if constexpr (D == 96 && HasL) {
-        // Residual loops (the anchor-only loop streams half the bytes per
-        // token and measured faster on decode_kernel).  Per-lane page offsets
-        // are 32-bit buffer offsets into one plane.
-        if (p.plane_stride > 0 && p.plane_stride <= (int64_t)UINT32_MAX) {
-            hipLaunchKernelGGL((decode96_kernel<PT, BA, GA, BL, GL, HasL>), dim3(blocks), dim3(kDecodeThreads), 0,
-                               stream, p);
+    if constexpr (D == 96) {
+        // Per-lane page offsets are 32-bit buffer offsets into one plane.
+        if (p.plane_stride > 0 && p.plane_stride <= (int64_t)UINT32_MAX - 0x10000) {
+            hipLaunchKernelGGL((decode96_dma_kernel<PT, BA, GA, BL, GL, HasL>), dim3(blocks), dim3(kDecodeThreads),
+                               0, stream, p);
             return;
         }
     }
