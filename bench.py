@@ -811,7 +811,7 @@ def run_huginn(args):
             "frac": residual_gbps / PEAK_HBM_GBPS,
             "traffic": measured_traffic("decode_c4_counters.json")["bytes"],
             "traffic_measured_at": measured_traffic("decode_c4_counters.json")["commit"],
-            "kernel": f"decode96_kernel<16,4,32,2,16,true> (residual loops 0-2), median of {launches} launches "
+            "kernel": f"decode96_dma_kernel<16,4,32,2,16,true> (residual loops 0-2), median of {launches} launches "
                       "(HIP events on the launch stream, step order, after 10 warm-up rounds)",
         },
         "bf16_baseline": {

@@ -19,7 +19,7 @@
 //                                    per wave iteration; lane = token x
 //                                    32-channel quarter (decode_kernel), or
 //                                    token x 48-channel half for D = 96
-//                                    residual loops (decode96_kernel); QK on
+//                                    (decode96_dma_kernel); QK on
 //                                    integer dot8 units, PV in FP32 registers,
 //                                    online softmax per wave, LDS merge of the
 //                                    waves; the split that finishes last for
@@ -1129,14 +1129,11 @@ void decode_kernel(AttentionParams p) {
 // ------------------------------------------------------------------ D = 96 packed decode
 //
 // decode_kernel maps lane = token x 32-channel quarter, which leaves one lane
-// in four idle at D = 96.  decode96_kernel gives every lane one token's
-// 48-channel half instead: lane = 2 * slot + half, and a wave iteration covers
-// two 16-token units (slots 0..15: unit u, slots 16..31: unit u + 1).  A half
-// is three 16-channel blocks: six INT4 or three INT2 code words; block b of
-// half h belongs to group (3h + b) * 16 / G.  The two units of an iteration
-// can lie in different pages, so each lane addresses its own page through a
-// buffer resource over the whole K (or V) plane; launch_decode uses this
-// kernel when a plane fits in 4 GiB of buffer offsets.
+// in four idle at D = 96.  The D = 96 kernel below gives every lane one
+// token's 48-channel half instead: lane = 2 * slot + half, and a wave
+// iteration covers two 16-token units (slots 0..15: unit u, slots 16..31:
+// unit u + 1).  A half is three 16-channel blocks: six INT4 or three INT2 code
+// words; block b of half h belongs to group (3h + b) * 16 / G.
 
 template <int Bits>
 struct HalfCodes {
@@ -1144,31 +1141,13 @@ struct HalfCodes {
     uint32_t w[kWords];
 };
 
-template <int Bits>
-__device__ __forceinline__ void load_half_codes(__amdgpu_buffer_rsrc_t plane, uint32_t offset, HalfCodes<Bits>& c) {
-    const auto a = __builtin_amdgcn_raw_buffer_load_b96(plane, offset, 0, PagePolicy<96>::kCodes);
-    c.w[0] = a[0]; c.w[1] = a[1]; c.w[2] = a[2];
-    if constexpr (Bits == 4) {
-        const auto b = __builtin_amdgcn_raw_buffer_load_b96(plane, offset + 12, 0, PagePolicy<96>::kCodes);
-        c.w[3] = b[0]; c.w[4] = b[1]; c.w[5] = b[2];
-    }
-}
-
 // Raw FP8 scale/offset bytes of a half's groups, first group in byte 0:
-// three groups for G16 (one per block), two for G32 (groups h and h + 1).
-// Each is one 8-byte load from the 4-byte-aligned address at or below the
-// first byte, shifted into place (v_alignbyte): fewer, wider loads than one
-// per byte.
+// three groups for G16 (one per block), two for G32 (groups h and h + 1),
+// read as the two aligned dwords at or below the first byte and shifted into
+// place (v_alignbyte).
 template <int G>
 struct HalfParams {
     uint32_t s, o;
-    __device__ __forceinline__ void load(__amdgpu_buffer_rsrc_t plane, uint32_t scale_word, uint32_t offset_word,
-                                         uint32_t shift) {
-        const auto sv = __builtin_amdgcn_raw_buffer_load_b64(plane, scale_word, 0, PagePolicy<96>::kParams);
-        const auto ov = __builtin_amdgcn_raw_buffer_load_b64(plane, offset_word, 0, PagePolicy<96>::kParams);
-        s = __builtin_amdgcn_alignbyte(sv[1], sv[0], shift);
-        o = __builtin_amdgcn_alignbyte(ov[1], ov[0], shift);
-    }
     // Scale and offset of each of the three blocks of half `upper`.
     __device__ __forceinline__ void decode(bool upper, float (&scale)[3], float (&offset)[3]) const {
         if constexpr (G == 16) {
@@ -1289,7 +1268,7 @@ __device__ __forceinline__ float slot_wave_max(float x) {
     return fmaxf(fmaxf(r0, r1), fmaxf(r2, r3));
 }
 
-// The four waves' (m, l, acc) of one split in decode96_kernel's layout, merged
+// The four waves' (m, l, acc) of one split in the half layout, merged
 // in LDS: thread c < 96 gets channel c of the unnormalized output, every
 // thread gets m and l.  Slot pairs are added with DPP first, so the LDS holds
 // [wave][slot pair][96] (kWaves * 16 * 96 floats of `lds`).
@@ -1343,250 +1322,22 @@ struct HalfUnit {
     uint32_t alpha_k_bits, alpha_v_bits;
 };
 
-template <int PT, int BA, int GA, int BL, int GL, bool HasL>
-__global__ __launch_bounds__(kDecodeThreads) __attribute__((amdgpu_waves_per_eu(RQ_DECODE_MIN_WAVES)))
-void decode96_kernel(AttentionParams p) {
-    constexpr int D = 96;
-    constexpr int UnitsPerPage = PT / kUnitTokens;
-    constexpr int CodeA = D * BA / 8, GroupsA = D / GA;
-    constexpr int CodeL = D * BL / 8, GroupsL = D / GL;
-    const int lane = threadIdx.x & 63;
-    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int slot = lane >> 1;          // token slot of the iteration, 0..31
-    const int h = lane & 1;              // channel half
-    const bool upper = slot >= 16;       // slot on the iteration's second unit
-    const int tok = PT == 32 ? slot : (slot & 15);  // token row inside the slot's page
-    const int split = blockIdx.x % p.splits;
-    const int64_t rh = blockIdx.x / p.splits;
-    const int head = (int)(rh % p.heads);
-    const int64_t row = rh / p.heads;
-    __shared__ __attribute__((aligned(16))) float prep_lds[kPrepFloats];
-    __shared__ __attribute__((aligned(16))) uint32_t half_planes[2][2][6][4];
-    // R_k staging of the fused prepare, then the wave merge at the end.
-    __shared__ __attribute__((aligned(16))) float scratch_lds[kWaves * 16 * 128];
-    __shared__ int request_counts[kWaves];
-
-    // Query record and request lookup as in decode_kernel: the lookup first,
-    // so the first iteration's page loads overlap the record's arithmetic.
-    SplitRange range;
-    PrepareInputs<D, kDecodeThreads> in;
-    _Float16* rotation_lds = reinterpret_cast<_Float16*>(scratch_lds);
-    if (p.fused_prepare) {
-        prepare_load<D, kDecodeThreads>(p, row, head, in);
-        range = fused_range(p, row, split, request_counts);
-        if (range.request >= 0) prepare_stage<D, kDecodeThreads>(p, in, rotation_lds);
-    } else {
-        range = split_range(p, p.row_request[row], split);
-    }
-    if (range.request < 0) return;
-    range.request = __builtin_amdgcn_readfirstlane(range.request);
-    range.history = uniform64(range.history);
-    range.unit_begin = uniform64(range.unit_begin);
-    range.unit_end = uniform64(range.unit_end);
-    float* partial = p.partials + (rh * p.splits + split) * (int64_t)(D + 2);
-
-    // Lane offsets inside a page (the page offset is added per iteration).
-    // Parameter regions start 16-byte aligned (pages and record regions are
-    // multiples of 16 bytes), so the 4-byte alignment of a lane's first group
-    // byte is fixed per lane.
-    const uint32_t first_a = tok * GroupsA + (GA == 16 ? 3 * h : h);
-    const uint32_t first_l = tok * GroupsL + (GL == 16 ? 3 * h : h);
-    const uint32_t shift_a = first_a & 3u, shift_l = first_l & 3u;
-    const uint32_t off_codes_a = p.anchor.offset + tok * CodeA + h * (CodeA / 2);
-    const uint32_t off_scale_a = p.anchor.offset + PT * CodeA + (first_a & ~3u);
-    const uint32_t off_offs_a = off_scale_a + PT * GroupsA;
-    const uint32_t off_codes_l = p.residual.offset + tok * CodeL + h * (CodeL / 2);
-    const uint32_t off_scale_l = p.residual.offset + PT * CodeL + (first_l & ~3u);
-    const uint32_t off_offs_l = off_scale_l + PT * GroupsL;
-    const uint32_t off_alpha = p.residual.offset + PT * (CodeL + 2 * GroupsL) + 2 * tok;
-
-    const ConstantInt32* table =
-        (const ConstantInt32*)(p.block_table + (int64_t)range.request * p.block_table_stride);
-    const uint32_t page_bytes = (uint32_t)PT * (uint32_t)p.page_width;
-    const __amdgpu_buffer_rsrc_t kplane = page_resource(p.cache, (uint32_t)p.plane_stride);
-    const __amdgpu_buffer_rsrc_t vplane = page_resource(p.cache + p.plane_stride, (uint32_t)p.plane_stride);
-    constexpr bool kPairSharesPage = UnitsPerPage % 2 == 0;
-    struct PairBlocks {
-        int first, second;
-    };
-    auto pair_blocks = [&](int64_t u) -> PairBlocks {
-        PairBlocks b{-1, -1};
-        if (u < range.unit_end) {
-            b.first = table[u / UnitsPerPage];
-            if (kPairSharesPage)
-                b.second = b.first;
-            else if (u + 1 < range.unit_end)
-                b.second = table[(u + 1) / UnitsPerPage];
-        }
-        return b;
-    };
-
-    // Loads of the lane's token of units (u, u + 1); false if its page is
-    // missing (the lane then reads page 0 and is masked).
-    auto load_slot = [&](const PairBlocks& blocks, HalfUnit<BA, GA, BL, GL, HasL>& d) -> bool {
-        const int block = upper ? blocks.second : blocks.first;
-        const bool ok = block >= 0 && block < p.num_blocks;
-        const uint32_t page = ok ? ((uint32_t)block * (uint32_t)p.heads + (uint32_t)head) * page_bytes : 0u;
-        load_half_codes<BA>(kplane, page + off_codes_a, d.kca);
-        d.kpa.load(kplane, page + off_scale_a, page + off_offs_a, shift_a);
-        load_half_codes<BA>(vplane, page + off_codes_a, d.vca);
-        d.vpa.load(vplane, page + off_scale_a, page + off_offs_a, shift_a);
-        if constexpr (HasL) {
-            load_half_codes<BL>(kplane, page + off_codes_l, d.kcl);
-            d.kpl.load(kplane, page + off_scale_l, page + off_offs_l, shift_l);
-            load_half_codes<BL>(vplane, page + off_codes_l, d.vcl);
-            d.vpl.load(vplane, page + off_scale_l, page + off_offs_l, shift_l);
-            d.alpha_k_bits = __builtin_amdgcn_raw_buffer_load_b16(kplane, page + off_alpha, 0, PagePolicy<96>::kParams);
-            d.alpha_v_bits = __builtin_amdgcn_raw_buffer_load_b16(vplane, page + off_alpha, 0, PagePolicy<96>::kParams);
-        }
-        return ok;
-    };
-
-    const int64_t first = range.unit_begin + 2 * wave;
-    HalfUnit<BA, GA, BL, GL, HasL> d;
-    wait_vector_memory();
-    PairBlocks blocks = pair_blocks(first);
-    bool ok = load_slot(blocks, d);
-    blocks = pair_blocks(first + 2 * kWaves);
-
-    if (p.fused_prepare) {
-        prepare_record<D, kDecodeThreads>(p, head, in, prep_lds, rotation_lds);
-    } else {
-        const float* src = p.prep + rh * (int64_t)kPrepFloats;
-        for (int i = threadIdx.x; i < kPrepFloats; i += kDecodeThreads) prep_lds[i] = src[i];
-        __syncthreads();
-    }
-    const float* prep = prep_lds;
-    const float delta = prep[0];
-    const float q_mean_anchor = h == 0 ? prep[2] : 0.f;  // added once per token
-    float q_sum[3];
-#pragma unroll
-    for (int b = 0; b < 3; ++b) q_sum[b] = prep[3 + 3 * h + b];
-    // Nibble planes per half, [record (anchor, loop)][half][word][plane]: the
-    // loop reads one word's four planes with one 16-byte LDS read instead of
-    // holding all 48 in registers (which would cost a wave per SIMD).
-    if (threadIdx.x < 96) {
-        const int record = threadIdx.x / 48, half = (threadIdx.x / 24) & 1;
-        const int word = (threadIdx.x >> 2) % 6, plane = threadIdx.x & 3;
-        const int bits = record == 0 ? BA : BL;
-        const uint32_t* base = reinterpret_cast<const uint32_t*>(prep + kPrepScalars + kPrepQuery) +
-                               (bits == 2 ? kPrepPlanes : 0);
-        half_planes[record][half][word][plane] = base[plane * 16 + 6 * half + word];
-    }
-    __syncthreads();
-    const uint32_t (*planes_a)[4] = half_planes[0][h];
-    const uint32_t (*planes_l)[4] = half_planes[1][h];
-
-    float acc[48];
-#pragma unroll
-    for (int i = 0; i < 48; ++i) acc[i] = 0.f;
-    float cst[3] = {0.f, 0.f, 0.f};
-    float m = -INFINITY, l = 0.f;
-
-    // Each iteration streams units (u, u + 1), one token per lane pair.
-    for (int64_t u = first; u < range.unit_end; u += 2 * kWaves) {
-        // Keeps the plane reads in the loop (nothing in LDS changes here).
-        asm volatile("" ::: "memory");
-        if (u != first) {
-            ok = load_slot(blocks, d);
-            blocks = pair_blocks(u + 2 * kWaves);
-        }
-        const int64_t unit = u + (upper ? 1 : 0);
-        const bool valid = ok && unit < range.unit_end && 16 * unit + (slot & 15) < range.history;
-
-        float sa[3], oa[3];
-        d.kpa.decode(h != 0, sa, oa);
-        int da[3];
-        half_dots<BA>(d.kca, planes_a, da);
-        float s = half_score(sa, oa, da, delta, q_sum);
-        if constexpr (HasL) {
-            float sl[3], ol[3];
-            d.kpl.decode(h != 0, sl, ol);
-            int dl[3];
-            half_dots<BL>(d.kcl, planes_l, dl);
-            s = __uint_as_float(d.alpha_k_bits << 16) * (s + q_mean_anchor) + half_score(sl, ol, dl, delta, q_sum);
-        }
-        float score = s + quad_xor1(s);  // the token's two halves
-        score = valid ? score : -INFINITY;
-
-        const float unit_max = slot_wave_max(score);
-        if (unit_max > m) {
-            const float factor = m == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m - unit_max);
-#pragma unroll
-            for (int i = 0; i < 48; ++i) acc[i] *= factor;
-#pragma unroll
-            for (int b = 0; b < 3; ++b) cst[b] *= factor;
-            l *= factor;
-            m = unit_max;
-        }
-        const float prob = valid ? __builtin_amdgcn_exp2f(score - m) : 0.f;
-        l += h == 0 ? prob : 0.f;
-
-        // Values: acc += p * (alpha_v * deq_A + deq_L); offsets go to cst.
-        // A token past the history has p = 0, but its slot may hold any
-        // bytes (0 x NaN is NaN): its raw scale, offset and alpha bits are
-        // selected to 0 before they are converted.
-        const float p512 = prob * 512.0f;
-        HalfParams<GA> vpa = d.vpa;
-        vpa.s = valid ? vpa.s : 0u;
-        vpa.o = valid ? vpa.o : 0u;
-        float sva[3], ova[3];
-        vpa.decode(h != 0, sva, ova);
-        float w_a[3];
-        if constexpr (HasL) {
-            HalfParams<GL> vpl = d.vpl;
-            vpl.s = valid ? vpl.s : 0u;
-            vpl.o = valid ? vpl.o : 0u;
-            const float alpha_v = __uint_as_float((valid ? d.alpha_v_bits : 0u) << 16);
-            const float pa = prob * alpha_v;
-            const float pa512 = p512 * alpha_v;
-            float svl[3], ovl[3];
-            vpl.decode(h != 0, svl, ovl);
-            float w_l[3];
-#pragma unroll
-            for (int b = 0; b < 3; ++b) {
-                w_a[b] = pa512 * sva[b];
-                w_l[b] = p512 * svl[b];
-                cst[b] += fmaf(pa, ova[b], prob * ovl[b]);
-            }
-            accumulate_half<BL>(d.vcl, w_l, acc);
-        } else {
-#pragma unroll
-            for (int b = 0; b < 3; ++b) {
-                w_a[b] = p512 * sva[b];
-                cst[b] += prob * ova[b];
-            }
-        }
-        accumulate_half<BA>(d.vca, w_a, acc);
-    }
-
-#pragma unroll
-    for (int b = 0; b < 3; ++b)
-#pragma unroll
-        for (int i = 0; i < 16; ++i) acc[16 * b + i] += cst[b];
-    if (p.splits == 1) {
-        finish_single<D>(p, row, head, prep_lds[1],
-                         [&] { return merge_waves_half(acc, m, l, lane, wave, scratch_lds); });
-    } else {
-        write_partial<D>(merge_waves_half(acc, m, l, lane, wave, scratch_lds), partial);
-        finish_split<D>(p, row, head);
-    }
-}
-
 // ------------------------------------------------------------------ D = 96 decode with DMA-staged pages
 //
-// decode96_kernel's arithmetic, with each wave iteration's page spans staged
-// in LDS by direct-to-LDS buffer loads (buffer_load_dwordx4 ... lds) instead
-// of per-lane register loads.  A 1 KB DMA load moves 64 lane-linear 16-byte
+// The half-lane arithmetic above, with each wave iteration's page spans
+// staged in LDS by direct-to-LDS buffer loads (buffer_load_dwordx4 ... lds)
+// instead of per-lane register loads.  A 1 KB DMA load moves 64 lane-linear 16-byte
 // chunks of the staged spans (the loop record with its alphas, then the
 // anchor record without them, async_copy.cuh:24-42), so one iteration's two
 // pages of K and V take 6 loads (C4 schedule) where the register form issues
 // 16 narrow loads per lane; and the staged bytes sit in LDS, not in
 // registers, so each wave keeps kDma96Stages iterations of loads in flight.
 // A no-arithmetic gather of a C4 residual call through such rings measured
-// 56.8 us against 71.7 us for the register loads of decode96_kernel.  Lanes
-// then read their token half's code words, FP8 parameters and alpha from LDS
-// in decode96_kernel's layout (lane = 2 * slot + half).
+// 56.8 us against 71.7 us for per-lane register loads of the same spans.
+// Lanes then read their token half's code words, FP8 parameters and alpha
+// from LDS (lane = 2 * slot + half).  The per-lane 32-bit page offsets
+// address one buffer resource per plane, so launch_decode uses this kernel
+// when a plane fits in 4 GiB of buffer offsets.
 constexpr int kDma96Stages = 3;
 
 template <int PT, int BA, int GA, int BL, int GL, bool HasL>

@@ -228,7 +228,7 @@ def test_multirow_rejections(device):
 def test_multirow_agrees_with_per_row_kernels(oracle, device, dim, mode, records):
     """At D96 and in adjacent mode, decode rows on the multi-row route agree
     with the same rows called one at a time (the per-row decode kernels:
-    decode96_kernel, decode_chain_kernel) within the bar, at every loop."""
+    decode96_dma_kernel, decode_chain_kernel) within the bar, at every loop."""
     d = make_decode([500, 300], 3, dim, records, seed=6, rows_per_request=[9, 7], mode=mode,
                     anchor=0 if mode == "adjacent" else None)
     g = d.group
