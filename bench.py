@@ -152,15 +152,23 @@ def settle(torch, fn, seconds):
 
 
 def host_description(torch):
-    model = platform.processor() or "cpu"
+    # A virtual machine may report a generic model name ("AMD EPYC"), so the
+    # family / model / stepping numbers of the first processor come with it.
+    fields = {}
     try:
         with open("/proc/cpuinfo") as handle:
             for line in handle:
-                if line.startswith("model name"):
-                    model = line.split(":", 1)[1].strip()
-                    break
+                if not line.strip():
+                    break  # end of the first processor's block
+                key, _, value = line.partition(":")
+                fields.setdefault(key.strip(), value.strip())
     except OSError:
         pass
+    model = fields.get("model name") or platform.processor() or "cpu"
+    ids = [f"{name} {fields[key]}" for key, name in (("cpu family", "family"), ("model", "model"),
+                                                      ("stepping", "stepping")) if key in fields]
+    if ids:
+        model = f"{model} ({', '.join(ids)})"
     return {"cpu_model": model, "host_cores": len(os.sched_getaffinity(0)), "torch": torch.__version__}
 
 
