@@ -51,57 +51,85 @@ def _require(condition: bool, message: str) -> None:
         raise AssertionError(message)
 
 
+def _check_finite(tensor: torch.Tensor, name: str, dtype: torch.dtype) -> None:
+    _require(tensor.dtype == dtype, f"{name} must be {'FP16' if dtype == torch.float16 else 'FP32'}")
+    _require(bool(torch.isfinite(tensor).all()), f"{name} must be finite")
+
+
+@dataclass(frozen=True)
+class _Expected:
+    """What a valid artifact holds for one model and packed_groups."""
+
+    bits: Tuple[int, ...]
+    group_sizes: Tuple[int, ...]
+    groups: int  # loop groups
+    matrices: Tuple[int, int, int, int]  # [layers, H, D, D] of one group's rotations
+    key_means: Tuple[int, int, int, int]  # [recurrence, layers, H, D]
+
+    @classmethod
+    def of(cls, packed_groups: Sequence[Records], geometry: ModelGeometry) -> "_Expected":
+        flat = [tuple(record) for schedule in packed_groups for record in schedule]
+        h, d, layers = geometry.heads, geometry.head_dim, geometry.layers
+        return cls(bits=tuple(b for b, _ in flat), group_sizes=tuple(g for _, g in flat),
+                   groups=len(packed_groups), matrices=(layers, h, d, d),
+                   key_means=(geometry.recurrence, layers, h, d))
+
+    def rotation_shape(self, ndim: int) -> Tuple[int, ...]:
+        # Shared by every group (4-D) or one set per group (5-D).
+        return self.matrices if ndim == 4 else (self.groups, *self.matrices)
+
+
 def load_rotation_artifact(path, sha256: str, packed_groups: Sequence[Records],
                            geometry: ModelGeometry) -> dict:
     """Read and validate a rotation artifact (plugin.py:25-64).
 
     ``packed_groups`` is the ``packed_groups`` configuration: one list of
-    ``(bits, group)`` records per loop group.  Returns the loaded dictionary
-    (CPU tensors)."""
-    path = Path(path)
-    if hashlib.sha256(path.read_bytes()).hexdigest() != sha256:
+    ``(bits, group)`` records per loop group.  The file must match ``sha256``;
+    its schedule must be ``packed_groups`` flattened; the groups together must
+    cover the model's recurrence; each rotation set must be FP16, finite and
+    shaped for the model (shared or per group), and the key means FP32 and
+    finite.  Returns the loaded dictionary (CPU tensors)."""
+    raw = Path(path).read_bytes()
+    if hashlib.sha256(raw).hexdigest() != sha256:
         raise ValueError("Rotation artifact hash mismatch")
     data = torch.load(path, map_location="cpu", weights_only=True)
-    records = [tuple(record) for schedule in packed_groups for record in schedule]
-    _require(list(data["schedule"]) == [bits for bits, _ in records], "artifact schedule differs from packed_groups")
-    _require(list(data["groups"]) == [group for _, group in records], "artifact groups differ from packed_groups")
-    h, d, layers = geometry.heads, geometry.head_dim, geometry.layers
+    want = _Expected.of(packed_groups, geometry)
+    _require(tuple(data["schedule"]) == want.bits, "artifact schedule differs from packed_groups")
+    _require(tuple(data["groups"]) == want.group_sizes, "artifact groups differ from packed_groups")
     _require(data["format_version"] == 2, "artifact format_version must be 2")
-    if geometry.model is not None:
-        _require(data["model"] == geometry.model, "artifact model differs from the loop model")
-    if sum(map(len, packed_groups)) != geometry.recurrence:
+    _require(geometry.model is None or data["model"] == geometry.model, "artifact model differs from the loop model")
+    if len(want.bits) != geometry.recurrence:
         raise ValueError("Packed groups must describe every model recurrence exactly once")
-    group_count = len(packed_groups)
-    matrix_shape = (layers, h, d, d)
     for name in ("key_rotations", "value_rotations"):
-        rotation = data[name]
-        if rotation.ndim not in (4, 5):
+        tensor = data[name]
+        if tensor.ndim not in (4, 5):
             raise ValueError(f"{name} must have four or five dimensions")
-        expected = (group_count, *matrix_shape) if rotation.ndim == 5 else matrix_shape
-        if tuple(rotation.shape) != expected:
-            raise ValueError(f"{name} shape {tuple(rotation.shape)} != model shape {expected}")
-        _require(rotation.dtype == torch.float16, f"{name} must be FP16")
-        _require(bool(torch.isfinite(rotation).all()), f"{name} must be finite")
-    _require(tuple(data["key_means"].shape) == (geometry.recurrence, layers, h, d), "key_means shape")
-    _require(data["key_means"].dtype == torch.float32, "key_means must be FP32")
-    _require(bool(torch.isfinite(data["key_means"]).all()), "key_means must be finite")
+        shape = want.rotation_shape(tensor.ndim)
+        if tuple(tensor.shape) != shape:
+            raise ValueError(f"{name} shape {tuple(tensor.shape)} != model shape {shape}")
+        _check_finite(tensor, name, torch.float16)
+    _require(tuple(data["key_means"].shape) == want.key_means, "key_means shape")
+    _check_finite(data["key_means"], "key_means", torch.float32)
     return data
 
 
 def prepare_value_rotation(artifact: Optional[dict]):
     """Split off 4-D value rotations for weight folding (weights.py:40-49).
 
-    Returns ``(artifact, rotations)``: 5-D value rotations stay in the
-    artifact (the kernels apply them) and ``rotations`` is None; 4-D ones are
-    returned for ``absorb_value_rotation`` and removed from the artifact."""
+    Returns ``(artifact, rotations)``: 5-D value rotations are applied by the
+    kernels and stay in the artifact (``rotations`` None); a 4-D set is
+    returned for ``absorb_value_rotation`` and cleared in a copy of the
+    artifact."""
     if artifact is None:
         return None, None
     rotation = artifact["value_rotations"]
+    if rotation.ndim not in (4, 5):
+        raise ValueError("Value rotations must have four or five dimensions")
     if rotation.ndim == 5:
         return artifact, None
-    if rotation.ndim != 4:
-        raise ValueError("Value rotations must have four or five dimensions")
-    return dict(artifact, value_rotations=None), rotation
+    kept = dict(artifact)
+    kept["value_rotations"] = None
+    return kept, rotation
 
 
 @dataclass

@@ -18,7 +18,7 @@ loaded before the KV pool is sized.
 from __future__ import annotations
 
 from dataclasses import dataclass
-from typing import Iterable, Iterator, List, Optional, Sequence, Tuple
+from typing import List, Optional, Sequence, Tuple
 
 import torch
 
@@ -91,39 +91,59 @@ class WarmupLayer:
     value_rotation: Optional[torch.Tensor] = None
     key_mean: Optional[torch.Tensor] = None
 
+    def signature(self) -> tuple:
+        """The fields that select compiled kernels and argument shapes: two
+        layers with equal signatures exercise the same code."""
+        present = tuple(t is not None for t in (self.key_mean, self.key_rotation, self.value_rotation))
+        return (self.heads, self.head_dim, tuple(self.records), self.page_tokens, self.reference_mode,
+                self.anchor_index, self.coefficient_method) + present
 
-def _distinct(layers: Iterable[WarmupLayer]) -> Iterator[WarmupLayer]:
-    seen = set()
-    for layer in layers:
-        key = (layer.heads, layer.head_dim, tuple(layer.records), layer.page_tokens, layer.reference_mode,
-               layer.anchor_index, layer.coefficient_method, layer.key_mean is not None,
-               layer.key_rotation is not None, layer.value_rotation is not None)
-        if key not in seen:
-            seen.add(key)
-            yield layer
+
+@dataclass
+class _EmptyCall:
+    """Device buffers of a one-token request with no history: the token, its
+    output, a one-block cache, slot 0, and the batch metadata."""
+
+    token: torch.Tensor
+    output: torch.Tensor
+    cache: torch.Tensor
+    slot: torch.Tensor
+    query_start_loc: torch.Tensor
+    seq_lens: torch.Tensor
+    block_table: torch.Tensor
+
+    @classmethod
+    def for_layer(cls, layer: WarmupLayer, device: torch.device) -> "_EmptyCall":
+        token = torch.zeros((1, layer.heads, layer.head_dim), dtype=torch.bfloat16, device=device)
+        shape = (2, 1, layer.heads, layer.page_tokens, page_width(layer.head_dim, layer.records))
+        return cls(token=token, output=torch.empty_like(token),
+                   cache=torch.zeros(shape, dtype=torch.uint8, device=device),
+                   slot=torch.zeros(1, dtype=torch.int64, device=device),
+                   query_start_loc=torch.arange(2, dtype=torch.int32, device=device),
+                   seq_lens=torch.ones(1, dtype=torch.int32, device=device),
+                   block_table=torch.zeros((1, 1), dtype=torch.int32, device=device))
 
 
 def warmup(layers: Sequence[WarmupLayer], device: torch.device) -> int:
-    """Run each distinct layer signature once with a single zero token and no
-    history; returns the number of signatures run.  Synchronizes the device
-    at the end, as the reference does."""
-    count = 0
-    for layer in _distinct(layers):
-        x = torch.zeros((1, layer.heads, layer.head_dim), dtype=torch.bfloat16, device=device)
-        output = torch.empty_like(x)
-        width = page_width(layer.head_dim, layer.records)
-        cache = torch.zeros((2, 1, layer.heads, layer.page_tokens, width), dtype=torch.uint8, device=device)
-        slots = torch.zeros(1, dtype=torch.int64, device=device)
-        starts = torch.tensor([0, 1], dtype=torch.int32, device=device)
-        lengths = torch.ones(1, dtype=torch.int32, device=device)
-        table = torch.zeros((1, 1), dtype=torch.int32, device=device)
-        ops.quantize([(x, x)] * len(layer.records), cache, slots, layer.key_rotation, layer.value_rotation,
-                     layer.key_mean, layer.records, layer.reference_mode, layer.anchor_index,
-                     layer.coefficient_method)
+    """Run each distinct layer signature once: quantize one zero token into a
+    fresh one-block cache, then one attention call per loop over it (no
+    history).  Returns the number of signatures run, and synchronizes the
+    device when any ran (the reference's start-up pass,
+    install_cache.py:187-256, before the KV pool is sized)."""
+    done = set()
+    for layer in layers:
+        key = layer.signature()
+        if key in done:
+            continue
+        done.add(key)
+        call = _EmptyCall.for_layer(layer, device)
+        rotations = (layer.key_rotation, layer.value_rotation, layer.key_mean)
+        schedule = (layer.records, layer.reference_mode, layer.anchor_index)
+        pairs = [(call.token, call.token) for _ in layer.records]
+        ops.quantize(pairs, call.cache, call.slot, *rotations, *schedule, layer.coefficient_method)
         for loop in range(len(layer.records)):
-            ops.attention(x, x, x, cache, output, starts, lengths, table, layer.key_rotation, layer.value_rotation,
-                          layer.key_mean, layer.records, layer.reference_mode, layer.anchor_index, loop)
-        count += 1
-    if count:
+            ops.attention(call.token, call.token, call.token, call.cache, call.output, call.query_start_loc,
+                          call.seq_lens, call.block_table, *rotations, *schedule, loop)
+    if done:
         torch.cuda.synchronize(device)
-    return count
+    return len(done)
