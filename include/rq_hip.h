@@ -144,9 +144,15 @@ int rq_packed_prefill_attention(const void* query, int64_t query_stride, const v
  * (132 x splits + 1) x 4 bytes, about 2 000 pairs at eight splits.
  * (rq_attention_workspace_bytes covers both routes, so it may exceed the
  * scratch for a call that still fits.)
- * Every noalloc call on one GPU shares that array: calls that overlap on one
- * GPU (concurrent streams or threads) race and must be serialized by the
- * caller.  Calls no hipMalloc/hipFree and records no timing events.
+ * Every noalloc call on one GPU shares that array.  Eager calls are ordered
+ * by the library, across streams and host threads: a call on another stream
+ * than the previous call first makes its stream wait for the previous
+ * call's kernels (one event per GPU, created with the scratch lookup on the
+ * first call on that GPU; it holds no device memory).  Calls captured into a
+ * graph are not ordered against work outside the graph: replays of a graph
+ * holding noalloc calls race with other noalloc work on the same GPU and
+ * must be serialized by the caller.  Calls no hipMalloc/hipFree and records
+ * no timing events.
  */
 #define RQ_ATTENTION_NOALLOC_MAX_BYTES ((size_t)8 << 20)
 int rq_attention_noalloc(const void* query, int64_t query_stride, const void* key, int64_t key_stride,

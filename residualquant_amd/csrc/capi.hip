@@ -131,8 +131,8 @@ struct WorkspaceLayout {
 constexpr int64_t kMultiRowMinRows = 3;          // anchor-loop calls
 constexpr int64_t kMultiRowMinRowsResidual = 2;  // residual-loop calls
 
-// Several rows per request (anchor mode, D = 128) run the multi-row MFMA
-// kernels: one workgroup per (request, head, 32-row tile, history split).
+// Several rows per request (either head dim, either mode) run the multi-row
+// MFMA kernels: one workgroup per (request, head, 32-row tile, history split).
 // Splits aim at two workgroups per compute unit over `groups` =
 // requests x heads x row tiles, at most kMultiRowMaxSplits, no more than the
 // history's 32-token tiles allow (four per split, one per wave), and at least
@@ -559,32 +559,47 @@ static int attention_packed(const void* query, int64_t query_stride, const void*
 // each row, split arrival counters, query records, split partials) for
 // callers that cannot allocate.  Each GPU holds its own copy for the life of
 // the process; host code reaches it only through the address that
-// hipGetSymbolAddress returns on that device (scratch_address), never
-// through the name.  Every noalloc call on a GPU shares it, so calls that
-// overlap on one GPU race; what must start at zero (the arrival counters) is
-// cleared by the call's own kernels.
+// hipGetSymbolAddress returns on that device (ScratchState::address), never
+// through the name.  Every noalloc call on a GPU shares it; what must start
+// at zero (the arrival counters) is cleared by the call's own kernels.
+// Calls made eagerly are ordered by the library: a call on another stream
+// than the previous one first makes its stream wait for an event recorded
+// after the previous call's kernels.  Calls captured into a graph are not
+// (a capture cannot wait on work outside it): replays of such a graph must
+// not overlap other noalloc work on the same GPU.
 constexpr size_t kAttentionScratchBytes = RQ_ATTENTION_NOALLOC_MAX_BYTES;
 static __device__ __align__(256) uint8_t scratch[kAttentionScratchBytes];
 
-static std::mutex g_scratch_mutex;
-static std::vector<void*> g_scratch_address;  // per device; null until looked up
+// Per device: the scratch address, and the event and stream of the last
+// eager call (the event holds no device memory and records no timing).
+struct ScratchState {
+    void* address = nullptr;
+    hipEvent_t last_call = nullptr;
+    hipStream_t last_stream = nullptr;
+    bool has_last = false;
+};
+static std::mutex g_scratch_mutex;  // held across a call's whole enqueue
+static std::vector<ScratchState> g_scratch;
 
-// The current device's address of `scratch`, looked up once per device with
-// that device current.
-static int scratch_address(void** address) {
+// The current device's state, set up once per device with that device
+// current (held lock: g_scratch_mutex).
+static int scratch_state(ScratchState** state) {
     int device = 0;
     hipError_t status = hipGetDevice(&device);
     if (status != hipSuccess) return fail(RQ_ELAUNCH, "hipGetDevice: %s", hipGetErrorString(status));
-    std::lock_guard<std::mutex> lock(g_scratch_mutex);
-    if ((int)g_scratch_address.size() <= device) g_scratch_address.resize(device + 1, nullptr);
-    if (g_scratch_address[device] == nullptr) {
+    if ((int)g_scratch.size() <= device) g_scratch.resize(device + 1);
+    ScratchState& s = g_scratch[device];
+    if (s.address == nullptr) {
         void* ptr = nullptr;
         status = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
         if (status != hipSuccess || ptr == nullptr)
             return fail(RQ_ELAUNCH, "hipGetSymbolAddress(scratch): %s", hipGetErrorString(status));
-        g_scratch_address[device] = ptr;
+        status = hipEventCreateWithFlags(&s.last_call, hipEventDisableTiming);
+        if (status != hipSuccess)
+            return fail(RQ_ELAUNCH, "hipEventCreateWithFlags(noalloc order): %s", hipGetErrorString(status));
+        s.address = ptr;
     }
-    *address = g_scratch_address[device];
+    *state = &s;
     return RQ_OK;
 }
 
@@ -631,15 +646,32 @@ int rq_attention_noalloc(const void* query, int64_t query_stride, const void* ke
                          hipStream_t stream) {
     // The route the call takes (per-row or multi-row kernels) checks its own
     // workspace size against the scratch, before any device work.
-    void* workspace = nullptr;
-    const int status = scratch_address(&workspace);
+    std::lock_guard<std::mutex> lock(g_scratch_mutex);
+    ScratchState* state = nullptr;
+    int status = scratch_state(&state);
     if (status != RQ_OK) return status;
-    return attention_packed(query, query_stride, key, key_stride, value, value_stride, output, output_stride,
-                            rows, heads, head_dim, kv_cache, num_blocks, page_tokens, page_width,
-                            query_start_loc, seq_lens, requests, block_table, block_table_stride, max_pages,
-                            key_rotation, value_rotation, key_mean, records, bits, groups, reference_mode,
-                            anchor_index, loop_index, workspace, kAttentionScratchBytes, stream, false, false,
-                            true);
+    hipStreamCaptureStatus capture = hipStreamCaptureStatusNone;
+    hipError_t error = hipStreamIsCapturing(stream, &capture);
+    if (error != hipSuccess) return fail(RQ_ELAUNCH, "hipStreamIsCapturing: %s", hipGetErrorString(error));
+    const bool eager = capture == hipStreamCaptureStatusNone;
+    if (eager && state->has_last && state->last_stream != stream) {
+        // The previous call ran on another stream: this one starts after it.
+        error = hipStreamWaitEvent(stream, state->last_call, 0);
+        if (error != hipSuccess) return fail(RQ_ELAUNCH, "hipStreamWaitEvent: %s", hipGetErrorString(error));
+    }
+    status = attention_packed(query, query_stride, key, key_stride, value, value_stride, output, output_stride,
+                              rows, heads, head_dim, kv_cache, num_blocks, page_tokens, page_width,
+                              query_start_loc, seq_lens, requests, block_table, block_table_stride, max_pages,
+                              key_rotation, value_rotation, key_mean, records, bits, groups, reference_mode,
+                              anchor_index, loop_index, state->address, kAttentionScratchBytes, stream, false,
+                              false, true);
+    if (status == RQ_OK && eager) {
+        error = hipEventRecord(state->last_call, stream);
+        if (error != hipSuccess) return fail(RQ_ELAUNCH, "hipEventRecord: %s", hipGetErrorString(error));
+        state->last_stream = stream;
+        state->has_last = true;
+    }
+    return status;
 }
 
 int rq_dequantize(const void* kv_cache, int64_t num_blocks, int heads, int page_tokens, int page_width,

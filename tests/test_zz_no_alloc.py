@@ -26,16 +26,18 @@ def _schedule(records):
     return bits, groups
 
 
-def _call(lib, d, device, cache, loop, noalloc):
+def _call(lib, d, device, cache, loop, noalloc, stream=None, sync=True, keep=None):
     g = d.group
     q, k, v = (t.to(device) for t in (d.query, d.key, d.value))
     out = torch.full_like(q, float("nan"))
     starts, lens, table = (t.to(device) for t in (d.query_start_loc, d.seq_lens, d.table))
     kr, vr, km = g.device_args(device)
+    if keep is not None:  # the inputs must outlive a call that is not synchronized here
+        keep.extend([q, k, v, starts, lens, table, kr, vr, km])
     rows, heads, dim = q.shape
     bits, groups = _schedule(g.records)
     ptr = (lambda t: None if t is None else t.data_ptr())
-    stream = torch.cuda.current_stream(device).cuda_stream
+    stream = (stream or torch.cuda.current_stream(device)).cuda_stream
     common = [q.data_ptr(), q.stride(0), k.data_ptr(), k.stride(0), v.data_ptr(), v.stride(0),
               out.data_ptr(), out.stride(0), rows, heads, dim, cache.data_ptr(), cache.size(1),
               cache.size(3), cache.size(4), starts.data_ptr(), lens.data_ptr(), len(d.lengths),
@@ -48,7 +50,8 @@ def _call(lib, d, device, cache, loop, noalloc):
         workspace = torch.empty(size, dtype=torch.uint8, device=device)
         status = lib.rq_attention(*common, workspace.data_ptr(), size, stream)
     _lib.check(status)
-    torch.cuda.synchronize(device)
+    if sync:
+        torch.cuda.synchronize(device)
     return out
 
 
@@ -72,6 +75,29 @@ def test_noalloc_matches_workspace_entry_point(oracle, device):
             assert torch.equal(got.view(torch.int16), want.view(torch.int16)), f"loop {loop}"
             err = np.abs(got.float().cpu().numpy() - oracle_attention(oracle, d, expected_cache, loop))
             assert err.max() <= 2e-2 and err.mean() <= 1e-3, (err.max(), err.mean())
+
+
+def test_noalloc_calls_on_two_streams_are_ordered(oracle, device):
+    """Back-to-back noalloc calls on two streams with no synchronization
+    between them: the library makes the second stream wait for the first
+    call (both share the scratch's arrival counters and partials), so each
+    output equals the workspace entry point's."""
+    lib = _lib.lib()
+    first = make_decode([700, 300, 129, 50], 4, 128, OURO_G32, seed=71)  # split over several workgroups
+    second = make_decode([600, 90, 33], 4, 128, OURO_G32, seed=72)
+    caches = [torch.from_numpy(d.group.oracle_cache(oracle)).to(device) for d in (first, second)]
+    for loop in (0, 3):
+        print(f"[case] noalloc two streams loop={loop}", flush=True)
+        want = [_call(lib, d, device, c, loop, noalloc=False) for d, c in zip((first, second), caches)]
+        streams = [torch.cuda.Stream(device), torch.cuda.Stream(device)]
+        keep = []
+        for s in streams:
+            s.wait_stream(torch.cuda.current_stream(device))
+        got = [_call(lib, d, device, c, loop, noalloc=True, stream=s, sync=False, keep=keep)
+               for d, c, s in zip((first, second), caches, streams)]
+        torch.cuda.synchronize(device)
+        for g, w in zip(got, want):
+            assert torch.equal(g.view(torch.int16), w.view(torch.int16)), f"loop {loop}"
 
 
 def test_noalloc_one_row_decode_at_batch_128(device):
