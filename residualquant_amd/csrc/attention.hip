@@ -112,6 +112,21 @@ __device__ __forceinline__ float rows_max(float x) {
                        __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), 48))));
 }
 
+// A workgroup barrier for data exchanged through LDS by ordinary LDS
+// accesses: this wave's LDS operations complete (s_waitcnt lgkmcnt(0)), then
+// s_barrier; the empty asm statements keep the compiler from moving memory
+// accesses across it.  __syncthreads (and an LDS release fence, which also
+// covers LDS writes of DMA loads) waits for every load in flight
+// (vmcnt(0)): in the decode prologues that would hold the query preparation
+// until the first page loads, issued before it, have landed.  Not for data
+// written to LDS by DMA loads or read from global memory.
+__device__ __forceinline__ void lds_barrier() {
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0); vmcnt and expcnt not waited
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+}
+
 // ------------------------------------------------------------------ prepare
 
 
@@ -170,8 +185,10 @@ __device__ __forceinline__ void prepare_stage(const AttentionParams& p, const Pr
 // (FP32, log2 units) and its four nibble planes in the INT4 and INT2 word
 // orders (prepare.cuh:13-229).  Called by every thread of a workgroup of 128
 // or 256 threads (threads c >= D contribute nothing) after prepare_stage;
-// `rotation_lds` holds D * D halves.  Returns after a barrier with `record`
-// complete.
+// `rotation_lds` holds D * D halves.  It reads no global memory, and its
+// barriers order LDS only, so page loads issued before it stay in flight.
+// Returns after a barrier with `record` complete when `record` is in LDS (a
+// record in global memory is read by a later launch).
 template <int D, int Threads>
 __device__ __forceinline__ void prepare_record(const AttentionParams& p, int head,
                                                const PrepareInputs<D, Threads>& in, float* record,
@@ -186,7 +203,7 @@ __device__ __forceinline__ void prepare_record(const AttentionParams& p, int hea
     const float q = active ? bf16_f32(in.q_bits) : 0.f;
     const float k_live = active ? bf16_f32(in.k_bits) : 0.f;
     if (c < 128) q_lds[c] = q;
-    __syncthreads();
+    lds_barrier();
 
     float qr = q;
     if (p.key_rotation != nullptr) {
@@ -238,7 +255,7 @@ __device__ __forceinline__ void prepare_record(const AttentionParams& p, int hea
                                       __int_as_float(__builtin_amdgcn_readlane(__float_as_int(q16), 16))
                                 : __int_as_float(__builtin_amdgcn_readlane(__float_as_int(q16), 32)) +
                                       __int_as_float(__builtin_amdgcn_readlane(__float_as_int(q16), 48));
-    __syncthreads();
+    lds_barrier();
 
     float sums[4] = {0.f, 0.f, 0.f, 0.f};
     for (int w = 0; w < waves; ++w) {
@@ -273,7 +290,7 @@ __device__ __forceinline__ void prepare_record(const AttentionParams& p, int hea
         if (active && (c & 7) == 0) planes4[j * 16 + c / 8] = w4;
         if (active && (c & 14) == 0) planes2[j * 16 + 2 * (c / 16) + (c & 1)] = w2;
     }
-    __syncthreads();
+    lds_barrier();
 }
 
 // Separate prepare pass (used when a (row, head) is split over several
@@ -1014,7 +1031,7 @@ void decode_kernel(AttentionParams p) {
     float q_sum_a[2], q_sum_l[2];
     group_sums<GA>(prep, lq, q_sum_a);
     group_sums<GL>(prep, lq, q_sum_l);
-    __syncthreads();
+    lds_barrier();
     const uint32_t* planes_a = &planes_lds[lq][0][0];
     const uint32_t* planes_l = &planes_lds[lq][4][0];
 
@@ -1503,16 +1520,20 @@ void decode96_dma_kernel(AttentionParams p) {
     // share vmcnt with the DMA loads).
     static_assert(kDma96Stages == 3, "the loop below rotates three stages");
     PagePair pages0 = pages_of(0), pages1 = pages_of(1), pages2;
+    if (!p.fused_prepare) {
+        const float* src = p.prep + rh * (int64_t)kPrepFloats;
+        for (int i = threadIdx.x; i < kPrepFloats; i += kDecodeThreads) prep_lds[i] = src[i];
+    }
+    // Every load other than the pages' has landed here (the prologue's
+    // inputs, the prepared record), so no wait after the page loads below
+    // has to count them: the prologue's barriers order LDS only and the
+    // first stages stream while the query record is prepared.
+    wait_vmcnt<0>();
     issue(pages0, Stage0{});
     issue(pages1, Stage1{});
 
-    if (p.fused_prepare) {
-        prepare_record<D, kDecodeThreads>(p, head, in, prep_lds, rotation_lds);
-    } else {
-        const float* src = p.prep + rh * (int64_t)kPrepFloats;
-        for (int i = threadIdx.x; i < kPrepFloats; i += kDecodeThreads) prep_lds[i] = src[i];
-        __syncthreads();
-    }
+    if (p.fused_prepare) prepare_record<D, kDecodeThreads>(p, head, in, prep_lds, rotation_lds);
+    else lds_barrier();
     const float* prep = prep_lds;
     const float delta = prep[0];
     const float q_mean_anchor = h == 0 ? prep[2] : 0.f;  // added once per token
@@ -1528,7 +1549,7 @@ void decode96_dma_kernel(AttentionParams p) {
                                (bits == 2 ? kPrepPlanes : 0);
         half_planes[record][half][word][plane] = base[plane * 16 + 6 * half + word];
     }
-    __syncthreads();
+    lds_barrier();
     const uint32_t (*planes_a)[4] = half_planes[0][h];
     const uint32_t (*planes_l)[4] = half_planes[1][h];
 
