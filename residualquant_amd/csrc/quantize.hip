@@ -570,6 +570,7 @@ __global__ __launch_bounds__(kMfmaThreads) void quantize_mfma_kernel(QuantizePar
         F32x16 acc[2];
         if constexpr (Rotated) {
             acc[0] = acc[1] = F32x16{};
+            float4 a, b0, b1;  // the operands of the next group of k
 #pragma unroll
             for (int chunk = 0; chunk < kChunks; ++chunk) {
                 // kChunks is even: chunk c of every pass sits in buffer c & 1.
@@ -587,11 +588,29 @@ __global__ __launch_bounds__(kMfmaThreads) void quantize_mfma_kernel(QuantizePar
                 // its first use and every chunk waits a full round trip.
                 __asm__ volatile("" ::: "memory");
                 const float4* a_read = &stage[chunk & 1][lane64 & 15][0];
+                // Operands one group ahead: group g + 1's reads are issued
+                // before group g's MFMAs, and the next chunk's first group
+                // before this chunk's last (its A was staged at this chunk's
+                // start); a pass's first group is read here.
+                if (chunk == 0) {
+                    a = a_read[0];
+                    b0 = rotation4[0];
+                    b1 = rotation4[64];
+                }
 #pragma unroll
                 for (int g = 0; g < C / 4; ++g) {
-                    const float4 a = a_read[g];
-                    const float4 b0 = rotation4[((chunk * C) / 2 + 2 * g) * 64];
-                    const float4 b1 = rotation4[((chunk * C) / 2 + 2 * g + 1) * 64];
+                    const float4 ca = a, cb0 = b0, cb1 = b1;
+                    if (g + 1 < C / 4) {
+                        a = a_read[g + 1];
+                        b0 = rotation4[((chunk * C) / 2 + 2 * g + 2) * 64];
+                        b1 = rotation4[((chunk * C) / 2 + 2 * g + 3) * 64];
+                    } else if (chunk + 1 < kChunks) {
+                        a = stage[(chunk + 1) & 1][lane64 & 15][0];
+                        b0 = rotation4[(((chunk + 1) * C) / 2) * 64];
+                        b1 = rotation4[(((chunk + 1) * C) / 2 + 1) * 64];
+                    }
+                    {
+                    const float4 a = ca, b0 = cb0, b1 = cb1;
                     acc[0] = __builtin_amdgcn_mfma_f32_16x16x1f32(a.x, b0.x, acc[0], 0, 0, 0);
                     acc[1] = __builtin_amdgcn_mfma_f32_16x16x1f32(a.x, b0.y, acc[1], 0, 0, 0);
                     acc[0] = __builtin_amdgcn_mfma_f32_16x16x1f32(a.y, b0.z, acc[0], 0, 0, 0);
@@ -600,6 +619,10 @@ __global__ __launch_bounds__(kMfmaThreads) void quantize_mfma_kernel(QuantizePar
                     acc[1] = __builtin_amdgcn_mfma_f32_16x16x1f32(a.z, b1.y, acc[1], 0, 0, 0);
                     acc[0] = __builtin_amdgcn_mfma_f32_16x16x1f32(a.w, b1.z, acc[0], 0, 0, 0);
                     acc[1] = __builtin_amdgcn_mfma_f32_16x16x1f32(a.w, b1.w, acc[1], 0, 0, 0);
+                    }
+                    // The next group's reads go out ahead of these MFMAs.
+                    __builtin_amdgcn_sched_group_barrier(0x100, 3, 0);
+                    __builtin_amdgcn_sched_group_barrier(0x008, 8, 0);
                 }
                 // Nothing of the next chunk moves above this chunk's MFMAs,
                 // so the load issued at its start has the chunk to land.
