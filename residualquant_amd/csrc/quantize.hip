@@ -50,9 +50,13 @@ constexpr int kStageRecords = 4;  // record slots per staged (token, k)
 
 // ---------------------------------------------------------------- lanes
 
+// Lane exchange within DPP rows.  Every control used here reads a lane of
+// the same 16-lane row, so all sources are valid and bound_ctrl never
+// applies; with it set the compiler folds the exchange into a consuming VOP2
+// add (v_add_f32_dpp) instead of a separate v_mov_b32_dpp.
 template <int Control>
 __device__ __forceinline__ float dpp(float v) {
-    return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), Control, 0xf, 0xf, false));
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), Control, 0xf, 0xf, true));
 }
 
 constexpr int kXor1 = 0xB1;        // quad_perm [1,0,3,2]
