@@ -93,6 +93,15 @@ __device__ __forceinline__ uint32_t e4m3_pair(float low_value, float high_value)
     return (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(a, b, 0, false) & 0xffffu;
 }
 
+// floor(-q + 0.5) as an integer in one instruction (v_cvt_rpi_i32_f32 with
+// a negated source), i.e. -ceil(q - 0.5): checked on gfx950 against the
+// clamped ceil(q - 0.5) of every finite FP32 q, for both code widths.
+__device__ __forceinline__ int round_half_up_negated(float q) {
+    int r;
+    asm("v_cvt_rpi_i32_f32_e64 %0, -%1" : "=v"(r) : "v"(q));
+    return r;
+}
+
 __device__ __forceinline__ float e4m3_value(uint32_t code) {
     return __builtin_amdgcn_cvt_f32_fp8((int)code, 0);
 }
@@ -205,7 +214,9 @@ __device__ __forceinline__ void commit_record(float (&x)[2][4], const bool (&act
         // RN(1/scale); 0 for a zero (or NaN) scale, which yields code 0.
         const float reciprocal = inverse_scale[(parameters[h] >> 8) & 0x7fu];
 
-        packed[h] = 0;
+        // The codes are packed negated: sum of (-code_i) << (i bits), mod 2^32,
+        // then one negation (the fields do not overlap).
+        uint32_t negated = 0;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             // |a| <= 2^100 keeps q0 finite; beyond it the code saturates anyway.
@@ -213,16 +224,19 @@ __device__ __forceinline__ void commit_record(float (&x)[2][4], const bool (&act
             const float q0 = a * reciprocal;
             const float r = fmaf(-q0, scale, a);
             const float q = fmaf(r, reciprocal, q0);
-            // floor(q) + (frac(q) > 0.5) == ceil(q - 0.5), clamped to [0, levels].
-            const uint32_t code = (uint32_t)__builtin_amdgcn_fmed3f(ceilf(q - 0.5f), 0.0f, levels);
-            packed[h] |= code << (i * bits);
+            // floor(q) + (frac(q) > 0.5) == ceil(q - 0.5), clamped to [0, levels],
+            // which equals ceil(q' - 0.5) for q' = q clamped to [0, levels]; its
+            // negation is floor(-q' + 0.5).
+            const int neg_code = round_half_up_negated(__builtin_amdgcn_fmed3f(q, 0.0f, levels));
+            negated += (uint32_t)neg_code << (i * bits);
             if (restore) {
-                uint32_t value = bf16_rn(fmaf((float)code, scale, offset));
+                uint32_t value = bf16_rn(fmaf(-(float)neg_code, scale, offset));
                 if (has_mean) value = bf16_rn(bf16_f32(value) + bf16_f32(bf16_rn(mean[h][i])));
                 if (!is_anchor) value = bf16_fma_rn(reference[h][i], alpha, bf16_f32(value));
                 reference[h][i] = bf16_f32(value);
             }
         }
+        packed[h] = 0u - negated;
     }
 
     if (store) {
