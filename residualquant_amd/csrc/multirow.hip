@@ -22,6 +22,12 @@
 // per (request, head, 32-row tile) merges the splits, applies R_v^T (on
 // MFMA) and adds the live tokens.
 //
+// Calls whose requests average 16 rows or fewer take 16-row tiles instead:
+// the same pages and dequantization, with the tile's products on
+// v_mfma_f32_16x16x32 (S^T: 2 token halves x D / 32 steps; O^T: D / 16
+// channel blocks, one 32-token step each), which halves the matrix work and
+// the softmax's per-lane scores of a tile that would otherwise be half empty.
+//
 // A lane dequantizes one token's 32-channel quarter of a 16-token unit
 // (lane = token x quarter); at D = 96 the fourth quarter's lanes load a copy
 // of the first quarter's bytes and store nothing.
@@ -40,7 +46,9 @@
 //
 // Lane layouts of v_mfma_f32_32x32x16_bf16 (checked on gfx950): A row l % 32,
 // k 8 (l / 32) + e; B column l % 32, k 8 (l / 32) + e; C register r holds row
-// 8 (r / 4) + 4 (l / 32) + r % 4, column l % 32.
+// 8 (r / 4) + 4 (l / 32) + r % 4, column l % 32.  Of v_mfma_f32_16x16x32:
+// A row l % 16, k 8 (l / 16) + e; B column l % 16, k 8 (l / 16) + e; C
+// register r holds row 4 (l / 16) + r, column l % 16.
 #include "rq_chain.h"
 #include "rq_device.h"
 #include "rq_kernels.h"
@@ -52,25 +60,30 @@ namespace {
 typedef __bf16 Bf16x8 __attribute__((ext_vector_type(8)));
 typedef _Float16 F16x8 __attribute__((ext_vector_type(8)));
 typedef float F32x16 __attribute__((ext_vector_type(16)));
+typedef float F32x4 __attribute__((ext_vector_type(4)));
 
 constexpr int kThreads = 256;
 constexpr int kWaves = 4;
 constexpr int kTile = 32;  // tokens per MFMA tile (two 16-token units)
 constexpr int kMaxD = 128;
 
-// LDS geometry of the stream kernel for head dim D.
-template <int D>
+// LDS geometry of the stream kernel for head dim D and TR-row tiles.
+template <int D, int TR = 32>
 struct Geometry {
     static constexpr int Quarters = D / 32;  // 32-channel quarters a token's lanes cover
     static constexpr int Parts = D / 16;     // 16-channel parts (MFMA k steps of the scores)
     static constexpr int KS = D + 8;         // K tile row stride (halves)
-    // V tile [token][VROW] BF16.  At D = 128 the row is unpadded and its four
-    // 32-channel chunks are swizzled by token (chunk q at position q ^
-    // (token % 4)), which keeps the transposed reads free of bank conflicts;
-    // at D = 96 the rows are padded to 104 halves instead (16-byte aligned
-    // rows for the stores, 8-byte aligned reads).
+    // V tile [token][VROW] BF16.  At D = 128 the row is unpadded and
+    // swizzled by token, which keeps the transposed reads free of bank
+    // conflicts: for 32-row tiles (a half-wave reads 4 tokens x 32 channels)
+    // its four 32-channel chunks sit at positions q ^ (token % 4), for 16-row
+    // tiles (8 tokens x 16 channels) its eight 16-channel units at positions
+    // u ^ (token % 8).  At D = 96 the rows are padded instead, to 104 halves
+    // (32-row tiles) or 112 (16-row tiles: a stride of 56 banks puts 8
+    // consecutive tokens on distinct 8-bank groups); rows stay 16-byte
+    // aligned for the stores and 8-byte aligned for the reads.
     static constexpr bool kSwizzleV = D == 128;
-    static constexpr int VROW = D == 128 ? D : D + 8;
+    static constexpr int VROW = D == 128 ? D : (TR == 32 ? D + 8 : D + 16);
     static constexpr int kVBytes = D == 128 ? D * (kTile + 8) * 2 : kTile * VROW * 2;
     static constexpr int kWaveBytes = kTile * KS * 2 + kVBytes + kTile * 4;  // K (FP16), V (BF16), alpha_K
     static constexpr int kLdsBytes = kWaves * kWaveBytes;
@@ -105,6 +118,25 @@ __device__ __forceinline__ F32x16 mfma(Bf16x8 a, Bf16x8 b, F32x16 c) {
 __device__ __forceinline__ F32x16 mfma(F16x8 a, F16x8 b, F32x16 c) {
     return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
 }
+
+__device__ __forceinline__ F32x4 mfma(Bf16x8 a, Bf16x8 b, F32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
+
+__device__ __forceinline__ F32x4 mfma(F16x8 a, F16x8 b, F32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+}
+
+// The O^T accumulator tiles of one lane: D / 32 of 32 x 32 (32-row tiles) or
+// D / 16 of 16 x 16 (16-row tiles).
+template <int TR>
+struct OutTile {
+    typedef F32x16 Type;
+};
+template <>
+struct OutTile<16> {
+    typedef F32x4 Type;
+};
 
 __device__ __forceinline__ uint32_t f16_bits(float x) { return __builtin_bit_cast(uint16_t, (_Float16)x); }
 
@@ -365,16 +397,16 @@ struct ChainDecoder {
     }
 };
 
-template <int D, int PT, class Decoder>
+template <int D, int PT, int TR, class Decoder>
 __device__ __forceinline__ void multirow_stream(const MultiRowParams& p, Decoder& dec, uint8_t* lds,
                                                 int* split_blocks) {
-    using G = Geometry<D>;
+    using G = Geometry<D, TR>;
     constexpr int KS = G::KS;
     constexpr int QRS = G::QRS;
     const int request = blockIdx.x;
     const int head = blockIdx.y;
     const int split = (int)blockIdx.z % p.splits;
-    const int row0 = 32 * ((int)blockIdx.z / p.splits);
+    const int row0 = TR * ((int)blockIdx.z / p.splits);
     const int first = p.query_start_loc[request];
     int n = p.query_start_loc[request + 1] - first;
     if (first < 0 || first >= p.rows) return;  // uniform over the workgroup, before any barrier
@@ -400,7 +432,8 @@ __device__ __forceinline__ void multirow_stream(const MultiRowParams& p, Decoder
     // q' = (q . R_k) * log2(e) / sqrt(D) for the tile's rows, held as FP16
     // q' 2^-e with 2^e the row's power-of-two scale, and the row dots
     // q'.bf16(mu_A) (added per token times alpha_L) and q'.mu_L (the shift of
-    // the history scores against the live ones).
+    // the history scores against the live ones).  The prologue always
+    // prepares 32 rows from row0; a 16-row tile uses the first 16.
     uint16_t* q16 = reinterpret_cast<uint16_t*>(lds + G::kQ16Offset);
     uint16_t* r_k = reinterpret_cast<uint16_t*>(lds + G::kRkOffset);
     float* q_raw = reinterpret_cast<float*>(lds + G::kQrawOffset);
@@ -576,14 +609,20 @@ __device__ __forceinline__ void multirow_stream(const MultiRowParams& p, Decoder
         }
     }
     __syncthreads();
-    // Q'^T operand (B of S^T = K Q'^T): chunk m holds channels 16 m + 8 half + e.
-    F16x8 q_operand[G::Parts];
+    // Q'^T operand (B of S^T = K Q'^T) for the lane's row of the tile,
+    // tile_row: chunk m holds channels 16 m + 8 half + e (32-row tiles:
+    // tile_row = l % 32, k_group = l / 32) or 32 m + 8 k_group + e (16-row
+    // tiles: tile_row = l % 16, k_group = l / 16).
+    constexpr int kQChunks = TR == 32 ? G::Parts : D / 32;
+    const int tile_row = lane & (TR - 1);
+    const int k_group = TR == 32 ? half : lane >> 4;
+    F16x8 q_operand[kQChunks];
 #pragma unroll
-    for (int m = 0; m < G::Parts; ++m)
-        q_operand[m] = *reinterpret_cast<const F16x8*>(&q_p[column * KS + 16 * m + 8 * half]);
-    const float q_mu_anchor = q_mu[column];
-    const float row_scale = q_scale[column];
-    if (split == 0 && tid < 32 && row0 + tid < n)
+    for (int m = 0; m < kQChunks; ++m)
+        q_operand[m] = *reinterpret_cast<const F16x8*>(&q_p[tile_row * KS + (TR == 32 ? 16 : 32) * m + 8 * k_group]);
+    const float q_mu_anchor = q_mu[tile_row];
+    const float row_scale = q_scale[tile_row];
+    if (split == 0 && tid < TR && row0 + tid < n)
         p.row_shift[(int64_t)(first + row0 + tid) * p.heads + head] = q_mu[32 + tid];
     __syncthreads();  // the scratch becomes the tiles
 
@@ -591,16 +630,23 @@ __device__ __forceinline__ void multirow_stream(const MultiRowParams& p, Decoder
     uint16_t* k_tile = reinterpret_cast<uint16_t*>(lds + wave * G::kWaveBytes);
     uint16_t* v_tile = k_tile + kTile * KS;  // [token][VROW] BF16
     float* alpha_tile = reinterpret_cast<float*>(reinterpret_cast<uint8_t*>(v_tile) + G::kVBytes);
-    // V^T operand reads (ds_read_b64_tr_b16): lane 16 g + 4 a + b (g = 2 half
-    // + g') addresses token 4 half + a of an 8-token block, channels
-    // 32 t + 16 g' + 4 b..+3, and receives channel 32 t + column of tokens
-    // 4 half..+3.  With the D = 128 swizzle, chunk 4 t + 2 g' + b / 2 sits at
-    // position chunk ^ 4 a.
+    // V^T operand reads (ds_read_b64_tr_b16).  32-row tiles: lane 16 g + 4 a
+    // + b (g = 2 half + g') addresses token 4 half + a of an 8-token block,
+    // channels 32 t + 16 g' + 4 b..+3, and receives channel 32 t + column of
+    // tokens 4 half..+3; with the D = 128 swizzle, the 32-channel chunk t
+    // sits at position t ^ a.  16-row tiles: lane 16 g + 4 a + b addresses
+    // token 4 g + a (and 16 + 4 g + a), channels 16 t + 4 b..+3, and receives
+    // channel 16 t + l % 16 of tokens 4 g..+3 (16 + 4 g..+3); with the
+    // swizzle, the 16-channel unit t sits at position t ^ (token % 8).
     const int tr_a = (lane >> 2) & 3, tr_b = lane & 3, tr_g = (lane >> 4) & 1;
-    const int v_lane = G::kSwizzleV ? D * (4 * half + tr_a) + 32 * tr_a + 16 * tr_g + 4 * tr_b
-                                    : G::VROW * (4 * half + tr_a) + 16 * tr_g + 4 * tr_b;
+    const int tr_token = TR == 32 ? 4 * half + tr_a : 4 * k_group + tr_a;
+    const int v_lane = TR == 32 ? (G::kSwizzleV ? D * tr_token + 32 * tr_a + 16 * tr_g + 4 * tr_b
+                                                : G::VROW * tr_token + 16 * tr_g + 4 * tr_b)
+                                : (G::kSwizzleV ? D * tr_token + 16 * (tr_token & 7) + 4 * tr_b
+                                                : G::VROW * tr_token + 4 * tr_b);
     auto v_read = [&](int t) __attribute__((always_inline)) {
-        return G::kSwizzleV ? v_lane ^ (32 * t) : v_lane + 32 * t;
+        constexpr int kStep = TR == 32 ? 32 : 16;
+        return G::kSwizzleV ? v_lane ^ (kStep * t) : v_lane + kStep * t;
     };
     const int unit_token = lane >> 2;  // token within a 16-token unit
     const int quarter = lane & 3;      // 32-channel quarter
@@ -633,11 +679,16 @@ __device__ __forceinline__ void multirow_stream(const MultiRowParams& p, Decoder
                          unit_first % PT + unit_token};
     };
 
-    F32x16 out[G::Quarters];
+    // O^T: tile t of a 32-row tile holds channels 32 t.. (register r: channel
+    // 32 t + 8 (r / 4) + 4 half + r % 4 of row tile_row), of a 16-row tile
+    // channels 16 t.. (register r: channel 16 t + 4 k_group + r).
+    constexpr int kOutTiles = TR == 32 ? G::Quarters : G::Parts;
+    constexpr int kOutRegs = TR == 32 ? 16 : 4;
+    typename OutTile<TR>::Type out[kOutTiles];
 #pragma unroll
-    for (int t = 0; t < G::Quarters; ++t)
+    for (int t = 0; t < kOutTiles; ++t)
 #pragma unroll
-        for (int r = 0; r < 16; ++r) out[t][r] = 0.f;
+        for (int r = 0; r < kOutRegs; ++r) out[t][r] = 0.f;
     float running_max = -__builtin_inff();
     float running_sum = 0.f;
 
@@ -687,13 +738,25 @@ __device__ __forceinline__ void multirow_stream(const MultiRowParams& p, Decoder
                     for (int c = 0; c < 16; ++c) vw[c] = valid ? vw[c] : 0u;
                 }
                 if (quarter_active) {
-                    // Row-major V: the lane's 4 chunks of 8 channels (at D =
-                    // 128 at chunk positions 4 (quarter ^ (token % 4)) + i).
-                    const int chunk = G::kSwizzleV ? (quarter ^ (local & 3)) : quarter;
-                    uint4* v_dst = reinterpret_cast<uint4*>(&v_tile[local * G::VROW + 32 * chunk]);
+                    if (TR == 16 && G::kSwizzleV) {
+                        // The lane's two 16-channel units 2 quarter and
+                        // 2 quarter + 1 at positions unit ^ (token % 8).
+                        uint4* lo_dst = reinterpret_cast<uint4*>(&v_tile[local * G::VROW + 16 * ((2 * quarter) ^ (local & 7))]);
+                        uint4* hi_dst =
+                            reinterpret_cast<uint4*>(&v_tile[local * G::VROW + 16 * ((2 * quarter + 1) ^ (local & 7))]);
+                        lo_dst[0] = make_uint4(vw[0], vw[1], vw[2], vw[3]);
+                        lo_dst[1] = make_uint4(vw[4], vw[5], vw[6], vw[7]);
+                        hi_dst[0] = make_uint4(vw[8], vw[9], vw[10], vw[11]);
+                        hi_dst[1] = make_uint4(vw[12], vw[13], vw[14], vw[15]);
+                    } else {
+                        // Row-major V: the lane's 4 chunks of 8 channels (at D =
+                        // 128 at chunk positions 4 (quarter ^ (token % 4)) + i).
+                        const int chunk = G::kSwizzleV ? (quarter ^ (local & 3)) : quarter;
+                        uint4* v_dst = reinterpret_cast<uint4*>(&v_tile[local * G::VROW + 32 * chunk]);
 #pragma unroll
-                    for (int c = 0; c < 4; ++c)
-                        v_dst[c] = make_uint4(vw[4 * c], vw[4 * c + 1], vw[4 * c + 2], vw[4 * c + 3]);
+                        for (int c = 0; c < 4; ++c)
+                            v_dst[c] = make_uint4(vw[4 * c], vw[4 * c + 1], vw[4 * c + 2], vw[4 * c + 3]);
+                    }
                 }
             };
             const float alpha_k = dec.unit(unit_pages(next_first), unit_pages(two_on_first), store_k, store_v);
@@ -705,68 +768,143 @@ __device__ __forceinline__ void multirow_stream(const MultiRowParams& p, Decoder
         // call 153.2 -> 151.4 us at 16 requests x 16 rows x 8k).
         __builtin_amdgcn_s_setprio(1);
 
-        // S^T: register r of lane l holds token 8 (r / 4) + 4 half + r % 4 against row `column`.
-        F32x16 s;
+        if constexpr (TR == 16) {
+            // S^T in two 16-token halves: register r of s[h] holds token
+            // 16 h + 4 k_group + r against row tile_row (the A operand's lane
+            // l % 16 takes token 16 h + l % 16).
+            F32x4 s[2];
 #pragma unroll
-        for (int r = 0; r < 16; ++r) s[r] = 0.f;
-        const uint16_t* k_row = &k_tile[column * KS + 8 * half];
+            for (int h = 0; h < 2; ++h) {
 #pragma unroll
-        for (int m = 0; m < G::Parts; ++m)
-            s = mfma(*reinterpret_cast<const F16x8*>(k_row + 16 * m), q_operand[m], s);
+                for (int r = 0; r < 4; ++r) s[h][r] = 0.f;
+                const uint16_t* k_row = &k_tile[(16 * h + tile_row) * KS + 8 * k_group];
+#pragma unroll
+                for (int m = 0; m < kQChunks; ++m)
+                    s[h] = mfma(*reinterpret_cast<const F16x8*>(k_row + 32 * m), q_operand[m], s[h]);
+            }
+#pragma unroll
+            for (int h = 0; h < 2; ++h)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const int local = 16 * h + 4 * k_group + r;
+                    float x = s[h][r] * row_scale;
+                    if (mean_anchor) x = fmaf(alpha_tile[local], q_mu_anchor, x);
+                    s[h][r] = x;
+                }
+            if (kTile * tile + kTile > history) {
+                asm volatile("");
+#pragma unroll
+                for (int h = 0; h < 2; ++h)
+#pragma unroll
+                    for (int r = 0; r < 4; ++r)
+                        s[h][r] = kTile * tile + 16 * h + 4 * k_group + r < history ? s[h][r] : -__builtin_inff();
+            }
+            // The row's scores sit in lanes l % 16 + 16 k_group.
+            float tile_max = -__builtin_inff();
+#pragma unroll
+            for (int h = 0; h < 2; ++h)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) tile_max = fmaxf(tile_max, s[h][r]);
+            tile_max = fmaxf(tile_max, __shfl_xor(tile_max, 16));
+            tile_max = fmaxf(tile_max, __shfl_xor(tile_max, 32));
+            const float new_max = fmaxf(running_max, tile_max);
+            const float base = new_max == -__builtin_inff() ? 0.f : new_max;
+            const float rescale = __builtin_amdgcn_exp2f(running_max - base);
+            running_max = new_max;
+            // P^T in BF16 as the B operand of O^T += V^T P^T: k-slot
+            // 8 k_group + e is token 4 k_group + e (s[0][e]) for e < 4 and
+            // 16 + 4 k_group + e - 4 (s[1][e - 4]) for e >= 4.
+            float tile_sum = 0.f;
+            Bf16x8 p_operand;
+#pragma unroll
+            for (int h = 0; h < 2; ++h)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const float w = __builtin_amdgcn_exp2f(s[h][r] - base);
+                    p_operand[4 * h + r] = (__bf16)w;
+                    tile_sum += w;
+                }
+            tile_sum += __shfl_xor(tile_sum, 16);
+            tile_sum += __shfl_xor(tile_sum, 32);
+            running_sum = running_sum * rescale + tile_sum;
+            if (!__all(rescale == 1.0f)) {
+#pragma unroll
+                for (int t = 0; t < kOutTiles; ++t)
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) out[t][r] *= rescale;
+            }
+#pragma unroll
+            for (int t = 0; t < kOutTiles; ++t) {
+                // Tokens 4 k_group + 0..3 and 16 + 4 k_group + 0..3, as P^T's k-slots.
+                const Short4 lo = read_transposed(v_tile + v_read(t));
+                const Short4 hi = read_transposed(v_tile + 16 * G::VROW + v_read(t));
+                out[t] = mfma(__builtin_bit_cast(Bf16x8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7)),
+                              p_operand, out[t]);
+            }
+        } else {
+            // S^T: register r of lane l holds token 8 (r / 4) + 4 half + r % 4 against row `column`.
+            F32x16 s;
+#pragma unroll
+            for (int r = 0; r < 16; ++r) s[r] = 0.f;
+            const uint16_t* k_row = &k_tile[column * KS + 8 * half];
+#pragma unroll
+            for (int m = 0; m < G::Parts; ++m)
+                s = mfma(*reinterpret_cast<const F16x8*>(k_row + 16 * m), q_operand[m], s);
 
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-            const int local = 8 * (r >> 2) + 4 * half + (r & 3);
-            float x = s[r] * row_scale;
-            if (mean_anchor) x = fmaf(alpha_tile[local], q_mu_anchor, x);
-            s[r] = x;
-        }
-        // Tokens past the history score -inf (only in the tile that reaches past it).
-        if (kTile * tile + kTile > history) {
-            asm volatile("");
-#pragma unroll
-            for (int r = 0; r < 16; ++r)
-                s[r] = kTile * tile + 8 * (r >> 2) + 4 * half + (r & 3) < history ? s[r] : -__builtin_inff();
-        }
-        float tile_max = -__builtin_inff();
-#pragma unroll
-        for (int r = 0; r < 16; ++r) tile_max = fmaxf(tile_max, s[r]);
-        tile_max = fmaxf(tile_max, __shfl_xor(tile_max, 32));
-        const float new_max = fmaxf(running_max, tile_max);
-        const float base = new_max == -__builtin_inff() ? 0.f : new_max;
-        const float rescale = __builtin_amdgcn_exp2f(running_max - base);
-        running_max = new_max;
-        // P^T in BF16 as the B operand of O^T += V^T P^T: step j takes
-        // registers 8j..8j+7, i.e. k-slot (half, e) is token
-        // 16 j + 4 half + e + (e >= 4 ? 4 : 0).
-        float tile_sum = 0.f;
-        Bf16x8 p_operand[2];
-#pragma unroll
-        for (int j = 0; j < 2; ++j)
-#pragma unroll
-            for (int e = 0; e < 8; ++e) {
-                const float w = __builtin_amdgcn_exp2f(s[8 * j + e] - base);
-                p_operand[j][e] = (__bf16)w;
-                tile_sum += w;
+            for (int r = 0; r < 16; ++r) {
+                const int local = 8 * (r >> 2) + 4 * half + (r & 3);
+                float x = s[r] * row_scale;
+                if (mean_anchor) x = fmaf(alpha_tile[local], q_mu_anchor, x);
+                s[r] = x;
             }
-        tile_sum += __shfl_xor(tile_sum, 32);
-        running_sum = running_sum * rescale + tile_sum;
-        if (!__all(rescale == 1.0f)) {
+            // Tokens past the history score -inf (only in the tile that reaches past it).
+            if (kTile * tile + kTile > history) {
+                asm volatile("");
 #pragma unroll
-            for (int t = 0; t < G::Quarters; ++t)
+                for (int r = 0; r < 16; ++r)
+                    s[r] = kTile * tile + 8 * (r >> 2) + 4 * half + (r & 3) < history ? s[r] : -__builtin_inff();
+            }
+            float tile_max = -__builtin_inff();
 #pragma unroll
-                for (int r = 0; r < 16; ++r) out[t][r] *= rescale;
-        }
+            for (int r = 0; r < 16; ++r) tile_max = fmaxf(tile_max, s[r]);
+            tile_max = fmaxf(tile_max, __shfl_xor(tile_max, 32));
+            const float new_max = fmaxf(running_max, tile_max);
+            const float base = new_max == -__builtin_inff() ? 0.f : new_max;
+            const float rescale = __builtin_amdgcn_exp2f(running_max - base);
+            running_max = new_max;
+            // P^T in BF16 as the B operand of O^T += V^T P^T: step j takes
+            // registers 8j..8j+7, i.e. k-slot (half, e) is token
+            // 16 j + 4 half + e + (e >= 4 ? 4 : 0).
+            float tile_sum = 0.f;
+            Bf16x8 p_operand[2];
 #pragma unroll
-        for (int j = 0; j < 2; ++j) {
-            const uint16_t* v_rows = v_tile + 16 * j * G::VROW;
+            for (int j = 0; j < 2; ++j)
 #pragma unroll
-            for (int t = 0; t < G::Quarters; ++t) {
-                // Tokens 4 half + 0..3 and 4 half + 8..11 of the 16, as P^T's k-slots.
-                const Short4 lo = read_transposed(v_rows + v_read(t));
-                const Short4 hi = read_transposed(v_rows + 8 * G::VROW + v_read(t));
-                out[t] = mfma(__builtin_bit_cast(Bf16x8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7)),
-                              p_operand[j], out[t]);
+                for (int e = 0; e < 8; ++e) {
+                    const float w = __builtin_amdgcn_exp2f(s[8 * j + e] - base);
+                    p_operand[j][e] = (__bf16)w;
+                    tile_sum += w;
+                }
+            tile_sum += __shfl_xor(tile_sum, 32);
+            running_sum = running_sum * rescale + tile_sum;
+            if (!__all(rescale == 1.0f)) {
+#pragma unroll
+                for (int t = 0; t < G::Quarters; ++t)
+#pragma unroll
+                    for (int r = 0; r < 16; ++r) out[t][r] *= rescale;
+            }
+#pragma unroll
+            for (int j = 0; j < 2; ++j) {
+                const uint16_t* v_rows = v_tile + 16 * j * G::VROW;
+#pragma unroll
+                for (int t = 0; t < G::Quarters; ++t) {
+                    // Tokens 4 half + 0..3 and 4 half + 8..11 of the 16, as P^T's k-slots.
+                    const Short4 lo = read_transposed(v_rows + v_read(t));
+                    const Short4 hi = read_transposed(v_rows + 8 * G::VROW + v_read(t));
+                    out[t] = mfma(__builtin_bit_cast(Bf16x8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7)),
+                                  p_operand[j], out[t]);
+                }
             }
         }
         __builtin_amdgcn_s_setprio(0);
@@ -778,19 +916,26 @@ __device__ __forceinline__ void multirow_stream(const MultiRowParams& p, Decoder
     constexpr int MS = G::MS;
     float* merge_o = reinterpret_cast<float*>(lds);
     float* merge_ml = reinterpret_cast<float*>(lds + G::kMlOffset);
+    if constexpr (TR == 16) {
 #pragma unroll
-    for (int t = 0; t < G::Quarters; ++t)
+        for (int t = 0; t < kOutTiles; ++t)
+            *reinterpret_cast<float4*>(&merge_o[(wave * 32 + tile_row) * MS + 16 * t + 4 * k_group]) =
+                make_float4(out[t][0], out[t][1], out[t][2], out[t][3]);
+    } else {
 #pragma unroll
-        for (int g = 0; g < 4; ++g)
-            *reinterpret_cast<float4*>(&merge_o[(wave * 32 + column) * MS + 32 * t + 8 * g + 4 * half]) =
-                make_float4(out[t][4 * g], out[t][4 * g + 1], out[t][4 * g + 2], out[t][4 * g + 3]);
-    if (half == 0) {
-        merge_ml[(wave * 32 + column) * 2] = running_max;
-        merge_ml[(wave * 32 + column) * 2 + 1] = running_sum;
+        for (int t = 0; t < kOutTiles; ++t)
+#pragma unroll
+            for (int g = 0; g < 4; ++g)
+                *reinterpret_cast<float4*>(&merge_o[(wave * 32 + column) * MS + 32 * t + 8 * g + 4 * half]) =
+                    make_float4(out[t][4 * g], out[t][4 * g + 1], out[t][4 * g + 2], out[t][4 * g + 3]);
+    }
+    if (k_group == 0) {
+        merge_ml[(wave * 32 + tile_row) * 2] = running_max;
+        merge_ml[(wave * 32 + tile_row) * 2 + 1] = running_sum;
     }
     __syncthreads();
-    {
-        const int r = tid >> 3, chunk = tid & 7;  // row, 16-channel chunk
+    const int r = tid >> 3, chunk = tid & 7;  // row, 16-channel chunk
+    if (r < TR) {
         float m_w[kWaves], total_max = -__builtin_inff();
 #pragma unroll
         for (int w = 0; w < kWaves; ++w) {
@@ -824,23 +969,23 @@ __device__ __forceinline__ void multirow_stream(const MultiRowParams& p, Decoder
     }
 }
 
-template <int D, int PT, bool HasL, int BA, int GA, int BL, int GL>
+template <int D, int PT, int TR, bool HasL, int BA, int GA, int BL, int GL>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2)))
 void multirow_stream_kernel(MultiRowParams p) {
-    __shared__ __attribute__((aligned(16))) uint8_t lds[Geometry<D>::kLdsBytes];
+    __shared__ __attribute__((aligned(16))) uint8_t lds[Geometry<D, TR>::kLdsBytes];
     __shared__ int split_blocks[kMaxSplitPages];  // block ids of the split's pages
     AnchorDecoder<PT, HasL, BA, GA, BL, GL> dec;
     dec.anchor = p.anchor;
     dec.residual = p.residual;
     const int quarter = threadIdx.x & 3;
     dec.lq = quarter < Geometry<D>::Quarters ? quarter : 0;
-    multirow_stream<D, PT>(p, dec, lds, split_blocks);
+    multirow_stream<D, PT, TR>(p, dec, lds, split_blocks);
 }
 
-template <int D, int PT, int Links>
+template <int D, int PT, int TR, int Links>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2)))
 void multirow_chain_kernel(MultiRowParams p) {
-    __shared__ __attribute__((aligned(16))) uint8_t lds[Geometry<D>::kLdsBytes];
+    __shared__ __attribute__((aligned(16))) uint8_t lds[Geometry<D, TR>::kLdsBytes];
     __shared__ int split_blocks[kMaxSplitPages];  // block ids of the split's pages
     // bf16(mu_r) of records 0 .. L - 1 (the K plane's chain), FP32.
     __shared__ __attribute__((aligned(16))) float mean_lds[Links - 1][kMaxD];
@@ -864,7 +1009,7 @@ void multirow_chain_kernel(MultiRowParams p) {
     asm("" : "+v"(pick_lo), "+v"(pick_hi));
     dec.pick_lo = pick_lo;
     dec.pick_hi = pick_hi;
-    multirow_stream<D, PT>(p, dec, lds, split_blocks);
+    multirow_stream<D, PT, TR>(p, dec, lds, split_blocks);
 }
 
 // ---------------------------------------------------------------- finish
@@ -1205,54 +1350,72 @@ __global__ __launch_bounds__(kThreads) void multirow_finish_kernel(MultiRowParam
     }
 }
 
-template <int D, int PT, bool HasL, int BA, int GA, int BL, int GL>
-void launch_one(const MultiRowParams& p, hipStream_t stream) {
-    const dim3 grid((unsigned)p.requests, (unsigned)p.heads, (unsigned)(p.splits * p.row_tiles));
-    hipLaunchKernelGGL((multirow_stream_kernel<D, PT, HasL, BA, GA, BL, GL>), grid, dim3(kThreads), 0, stream, p);
+// Rows per stream tile: 16 when the call's requests average 16 rows or
+// fewer (and the grid's z extent allows it), else 32.  The finish kernel
+// always takes 32-row tiles (the partials are per row).
+int stream_tile_rows(const MultiRowParams& p) {
+    const int64_t tiles16 = (p.rows + 15) / 16;
+    return (p.rows <= 16 * p.requests && (int64_t)p.splits * tiles16 <= 65535) ? 16 : 32;
 }
 
-template <int D, int PT, int BA, int GA, int BL>
+template <int TR>
+dim3 stream_grid(const MultiRowParams& p) {
+    return dim3((unsigned)p.requests, (unsigned)p.heads, (unsigned)(p.splits * ((p.rows + TR - 1) / TR)));
+}
+
+template <int D, int PT, int TR, bool HasL, int BA, int GA, int BL, int GL>
+void launch_one(const MultiRowParams& p, hipStream_t stream) {
+    hipLaunchKernelGGL((multirow_stream_kernel<D, PT, TR, HasL, BA, GA, BL, GL>), stream_grid<TR>(p),
+                       dim3(kThreads), 0, stream, p);
+}
+
+template <int D, int PT, int TR, int BA, int GA, int BL>
 void launch_residual_group(const MultiRowParams& p, hipStream_t stream) {
     if (p.residual.group == 32)
-        launch_one<D, PT, true, BA, GA, BL, 32>(p, stream);
+        launch_one<D, PT, TR, true, BA, GA, BL, 32>(p, stream);
     else
-        launch_one<D, PT, true, BA, GA, BL, 16>(p, stream);
+        launch_one<D, PT, TR, true, BA, GA, BL, 16>(p, stream);
 }
 
-template <int D, int PT, int BA, int GA>
+template <int D, int PT, int TR, int BA, int GA>
 void launch_anchor(const MultiRowParams& p, hipStream_t stream) {
     if (!p.has_residual)
-        launch_one<D, PT, false, BA, GA, 2, 32>(p, stream);
+        launch_one<D, PT, TR, false, BA, GA, 2, 32>(p, stream);
     else if (p.residual.bits == 2)
-        launch_residual_group<D, PT, BA, GA, 2>(p, stream);
+        launch_residual_group<D, PT, TR, BA, GA, 2>(p, stream);
     else
-        launch_residual_group<D, PT, BA, GA, 4>(p, stream);
+        launch_residual_group<D, PT, TR, BA, GA, 4>(p, stream);
 }
 
-template <int D, int PT, int BA>
+template <int D, int PT, int TR, int BA>
 void launch_anchor_group(const MultiRowParams& p, hipStream_t stream) {
     if (p.anchor.group == 32)
-        launch_anchor<D, PT, BA, 32>(p, stream);
+        launch_anchor<D, PT, TR, BA, 32>(p, stream);
     else
-        launch_anchor<D, PT, BA, 16>(p, stream);
+        launch_anchor<D, PT, TR, BA, 16>(p, stream);
 }
 
-template <int D, int PT>
-bool launch_pt(const MultiRowParams& p, hipStream_t stream) {
+template <int D, int PT, int TR>
+bool launch_tr(const MultiRowParams& p, hipStream_t stream) {
     if (p.chain_length > 1) {
-        const dim3 grid((unsigned)p.requests, (unsigned)p.heads, (unsigned)(p.splits * p.row_tiles));
+        const dim3 grid = stream_grid<TR>(p);
         switch (p.chain_length) {
-            case 2: hipLaunchKernelGGL((multirow_chain_kernel<D, PT, 2>), grid, dim3(kThreads), 0, stream, p); return true;
-            case 3: hipLaunchKernelGGL((multirow_chain_kernel<D, PT, 3>), grid, dim3(kThreads), 0, stream, p); return true;
-            case 4: hipLaunchKernelGGL((multirow_chain_kernel<D, PT, 4>), grid, dim3(kThreads), 0, stream, p); return true;
+            case 2: hipLaunchKernelGGL((multirow_chain_kernel<D, PT, TR, 2>), grid, dim3(kThreads), 0, stream, p); return true;
+            case 3: hipLaunchKernelGGL((multirow_chain_kernel<D, PT, TR, 3>), grid, dim3(kThreads), 0, stream, p); return true;
+            case 4: hipLaunchKernelGGL((multirow_chain_kernel<D, PT, TR, 4>), grid, dim3(kThreads), 0, stream, p); return true;
             default: return false;
         }
     }
     if (p.anchor.bits == 4)
-        launch_anchor_group<D, PT, 4>(p, stream);
+        launch_anchor_group<D, PT, TR, 4>(p, stream);
     else
-        launch_anchor_group<D, PT, 2>(p, stream);
+        launch_anchor_group<D, PT, TR, 2>(p, stream);
     return true;
+}
+
+template <int D, int PT>
+bool launch_pt(const MultiRowParams& p, hipStream_t stream) {
+    return stream_tile_rows(p) == 16 ? launch_tr<D, PT, 16>(p, stream) : launch_tr<D, PT, 32>(p, stream);
 }
 
 template <int D>

@@ -229,7 +229,7 @@ struct MultiRowParams {
     const float* key_mean_all;
     int causal;
     int splits;     // history splits per (request, head, row tile)
-    int row_tiles;  // 32-row tiles per request in the grid
+    int row_tiles;  // 32-row tiles per request in the finish grid (the stream grid takes 16 or 32 rows a tile)
     float* partials;   // workspace [rows, heads, splits, kMultiRowEntry]
     float* row_shift;  // workspace [rows, heads]: q'.mu_L in log2 units
 };

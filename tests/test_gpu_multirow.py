@@ -12,6 +12,8 @@ MFMA kernels (residualquant_amd/csrc/multirow.hip) against the CPU oracle.
 Both head dims of the reference's attention registry (96 and 128) and both
 reference modes: anchor mode (compute.cuh:397-505) and adjacent mode, whose
 loops past 0 rebuild the BF16 restore chain (compute.cuh:120-197, :506-623).
+Calls whose requests average 16 rows or fewer run on 16-row tiles
+(v_mfma_f32_16x16x32), the others on 32-row tiles; the cases hold both.
 
 Bar: within 2e-2 max-abs / 1e-3 mean-abs of the oracle, both in BF16 (the
 oracle's FP64 output rounded to BF16: the BF16 quantum of outputs of
@@ -84,6 +86,7 @@ CASES = [
     ([300, 70], [33, 70], 2, OURO_G32, 32, True, True, 96, "anchor"),    # two row tiles; no history (prefill)
     ([2100], [3], 2, OURO_G16, 16, False, True, 96, "anchor"),           # eight history splits
     ([77, 50], [5, 0], 1, ((4, 16),), 16, True, False, 96, "anchor"),    # single-record group, no rotation
+    ([300, 60, 9], [33, 1, 2], 2, OURO_G16, 32, True, True, 96, "anchor"),  # 16-row tiles, three in one request
     # adjacent mode (every loop past 0 rebuilds the restore chain of records 0..L)
     ([100, 37, 9], [4, 1, 8], 3, ADJACENT_G32, 16, True, True, 128, "adjacent"),
     ([300, 40], [33, 2], 2, ADJACENT_G16, 32, True, True, 128, "adjacent"),
