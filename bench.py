@@ -586,12 +586,14 @@ def run_multiquery(args):
     measured_bytes = statistics.mean(call_bytes(loop) for loop in measured)
     m = results["multirow"]
     measured_gbps = measured_bytes / (m["measured_call_us"] * 1e-6) / 1e9
-    # MFMA work of one call: per (request, head) and 32-token tile, D / 16 +
-    # D / 16 32x32x16 MFMAs (2 * 32 * 32 * 16 FLOP each) per 32-row tile.
-    tiles = batch * heads * ((history + 31) // 32) * ((rows_per + 31) // 32)
-    mfma_flop = tiles * 2 * (dim // 16) * 2 * 32 * 32 * 16
-    kernel = (f"multirow_chain_kernel<{dim},16,4>" if adjacent else
-              f"multirow_stream_kernel<{dim},16,true,...>") + " + multirow_finish_kernel"
+    # MFMA work of one call: per (request, head), 32-token tile and row tile,
+    # S and P.V take 2 * 32 * tile_rows * D FLOP each; calls averaging 16 rows
+    # per request or fewer run on 16-row tiles.
+    tile_rows = 16 if rows_per <= 16 else 32
+    tiles = batch * heads * ((history + 31) // 32) * ((rows_per + tile_rows - 1) // tile_rows)
+    mfma_flop = tiles * 2 * 2 * 32 * tile_rows * dim
+    kernel = (f"multirow_chain_kernel<{dim},16,{tile_rows},4>" if adjacent else
+              f"multirow_stream_kernel<{dim},16,{tile_rows},true,...>") + " + multirow_finish_kernel"
     result = {
         "metric": "paged decode-attn µs/step + achieved HBM GB/s (% peak), INT2/INT4 vs bf16, 1 GPU",
         "value": step_bytes / (m["us_per_step"] * 1e-6) / 1e9,

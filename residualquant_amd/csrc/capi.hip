@@ -437,12 +437,13 @@ static int attention_packed(const void* query, int64_t query_stride, const void*
     // the multi-row MFMA kernels, which stream each request's pages once for
     // all its rows but dequantize every page tile into LDS.  Measured at 8192
     // history tokens x 16 heads x D128 in anchor mode (4-call step, multi-row
-    // against per-row decode kernel): 3 rows per request 973 against 1468 us
-    // (B32), 4 rows 260 against 500 us per residual call, 16 rows 530 against
-    // 3280 us (B16); at 2 rows the residual-loop call is faster (256 against
-    // 283 us at B32, 84 against 88 us at B8) but the anchor-loop call slower
-    // (192 against 183 us), so decode calls take them from an average of
-    // kMultiRowMinRowsResidual rows per request in a residual loop (and in
+    // against per-row decode kernel): 3 rows per request 868 against 1462 us
+    // (B32), 4 rows 233 against 500 us per residual call, 16 rows 480 against
+    // 3280 us (B16); at 2 rows the residual-loop call is faster (228 against
+    // 284 us at B32; 129 against 145 us on the 55-head D96 history at B8) but
+    // the anchor-only call is not always (D96: 102 against 90 us; adjacent
+    // loop 0: 170 against 163 us), so decode calls take them from an average
+    // of kMultiRowMinRowsResidual rows per request in a residual loop (and in
     // adjacent mode past loop 0, where the per-row kernel rebuilds the chain
     // once per row) and kMultiRowMinRows in the anchor-only loop.
     const bool anchor_only = adjacent ? loop_index == 0 : loop_index == anchor_index;
