@@ -1120,7 +1120,12 @@ void decode_kernel(AttentionParams p) {
 
     // Each iteration streams two consecutive 16-token units of the split
     // (the first iteration's were loaded before the query preparation).
-    for (int64_t u = first; u < range.unit_end; u += 2 * kWaves) {
+    const int iterations =
+        first < range.unit_end ? (int)((range.unit_end - first + 2 * kWaves - 1) / (2 * kWaves)) : 0;
+    const StreamPriority priority(iterations);
+    int step = 0;
+    for (int64_t u = first; u < range.unit_end; u += 2 * kWaves, ++step) {
+        priority.set(step);
         if (u != first) {
             ok0 = load_unit(blocks.first, u, d0);
             ok1 = load_unit(blocks.second, u + 1, d1);
@@ -1128,6 +1133,7 @@ void decode_kernel(AttentionParams p) {
         }
         process(d0, d1, ok0, ok1, u);
     }
+    __builtin_amdgcn_s_setprio(0);
 
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
@@ -1596,9 +1602,11 @@ void decode96_dma_kernel(AttentionParams p) {
 
     // Iteration g consumes stage g % 3 after issuing stage (g + 2) % 3
     // (iteration g - 1's stage, whose reads are complete).
+    const StreamPriority priority(iterations);
     auto iteration = [&](int g, auto stage_constant) __attribute__((always_inline)) {
         constexpr int stage = decltype(stage_constant)::value;
         constexpr int ahead = (stage + 2) % 3;
+        priority.set(g);
         const PagePair next = pages_of(g + 2);
         issue(next, std::integral_constant<int, ahead>{});
         const PagePair cur = stage == 0 ? pages0 : stage == 1 ? pages1 : pages2;
@@ -1707,6 +1715,7 @@ void decode96_dma_kernel(AttentionParams p) {
         if (g + 1 < iterations) iteration(g + 1, Stage1{});
         if (g + 2 < iterations) iteration(g + 2, Stage2{});
     }
+    __builtin_amdgcn_s_setprio(0);
     // The loads of the stages past the last iteration (zero-byte fetches of
     // missing pages) have landed before the LDS is reused or the wave exits.
     wait_vmcnt<0>();
@@ -2089,10 +2098,11 @@ bool launch_chain(const AttentionParams& p, hipStream_t stream) {
 template <int D>
 hipError_t launch_all(const AttentionParams& p, hipStream_t stream, hipEvent_t begin, hipEvent_t end,
                       bool bf16) {
+    // The timed window holds every launch of the call.
+    if (begin) (void)hipEventRecord(begin, stream);
     if (bf16 || !p.fused_prepare)
         hipLaunchKernelGGL((prepare_kernel<D>), dim3((unsigned)p.rows, (unsigned)p.heads), dim3(128), 0,
                            stream, p);
-    if (begin) (void)hipEventRecord(begin, stream);
     if (bf16) {
         const unsigned blocks = (unsigned)(p.rows * p.heads * p.splits);
         hipLaunchKernelGGL((decode_bf16_kernel<D>), dim3(blocks), dim3(kDecodeThreads), 0, stream, p);
@@ -2101,10 +2111,10 @@ hipError_t launch_all(const AttentionParams& p, hipStream_t stream, hipEvent_t b
     } else if (!dispatch_anchor<D>(p, stream)) {
         return hipErrorInvalidValue;
     }
-    if (end) (void)hipEventRecord(end, stream);
     if (bf16)
         hipLaunchKernelGGL((merge_kernel<D>), dim3((unsigned)p.rows, (unsigned)p.heads), dim3(kMergeThreads), 0,
                            stream, p);
+    if (end) (void)hipEventRecord(end, stream);
     return hipGetLastError();
 }
 

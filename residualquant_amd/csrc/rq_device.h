@@ -168,6 +168,30 @@ typedef const int32_t __attribute__((address_space(4))) ConstantInt32;
 // operations (loads and stores) are waited for.
 __device__ __forceinline__ void wait_vector_memory() { __builtin_amdgcn_s_waitcnt(0xF70); }
 
+// Wave priority by the progress of a page stream of `steps` steps: 3 for
+// the first 10/16 of the steps, then 2, 1 and from 15/16 on 0.  Two
+// workgroups whose waves share the SIMDs of a compute unit otherwise
+// progress unevenly (the older wave issues first), so one finishes well
+// before the other, which then streams alone at a lower rate; with the
+// priority falling as a wave advances, the one behind issues first and the
+// two finish together.  The last bucket is short because the two waves' lag
+// at the end is at most its length.
+struct StreamPriority {
+    int to2, to1, to0;  // the first steps at priority 2, 1 and 0
+    __device__ explicit StreamPriority(int steps)
+        : to2((10 * steps + 15) / 16), to1((13 * steps + 15) / 16), to0((15 * steps + 15) / 16) {}
+    __device__ __forceinline__ void set(int step) const {
+        if (step < to2)
+            __builtin_amdgcn_s_setprio(3);
+        else if (step < to1)
+            __builtin_amdgcn_s_setprio(2);
+        else if (step < to0)
+            __builtin_amdgcn_s_setprio(1);
+        else
+            __builtin_amdgcn_s_setprio(0);
+    }
+};
+
 // Request of `row` for a workgroup of whole waves (at most 16): the number of boundaries
 // qsl[1..requests] at or below the row (qsl is nondecreasing), -1 if the row
 // lies outside [qsl[0], qsl[requests]).  One round of parallel loads instead
