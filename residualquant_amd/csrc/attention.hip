@@ -132,16 +132,21 @@ __device__ __forceinline__ void lds_barrier() {
 
 // Loads of the prepare that do not depend on the request: q, the live key and
 // the two key means of (row, head), and R_k, all into registers.  Issued
-// before the request lookup so their round trips overlap; prepare_stage then
-// writes R_k to LDS, which the lookup's barrier or prepare_record's first
-// barrier publishes.  prepare_record reads no global memory, so loads issued
-// after prepare_stage are not waited on before it ends.
-
+// before the request lookup so their round trips overlap.  R_k stays in
+// registers: thread t holds rows t % S, t % S + S, ... of the 8-channel
+// column block t / S (S = 16 threads per block, or 8 in a 128-thread
+// workgroup), so prepare_record multiplies q by its rows and the S threads of
+// a block (adjacent lanes) add their sums with DPP.  prepare_record reads no
+// global memory, so page loads issued after prepare_load and before
+// prepare_record stay in flight (the waits for R_k count only the loads
+// issued before them).
 template <int D, int Threads>
 struct PrepareInputs {
-    static constexpr int kChunks = D * D / 8;  // 16-byte pieces of R_k
-    static constexpr int kPerThread = (kChunks + Threads - 1) / Threads;
-    Chunk16 chunk[kPerThread];
+    static constexpr int kBlocks = D / 8;                          // 8-channel column blocks of R_k
+    static constexpr int kSpan = Threads / kBlocks >= 16 ? 16 : 8;  // threads per block
+    static constexpr int kRows = D / kSpan;                         // rows of R_k per thread
+    static_assert(kBlocks * kSpan <= Threads && D % kSpan == 0, "every block has its threads");
+    Chunk16 chunk[kRows];          // R_k[kSpan i + t % kSpan][8 (t / kSpan) .. + 7], FP16
     float mean_loop, mean_anchor;  // FP32 key means of channel min(c, D - 1) (0 without)
     uint32_t q_bits, k_bits;       // BF16 q and live key of that channel
 };
@@ -159,24 +164,20 @@ __device__ __forceinline__ void prepare_load(const AttentionParams& p, int64_t r
     in.mean_loop = p.key_mean_loop ? p.key_mean_loop[head * D + channel] : 0.f;
     in.mean_anchor = p.key_mean_anchor ? p.key_mean_anchor[head * D + channel] : 0.f;
     if (p.key_rotation != nullptr) {
-        const Chunk16* src = reinterpret_cast<const Chunk16*>(p.key_rotation + (int64_t)head * D * D);
+        // Threads past the blocks read block 0 (prepare_record drops them).
+        const int block = c < In::kBlocks * In::kSpan ? c / In::kSpan : 0;
+        const Chunk16* src =
+            reinterpret_cast<const Chunk16*>(p.key_rotation + (int64_t)head * D * D) + block + (c % In::kSpan) * (D / 8);
 #pragma unroll
-        for (int j = 0; j < In::kPerThread; ++j)
-            if (In::kChunks % Threads == 0 || c + j * Threads < In::kChunks) in.chunk[j] = src[c + j * Threads];
+        for (int i = 0; i < In::kRows; ++i) in.chunk[i] = src[i * In::kSpan * (D / 8)];
     }
 }
 
-template <int D, int Threads>
-__device__ __forceinline__ void prepare_stage(const AttentionParams& p, const PrepareInputs<D, Threads>& in,
-                                              _Float16* rotation_lds) {
-    using In = PrepareInputs<D, Threads>;
-    const int c = threadIdx.x;
-    if (p.key_rotation != nullptr) {
-        Chunk16* dst = reinterpret_cast<Chunk16*>(rotation_lds);
-#pragma unroll
-        for (int j = 0; j < In::kPerThread; ++j)
-            if (In::kChunks % Threads == 0 || c + j * Threads < In::kChunks) dst[c + j * Threads] = in.chunk[j];
-    }
+// Sum over the aligned 8 lanes of x's lane, in every one of them.
+__device__ __forceinline__ float lanes8_sum(float x) {
+    x += __int_as_float(dpp_i<0xB1>(__float_as_int(x)));   // quad_perm [1,0,3,2]
+    x += __int_as_float(dpp_i<0x4E>(__float_as_int(x)));   // quad_perm [2,3,0,1]
+    return x + __int_as_float(dpp_i<0x141>(__float_as_int(x)));  // row_half_mirror
 }
 
 // The prepared query record of one (row, head), written to `record`
@@ -184,16 +185,17 @@ __device__ __forceinline__ void prepare_stage(const AttentionParams& p, const Pr
 // [3..10] 16-channel and [11..14] 32-channel group sums of q', then q'
 // (FP32, log2 units) and its four nibble planes in the INT4 and INT2 word
 // orders (prepare.cuh:13-229).  Called by every thread of a workgroup of 128
-// or 256 threads (threads c >= D contribute nothing) after prepare_stage;
-// `rotation_lds` holds D * D halves.  It reads no global memory, and its
-// barriers order LDS only, so page loads issued before it stay in flight.
-// Returns after a barrier with `record` complete when `record` is in LDS (a
-// record in global memory is read by a later launch).
+// or 256 threads (threads c >= D contribute nothing) after prepare_load.  It
+// reads no global memory, and its barriers order LDS only, so page loads
+// issued before it stay in flight.  Returns after a barrier with `record`
+// complete when `record` is in LDS (a record in global memory is read by a
+// later launch).
 template <int D, int Threads>
 __device__ __forceinline__ void prepare_record(const AttentionParams& p, int head,
-                                               const PrepareInputs<D, Threads>& in, float* record,
-                                               const _Float16* rotation_lds) {
+                                               const PrepareInputs<D, Threads>& in, float* record) {
+    using In = PrepareInputs<D, Threads>;
     __shared__ __attribute__((aligned(16))) float q_lds[128];
+    __shared__ __attribute__((aligned(16))) float rotated_lds[128];
     __shared__ float totals[4][kDecodeThreads / 64];
     const int c = threadIdx.x;
     const int lane = c & 63;
@@ -207,30 +209,27 @@ __device__ __forceinline__ void prepare_record(const AttentionParams& p, int hea
 
     float qr = q;
     if (p.key_rotation != nullptr) {
-        // Four interleaved partial sums (a[j] takes k = j mod 4, ascending).
-        // Sixteen column reads are issued before their FMAs (sched_barrier),
-        // so the LDS round trips overlap instead of one per k.
-        float a[4] = {0.f, 0.f, 0.f, 0.f};
-        if (active) {
-#pragma unroll 2
-            for (int k = 0; k < D; k += 16) {
-                _Float16 r[16];
+        // q.R_k: the thread's rows of its column block, then the block's
+        // kSpan threads added; the block's first thread publishes its 8
+        // channels.
+        const int r = c % In::kSpan;
+        float a[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-                for (int j = 0; j < 16; ++j) r[j] = rotation_lds[(k + j) * D + c];
-                float4 qv[4];
+        for (int i = 0; i < In::kRows; ++i) {
+            const float qk = q_lds[In::kSpan * i + r];
+            const auto h = __builtin_bit_cast(_Float16 __attribute__((ext_vector_type(8))), in.chunk[i]);
 #pragma unroll
-                for (int j = 0; j < 4; ++j) qv[j] = *reinterpret_cast<const float4*>(q_lds + k + 4 * j);
-                __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-                for (int j = 0; j < 4; ++j) {
-                    a[0] = fmaf(qv[j].x, (float)r[4 * j], a[0]);
-                    a[1] = fmaf(qv[j].y, (float)r[4 * j + 1], a[1]);
-                    a[2] = fmaf(qv[j].z, (float)r[4 * j + 2], a[2]);
-                    a[3] = fmaf(qv[j].w, (float)r[4 * j + 3], a[3]);
-                }
-            }
+            for (int e = 0; e < 8; ++e) a[e] = fmaf(qk, (float)h[e], a[e]);
         }
-        qr = (a[0] + a[1]) + (a[2] + a[3]);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) a[e] = In::kSpan == 16 ? row_sum16(a[e]) : lanes8_sum(a[e]);
+        if (r == 0 && c < In::kBlocks * In::kSpan) {
+            float4* dst = reinterpret_cast<float4*>(rotated_lds + 8 * (c / In::kSpan));
+            dst[0] = make_float4(a[0], a[1], a[2], a[3]);
+            dst[1] = make_float4(a[4], a[5], a[6], a[7]);
+        }
+        lds_barrier();
+        qr = active ? rotated_lds[c] : 0.f;
     }
     const float scale = kLog2e / sqrtf((float)D);
     qr *= scale;
@@ -298,7 +297,6 @@ __device__ __forceinline__ void prepare_record(const AttentionParams& p, int hea
 template <int D>
 __global__ __launch_bounds__(128) void prepare_kernel(AttentionParams p) {
     __shared__ int request_counts[2];
-    __shared__ __attribute__((aligned(16))) _Float16 rotation_lds[D * D];
     const int64_t row = blockIdx.x;
     const int head = blockIdx.y;
     const int64_t rh = row * p.heads + head;
@@ -308,8 +306,7 @@ __global__ __launch_bounds__(128) void prepare_kernel(AttentionParams p) {
     const int request = find_request_parallel(p.query_start_loc, p.requests, row, request_counts);
     if (head == 0 && threadIdx.x == 0) p.row_request[row] = request;
     if (request < 0) return;
-    prepare_stage<D, 128>(p, in, rotation_lds);
-    prepare_record<D, 128>(p, head, in, p.prep + rh * (int64_t)kPrepFloats, rotation_lds);
+    prepare_record<D, 128>(p, head, in, p.prep + rh * (int64_t)kPrepFloats);
 }
 
 // ------------------------------------------------------------------ packed decode
@@ -901,7 +898,7 @@ void decode_kernel(AttentionParams p) {
     // Nibble planes of q' per quarter: [quarter][anchor words 0..3 | loop words 0..3][plane]
     __shared__ __attribute__((aligned(16))) uint32_t planes_lds[4][8][4];
     __shared__ __attribute__((aligned(16))) float prep_lds[kPrepFloats];
-    // R_k staging of the fused prepare, then the wave merge at the end.
+    // The wave merge at the end.
     __shared__ __attribute__((aligned(16))) float scratch_lds[kWaves * 16 * 128];
     __shared__ int request_counts[kWaves];
 
@@ -911,11 +908,9 @@ void decode_kernel(AttentionParams p) {
     // while the query record is computed (the loop's first iteration uses them).
     SplitRange range;
     PrepareInputs<D, kDecodeThreads> in;
-    _Float16* rotation_lds = reinterpret_cast<_Float16*>(scratch_lds);
     if (p.fused_prepare) {
         prepare_load<D, kDecodeThreads>(p, row, head, in);
         range = fused_range(p, row, split, request_counts);
-        if (range.request >= 0) prepare_stage<D, kDecodeThreads>(p, in, rotation_lds);
     } else {
         range = split_range(p, p.row_request[row], split);
     }
@@ -998,10 +993,9 @@ void decode_kernel(AttentionParams p) {
     const int64_t first = range.unit_begin + 2 * wave;
     Unit<BA, GA, BL, GL, HasL> d0, d1;
     bool ok0 = false, ok1 = false;
-    // The prologue's own loads have all been consumed or are due now; with
-    // nothing older outstanding, the record's arithmetic below waits for none
-    // of the page loads.
-    wait_vector_memory();
+    // Issued while the prologue's own loads (R_k, q) may still be in flight:
+    // those are older, so the record's arithmetic below waits for them and
+    // for none of the page loads.
     PairBlocks blocks = pair_blocks(first);
     ok0 = load_unit(blocks.first, first, d0);
     ok1 = load_unit(blocks.second, first + 1, d1);
@@ -1009,7 +1003,7 @@ void decode_kernel(AttentionParams p) {
     blocks = pair_blocks(first + 2 * kWaves);
 
     if (p.fused_prepare) {
-        prepare_record<D, kDecodeThreads>(p, head, in, prep_lds, rotation_lds);
+        prepare_record<D, kDecodeThreads>(p, head, in, prep_lds);
     } else {
         const float* src = p.prep + rh * (int64_t)kPrepFloats;
         for (int i = threadIdx.x; i < kPrepFloats; i += kDecodeThreads) prep_lds[i] = src[i];
@@ -1425,11 +1419,9 @@ void decode96_dma_kernel(AttentionParams p) {
     // compiler makes an LDS read wait for every DMA load in flight that may
     // write the object it reads, so with one object for all stages the
     // reads of one stage would wait for the loads of the others.  Stage 2
-    // also holds the R_k staging of the fused prepare (D x D halves), before
-    // its first load (the prologue's barriers order the two), and the wave
-    // merge (kWaves x 16 x D floats), after the last.
+    // also holds the wave merge (kWaves x 16 x D floats), after the last
+    // load.
     constexpr int kScratchBytes = (int)sizeof(float) * kWaves * 16 * D;
-    static_assert(D * D * 2 <= kScratchBytes, "R_k staging fits the merge scratch");
     __shared__ __attribute__((aligned(16))) uint8_t ring0[L::RingStageBytes];
     __shared__ __attribute__((aligned(16))) uint8_t ring1[L::RingStageBytes];
     __shared__ __attribute__((aligned(16))) uint8_t ring2[L::RingStageBytes > kScratchBytes ? L::RingStageBytes
@@ -1438,11 +1430,9 @@ void decode96_dma_kernel(AttentionParams p) {
 
     SplitRange range;
     PrepareInputs<D, kDecodeThreads> in;
-    _Float16* rotation_lds = reinterpret_cast<_Float16*>(scratch_lds);
     if (p.fused_prepare) {
         prepare_load<D, kDecodeThreads>(p, row, head, in);
         range = fused_range(p, row, split, request_counts);
-        if (range.request >= 0) prepare_stage<D, kDecodeThreads>(p, in, rotation_lds);
     } else {
         range = split_range(p, p.row_request[row], split);
     }
@@ -1530,15 +1520,16 @@ void decode96_dma_kernel(AttentionParams p) {
         const float* src = p.prep + rh * (int64_t)kPrepFloats;
         for (int i = threadIdx.x; i < kPrepFloats; i += kDecodeThreads) prep_lds[i] = src[i];
     }
-    // Every load other than the pages' has landed here (the prologue's
-    // inputs, the prepared record), so no wait after the page loads below
-    // has to count them: the prologue's barriers order LDS only and the
-    // first stages stream while the query record is prepared.
-    wait_vmcnt<0>();
+    // The prologue's own loads (R_k, q) may still be in flight: they are
+    // older than the page loads, so the query preparation waits for them
+    // only, and every wait of the loop below, which counts the page loads
+    // issued after the stage it consumes, also covers them.  The
+    // prologue's barriers order LDS only, so the first stages stream while
+    // the query record is prepared.
     issue(pages0, Stage0{});
     issue(pages1, Stage1{});
 
-    if (p.fused_prepare) prepare_record<D, kDecodeThreads>(p, head, in, prep_lds, rotation_lds);
+    if (p.fused_prepare) prepare_record<D, kDecodeThreads>(p, head, in, prep_lds);
     else lds_barrier();
     const float* prep = prep_lds;
     const float delta = prep[0];
@@ -1770,11 +1761,9 @@ void decode_chain_kernel(AttentionParams p) {
 
     SplitRange range;
     PrepareInputs<D, kDecodeThreads> in;
-    _Float16* rotation_lds = reinterpret_cast<_Float16*>(scratch_lds);
     if (p.fused_prepare) {
         prepare_load<D, kDecodeThreads>(p, row, head, in);
         range = fused_range(p, row, split, request_counts);
-        if (range.request >= 0) prepare_stage<D, kDecodeThreads>(p, in, rotation_lds);
     } else {
         range = split_range(p, p.row_request[row], split);
     }
@@ -1792,7 +1781,7 @@ void decode_chain_kernel(AttentionParams p) {
                              : 0.f;
     }
     if (p.fused_prepare) {
-        prepare_record<D, kDecodeThreads>(p, head, in, prep_lds, rotation_lds);
+        prepare_record<D, kDecodeThreads>(p, head, in, prep_lds);
     } else {
         const float* src = p.prep + rh * (int64_t)kPrepFloats;
         for (int i = threadIdx.x; i < kPrepFloats; i += kDecodeThreads) prep_lds[i] = src[i];
