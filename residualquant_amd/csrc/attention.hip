@@ -1860,7 +1860,11 @@ void decode_chain_kernel(AttentionParams p) {
     UnitPages pages = unit_pages(u);
     load_plane(pages.k, pages.tok, rk);
     load_plane(pages.v, pages.tok, rv);
-    for (; u < range.unit_end; u += kWaves) {
+    const int wave_units = u < range.unit_end ? (int)((range.unit_end - u + kWaves - 1) / kWaves) : 0;
+    const StreamPriority priority(wave_units);
+    int step = 0;
+    for (; u < range.unit_end; u += kWaves, ++step) {
+        priority.set(step);
         const int64_t pos = u * kUnitTokens + t;
         const bool valid = pages.ok && lane_active && pos < range.history;
         const UnitPages next = unit_pages(u + kWaves);
@@ -1918,6 +1922,7 @@ void decode_chain_kernel(AttentionParams p) {
         load_plane(next.v, next.tok, rv);
         pages = next;
     }
+    __builtin_amdgcn_s_setprio(0);
 
     if (p.splits == 1) {
         finish_single<D>(p, row, head, prep_lds[1],
