@@ -581,7 +581,11 @@ __global__ __launch_bounds__(kMfmaThreads) void quantize_mfma_kernel(QuantizePar
         pending = load_chunk(row, 1);
         next_slot = load_slot(first);
     }
-    for (; first < block_end; first += kStride) {
+    const int passes = first < block_end ? (int)((block_end - first + kStride - 1) / kStride) : 0;
+    const StreamPriority priority(passes);
+    int pass = 0;
+    for (; first < block_end; first += kStride, ++pass) {
+        priority.set(pass);
         const int64_t n = first + q;
         // Rotated passes take the slot prefetched with their first chunk.
         const int64_t slot = Rotated ? next_slot : load_slot(first);
