@@ -1116,7 +1116,7 @@ void decode_kernel(AttentionParams p) {
     // (the first iteration's were loaded before the query preparation).
     const int iterations =
         first < range.unit_end ? (int)((range.unit_end - first + 2 * kWaves - 1) / (2 * kWaves)) : 0;
-    const StreamPriority priority(iterations);
+    const StreamPriority priority(iterations, p.stream_priority != 0);
     int step = 0;
     for (int64_t u = first; u < range.unit_end; u += 2 * kWaves, ++step) {
         priority.set(step);
@@ -1593,7 +1593,7 @@ void decode96_dma_kernel(AttentionParams p) {
 
     // Iteration g consumes stage g % 3 after issuing stage (g + 2) % 3
     // (iteration g - 1's stage, whose reads are complete).
-    const StreamPriority priority(iterations);
+    const StreamPriority priority(iterations, p.stream_priority != 0);
     auto iteration = [&](int g, auto stage_constant) __attribute__((always_inline)) {
         constexpr int stage = decltype(stage_constant)::value;
         constexpr int ahead = (stage + 2) % 3;
@@ -1861,7 +1861,7 @@ void decode_chain_kernel(AttentionParams p) {
     load_plane(pages.k, pages.tok, rk);
     load_plane(pages.v, pages.tok, rv);
     const int wave_units = u < range.unit_end ? (int)((range.unit_end - u + kWaves - 1) / kWaves) : 0;
-    const StreamPriority priority(wave_units);
+    const StreamPriority priority(wave_units, p.stream_priority != 0);
     int step = 0;
     for (; u < range.unit_end; u += kWaves, ++step) {
         priority.set(step);
@@ -2024,19 +2024,29 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_bf16_kernel(AttentionPa
 
 // ------------------------------------------------------------------ launch
 
+// The launch parameters with stream_priority set: whether `blocks`
+// workgroups of `kernel` fit the device at once.
+inline AttentionParams with_priority(const AttentionParams& params, int per_cu, int64_t blocks) {
+    AttentionParams p = params;
+    p.stream_priority = blocks <= (int64_t)per_cu * p.compute_units ? 1 : 0;
+    return p;
+}
+
 template <int D, int PT, int BA, int GA, int BL, int GL, bool HasL>
 void launch_decode(const AttentionParams& p, hipStream_t stream) {
     const unsigned blocks = (unsigned)(p.rows * p.heads * p.splits);
     if constexpr (D == 96) {
         // Per-lane page offsets are 32-bit buffer offsets into one plane.
         if (p.plane_stride > 0 && p.plane_stride <= (int64_t)UINT32_MAX - 0x10000) {
-            hipLaunchKernelGGL((decode96_dma_kernel<PT, BA, GA, BL, GL, HasL>), dim3(blocks), dim3(kDecodeThreads),
-                               0, stream, p);
+            const auto kernel = decode96_dma_kernel<PT, BA, GA, BL, GL, HasL>;
+            static const int per_cu = resident_per_cu(reinterpret_cast<const void*>(kernel), kDecodeThreads);
+            hipLaunchKernelGGL(kernel, dim3(blocks), dim3(kDecodeThreads), 0, stream, with_priority(p, per_cu, blocks));
             return;
         }
     }
-    hipLaunchKernelGGL((decode_kernel<D, PT, BA, GA, BL, GL, HasL>), dim3(blocks), dim3(kDecodeThreads), 0,
-                       stream, p);
+    const auto kernel = decode_kernel<D, PT, BA, GA, BL, GL, HasL>;
+    static const int per_cu = resident_per_cu(reinterpret_cast<const void*>(kernel), kDecodeThreads);
+    hipLaunchKernelGGL(kernel, dim3(blocks), dim3(kDecodeThreads), 0, stream, with_priority(p, per_cu, blocks));
 }
 
 template <int D, int PT, int BA, int GA>
@@ -2071,13 +2081,20 @@ bool dispatch_anchor(const AttentionParams& p, hipStream_t stream) {
     return false;
 }
 
+template <int D, int PT, int Links>
+void launch_chain_links(const AttentionParams& p, hipStream_t stream) {
+    const unsigned blocks = (unsigned)(p.rows * p.heads * p.splits);
+    const auto kernel = decode_chain_kernel<D, PT, Links>;
+    static const int per_cu = resident_per_cu(reinterpret_cast<const void*>(kernel), kDecodeThreads);
+    hipLaunchKernelGGL(kernel, dim3(blocks), dim3(kDecodeThreads), 0, stream, with_priority(p, per_cu, blocks));
+}
+
 template <int D, int PT>
 bool launch_chain_pt(const AttentionParams& p, hipStream_t stream) {
-    const unsigned blocks = (unsigned)(p.rows * p.heads * p.splits);
     switch (p.chain_length) {
-        case 2: hipLaunchKernelGGL((decode_chain_kernel<D, PT, 2>), dim3(blocks), dim3(kDecodeThreads), 0, stream, p); return true;
-        case 3: hipLaunchKernelGGL((decode_chain_kernel<D, PT, 3>), dim3(blocks), dim3(kDecodeThreads), 0, stream, p); return true;
-        case 4: hipLaunchKernelGGL((decode_chain_kernel<D, PT, 4>), dim3(blocks), dim3(kDecodeThreads), 0, stream, p); return true;
+        case 2: launch_chain_links<D, PT, 2>(p, stream); return true;
+        case 3: launch_chain_links<D, PT, 3>(p, stream); return true;
+        case 4: launch_chain_links<D, PT, 4>(p, stream); return true;
         default: return false;
     }
 }

@@ -506,6 +506,7 @@ static int attention_packed(const void* query, int64_t query_stride, const void*
         m.causal = causal ? 1 : 0;
         m.splits = splits;
         m.row_tiles = (int)row_tiles;
+        m.compute_units = compute_units();
         uint8_t* ws = static_cast<uint8_t*>(workspace);
         m.partials = reinterpret_cast<float*>(ws + layout.partials);
         m.row_shift = reinterpret_cast<float*>(ws + layout.row_shift);
@@ -545,6 +546,7 @@ static int attention_packed(const void* query, int64_t query_stride, const void*
     p.key_mean_loop = key_mean ? key_mean + (int64_t)loop_index * heads * head_dim : nullptr;
     p.key_mean_anchor = (key_mean && p.has_residual) ? key_mean + (int64_t)anchor * heads * head_dim : nullptr;
     p.fused_prepare = p.splits == 1 ? 1 : 0;
+    p.compute_units = compute_units();
     // Adjacent mode past loop 0 decodes the restore chain of records 0..loop.
     p.chain_length = adjacent && loop_index > 0 ? loop_index + 1 : 0;
     for (int r = 0; r < p.chain_length; ++r) p.chain[r] = regions[r];

@@ -703,7 +703,7 @@ __device__ __forceinline__ void multirow_stream(const MultiRowParams& p, Decoder
     // priority over each tile's MFMAs and softmax (residual call 129.3 ->
     // 122.5 us at 16 requests x 16 rows x 8k, A/B on one box).
     const int wave_tiles = first_tile < tile_end ? (tile_end - first_tile + kWaves - 1) / kWaves : 0;
-    const StreamPriority priority(wave_tiles);
+    const StreamPriority priority(wave_tiles, p.stream_priority != 0);
     int step = 0;
     for (int tile = first_tile; tile < tile_end; tile += kWaves, ++step) {
         priority.set(step);
@@ -1367,10 +1367,31 @@ dim3 stream_grid(const MultiRowParams& p) {
     return dim3((unsigned)p.requests, (unsigned)p.heads, (unsigned)(p.splits * ((p.rows + TR - 1) / TR)));
 }
 
+// The launch parameters with stream_priority set: whether the grid's active
+// workgroups, about requests x heads x splits x the average request's row
+// tiles (the others exit at once), fit the device at once.
+template <int TR>
+MultiRowParams with_priority(const MultiRowParams& params, int per_cu) {
+    MultiRowParams p = params;
+    const int64_t average_rows = p.requests > 0 ? p.rows / p.requests : p.rows;
+    const int64_t average_tiles = average_rows > TR ? (average_rows + TR - 1) / TR : 1;
+    const int64_t active = p.requests * p.heads * p.splits * average_tiles;
+    p.stream_priority = active <= (int64_t)per_cu * p.compute_units ? 1 : 0;
+    return p;
+}
+
 template <int D, int PT, int TR, bool HasL, int BA, int GA, int BL, int GL>
 void launch_one(const MultiRowParams& p, hipStream_t stream) {
-    hipLaunchKernelGGL((multirow_stream_kernel<D, PT, TR, HasL, BA, GA, BL, GL>), stream_grid<TR>(p),
-                       dim3(kThreads), 0, stream, p);
+    const auto kernel = multirow_stream_kernel<D, PT, TR, HasL, BA, GA, BL, GL>;
+    static const int per_cu = resident_per_cu(reinterpret_cast<const void*>(kernel), kThreads);
+    hipLaunchKernelGGL(kernel, stream_grid<TR>(p), dim3(kThreads), 0, stream, with_priority<TR>(p, per_cu));
+}
+
+template <int D, int PT, int TR, int Links>
+void launch_chain(const MultiRowParams& p, hipStream_t stream) {
+    const auto kernel = multirow_chain_kernel<D, PT, TR, Links>;
+    static const int per_cu = resident_per_cu(reinterpret_cast<const void*>(kernel), kThreads);
+    hipLaunchKernelGGL(kernel, stream_grid<TR>(p), dim3(kThreads), 0, stream, with_priority<TR>(p, per_cu));
 }
 
 template <int D, int PT, int TR, int BA, int GA, int BL>
@@ -1402,11 +1423,10 @@ void launch_anchor_group(const MultiRowParams& p, hipStream_t stream) {
 template <int D, int PT, int TR>
 bool launch_tr(const MultiRowParams& p, hipStream_t stream) {
     if (p.chain_length > 1) {
-        const dim3 grid = stream_grid<TR>(p);
         switch (p.chain_length) {
-            case 2: hipLaunchKernelGGL((multirow_chain_kernel<D, PT, TR, 2>), grid, dim3(kThreads), 0, stream, p); return true;
-            case 3: hipLaunchKernelGGL((multirow_chain_kernel<D, PT, TR, 3>), grid, dim3(kThreads), 0, stream, p); return true;
-            case 4: hipLaunchKernelGGL((multirow_chain_kernel<D, PT, TR, 4>), grid, dim3(kThreads), 0, stream, p); return true;
+            case 2: launch_chain<D, PT, TR, 2>(p, stream); return true;
+            case 3: launch_chain<D, PT, TR, 3>(p, stream); return true;
+            case 4: launch_chain<D, PT, TR, 4>(p, stream); return true;
             default: return false;
         }
     }

@@ -582,7 +582,8 @@ __global__ __launch_bounds__(kMfmaThreads) void quantize_mfma_kernel(QuantizePar
         next_slot = load_slot(first);
     }
     const int passes = first < block_end ? (int)((block_end - first + kStride - 1) / kStride) : 0;
-    const StreamPriority priority(passes);
+    // One round of workgroups (launch_quantize_mfma): every one takes it.
+    const StreamPriority priority(passes, true);
     int pass = 0;
     for (; first < block_end; first += kStride, ++pass) {
         priority.set(pass);

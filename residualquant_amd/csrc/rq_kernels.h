@@ -8,6 +8,15 @@
 
 namespace rq {
 
+// Workgroups of `threads` threads of `kernel` that one compute unit holds at
+// once (its registers and LDS decide), at least 1.
+inline int resident_per_cu(const void* kernel, int threads) {
+    int blocks = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&blocks, kernel, threads, 0) != hipSuccess || blocks < 1)
+        return 1;
+    return blocks;
+}
+
 // Coefficient methods (same values as RQ_COEF_* in include/rq_hip.h).
 constexpr int RQ_COEF_UNIT_ = 0;
 constexpr int RQ_COEF_NORM_ = 1;
@@ -170,6 +179,8 @@ struct AttentionParams {
     float* partials;       // workspace [rows, heads, splits, D + 2]
     int splits;
     int fused_prepare;     // 1: each decode workgroup prepares its own query (requires splits == 1)
+    int compute_units;     // of the launching device
+    int stream_priority;   // set by the launch: the grid fits the device at once, so its waves take StreamPriority
     // Adjacent mode, loop L > 0: records 0..L of the restore chain (chain_length = L + 1, else 0)
     // and the key means of every record [records, heads, D] (or null).
     RecordRegion chain[kMaxRecords];
@@ -229,6 +240,9 @@ struct MultiRowParams {
     const float* key_mean_all;
     int causal;
     int splits;     // history splits per (request, head, row tile)
+    int compute_units;    // of the launching device
+    int stream_priority;  // set by the launch: the active workgroups fit the device at once, so their
+                          // waves take StreamPriority
     int row_tiles;  // 32-row tiles per request in the finish grid (the stream grid takes 16 or 32 rows a tile)
     float* partials;   // workspace [rows, heads, splits, kMultiRowEntry]
     float* row_shift;  // workspace [rows, heads]: q'.mu_L in log2 units
