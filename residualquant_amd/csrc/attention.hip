@@ -1841,8 +1841,10 @@ void decode_chain_kernel(AttentionParams p) {
     // such care).
     auto build_chain = [&](auto half, const ChainRaw (&raw)[Links], bool key_plane, bool live, float (&x)[16]) {
         constexpr int H = decltype(half)::value;
-        chain_build<H, Links>(raw, regs, key_plane && has_mean, &mean_lds[0][32 * lq + 16 * H], 128, live, pick_lo,
-                              pick_hi, x);
+        chain_build<H, Links>(
+            raw, regs, key_plane && has_mean,
+            [&](int r, int i) __attribute__((always_inline)) { return mean_lds[r][32 * lq + 16 * H + i]; }, live,
+            pick_lo, pick_hi, x);
     };
     using Half0 = std::integral_constant<int, 0>;
     using Half1 = std::integral_constant<int, 1>;
@@ -1860,11 +1862,7 @@ void decode_chain_kernel(AttentionParams p) {
     UnitPages pages = unit_pages(u);
     load_plane(pages.k, pages.tok, rk);
     load_plane(pages.v, pages.tok, rv);
-    const int wave_units = u < range.unit_end ? (int)((range.unit_end - u + kWaves - 1) / kWaves) : 0;
-    const StreamPriority priority(wave_units, p.stream_priority != 0);
-    int step = 0;
-    for (; u < range.unit_end; u += kWaves, ++step) {
-        priority.set(step);
+    for (; u < range.unit_end; u += kWaves) {
         const int64_t pos = u * kUnitTokens + t;
         const bool valid = pages.ok && lane_active && pos < range.history;
         const UnitPages next = unit_pages(u + kWaves);
@@ -1922,7 +1920,6 @@ void decode_chain_kernel(AttentionParams p) {
         load_plane(next.v, next.tok, rv);
         pages = next;
     }
-    __builtin_amdgcn_s_setprio(0);
 
     if (p.splits == 1) {
         finish_single<D>(p, row, head, prep_lds[1],

@@ -371,13 +371,17 @@ struct ChainDecoder {
         fetch_plane(first.k, first.row, k);
         fetch_plane(first.v, first.row, v);
     }
+    // bf16(mu_r) of channel i of the 16 channels from `base` (record r's copy kMaxD floats on).
+    __device__ __forceinline__ static auto mean_of(const float* base) {
+        return [base](int r, int i) __attribute__((always_inline)) { return base[r * kMaxD + i]; };
+    }
     template <class StoreK, class StoreV>
     __device__ __forceinline__ float unit(const UnitPages& next, const UnitPages& /*two_on*/, StoreK store_k,
                                           StoreV store_v) {
         const float* m = mean + 32 * lq;
         float lo[16], hi[16];
-        chain_build<0, Links>(k, regs, add_mean, m, kMaxD, true, pick_lo, pick_hi, lo);
-        chain_build<1, Links>(k, regs, add_mean, m + 16, kMaxD, true, pick_lo, pick_hi, hi);
+        chain_build<0, Links>(k, regs, add_mean, mean_of(m), true, pick_lo, pick_hi, lo);
+        chain_build<1, Links>(k, regs, add_mean, mean_of(m + 16), true, pick_lo, pick_hi, hi);
         // The last link's BF16 rounding, one pack per channel pair.
 #pragma unroll
         for (int i = 0; i < 16; i += 2) {
@@ -389,8 +393,8 @@ struct ChainDecoder {
         }
         fetch_plane(next.k, next.row, k);
         store_k(lo, hi);
-        chain_build<0, Links>(v, regs, false, m, kMaxD, true, pick_lo, pick_hi, lo);
-        chain_build<1, Links>(v, regs, false, m, kMaxD, true, pick_lo, pick_hi, hi);
+        chain_build<0, Links>(v, regs, false, mean_of(m), true, pick_lo, pick_hi, lo);
+        chain_build<1, Links>(v, regs, false, mean_of(m), true, pick_lo, pick_hi, hi);
         fetch_plane(next.v, next.row, v);
         store_v(lo, hi);
         return 1.f;
