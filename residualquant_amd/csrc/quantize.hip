@@ -217,6 +217,7 @@ __device__ __forceinline__ void commit_record(float (&x)[2][4], const bool (&act
         // The codes are packed negated: sum of (-code_i) << (i bits), mod 2^32,
         // then one negation (the fields do not overlap).
         uint32_t negated = 0;
+        int neg_code[4];
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             // |a| <= 2^100 keeps q0 finite; beyond it the code saturates anyway.
@@ -227,16 +228,35 @@ __device__ __forceinline__ void commit_record(float (&x)[2][4], const bool (&act
             // floor(q) + (frac(q) > 0.5) == ceil(q - 0.5), clamped to [0, levels],
             // which equals ceil(q' - 0.5) for q' = q clamped to [0, levels]; its
             // negation is floor(-q' + 0.5).
-            const int neg_code = round_half_up_negated(__builtin_amdgcn_fmed3f(q, 0.0f, levels));
-            negated += (uint32_t)neg_code << (i * bits);
-            if (restore) {
-                uint32_t value = bf16_rn(fmaf(-(float)neg_code, scale, offset));
-                if (has_mean) value = bf16_rn(bf16_f32(value) + bf16_f32(bf16_rn(mean[h][i])));
-                if (!is_anchor) value = bf16_fma_rn(reference[h][i], alpha, bf16_f32(value));
-                reference[h][i] = bf16_f32(value);
-            }
+            neg_code[i] = round_half_up_negated(__builtin_amdgcn_fmed3f(q, 0.0f, levels));
+            negated += (uint32_t)neg_code[i] << (i * bits);
         }
         packed[h] = 0u - negated;
+        if (restore) {
+            // The restored record, two channels per rounding: bf16(c s + o),
+            // then bf16(that + bf16(mu)) on the K plane with key means.
+            float value[4];
+#pragma unroll
+            for (int i = 0; i < 4; i += 2) {
+                const uint32_t pair = bf16x2_rn(fmaf(-(float)neg_code[i], scale, offset),
+                                                fmaf(-(float)neg_code[i + 1], scale, offset));
+                value[i] = bf16_f32(pair & 0xffffu);
+                value[i + 1] = bf16_f32(pair >> 16);
+            }
+            if (has_mean) {
+#pragma unroll
+                for (int i = 0; i < 4; i += 2) {
+                    const uint32_t mu = bf16x2_rn(mean[h][i], mean[h][i + 1]);
+                    const uint32_t pair = bf16x2_rn(value[i] + bf16_f32(mu & 0xffffu),
+                                                    value[i + 1] + bf16_f32(mu >> 16));
+                    value[i] = bf16_f32(pair & 0xffffu);
+                    value[i + 1] = bf16_f32(pair >> 16);
+                }
+            }
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+                reference[h][i] = is_anchor ? value[i] : bf16_f32(bf16_fma_rn(reference[h][i], alpha, value[i]));
+        }
     }
 
     if (store) {

@@ -9,14 +9,22 @@ namespace rq {
 
 // ------------------------------------------------------------------ BF16
 
-// __float2bfloat16_rn semantics: one round-to-nearest-even of an FP32 value.
-__device__ __forceinline__ uint32_t bf16_rn(float f) {
-    // A select rather than a branch: the NaN case costs two instructions
-    // instead of an exec-mask branch around every rounding.
-    const uint32_t u = __float_as_uint(f);
-    const uint32_t rounded = (u + 0x7fffu + ((u >> 16) & 1u)) >> 16;
-    const uint32_t quiet = (u >> 16) | 0x40u;
-    return (u & 0x7fffffffu) > 0x7f800000u ? quiet : rounded;
+// __float2bfloat16_rn semantics: one round-to-nearest-even of an FP32 value,
+// a NaN kept with its upper payload bits and the quiet bit set.  gfx950's
+// v_cvt_pk_bf16_f32 (under the default rounding and denormal modes these
+// kernels run with) gives exactly the integer form
+//   NaN ? (u >> 16) | 0x40 : (u + 0x7fff + ((u >> 16) & 1)) >> 16
+// for all 2^32 FP32 inputs (checked on the device, both halves of the pair),
+// in one instruction for two values instead of six per value.
+typedef __bf16 Bf16Pair __attribute__((ext_vector_type(2)));
+typedef float F32Pair __attribute__((ext_vector_type(2)));
+
+__device__ __forceinline__ uint32_t bf16_rn(float f) { return __builtin_bit_cast(uint16_t, (__bf16)f); }
+
+// bf16_rn of a and b packed (a in the low half): one v_cvt_pk_bf16_f32.
+__device__ __forceinline__ uint32_t bf16x2_rn(float a, float b) {
+    const F32Pair f = {a, b};
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(f, Bf16Pair));
 }
 
 __device__ __forceinline__ float bf16_f32(uint32_t h) { return __uint_as_float(h << 16); }

@@ -65,15 +65,24 @@ def test_step_logits_match_independent_forward(oracle, device, batch):
 
 
 def assert_layers(stats: dict) -> None:
-    """Bars of check_layers: BF16 tensors within one BF16 ulp of the largest
-    reference value (max) and 2**-10 relative on average (they are equal but
-    for rare rounding flips), attention within the parity bar of the oracle,
-    logits within one ulp at their scale."""
+    """Bars of check_layers: q/k/v (one product and RoPE from the layer input)
+    within 2**-7 of the largest reference value (max: one to two BF16 ulps of
+    that value, by where it sits in its binade) and 2**-10 relative on average
+    (they are equal but for rare rounding flips); attention within the parity
+    bar of the oracle; logits within 2**-7 of their scale.  A layer output,
+    residual or loop input follows three products (o_proj, then the MLP's
+    two) whose FP32 accumulation order differs from the float64 recompute,
+    each rounded to BF16, then the residual adds and the norms: flips there
+    reach the output as two ulps (0.03125 at values below 3.92 measured, just
+    over 2**-7 of 3.92), so their max bar is 2**-6 of the largest reference
+    value, with the same 2**-10 mean bar."""
     for name, (err_max, err_mean, ref_max, ref_mean) in stats.items():
         if name.startswith("attention"):
             assert err_max <= 2e-2 and err_mean <= 1e-3, (name, err_max, err_mean)
         elif name == "logits":
             assert err_max <= 2.0 ** -7 * ref_max and err_mean <= 2.0 ** -8 * ref_mean, (name, err_max, err_mean)
+        elif name.startswith(("output", "residual", "loop_input")):
+            assert err_max <= 2.0 ** -6 * ref_max and err_mean <= 2.0 ** -10 * ref_mean, (name, err_max, err_mean)
         else:
             assert err_max <= 2.0 ** -7 * ref_max and err_mean <= 2.0 ** -10 * ref_mean, (name, err_max, err_mean)
 
