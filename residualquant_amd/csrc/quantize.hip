@@ -260,29 +260,30 @@ __device__ __forceinline__ void commit_record(float (&x)[2][4], const bool (&act
     }
 
     if (store) {
-        uint8_t* record = page + region.offset;
-        uint8_t* token_codes = record + token * region.code_bytes;
-        uint8_t* group_parameters = record + page_tokens * region.code_bytes;
-        const int lanes_per_group = region.group / 4;
+        // 32-bit offsets from the page base (a page is far below 4 GiB), so
+        // the per-record terms stay single registers.
+        const uint32_t codes = (uint32_t)region.offset;
+        const uint32_t scales = codes + (uint32_t)(page_tokens * region.code_bytes);
+        const uint32_t offsets = scales + (uint32_t)(page_tokens * region.groups);
+        const uint32_t alphas = offsets + (uint32_t)(page_tokens * region.groups);
+        const int group_shift = region.group == 32 ? 3 : 2;  // log2(canonical lanes per group)
 #pragma unroll
         for (int h = 0; h < 2; ++h) {
             if (!active[h]) continue;
             const int lane = j + 16 * h;
             if (bits == 2) {
-                token_codes[lane] = (uint8_t)packed[h];
+                page[codes + (uint32_t)(token * region.code_bytes + lane)] = (uint8_t)packed[h];
             } else {
-                *reinterpret_cast<uint16_t*>(token_codes + 2 * lane) = (uint16_t)packed[h];
+                *reinterpret_cast<uint16_t*>(page + codes + (uint32_t)(token * region.code_bytes + 2 * lane)) =
+                    (uint16_t)packed[h];
             }
-            if (lane % lanes_per_group == 0) {
-                const int index = token * region.groups + lane / lanes_per_group;
-                group_parameters[index] = (uint8_t)(parameters[h] >> 8);
-                group_parameters[page_tokens * region.groups + index] = (uint8_t)(parameters[h] & 0xffu);
+            if ((lane & ((1 << group_shift) - 1)) == 0) {
+                const uint32_t index = (uint32_t)(token * region.groups + (lane >> group_shift));
+                page[scales + index] = (uint8_t)(parameters[h] >> 8);
+                page[offsets + index] = (uint8_t)(parameters[h] & 0xffu);
             }
         }
-        if (j == 0) {
-            uint8_t* target = record + page_tokens * (region.code_bytes + 2 * region.groups) + 2 * token;
-            *reinterpret_cast<uint16_t*>(target) = (uint16_t)stored_alpha;
-        }
+        if (j == 0) *reinterpret_cast<uint16_t*>(page + alphas + (uint32_t)(2 * token)) = (uint16_t)stored_alpha;
     }
 }
 
