@@ -13,26 +13,17 @@
 // sums, IEEE division/sqrt, RNE satfinite FP8, single rounded BF16 restores.
 // Contraction is disabled for this file.
 //
-// Two kernels share the commit code: quantize_kernel below (VALU rotation,
-// used for short calls such as decode steps) and quantize_mfma_kernel (the
-// rotation on the matrix cores, for calls of kMfmaMinTokens tokens or more).
-// On gfx950 the FP32 MFMAs and the VALU do not execute concurrently (a wave
-// interleaving 8 MFMAs with 64 independent FMAs takes the sum of the two
-// times, at one and at two waves per SIMD), so a call costs its rotation
-// plus its commit.
+// One kernel, quantize_mfma_kernel, does every call: the rotation on the
+// matrix cores, then the commit on the VALU.  On gfx950 the FP32 MFMAs and
+// the VALU do not execute concurrently (a wave interleaving 8 MFMAs with 64
+// independent FMAs takes the sum of the two times, at one and at two waves
+// per SIMD), so a call costs its rotation plus its commit.
 //
-// VALU work mapping: one workgroup = one (head, plane) and a run of tokens; its 16
-// waves share the FP32 rotation in LDS.  A wave takes 4 tokens per pass, 16
-// lanes per token.  Lane j of a token owns canonical lanes j and j + 16, i.e.
-// channels 4j..4j+3 and 64+4j..64+4j+3 of every record, in both phases:
-//  - rotation: per k, one LDS broadcast read brings x[token][k][records],
-//    two 16-byte reads bring the lane's 8 rotation entries, and the
-//    8 * records FMAs are plain VOP2 v_fmac_f32 (the full-rate form; the
-//    v_fma_mix and DPP forms issue at half rate).  Inputs are staged per
-//    wave as FP32 in a double-buffered LDS chunk of 32 k.
-//  - commit: the xor-16 level of the butterfly is the in-lane sum of the two
-//    canonical lanes, the other levels and the group min/max run across the
-//    16 lanes of the token with DPP.
+// Commit lanes: a wave commits 4 tokens at a time, 16 lanes per token.  Lane
+// j of a token owns canonical lanes j and j + 16, i.e. channels 4j..4j+3 and
+// 64+4j..64+4j+3 of every record; the xor-16 level of the butterfly is the
+// in-lane sum of the two canonical lanes, the other levels and the group
+// min/max run across the 16 lanes of the token with DPP.
 #include "rq_device.h"
 #include "rq_kernels.h"
 
@@ -41,12 +32,6 @@
 namespace rq {
 
 namespace {
-
-constexpr int kQuantizeWaves = 16;
-constexpr int kQuantizeThreads = 64 * kQuantizeWaves;
-constexpr int kWaveTokens = 4;    // tokens per wave per pass, 16 lanes each
-constexpr int kChunk = 32;        // k per staged input chunk
-constexpr int kStageRecords = 4;  // record slots per staged (token, k)
 
 // ---------------------------------------------------------------- lanes
 
@@ -288,190 +273,8 @@ __device__ __forceinline__ void commit_record(float (&x)[2][4], const bool (&act
 }
 
 // ---------------------------------------------------------------- kernel
-
-template <int D, int R, int A>
-__global__ __launch_bounds__(kQuantizeThreads) void quantize_kernel(QuantizeParams p, int block_tokens) {
-    // FP32 rotation [k][D], per-record key means [R][D], the per-wave input
-    // stage [wave][buffer][token][k][record] and RN(1/scale) per E4M3 code.
-    __shared__ float stage[kQuantizeWaves][2][kWaveTokens][kChunk][kStageRecords];
-    __shared__ float rotation_lds[D * D];
-    __shared__ float mean_lds[R * D];
-    __shared__ float inverse_scale[128];
-
-    const int plane = blockIdx.z;
-    const int head = blockIdx.y;
-    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int lane64 = threadIdx.x & 63;
-    const int group = lane64 >> 4;  // token of the pass
-    const int j = lane64 & 15;
-    const bool active[2] = {4 * j < D, 4 * (j + 16) < D};
-    const int column[2] = {4 * j, active[1] ? 64 + 4 * j : 64};
-
-    const uint16_t* rotation = plane == 0 ? p.key_rotation : p.value_rotation;
-    if (rotation != nullptr) {
-        const uint4* source = reinterpret_cast<const uint4*>(rotation + (int64_t)head * D * D);
-        for (int i = threadIdx.x; i < D * D / 8; i += kQuantizeThreads) {
-            const uint4 v = source[i];
-            const uint32_t w[4] = {v.x, v.y, v.z, v.w};
-            float f[8];
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                f[2 * e] = (float)__builtin_bit_cast(_Float16, (uint16_t)(w[e] & 0xffffu));
-                f[2 * e + 1] = (float)__builtin_bit_cast(_Float16, (uint16_t)(w[e] >> 16));
-            }
-            *reinterpret_cast<float4*>(&rotation_lds[8 * i]) = make_float4(f[0], f[1], f[2], f[3]);
-            *reinterpret_cast<float4*>(&rotation_lds[8 * i + 4]) = make_float4(f[4], f[5], f[6], f[7]);
-        }
-    }
-    const bool has_mean = plane == 0 && p.key_mean != nullptr;
-    if (has_mean)
-        for (int i = threadIdx.x; i < R * D; i += kQuantizeThreads)
-            mean_lds[i] = p.key_mean[((int64_t)(i / D) * p.heads + head) * D + i % D];
-    if (threadIdx.x < 128) {
-        const uint32_t code = threadIdx.x;
-        inverse_scale[code] = (code == 0 || code == 0x7f) ? 0.0f : 1.0f / e4m3_value(code);
-    }
-    __syncthreads();
-
-    const int64_t block_first = (int64_t)blockIdx.x * block_tokens;
-    const int64_t block_end = block_first + block_tokens < p.tokens ? block_first + block_tokens : p.tokens;
-    // Stage loader role: token `load_token`, record `load_record`, 8-k segment `segment`.
-    const int load_token = lane64 >> 4;
-    const int load_record = (lane64 >> 2) & 3;
-    const int segment = lane64 & 3;
-
-    for (int64_t first = block_first + wave * kWaveTokens; first < block_end;
-         first += kQuantizeWaves * kWaveTokens) {
-        float x[R][2][4];
-
-        if (rotation != nullptr) {
-            const int64_t n_load = first + load_token < block_end ? first + load_token : block_end - 1;
-            const uint16_t* row = nullptr;
-            if (load_record < R)
-                row = (plane == 0 ? p.key_ptrs[load_record] + n_load * p.key_strides[load_record]
-                                  : p.value_ptrs[load_record] + n_load * p.value_strides[load_record]) +
-                      head * D + 8 * segment;
-            float (*buffers)[kWaveTokens][kChunk][kStageRecords] = stage[wave];
-            auto stage_chunk = [&](uint4 v, int buffer) {
-                if (load_record < R) {
-                    const uint32_t w[4] = {v.x, v.y, v.z, v.w};
-#pragma unroll
-                    for (int e = 0; e < 4; ++e) {
-                        buffers[buffer][load_token][8 * segment + 2 * e][load_record] = bf16_f32(w[e] & 0xffffu);
-                        buffers[buffer][load_token][8 * segment + 2 * e + 1][load_record] = bf16_f32(w[e] >> 16);
-                    }
-                }
-            };
-            // Rows are only guaranteed 8-byte aligned: two 8-byte loads per segment.
-            auto load_segment = [&](int chunk) {
-                const uint2* source = reinterpret_cast<const uint2*>(row + chunk * kChunk);
-                const uint2 a = source[0], b = source[1];
-                return make_uint4(a.x, a.y, b.x, b.y);
-            };
-            uint4 incoming = load_record < R ? load_segment(0) : make_uint4(0, 0, 0, 0);
-            stage_chunk(incoming, 0);
-
-            float acc[R][2][4];
-#pragma unroll
-            for (int r = 0; r < R; ++r)
-#pragma unroll
-                for (int h = 0; h < 2; ++h)
-#pragma unroll
-                    for (int i = 0; i < 4; ++i) acc[r][h][i] = 0.f;
-
-#pragma unroll 1
-            for (int chunk = 0; chunk < D / kChunk; ++chunk) {
-                const bool more = chunk + 1 < D / kChunk;
-                if (more && load_record < R) incoming = load_segment(chunk + 1);
-                // Operands of step k + 1 are read while step k computes.
-                const float4* xs_row = reinterpret_cast<const float4*>(&buffers[chunk & 1][group][0][0]);
-                const float* ra_row = rotation_lds + chunk * kChunk * D + column[0];
-                const float* rb_row = rotation_lds + chunk * kChunk * D + column[1];
-                float4 xv = xs_row[0];
-                float4 ra = *reinterpret_cast<const float4*>(ra_row);
-                float4 rb = *reinterpret_cast<const float4*>(rb_row);
-#pragma unroll 8
-                for (int k = 0; k < kChunk; ++k) {
-                    const int next = k + 1 < kChunk ? k + 1 : k;  // the last step re-reads its own row
-                    const float4 xn = xs_row[next];
-                    const float4 an = *reinterpret_cast<const float4*>(ra_row + next * D);
-                    const float4 bn = *reinterpret_cast<const float4*>(rb_row + next * D);
-                    __builtin_amdgcn_sched_barrier(0);  // keep the prefetch above this step's FMAs
-                    const float xs[4] = {xv.x, xv.y, xv.z, xv.w};
-                    const float rs[2][4] = {{ra.x, ra.y, ra.z, ra.w}, {rb.x, rb.y, rb.z, rb.w}};
-#pragma unroll
-                    for (int r = 0; r < R; ++r)
-#pragma unroll
-                        for (int h = 0; h < 2; ++h)
-#pragma unroll
-                            for (int i = 0; i < 4; ++i) acc[r][h][i] = fmaf(xs[r], rs[h][i], acc[r][h][i]);
-                    xv = xn;
-                    ra = an;
-                    rb = bn;
-                }
-                // The stage is private to this wave and one wave's LDS
-                // operations complete in order, so no barrier is needed.
-                if (more) stage_chunk(incoming, (chunk + 1) & 1);
-            }
-#pragma unroll
-            for (int r = 0; r < R; ++r)
-#pragma unroll
-                for (int h = 0; h < 2; ++h)
-#pragma unroll
-                    for (int i = 0; i < 4; ++i) x[r][h][i] = active[h] ? acc[r][h][i] : 0.f;
-        } else {
-            const int64_t n = first + group < block_end ? first + group : block_end - 1;
-#pragma unroll
-            for (int r = 0; r < R; ++r) {
-                const uint16_t* src = (plane == 0 ? p.key_ptrs[r] + n * p.key_strides[r]
-                                                  : p.value_ptrs[r] + n * p.value_strides[r]) + head * D;
-#pragma unroll
-                for (int h = 0; h < 2; ++h) {
-                    uint2 v = make_uint2(0, 0);
-                    if (active[h]) v = *reinterpret_cast<const uint2*>(src + column[h]);
-                    x[r][h][0] = bf16_f32(v.x & 0xffffu);
-                    x[r][h][1] = bf16_f32(v.x >> 16);
-                    x[r][h][2] = bf16_f32(v.y & 0xffffu);
-                    x[r][h][3] = bf16_f32(v.y >> 16);
-                }
-            }
-        }
-
-        // Commit phase: lanes 16g..16g+15 own token first + g.
-        const int64_t n = first + group;
-        int64_t slot = -1;
-        if (n < block_end) slot = p.slots[n];
-        const bool valid = slot >= 0 && (slot >> p.page_shift) < p.num_blocks;
-        uint8_t* page = nullptr;
-        int token = 0;
-        if (valid) {
-            const int64_t block = slot >> p.page_shift;
-            token = (int)(slot & (p.page_tokens - 1));
-            page = p.cache + plane * p.plane_stride + (block * p.heads + head) * (int64_t)p.page_tokens * p.page_width;
-        }
-
-        float reference[2][4] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};  // restored BF16 values
-        // Anchor first, then every other record ascending (kernel.cuh:321-329).
-#pragma unroll
-        for (int step = 0; step < R; ++step) {
-            const int r = step == 0 ? A : (step - 1 < A ? step - 1 : step);
-            const bool is_anchor = r == A;
-            float mean[2][4];
-#pragma unroll
-            for (int h = 0; h < 2; ++h) {
-                float4 m = make_float4(0.f, 0.f, 0.f, 0.f);
-                if (has_mean && active[h]) m = *reinterpret_cast<const float4*>(&mean_lds[r * D + column[h]]);
-                mean[h][0] = m.x; mean[h][1] = m.y; mean[h][2] = m.z; mean[h][3] = m.w;
-            }
-            commit_record(x[r], active, is_anchor, is_anchor || p.adjacent, p.coefficient, mean, has_mean,
-                          reference, p.region[r], page, token, p.page_tokens, j, valid, inverse_scale);
-        }
-    }
-}
-
-// ---------------------------------------------------------------- MFMA rotation kernel
 //
-// The same quantize with the rotation on the matrix cores.  A chain of K = 1
+// The rotation on the matrix cores: a chain of K = 1
 // FP32 MFMAs (v_mfma_f32_16x16x1_4b_f32) accumulates each output with one
 // rounding per step in k order, i.e. exactly the k-ascending fmaf chain
 // (checked on gfx950 including subnormals, signed zeros and cancellation).
@@ -526,19 +329,52 @@ __global__ __launch_bounds__(kMfmaThreads) void quantize_mfma_kernel(QuantizePar
     const bool active[2] = {4 * j < D, 4 * (j + 16) < D};
     const int column[2] = {4 * j, active[1] ? 64 + 4 * j : 64};
 
+    // Prologue loads all go out before any of them is waited for: the
+    // rotation as 16-byte chunks (8 consecutive columns of one row; the
+    // addresses are 16-byte aligned, checked on the host) and the key means.
+    // Staged one 2-byte load per iteration, each waiting for the last, the
+    // rotation took 16 memory round trips per workgroup.
+    constexpr int kRowChunks = D / 8;
+    constexpr int kRotationChunks = D * kRowChunks;
+    constexpr int kChunksPerThread = (kRotationChunks + kMfmaThreads - 1) / kMfmaThreads;
+    uint4 chunk_words[kChunksPerThread];
     if constexpr (Rotated) {
         const uint16_t* rotation = plane == 0 ? p.key_rotation : p.value_rotation;
-        const uint16_t* source = rotation + (int64_t)head * D * D;
-        for (int i = threadIdx.x; i < D * 128; i += kMfmaThreads) {
-            const int k = i >> 7, c = i & 127;
-            const float v = c < D ? (float)__builtin_bit_cast(_Float16, source[k * D + c]) : 0.f;
-            rotation_lds[((k >> 1) * 64 + (c & 63)) * 4 + 2 * (k & 1) + (c >> 6)] = v;
+        const uint4* source = reinterpret_cast<const uint4*>(rotation + (int64_t)head * D * D);
+#pragma unroll
+        for (int u = 0; u < kChunksPerThread; ++u) {
+            const int i = (int)threadIdx.x + u * kMfmaThreads;
+            chunk_words[u] = i < kRotationChunks ? source[i] : make_uint4(0u, 0u, 0u, 0u);
         }
     }
     const bool has_mean = plane == 0 && p.key_mean != nullptr;
-    if (has_mean)
-        for (int i = threadIdx.x; i < R * D; i += kMfmaThreads)
-            mean_lds[i] = p.key_mean[((int64_t)(i / D) * p.heads + head) * D + i % D];
+    float mean_value = 0.f;
+    static_assert(R * D <= kMfmaThreads, "one key mean per thread");
+    if (has_mean && (int)threadIdx.x < R * D)
+        mean_value = p.key_mean[((int64_t)(threadIdx.x / D) * p.heads + head) * D + threadIdx.x % D];
+    if constexpr (Rotated) {
+        // Element (k, c) sits at [k / 2][c % 64][2 (k % 2) + c / 64]; columns
+        // from D to 127 (D = 96) are zeros.
+#pragma unroll
+        for (int u = 0; u < kChunksPerThread; ++u) {
+            const int i = (int)threadIdx.x + u * kMfmaThreads;
+            if (i < kRotationChunks) {
+                const int k = i / kRowChunks, c0 = 8 * (i % kRowChunks);
+                const uint32_t w[4] = {chunk_words[u].x, chunk_words[u].y, chunk_words[u].z, chunk_words[u].w};
+                float* dst = rotation_lds + ((k >> 1) * 64 + (c0 & 63)) * 4 + 2 * (k & 1) + (c0 >> 6);
+#pragma unroll
+                for (int e = 0; e < 8; ++e)
+                    dst[4 * e] = (float)__builtin_bit_cast(_Float16, (uint16_t)(w[e >> 1] >> (16 * (e & 1))));
+            }
+        }
+        if constexpr (D < 128) {
+            for (int i = threadIdx.x; i < D * (128 - D); i += kMfmaThreads) {
+                const int k = i / (128 - D), c = D + i % (128 - D);
+                rotation_lds[((k >> 1) * 64 + (c & 63)) * 4 + 2 * (k & 1) + (c >> 6)] = 0.f;
+            }
+        }
+    }
+    if (has_mean && (int)threadIdx.x < R * D) mean_lds[threadIdx.x] = mean_value;
     if (threadIdx.x < 128) {
         const uint32_t code = threadIdx.x;
         inverse_scale[code] = (code == 0 || code == 0x7f) ? 0.0f : 1.0f / e4m3_value(code);
@@ -762,35 +598,13 @@ hipError_t launch_quantize_mfma(const QuantizeParams& p, hipStream_t stream) {
     return hipSuccess;
 }
 
-// From this many tokens the matrix-core kernel runs (one MI355X, C1 shapes,
-// median call after a settle phase): 26.7 vs 36.9 us at 128 tokens, 25.0 vs
-// 37.3 us at 256, within 3% either way from 512 to 2048.  Decode-step calls
-// (a few tokens) keep the VALU kernel.
-constexpr int64_t kMfmaMinTokens = 64;
-
-template <int D, int R, int A>
-hipError_t launch_quantize_kernel(const QuantizeParams& p, hipStream_t stream) {
-    if (p.tokens >= kMfmaMinTokens) return launch_quantize_mfma<D, R, A>(p, stream);
-    // A workgroup pass covers 64 tokens of one (head, plane).  Long calls give
-    // each workgroup several passes so the rotation staging is amortised,
-    // keeping about two workgroups per CU; short calls (decode steps) use one.
-    const int64_t per_pass = kQuantizeWaves * kWaveTokens;
-    const int64_t work = (p.tokens + per_pass - 1) / per_pass * p.heads * 2;
-    int64_t passes = work / 512;
-    passes = passes < 1 ? 1 : (passes > 8 ? 8 : passes);
-    const int block_tokens = (int)(per_pass * passes);
-    const dim3 grid((unsigned)((p.tokens + block_tokens - 1) / block_tokens), (unsigned)p.heads, 2);
-    hipLaunchKernelGGL((quantize_kernel<D, R, A>), grid, dim3(kQuantizeThreads), 0, stream, p, block_tokens);
-    return hipGetLastError();
-}
-
 template <int D, int R>
 hipError_t dispatch_anchor(const QuantizeParams& p, int anchor, hipStream_t stream) {
     switch (anchor) {
-        case 0: return launch_quantize_kernel<D, R, 0>(p, stream);
-        case 1: if constexpr (R > 1) return launch_quantize_kernel<D, R, 1>(p, stream); break;
-        case 2: if constexpr (R > 2) return launch_quantize_kernel<D, R, 2>(p, stream); break;
-        case 3: if constexpr (R > 3) return launch_quantize_kernel<D, R, 3>(p, stream); break;
+        case 0: return launch_quantize_mfma<D, R, 0>(p, stream);
+        case 1: if constexpr (R > 1) return launch_quantize_mfma<D, R, 1>(p, stream); break;
+        case 2: if constexpr (R > 2) return launch_quantize_mfma<D, R, 2>(p, stream); break;
+        case 3: if constexpr (R > 3) return launch_quantize_mfma<D, R, 3>(p, stream); break;
         default: break;
     }
     return hipErrorInvalidValue;

@@ -24,7 +24,7 @@ MEAN_ABS = 1e-3
 
 QUANTIZE_CASES = [
     # tokens, heads, dim, records, page_tokens, mode, anchor, coefficient, rotation, mean, skipped
-    # (calls of fewer than 64 tokens run the VALU kernel, 64 and more the matrix-core one)
+    # (short calls give workgroups one partial pass; the long ones several passes each)
     (37, 4, 128, OURO_G32, 16, "anchor", 3, "ls", True, True, 3),
     (20, 3, 128, OURO_G16, 16, "anchor", 3, "ls", True, False, 0),
     (19, 5, 96, OURO_G16, 16, "anchor", 3, "ls", True, True, 2),
@@ -32,8 +32,8 @@ QUANTIZE_CASES = [
     (9, 2, 128, ((2, 32),), 16, "anchor", 0, "unit", True, True, 0),
     (17, 2, 128, ((4, 32),) * 4, 16, "anchor", 3, "unit", False, False, 0),
     (25, 3, 96, ((2, 32),) * 4, 32, "anchor", 0, "ls", True, False, 4),
-    (64, 2, 128, ((4, 16), (2, 16)), 16, "adjacent", 0, "ls", True, True, 0),  # the first MFMA-kernel size
-    (63, 2, 128, OURO_G32, 16, "anchor", 3, "ls", True, True, 1),  # the last VALU-kernel size
+    (64, 2, 128, ((4, 16), (2, 16)), 16, "adjacent", 0, "ls", True, True, 0),
+    (63, 2, 128, OURO_G32, 16, "anchor", 3, "ls", True, True, 1),
     (300, 4, 128, OURO_G32, 16, "anchor", 3, "norm", True, True, 7),
     (2100, 2, 128, OURO_G32, 16, "anchor", 3, "ls", True, True, 5),
     (2048, 2, 96, OURO_G16, 16, "anchor", 3, "ls", True, True, 3),
