@@ -107,7 +107,11 @@ int compute_units() {
 // Splits per (row, head): enough workgroups for `target` (by default
 // `per_cu` per compute unit: two for the streaming decode kernels, whose long
 // page streams per workgroup measured best at batch 32 x 8k, one at D = 96),
-// at least 4 pages per split, at most rq::kMaxSplits.
+// at least 16 pages per split, at most rq::kMaxSplits.  With 4 pages per
+// split a one-row call's 512 workgroups spent their time in the prologue and
+// the merge: 4-call step at batch 1, 16 heads, 2048 history 90.3 -> 74.1 us
+// with 16 pages (4096: 93.3 -> 83.9 us; 8192 and every batch-8 shape keep
+// their counts and times).
 int split_count(int64_t rows, int heads, int64_t max_pages, int per_cu = 2) {
     int64_t target;
     {
@@ -117,7 +121,7 @@ int split_count(int64_t rows, int heads, int64_t max_pages, int per_cu = 2) {
     if (target <= 0) target = (int64_t)per_cu * compute_units();
     const int64_t pairs = std::max<int64_t>(1, rows * heads);
     int64_t splits = (target + pairs - 1) / pairs;
-    const int64_t by_pages = std::max<int64_t>(1, (max_pages + 3) / 4);
+    const int64_t by_pages = std::max<int64_t>(1, (max_pages + 15) / 16);
     splits = std::min<int64_t>(splits, std::min<int64_t>(by_pages, rq::kMaxSplits));
     return (int)std::max<int64_t>(1, splits);
 }
