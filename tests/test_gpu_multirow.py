@@ -87,6 +87,8 @@ CASES = [
     ([2100], [3], 2, OURO_G16, 16, False, True, 96, "anchor"),           # eight history splits
     ([77, 50], [5, 0], 1, ((4, 16),), 16, True, False, 96, "anchor"),    # single-record group, no rotation
     ([300, 60, 9], [33, 1, 2], 2, OURO_G16, 32, True, True, 96, "anchor"),  # 16-row tiles, three in one request
+    # 8 requests x 55 heads: 440 (request, head, tile) groups, one history split each
+    ([260, 131, 99, 64, 300, 17, 180, 222], [2] * 8, 55, OURO_G16, 16, True, True, 96, "anchor"),
     # adjacent mode (every loop past 0 rebuilds the restore chain of records 0..L)
     ([100, 37, 9], [4, 1, 8], 3, ADJACENT_G32, 16, True, True, 128, "adjacent"),
     ([300, 40], [33, 2], 2, ADJACENT_G16, 32, True, True, 128, "adjacent"),
